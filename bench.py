@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-matmul path (one GPU).
+
+Headline (BASELINE.json metric, config 1): q4_0 GEMV, M=1, K=4096 -> N=14336,
+reported as algorithmic GB/s (packed weight bytes + 4K + 4N per step, the
+reference's bytes_moved, benchmarks/cases/qgemv.cpp:119-124).  A "step" is
+one GEMV over one synthetic batch; the K timed steps are captured in one HIP
+graph and replayed once, between two device synchronisations.  Each step
+reads a different copy of the weights (ceil(256 MB / footprint) + 1 copies)
+so that every step streams from HBM, not from the 256 MB Infinity Cache.
+
+Secondary lines (same discipline) cover the other BASELINE configs: q8_0 GEMV
+(config 0), q4_0 K=14336 -> N=4096, the q8_0 small-batch GEMM (config 2), the
+activation quantizer and the W8A8 GEMM at M=2048 (config 3).
+
+cpu_baseline: the reference's own x86 route for the headline op (AVX2
+q4_rows, compiled from the reference sources into oracle/_ref by
+oracle/Makefile), timed on this host's cores; the same call provides the
+correctness gate of the GPU result before its number is reported.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "quixicore-cpu_amd"))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published (POP/s)
+FP32_PEAK_TFLOPS = 157.3     # MI355X fp32, published
+MALL_BYTES = 256 << 20       # Infinity Cache
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--only", choices=["headline", "all"], default="all")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--rows-per-wave", type=int, default=0)
+    return p.parse_args()
+
+
+def rotation(footprint):
+    return int(math.ceil(MALL_BYTES / footprint)) + 1
+
+
+def time_steps(launch, steps, warmup):
+    """W eager warmup steps, then exactly K steps captured in one graph and
+    replayed between synchronisations.  Returns (wall ms/step, GPU ms/step
+    from HIP events recorded on the launch stream around the replay)."""
+    import torch
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            launch(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            launch(warmup + i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / steps
+    gpu_ms = start.elapsed_time(end) / steps
+    del graph
+    return wall_ms, gpu_ms
+
+
+def gemv_case(qc, fmt, n, k, steps, warmup, seed):
+    """Rotated copies of packed weights; returns timing and one output."""
+    import torch
+    dev = torch.device("cuda:0")
+    bb = qc.BLOCK_BYTES[fmt]
+    wbytes = n * (k // 32) * bb
+    copies = rotation(wbytes)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    packs = []
+    for c in range(copies):
+        w = torch.randn((n, k), generator=g, device=dev) * 0.02
+        packs.append(qc.pack(fmt, w))
+        del w
+    x = torch.randn(k, generator=g, device=dev)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+
+    def launch(i):
+        st = qc.qgemv_raw(fmt, packs[i % copies], x, y, n, k)
+        if st:
+            raise RuntimeError(f"qgemv status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    alg = wbytes + 4 * k + 4 * n
+    return {"bytes": alg, "weight_bytes": wbytes, "copies": copies, "wall_ms": wall,
+            "gpu_ms": gpu, "gbs": alg / (wall * 1e-3) / 1e9,
+            "kernel_gbs": alg / (gpu * 1e-3) / 1e9}, packs[0], x, y
+
+
+def qgemm_case(qc, n, k, m, steps, warmup, seed):
+    import torch
+    dev = torch.device("cuda:0")
+    wbytes = n * (k // 32) * 34
+    copies = rotation(wbytes + 4 * m * k)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    packs = [qc.pack(0, torch.randn((n, k), generator=g, device=dev) * 0.02) for _ in range(copies)]
+    x = torch.randn((m, k), generator=g, device=dev)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+
+    def launch(i):
+        st = qc.qgemm_raw(0, packs[i % copies], x, y, m, n, k)
+        if st:
+            raise RuntimeError(f"qgemm status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    alg = wbytes + 4 * m * k + 4 * m * n
+    flops = 2.0 * m * n * k
+    return {"m": m, "n": n, "k": k, "bytes": alg, "wall_ms": wall, "gpu_ms": gpu,
+            "gbs": alg / (wall * 1e-3) / 1e9, "kernel_gbs": alg / (gpu * 1e-3) / 1e9,
+            "kernel_tflops": flops / (gpu * 1e-3) / 1e12}
+
+
+def quant_case(qc, m, k, steps, warmup):
+    import torch
+    dev = torch.device("cuda:0")
+    fp = 4 * m * k + m * k + 4 * m
+    copies = rotation(fp)
+    xs = [torch.randn((m, k), device=dev) for _ in range(copies)]
+    codes = torch.empty((m, k), dtype=torch.int8, device=dev)
+    scales = torch.empty((m, 1), dtype=torch.float32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def launch(i):
+        st = qc.quantize_int8_raw(xs[i % copies], codes, scales, m, k, 0, status)
+        if st:
+            raise RuntimeError(f"quantize status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu,
+            "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
+
+
+def w8a8_case(qc, m, n, k, steps, warmup):
+    import torch
+    dev = torch.device("cuda:0")
+    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev)
+    x = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev)
+    ws = torch.rand(n, device=dev) * 0.01
+    as_ = torch.rand(m, device=dev) * 0.1
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def launch(i):
+        st = qc.int8_gemm_raw(w, x, ws, as_, None, None, y, m, n, k, False, status)
+        if st:
+            raise RuntimeError(f"int8_gemm status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    ops = 2.0 * m * n * k
+    return {"m": m, "n": n, "k": k, "ops": ops, "wall_ms": wall, "gpu_ms": gpu,
+            "tops": ops / (wall * 1e-3) / 1e12, "kernel_tops": ops / (gpu * 1e-3) / 1e12}
+
+
+def cpu_baseline(packed_dev, x_dev, y_dev, n, k, seconds):
+    """Reference x86 q4_0 route (oracle/_ref) on this host: timing + gate."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+    if not oracle.Reference.available():
+        return None, None
+    ref = oracle.Reference()
+    packed = packed_dev.cpu().numpy()
+    x = x_dev.cpu().numpy()
+    y_gpu = y_dev.cpu().numpy()
+    # correctness gate: GPU vs f64 contract oracle (1e-4 normalised) and vs
+    # the reference's own f32 output
+    y64, wn = oracle.gemv_f64(oracle.Q4_0, packed, x, n, k)
+    ok, worst = oracle.within_contract(y_gpu, y64, wn, x, 1e-4)
+    y_ref = ref.gemv(oracle.Q4_0, packed, x, n, k)
+    ok_ref, worst_ref = oracle.within_contract(y_gpu, y_ref.astype(np.float64), wn, x, 1e-4)
+    gate = {"pass": bool(ok and ok_ref), "max_norm_err_vs_f64": worst,
+            "max_norm_err_vs_reference": worst_ref}
+
+    def timed(threads, budget):
+        ref.set_threads(threads)
+        y = np.empty(n, dtype=np.float32)
+        t_end = time.perf_counter() + 0.05
+        calls = 0
+        while calls < 3 or time.perf_counter() < t_end:     # warmup >= 3 calls and >= 50 ms
+            ref.lib.qcref_q4_0_gemv_avx2(oracle._ptr(packed), oracle._ptr(x), oracle._ptr(y), n, k)
+            calls += 1
+        samples = []
+        deadline = time.perf_counter() + budget
+        while len(samples) < 20 or time.perf_counter() < deadline:
+            t0 = time.perf_counter()
+            reps = 0
+            while True:                                      # batch >= 2 ms
+                ref.lib.qcref_q4_0_gemv_avx2(oracle._ptr(packed), oracle._ptr(x), oracle._ptr(y),
+                                             n, k)
+                reps += 1
+                if time.perf_counter() - t0 >= 2e-3:
+                    break
+            samples.append((time.perf_counter() - t0) / reps)
+        return float(np.median(samples)), len(samples)
+
+    threads = min(16, os.cpu_count() or 1)
+    alg = n * (k // 32) * 18 + 4 * k + 4 * n
+    t_all, s_all = timed(threads, seconds * 0.7)
+    t_one, s_one = timed(1, seconds * 0.3)
+    ref.set_threads(1)
+    base = {"value": alg / t_all / 1e9, "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": (f"reference gguf_gemv_avx2 (q4_rows) q4_0 GEMV K={k} N={n} on the same "
+                       f"packed bytes, median of {s_all} samples (>=2 ms batches, "
+                       f"~{seconds * 0.7:.0f} s) at {threads} threads"),
+            "value_1thread": alg / t_one / 1e9, "ms_per_call": t_all * 1e3,
+            "ms_per_call_1thread": t_one * 1e3}
+    return base, gate
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is design-only (see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import quixicore_hip as qc
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    if args.rows_per_wave:
+        qc.set_gemv_rows_per_wave(args.rows_per_wave)
+    K, W = args.steps, args.warmup
+    n, k = 14336, 4096
+    head, packed, x, y = gemv_case(qc, 1, n, k, K, W, seed=1)
+    print(f"# headline q4_0 GEMV K={k} N={n}: {head['gbs']:.1f} GB/s wall, "
+          f"{head['kernel_gbs']:.1f} GB/s kernel ({head['gpu_ms'] * 1e3:.2f} us)",
+          file=sys.stderr, flush=True)
+    secondary = {}
+    if args.only == "all":
+        s = {}
+        r, *_ = gemv_case(qc, 0, 4096, 4096, K, W, seed=2)
+        s["q8_0_gemv_k4096_n4096"] = r
+        r, *_ = gemv_case(qc, 1, 4096, 14336, K, W, seed=3)
+        s["q4_0_gemv_k14336_n4096"] = r
+        for m in (4, 8, 16, 32):
+            s[f"q8_0_qgemm_m{m}_k4096_n14336"] = qgemm_case(qc, 14336, 4096, m, K, W, seed=4 + m)
+        s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
+        s["w8a8_m2048_k4096_n4096"] = w8a8_case(qc, 2048, 4096, 4096, max(20, K // 4), W)
+        s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, max(20, K // 4), W)
+        for key, r in s.items():
+            print(f"# {key}: " + ", ".join(f"{a}={b:.4g}" if isinstance(b, float) else f"{a}={b}"
+                                          for a, b in r.items()), file=sys.stderr, flush=True)
+        secondary = s
+    base, gate = (None, None)
+    if not args.no_cpu:
+        base, gate = cpu_baseline(packed, x, y, n, k, args.cpu_seconds)
+    achieved = head["kernel_gbs"]
+    line = {
+        "metric": "q4_0 GEMV GB/s (% HBM peak) at K4096xN14336",
+        "value": round(head["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": head["wall_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights (u8 nibbles + fp16 scales), f32 activations/accumulation",
+        "data": ("synthetic: torch-seeded N(0,0.02) f32 weights packed to q4_0 on the GPU, "
+                 f"{head['copies']} rotated copies (HBM-resident, > Infinity Cache); x ~ N(0,1)"),
+        "config": {"workload": "qgemv q4_0 M=1 K=4096 N=14336 (BASELINE config 1, up/gate)",
+                   "m": 1, "k": k, "n": n, "bytes_per_step": head["bytes"],
+                   "weight_bytes_per_step": head["weight_bytes"],
+                   "parallelism": "single GPU"},
+        "pct_hbm_peak": round(100.0 * head["gbs"] / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel_us": round(head["gpu_ms"] * 1e3, 3)},
+        "cpu_baseline": base,
+        "check": gate,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,71 @@
+// Drop-in of the qgemv family (include/quixicore_cpu/qgemv.h of the
+// reference), for q8_0 and q4_0 on gfx950.  Same names, argument order and
+// Status semantics; every call is synchronous (outputs are ready on return).
+// Pointers may be host or device memory: device pointers are used in place,
+// host buffers are staged through device memory.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "quixicore_cpu/status.h"
+
+namespace quixicore_cpu {
+
+// Numbering kept from include/quixicore_cpu/qgemv.h:10-47 of the reference so
+// stored format ids stay valid; only kQ8_0 and kQ4_0 have kernels here.
+enum class QuantFormat {
+  kQ8_0,  // GGUF q8_0: 32-element blocks, fp16 scale + 32 int8 values
+  kQ4_0,  // GGUF q4_0: 32-element blocks, fp16 scale + 16 packed nibbles (-8 offset)
+  kQ4_1,
+  kQ5_0,
+  kQ5_1,
+  kU4B8,
+  kU4,
+  kHQQ,
+  kFP8E4M3,
+  kFP8E5M2,
+  kFP8Block,
+  kFP8Raw,
+  kFP4E2M1,
+  kMXFP8,
+  kNVFP4,
+  kMXFP4,
+  kMXFP6E3M2,
+  kMXFP6E2M3,
+  kBitnet,
+  kQ2_K,
+  kQ3_K,
+  kQ4_K,
+  kQ5_K,
+  kQ6_K,
+  kIQ4_NL,
+  kIQ4_XS,
+  kIQ2_XXS,
+  kIQ2_XS,
+  kIQ3_XXS,
+  kIQ1_S,
+  kTQ2_0,
+  kQ1_0,
+  kQ2_0,
+  kIQ3_S,
+  kIQ2_S,
+  kIQ1_M,
+  kTQ1_0,
+};
+
+// include/quixicore_cpu/qgemv.h:70
+Status qgemv_packed_size(QuantFormat format, long long n, long long k, size_t* size);
+// include/quixicore_cpu/qgemv.h:77 (bit-identical blocks, packed on the GPU)
+Status qgemv_pack(QuantFormat format, const float* weights, long long n, long long k,
+                  void* packed);
+// include/quixicore_cpu/qgemv.h:89
+Status qgemv_unpack(QuantFormat format, const void* packed, long long n, long long k,
+                    float* weights);
+// include/quixicore_cpu/qgemv.h:108: y = dequantize(wq) @ x, f32 accumulation.
+Status qgemv(QuantFormat format, const void* packed, const float* x, float* y, long long n,
+             long long k);
+// include/quixicore_cpu/qgemv.h:166
+const char* qgemv_variant(QuantFormat format);
+
+}  // namespace quixicore_cpu

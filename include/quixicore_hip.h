@@ -1,0 +1,131 @@
+/*
+ * quixicore_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul path.
+ *
+ * Drop-in for the reference QuixiAI/QuixiCore-CPU ops listed beside each
+ * entry point (paths relative to the reference root).  Plain C: pointers,
+ * sizes and an opaque stream; no C++ or torch types.
+ *
+ * Conventions
+ *   - Return value: the reference Status integers
+ *     (include/quixicore_cpu/status.h:5-11) -- 0 kOk, 1 kInvalidShape,
+ *     2 kUnsupportedFormat, 3 kInvalidArgument, 4 kOutOfMemory -- plus
+ *     5 (QC_DEVICE_ERROR) when the HIP runtime rejects a launch or copy; that
+ *     value has no counterpart in the reference.  Host-visible validation
+ *     runs first, in the reference's order, and nothing is launched on error.
+ *   - Tensor pointers are device pointers (hipMalloc, or managed memory)
+ *     unless stated otherwise.  `stream` is a hipStream_t or NULL for the null
+ *     stream.  Calls are asynchronous on `stream` unless stated otherwise.
+ *   - Data-dependent checks (non-finite values) cannot return synchronously
+ *     from an asynchronous call.  Entry points that have them take
+ *     `int* dev_status`: a device int the caller zeroes beforehand, which
+ *     the kernels set to 3 (kInvalidArgument) on a non-finite input.  Passing
+ *     dev_status == NULL selects the reference's synchronous semantics
+ *     instead: the inputs are scanned first, the call blocks, returns 3 and
+ *     writes no output if any value is non-finite.
+ *   - Results are deterministic: rerunning a call gives bit-identical output.
+ */
+#ifndef QUIXICORE_HIP_H
+#define QUIXICORE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QC_OK 0
+#define QC_INVALID_SHAPE 1
+#define QC_UNSUPPORTED_FORMAT 2
+#define QC_INVALID_ARGUMENT 3
+#define QC_OUT_OF_MEMORY 4
+#define QC_DEVICE_ERROR 5
+
+/* QuantFormat numbering (include/quixicore_cpu/qgemv.h:10-13). Other
+ * reference formats return QC_UNSUPPORTED_FORMAT. */
+#define QC_Q8_0 0
+#define QC_Q4_0 1
+
+/* Library version string, and the text of the last HIP error seen by this
+ * thread ("" if none). */
+const char* qc_hip_version(void);
+const char* qc_hip_last_error(void);
+
+/* Packed byte count of an n x k matrix: n * (k/32) * {34, 18}.  Host only.
+ * Replaces qgemv_packed_size (include/quixicore_cpu/qgemv.h:70;
+ * src/dispatch/qgemv.cpp:199-209). */
+int qc_hip_qgemv_packed_size(int format, long long n, long long k, size_t* size);
+
+/* Quantize row-major f32 weights w[n][k] (device) into canonical GGUF blocks
+ * (device), bit-identical to the reference packers.  Replaces qgemv_pack
+ * (include/quixicore_cpu/qgemv.h:77; src/dispatch/qgemv.cpp:210-275;
+ * kernels/quantization/qgemv_ref.cpp:14-41, qgemv_w8a8_ref.cpp:45-77).  As in
+ * the reference, blocks may be partially written when 3 is reported. */
+int qc_hip_qgemv_pack(int format, const float* w, long long n, long long k, void* packed,
+                      int* dev_status, void* stream);
+
+/* Dequantize blocks to f32 w[n][k].  Replaces qgemv_unpack
+ * (include/quixicore_cpu/qgemv.h:89; src/dispatch/qgemv.cpp:277-297). */
+int qc_hip_qgemv_unpack(int format, const void* packed, long long n, long long k, float* w,
+                        void* stream);
+
+/* y[n] = dequant(W) . x, f32 activations and accumulation.  Replaces qgemv
+ * (include/quixicore_cpu/qgemv.h:108; src/dispatch/qgemv.cpp:337-365). */
+int qc_hip_qgemv(int format, const void* packed, const float* x, float* y, long long n,
+                 long long k, void* stream);
+
+/* Y[m][n] = X[m][:] . dequant(W)[n][:].  Replaces qgemm
+ * (include/quixicore_cpu/qgemm.h:19; kernels/quantization/qgemm_ref.cpp:141-164);
+ * every row equals qc_hip_qgemv of that row within the contract tolerance. */
+int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long long m,
+                 long long n, long long k, void* stream);
+
+/* Per-group symmetric int8 quantization; group_size 0 means one group per
+ * row.  Bit-identical codes and scales.  Replaces quantize_int8
+ * (include/quixicore_cpu/quantization.h:42;
+ * kernels/quantization/quantization_ref.cpp:143-168).  With dev_status set,
+ * groups holding a non-finite value are left unwritten. */
+int qc_hip_quantize_int8(const float* x, int8_t* codes, float* scales, long long rows,
+                         long long dim, long long group_size, int* dev_status, void* stream);
+
+/* y[m][n] = (float(sum_k W[n][k]*X[m][k] - zp[m]*row_sum[n]) * ws[n]) * as[m]
+ * (the zp term only when asymmetric != 0).  Exact integer accumulation.
+ * Replaces int8_gemm (include/quixicore_cpu/qgemm.h:235;
+ * src/dispatch/int8_gemm.cpp:67-94).  With dev_status set, outputs are
+ * written and 3 is reported when any scale is non-finite. */
+int qc_hip_int8_gemm(const int8_t* w, const int8_t* x, const float* ws, const float* as,
+                     const int32_t* row_sum, const int* zp, float* y, long long m, long long n,
+                     long long k, int asymmetric, int* dev_status, void* stream);
+
+/* Symmetric alias.  Replaces qgemm_w8a8 (include/quixicore_cpu/qgemm.h:250;
+ * kernels/quantization/qgemm_extended_ref.cpp:142-147). */
+int qc_hip_qgemm_w8a8(const int8_t* w, const int8_t* x, const float* ws, const float* as,
+                      float* y, long long m, long long n, long long k, int* dev_status,
+                      void* stream);
+
+/* Test seam: the exact int32 accumulators sum_k W[n][k]*X[m][k] into
+ * acc[m][n] (k <= 131071).  No reference counterpart (the reference's
+ * accumulators are internal to kernels/quantization/int8_gemm_*.cpp). */
+int qc_hip_int8_gemm_i32(const int8_t* w, const int8_t* x, int32_t* acc, long long m,
+                         long long n, long long k, void* stream);
+
+/* Sets *dev_flag = 1 (device int, zeroed by the caller) if any of x[0..count)
+ * is NaN or infinite.  The device form of all_finite
+ * (kernels/quantization/quantization_ref.cpp:70-75). */
+int qc_hip_nonfinite_scan(const float* x, long long count, int* dev_flag, void* stream);
+
+/* Names of the routes the dispatch resolves to, like qgemv_variant
+ * (include/quixicore_cpu/qgemv.h:166) and int8_gemm_variant
+ * (include/quixicore_cpu/qgemm.h:240). */
+const char* qc_hip_qgemv_variant(int format);
+const char* qc_hip_int8_gemm_variant(void);
+
+/* Rows each GEMV wavefront keeps in flight (1, 2, 4 or 8; default 4). Tuning
+ * knob with no reference counterpart. */
+int qc_hip_set_gemv_rows_per_wave(int rows);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUIXICORE_HIP_H */

@@ -1,0 +1,246 @@
+"""ctypes front end of the CPU oracle -- TEST INFRASTRUCTURE ONLY.
+
+Loads oracle/liboracle.so (the plain-C restatement, qc_oracle.c) and, when it
+has been built, oracle/_ref/libqcref.so (the reference's own sources compiled
+by oracle/Makefile `ref`).  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg import this module, and only as the checker.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libqcref.so")
+
+Q8_0, Q4_0 = 0, 1
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+
+_P = ctypes.c_void_p
+_LL = ctypes.c_longlong
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def build():
+    subprocess.check_call(["make", "-s", "-C", HERE, "all"])
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.qco_fp16_to_fp32.restype = ctypes.c_float
+    lib.qco_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+    lib.qco_fp32_to_fp16.restype = ctypes.c_uint16
+    lib.qco_fp32_to_fp16.argtypes = [ctypes.c_float]
+    lib.qco_packed_size.argtypes = [ctypes.c_int, _LL, _LL, ctypes.POINTER(ctypes.c_size_t)]
+    lib.qco_pack.argtypes = [ctypes.c_int, _P, _LL, _LL, _P]
+    lib.qco_unpack.argtypes = [ctypes.c_int, _P, _LL, _LL, _P]
+    for name in ("qco_q8_0_gemv", "qco_q4_0_gemv_ref"):
+        getattr(lib, name).argtypes = [_P, _P, _P, _LL, _LL]
+        getattr(lib, name).restype = None
+    lib.qco_q4_0_gemv_avx2order.argtypes = [_P, _P, _P, _LL, _LL, ctypes.c_int]
+    lib.qco_q4_0_gemv_avx2order.restype = None
+    lib.qco_qgemv_f64.argtypes = [ctypes.c_int, _P, _P, _P, _P, _LL, _LL]
+    lib.qco_quantize_int8.argtypes = [_P, _P, _P, _LL, _LL, _LL]
+    lib.qco_int8_gemm.argtypes = [_P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, ctypes.c_int]
+    lib.qco_int8_gemm_entries.argtypes = [_P, _P, _P, _P, _P, _P, _LL, _LL, _P, _P]
+    lib.qco_int8_gemm_entries.restype = None
+    return lib
+
+
+lib = _load()
+
+
+def fp16_to_fp32(h: int) -> float:
+    return lib.qco_fp16_to_fp32(h)
+
+
+def fp32_to_fp16(f: float) -> int:
+    return lib.qco_fp32_to_fp16(f)
+
+
+def packed_size(fmt, n, k):
+    size = ctypes.c_size_t(0)
+    st = lib.qco_packed_size(fmt, n, k, ctypes.byref(size))
+    return st, size.value
+
+
+def pack(fmt, w: np.ndarray):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    st, size = packed_size(fmt, n, k)
+    if st:
+        return st, None
+    out = np.zeros(size, dtype=np.uint8)
+    st = lib.qco_pack(fmt, _ptr(w), n, k, _ptr(out))
+    return st, out
+
+
+def unpack(fmt, packed: np.ndarray, n, k):
+    out = np.empty((n, k), dtype=np.float32)
+    st = lib.qco_unpack(fmt, _ptr(packed), n, k, _ptr(out))
+    assert st == 0, st
+    return out
+
+
+def gemv(fmt, packed, x, n, k, order="reference"):
+    """f32 GEMV in the summation order of the reference's x86 route.
+
+    q8_0: the sequential ref kernel; q4_0: the AVX2 q4_rows order
+    (order="portable" selects q4_0_gemv_ref instead)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(n, dtype=np.float32)
+    if fmt == Q8_0:
+        lib.qco_q8_0_gemv(_ptr(packed), _ptr(x), _ptr(y), n, k)
+    elif order == "portable":
+        lib.qco_q4_0_gemv_ref(_ptr(packed), _ptr(x), _ptr(y), n, k)
+    else:
+        lib.qco_q4_0_gemv_avx2order(_ptr(packed), _ptr(x), _ptr(y), n, k, AVX2_FLAGS)
+    return y
+
+
+# Contraction pattern of the reference's AVX2 q4_0 build, pinned against
+# oracle/_ref in tests/test_oracle.py (bit 0: fused scale-add, bit 1: fused
+# lane-pair sum).
+AVX2_FLAGS = 3
+
+
+def gemv_f64(fmt, packed, x, n, k):
+    """f64 contract oracle over exactly dequantized weights, plus row norms."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(n, dtype=np.float64)
+    wn = np.empty(n, dtype=np.float64)
+    st = lib.qco_qgemv_f64(fmt, _ptr(packed), _ptr(x), _ptr(y), _ptr(wn), n, k)
+    assert st == 0, st
+    return y, wn
+
+
+def qgemm_f64(fmt, packed, x, n, k):
+    """Per-row contract oracle of qgemm (kernels/quantization/qgemm_ref.cpp:156-162)."""
+    m = x.shape[0]
+    y = np.empty((m, n), dtype=np.float64)
+    wn = None
+    for r in range(m):
+        y[r], wn = gemv_f64(fmt, packed, x[r], n, k)
+    return y, wn
+
+
+def quantize_int8(x: np.ndarray, group_size=0):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, dim = x.shape
+    g = dim if group_size == 0 else group_size
+    codes = np.zeros((rows, dim), dtype=np.int8)
+    scales = np.zeros((rows, dim // g if g and dim % g == 0 else 1), dtype=np.float32)
+    st = lib.qco_quantize_int8(_ptr(x), _ptr(codes), _ptr(scales), rows, dim, group_size)
+    return st, codes, scales
+
+
+def int8_gemm(w, x, ws, as_, row_sum=None, zp=None, asymmetric=False):
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.zeros((m, n), dtype=np.float32)
+    st = lib.qco_int8_gemm(_ptr(w), _ptr(x), _ptr(ws), _ptr(as_), _ptr(row_sum), _ptr(zp),
+                           _ptr(y), m, n, k, int(asymmetric))
+    return st, y
+
+
+def int8_gemm_entries(w, x, ws, as_, rows, cols):
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    cols = np.ascontiguousarray(cols, dtype=np.int64)
+    acc = np.empty(len(rows), dtype=np.int64)
+    y = np.empty(len(rows), dtype=np.float32)
+    lib.qco_int8_gemm_entries(_ptr(w), _ptr(x), _ptr(ws), _ptr(as_), _ptr(rows), _ptr(cols),
+                              len(rows), x.shape[1], _ptr(acc), _ptr(y))
+    return acc, y
+
+
+def within_contract(y, y64, wnorm, x, tol=1e-4):
+    """BASELINE gate: |y - y64| <= tol * ||x||_2 * ||w_hat_row||_2, per output."""
+    xn = float(np.linalg.norm(np.asarray(x, dtype=np.float64)))
+    err = np.abs(np.asarray(y, dtype=np.float64) - y64)
+    bound = tol * xn * wnorm
+    worst = float(np.max(err / np.maximum(bound, 1e-300) * tol)) if err.size else 0.0
+    return bool(np.all(err <= bound)), worst
+
+
+# ------------------------------------------------------------ reference ---
+
+class Reference:
+    """The reference's own compiled hot-path functions (oracle/_ref)."""
+
+    def __init__(self, path=REF_PATH):
+        self.lib = ctypes.CDLL(path)
+        L = self.lib
+        L.qcref_q8_0_pack.argtypes = [_P, _LL, _LL, _P]
+        L.qcref_q4_0_pack.argtypes = [_P, _LL, _LL, _P]
+        for name in ("qcref_q8_0_gemv", "qcref_q4_0_gemv_avx2", "qcref_q4_0_gemv_portable"):
+            getattr(L, name).argtypes = [_P, _P, _P, _LL, _LL]
+            getattr(L, name).restype = None
+        L.qcref_qgemm.argtypes = [ctypes.c_int, _P, _P, _P, _LL, _LL, _LL]
+        L.qcref_qgemm.restype = None
+        L.qcref_quantize_int8.argtypes = [_P, _P, _P, _LL, _LL, _LL]
+        L.qcref_int8_gemm.argtypes = [_P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, ctypes.c_int]
+        L.qcref_int8_gemm_variant.restype = ctypes.c_char_p
+        L.qcref_set_num_threads.argtypes = [ctypes.c_int]
+        L.qcref_set_num_threads.restype = None
+
+    @staticmethod
+    def available(path=REF_PATH):
+        return os.path.exists(path)
+
+    def pack(self, fmt, w):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        n, k = w.shape
+        out = np.zeros(n * (k // 32) * BLOCK_BYTES[fmt], dtype=np.uint8)
+        fn = self.lib.qcref_q8_0_pack if fmt == Q8_0 else self.lib.qcref_q4_0_pack
+        st = fn(_ptr(w), n, k, _ptr(out))
+        return st, out
+
+    def gemv(self, fmt, packed, x, n, k, portable=False):
+        y = np.empty(n, dtype=np.float32)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if fmt == Q8_0:
+            self.lib.qcref_q8_0_gemv(_ptr(packed), _ptr(x), _ptr(y), n, k)
+        elif portable:
+            self.lib.qcref_q4_0_gemv_portable(_ptr(packed), _ptr(x), _ptr(y), n, k)
+        else:
+            self.lib.qcref_q4_0_gemv_avx2(_ptr(packed), _ptr(x), _ptr(y), n, k)
+        return y
+
+    def qgemm(self, fmt, packed, x, n, k):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty((x.shape[0], n), dtype=np.float32)
+        self.lib.qcref_qgemm(fmt, _ptr(packed), _ptr(x), _ptr(y), x.shape[0], n, k)
+        return y
+
+    def quantize_int8(self, x, group_size=0):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, dim = x.shape
+        g = dim if group_size == 0 else group_size
+        codes = np.zeros((rows, dim), dtype=np.int8)
+        scales = np.zeros((rows, max(dim // g, 1)), dtype=np.float32)
+        st = self.lib.qcref_quantize_int8(_ptr(x), _ptr(codes), _ptr(scales), rows, dim,
+                                          group_size)
+        return st, codes, scales
+
+    def int8_gemm(self, w, x, ws, as_, row_sum=None, zp=None, asymmetric=False):
+        m, k = x.shape
+        n = w.shape[0]
+        y = np.zeros((m, n), dtype=np.float32)
+        st = self.lib.qcref_int8_gemm(_ptr(w), _ptr(x), _ptr(ws), _ptr(as_), _ptr(row_sum),
+                                      _ptr(zp), _ptr(y), m, n, k, int(asymmetric))
+        return st, y
+
+    def variant(self):
+        return self.lib.qcref_int8_gemm_variant().decode()
+
+    def set_threads(self, n):
+        self.lib.qcref_set_num_threads(n)

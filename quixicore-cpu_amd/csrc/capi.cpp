@@ -1,0 +1,261 @@
+// extern "C" boundary (include/quixicore_hip.h): host-visible validation in
+// the reference's order, then the HIP launches.  No compute happens on the
+// host and there is no CPU fallback: every result comes from a gfx950 kernel.
+#include "quixicore_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdlib>
+#include <cstring>
+#include <initializer_list>
+#include <limits>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "qc_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+qc::GemvTuning g_tuning;
+
+int device_error(hipError_t e) {
+  g_last_error = hipGetErrorString(e);
+  return QC_DEVICE_ERROR;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// kernels/common/validation.h:8-18 (valid_product).
+bool valid_product(std::initializer_list<long long> dims) {
+  long long product = 1;
+  for (long long d : dims) {
+    if (d <= 0 || product > LLONG_MAX / d) return false;
+    product *= d;
+  }
+  return true;
+}
+
+int block_bytes(int format) {
+  return format == QC_Q8_0 ? 34 : (format == QC_Q4_0 ? 18 : 0);
+}
+
+// src/dispatch/qgemv.cpp:125-141 (validate): format, then n, k > 0 and
+// k % 32 == 0, then the signed-offset overflow guard.  The int32 limit on n
+// and k is this library's (grid and index width).
+int validate(int format, long long n, long long k) {
+  if (block_bytes(format) == 0) return QC_UNSUPPORTED_FORMAT;
+  if (n <= 0 || k <= 0 || k % 32 != 0) return QC_INVALID_SHAPE;
+  if (n > LLONG_MAX / k || n > LLONG_MAX / (k / 32)) return QC_INVALID_SHAPE;
+  if (n > INT_MAX || k > INT_MAX) return QC_INVALID_SHAPE;
+  return QC_OK;
+}
+
+// src/dispatch/qgemv.cpp:151-164 (packed_size).
+int packed_bytes(int format, long long n, long long k, size_t* size) {
+  const size_t blocks_per_row = static_cast<size_t>(k / 32);
+  const size_t bb = static_cast<size_t>(block_bytes(format));
+  if (static_cast<size_t>(n) > std::numeric_limits<size_t>::max() / blocks_per_row)
+    return QC_INVALID_SHAPE;
+  const size_t blocks = static_cast<size_t>(n) * blocks_per_row;
+  if (blocks > std::numeric_limits<size_t>::max() / bb) return QC_INVALID_SHAPE;
+  *size = blocks * bb;
+  return QC_OK;
+}
+
+// One device int per device for the synchronous (dev_status == NULL) paths.
+struct Scratch {
+  std::mutex mu;
+  std::vector<int*> flag;
+};
+Scratch& scratch() {
+  static Scratch s;
+  return s;
+}
+
+int* device_flag(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  Scratch& s = scratch();
+  std::lock_guard<std::mutex> lock(s.mu);
+  if (static_cast<int>(s.flag.size()) <= dev) s.flag.resize(dev + 1, nullptr);
+  if (s.flag[dev] == nullptr) {
+    *err = hipMalloc(&s.flag[dev], sizeof(int));
+    if (*err != hipSuccess) {
+      s.flag[dev] = nullptr;
+      return nullptr;
+    }
+  }
+  return s.flag[dev];
+}
+
+// Runs `launch(flag)` with a zeroed device flag and returns its value.
+template <class F>
+int with_flag(hipStream_t s, int* value, F&& launch) {
+  hipError_t e = hipSuccess;
+  int* flag = device_flag(&e);
+  if (flag == nullptr) return device_error(e);
+  if ((e = hipMemsetAsync(flag, 0, sizeof(int), s)) != hipSuccess) return device_error(e);
+  if ((e = launch(flag)) != hipSuccess) return device_error(e);
+  if ((e = hipMemcpyAsync(value, flag, sizeof(int), hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return device_error(e);
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return device_error(e);
+  return QC_OK;
+}
+
+// Synchronous all_finite over a device array.
+int all_finite(const float* x, long long count, hipStream_t s, bool* finite) {
+  int bad = 0;
+  const int st = with_flag(s, &bad, [&](int* flag) {
+    return qc::launch_nonfinite_scan(x, count, flag, s);
+  });
+  *finite = bad == 0;
+  return st;
+}
+
+int finish(hipError_t e) { return e == hipSuccess ? QC_OK : device_error(e); }
+
+}  // namespace
+
+extern "C" {
+
+const char* qc_hip_version(void) { return "quixicore-hip 0.1 (gfx950)"; }
+
+const char* qc_hip_last_error(void) { return g_last_error.c_str(); }
+
+int qc_hip_qgemv_packed_size(int format, long long n, long long k, size_t* size) {
+  const int st = validate(format, n, k);
+  if (st != QC_OK) return st;
+  if (size == nullptr) return QC_INVALID_ARGUMENT;
+  return packed_bytes(format, n, k, size);
+}
+
+int qc_hip_qgemv_pack(int format, const float* w, long long n, long long k, void* packed,
+                      int* dev_status, void* stream) {
+  int st = validate(format, n, k);
+  if (st != QC_OK) return st;
+  size_t ignored = 0;
+  if (packed_bytes(format, n, k, &ignored) != QC_OK) return QC_INVALID_SHAPE;
+  if (w == nullptr || packed == nullptr) return QC_INVALID_ARGUMENT;
+  const hipStream_t s = as_stream(stream);
+  if (dev_status != nullptr) return finish(qc::launch_pack(format, w, packed, n, k, dev_status, s));
+  int bad = 0;
+  st = with_flag(s, &bad, [&](int* flag) { return qc::launch_pack(format, w, packed, n, k, flag, s); });
+  if (st != QC_OK) return st;
+  return bad ? QC_INVALID_ARGUMENT : QC_OK;
+}
+
+int qc_hip_qgemv_unpack(int format, const void* packed, long long n, long long k, float* w,
+                        void* stream) {
+  const int st = validate(format, n, k);
+  if (st != QC_OK) return st;
+  size_t ignored = 0;
+  if (packed_bytes(format, n, k, &ignored) != QC_OK) return QC_INVALID_SHAPE;
+  if (packed == nullptr || w == nullptr) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_unpack(format, packed, w, n, k, as_stream(stream)));
+}
+
+int qc_hip_qgemv(int format, const void* packed, const float* x, float* y, long long n,
+                 long long k, void* stream) {
+  const int st = validate(format, n, k);
+  if (st != QC_OK) return st;
+  size_t ignored = 0;
+  if (packed_bytes(format, n, k, &ignored) != QC_OK) return QC_INVALID_SHAPE;
+  if (packed == nullptr || x == nullptr || y == nullptr) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_qgemm(format, packed, x, y, 1, n, k, as_stream(stream), g_tuning));
+}
+
+// kernels/quantization/qgemm_ref.cpp:141-164: shape products first, then the
+// null checks, then qgemv_packed_size (format and k validation).
+int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long long m,
+                 long long n, long long k, void* stream) {
+  if (!valid_product({m, k}) || !valid_product({m, n})) return QC_INVALID_SHAPE;
+  if (packed == nullptr || x == nullptr || y == nullptr) return QC_INVALID_ARGUMENT;
+  size_t size = 0;
+  const int st = qc_hip_qgemv_packed_size(format, n, k, &size);
+  if (st != QC_OK) return st;
+  return finish(qc::launch_qgemm(format, packed, x, y, m, n, k, as_stream(stream), g_tuning));
+}
+
+// kernels/quantization/quantization_ref.cpp:17-21 (quant_shape), 143-147.
+int qc_hip_quantize_int8(const float* x, int8_t* codes, float* scales, long long rows,
+                         long long dim, long long group_size, int* dev_status, void* stream) {
+  if (!valid_product({rows, dim})) return QC_INVALID_SHAPE;
+  if (group_size == 0) group_size = dim;
+  if (group_size <= 0 || dim % group_size != 0) return QC_INVALID_SHAPE;
+  if (x == nullptr || codes == nullptr || scales == nullptr) return QC_INVALID_ARGUMENT;
+  const hipStream_t s = as_stream(stream);
+  if (dev_status != nullptr)
+    return finish(qc::launch_quantize_int8(x, codes, scales, rows, dim, group_size, dev_status, s));
+  bool finite = false;
+  int st = all_finite(x, rows * dim, s, &finite);
+  if (st != QC_OK) return st;
+  if (!finite) return QC_INVALID_ARGUMENT;
+  hipError_t e = qc::launch_quantize_int8(x, codes, scales, rows, dim, group_size, nullptr, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return finish(e);
+}
+
+// src/dispatch/int8_gemm.cpp:67-94: shape, nulls, finite scales.
+int qc_hip_int8_gemm(const int8_t* w, const int8_t* x, const float* ws, const float* as,
+                     const int32_t* row_sum, const int* zp, float* y, long long m, long long n,
+                     long long k, int asymmetric, int* dev_status, void* stream) {
+  if (!valid_product({m, n, k})) return QC_INVALID_SHAPE;
+  if (w == nullptr || x == nullptr || ws == nullptr || as == nullptr || y == nullptr ||
+      (asymmetric && (row_sum == nullptr || zp == nullptr)))
+    return QC_INVALID_ARGUMENT;
+  const hipStream_t s = as_stream(stream);
+  if (dev_status != nullptr)
+    return finish(qc::launch_int8_gemm(w, x, ws, as, row_sum, zp, y, nullptr, m, n, k,
+                                       asymmetric != 0, dev_status, s));
+  bool finite = false;
+  int st = all_finite(ws, n, s, &finite);
+  if (st != QC_OK) return st;
+  if (!finite) return QC_INVALID_ARGUMENT;
+  st = all_finite(as, m, s, &finite);
+  if (st != QC_OK) return st;
+  if (!finite) return QC_INVALID_ARGUMENT;
+  hipError_t e = qc::launch_int8_gemm(w, x, ws, as, row_sum, zp, y, nullptr, m, n, k,
+                                      asymmetric != 0, nullptr, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return finish(e);
+}
+
+int qc_hip_qgemm_w8a8(const int8_t* w, const int8_t* x, const float* ws, const float* as,
+                      float* y, long long m, long long n, long long k, int* dev_status,
+                      void* stream) {
+  return qc_hip_int8_gemm(w, x, ws, as, nullptr, nullptr, y, m, n, k, 0, dev_status, stream);
+}
+
+int qc_hip_int8_gemm_i32(const int8_t* w, const int8_t* x, int32_t* acc, long long m,
+                         long long n, long long k, void* stream) {
+  if (!valid_product({m, n, k})) return QC_INVALID_SHAPE;
+  if (k > 131071) return QC_INVALID_SHAPE;
+  if (w == nullptr || x == nullptr || acc == nullptr) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_int8_gemm(w, x, nullptr, nullptr, nullptr, nullptr, nullptr, acc, m,
+                                     n, k, false, nullptr, as_stream(stream)));
+}
+
+int qc_hip_nonfinite_scan(const float* x, long long count, int* dev_flag, void* stream) {
+  if (count <= 0) return QC_INVALID_SHAPE;
+  if (x == nullptr || dev_flag == nullptr) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_nonfinite_scan(x, count, dev_flag, as_stream(stream)));
+}
+
+const char* qc_hip_qgemv_variant(int format) {
+  if (block_bytes(format) == 0) return "unsupported";
+  return format == QC_Q8_0 ? "hip_gfx950_q8_0" : "hip_gfx950_q4_0";
+}
+
+const char* qc_hip_int8_gemm_variant(void) { return "hip_gfx950_mfma_i8"; }
+
+int qc_hip_set_gemv_rows_per_wave(int rows) {
+  if (rows != 1 && rows != 2 && rows != 4 && rows != 8) return QC_INVALID_ARGUMENT;
+  g_tuning.rows_per_wave = rows;
+  return QC_OK;
+}
+
+}  // extern "C"

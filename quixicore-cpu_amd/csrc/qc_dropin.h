@@ -1,0 +1,56 @@
+// Internal helpers of the C++ drop-in layer: the per-device library stream and
+// host<->device staging of the reference API's untyped pointers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <vector>
+
+#include "quixicore_cpu/status.h"
+#include "quixicore_cpu/workspace.h"
+
+namespace quixicore_cpu::detail {
+
+// One non-blocking, default-priority stream per device, created on first use.
+hipStream_t library_stream();
+
+// True for hipMalloc'd or managed memory.
+bool device_accessible(const void* p);
+
+Status from_hip(hipError_t e);
+
+// Per-call staging.  in()/out() return a device view of a caller buffer:
+// the buffer itself when the GPU can address it, else a device copy (taken
+// from `workspace` when one is given, else hipMalloc'd and freed on scope
+// exit).  finish() copies staged outputs back and waits for the stream.
+class Staging {
+ public:
+  explicit Staging(Workspace* workspace)
+      : workspace_(workspace), stream_(library_stream()) {}
+  ~Staging();
+  Staging(const Staging&) = delete;
+  Staging& operator=(const Staging&) = delete;
+
+  const void* in(const void* host_or_device, std::size_t bytes);
+  void* out(void* host_or_device, std::size_t bytes);
+  Status finish(int capi_status);
+  Status status() const { return status_; }
+  hipStream_t stream() const { return stream_; }
+
+ private:
+  struct Back {
+    void* host;
+    void* dev;
+    std::size_t bytes;
+  };
+  void* device(std::size_t bytes);
+
+  Workspace* workspace_;
+  hipStream_t stream_;
+  Status status_ = Status::kOk;
+  std::vector<void*> owned_;
+  std::vector<Back> back_;
+};
+
+}  // namespace quixicore_cpu::detail

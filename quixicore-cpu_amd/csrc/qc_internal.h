@@ -1,0 +1,43 @@
+// Launchers shared between the kernel translation units and the C-ABI layer.
+// Host-side only; every pointer here is a device pointer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qc {
+
+struct GemvTuning {
+  int rows_per_wave = 4;  // rows each wavefront keeps in flight (1, 2, 4, 8)
+};
+
+// y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
+hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long long m,
+                        long long n, long long k, hipStream_t s, const GemvTuning& t);
+
+// Per-group symmetric int8 quantization.  status == nullptr: caller has
+// already verified that x is finite.  Otherwise non-finite groups are left
+// unwritten and *status is set to 3 (kInvalidArgument).
+hipError_t launch_quantize_int8(const float* x, int8_t* codes, float* scales, long long rows,
+                                long long dim, long long group, int* status, hipStream_t s);
+
+// *flag = 1 if any of x[0..count) is NaN or +-inf (flag must start at 0).
+hipError_t launch_nonfinite_scan(const float* x, long long count, int* flag, hipStream_t s);
+
+// y[m][n] = (float(sum_k W[n][k] X[m][k] - zp[m]*row_sum[n]) * ws[n]) * as[m].
+// acc_out (optional, test seam) receives the exact accumulators as int32
+// instead of y when non-null.  status (optional): set to 3 when a scale is
+// non-finite.
+hipError_t launch_int8_gemm(const int8_t* W, const int8_t* X, const float* ws, const float* as,
+                            const int32_t* row_sum, const int* zp, float* y, int32_t* acc_out,
+                            long long m, long long n, long long k, bool asymmetric,
+                            int* status, hipStream_t s);
+
+// Weight packing / unpacking on the device (bit-exact with the reference
+// packers).  status: set to 3 on a non-finite weight (block left unwritten).
+hipError_t launch_pack(int fmt, const float* w, void* packed, long long n, long long k,
+                       int* status, hipStream_t s);
+hipError_t launch_unpack(int fmt, const void* packed, float* w, long long n, long long k,
+                         hipStream_t s);
+
+}  // namespace qc

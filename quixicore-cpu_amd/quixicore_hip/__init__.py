@@ -1,0 +1,200 @@
+"""Python binding of the gfx950 C ABI (include/quixicore_hip.h) over ctypes.
+
+Tensors are torch tensors on the GPU; their data pointers and the current
+torch stream are handed to the C ABI unchanged.  There is no CPU fallback:
+importing this module without the built library raises, and every call runs
+a HIP kernel.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libquixicore_hip.so")
+SYNTH_PATH = os.path.join(HERE, "libqcsynth.so")
+
+Q8_0, Q4_0 = 0, 1
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+STATUS = {0: "kOk", 1: "kInvalidShape", 2: "kUnsupportedFormat", 3: "kInvalidArgument",
+          4: "kOutOfMemory", 5: "kDeviceError"}
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is not built; run `make -C quixicore-cpu_amd` (or __graft_entry__.build())")
+
+_P = ctypes.c_void_p
+_LL = ctypes.c_longlong
+_I = ctypes.c_int
+
+lib = ctypes.CDLL(LIB_PATH)
+
+_SIGS = {
+    "qc_hip_version": ([], ctypes.c_char_p),
+    "qc_hip_last_error": ([], ctypes.c_char_p),
+    "qc_hip_qgemv_packed_size": ([_I, _LL, _LL, ctypes.POINTER(ctypes.c_size_t)], _I),
+    "qc_hip_qgemv_pack": ([_I, _P, _LL, _LL, _P, _P, _P], _I),
+    "qc_hip_qgemv_unpack": ([_I, _P, _LL, _LL, _P, _P], _I),
+    "qc_hip_qgemv": ([_I, _P, _P, _P, _LL, _LL, _P], _I),
+    "qc_hip_qgemm": ([_I, _P, _P, _P, _LL, _LL, _LL, _P], _I),
+    "qc_hip_quantize_int8": ([_P, _P, _P, _LL, _LL, _LL, _P, _P], _I),
+    "qc_hip_int8_gemm": ([_P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _I, _P, _P], _I),
+    "qc_hip_qgemm_w8a8": ([_P, _P, _P, _P, _P, _LL, _LL, _LL, _P, _P], _I),
+    "qc_hip_int8_gemm_i32": ([_P, _P, _P, _LL, _LL, _LL, _P], _I),
+    "qc_hip_nonfinite_scan": ([_P, _LL, _P, _P], _I),
+    "qc_hip_qgemv_variant": ([_I], ctypes.c_char_p),
+    "qc_hip_int8_gemm_variant": ([], ctypes.c_char_p),
+    "qc_hip_set_gemv_rows_per_wave": ([_I], _I),
+}
+for _name, (_args, _res) in _SIGS.items():
+    _fn = getattr(lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _res
+
+EXPORTED = tuple(_SIGS)
+
+
+class QcError(RuntimeError):
+    def __init__(self, status, what):
+        detail = lib.qc_hip_last_error().decode()
+        super().__init__(f"{what}: {STATUS.get(status, status)}" + (f" ({detail})" if detail else ""))
+        self.status = status
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is not None:
+        return ctypes.c_void_p(stream)
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(status, what):
+    if status != 0:
+        raise QcError(status, what)
+
+
+def packed_size(fmt, n, k):
+    size = ctypes.c_size_t(0)
+    st = lib.qc_hip_qgemv_packed_size(fmt, n, k, ctypes.byref(size))
+    return st, size.value
+
+
+# Raw entry points: return the status integer (tests exercise error paths).
+def qgemv_raw(fmt, packed, x, y, n, k, stream=None):
+    return lib.qc_hip_qgemv(fmt, _ptr(packed), _ptr(x), _ptr(y), n, k, _stream(stream))
+
+
+def qgemm_raw(fmt, packed, x, y, m, n, k, stream=None):
+    return lib.qc_hip_qgemm(fmt, _ptr(packed), _ptr(x), _ptr(y), m, n, k, _stream(stream))
+
+
+def pack_raw(fmt, w, packed, n, k, dev_status=None, stream=None):
+    return lib.qc_hip_qgemv_pack(fmt, _ptr(w), n, k, _ptr(packed), _ptr(dev_status),
+                                 _stream(stream))
+
+
+def unpack_raw(fmt, packed, w, n, k, stream=None):
+    return lib.qc_hip_qgemv_unpack(fmt, _ptr(packed), n, k, _ptr(w), _stream(stream))
+
+
+def quantize_int8_raw(x, codes, scales, rows, dim, group_size=0, dev_status=None, stream=None):
+    return lib.qc_hip_quantize_int8(_ptr(x), _ptr(codes), _ptr(scales), rows, dim, group_size,
+                                    _ptr(dev_status), _stream(stream))
+
+
+def int8_gemm_raw(w, x, ws, as_, row_sum, zp, y, m, n, k, asymmetric=False, dev_status=None,
+                  stream=None):
+    return lib.qc_hip_int8_gemm(_ptr(w), _ptr(x), _ptr(ws), _ptr(as_), _ptr(row_sum), _ptr(zp),
+                                _ptr(y), m, n, k, int(asymmetric), _ptr(dev_status),
+                                _stream(stream))
+
+
+def int8_gemm_i32_raw(w, x, acc, m, n, k, stream=None):
+    return lib.qc_hip_int8_gemm_i32(_ptr(w), _ptr(x), _ptr(acc), m, n, k, _stream(stream))
+
+
+# Tensor-level helpers (torch GPU tensors in, new tensors out).
+def pack(fmt, w):
+    import torch
+    n, k = w.shape
+    st, size = packed_size(fmt, n, k)
+    _check(st, "qgemv_packed_size")
+    out = torch.empty(size, dtype=torch.uint8, device=w.device)
+    _check(pack_raw(fmt, w, out, n, k), "qgemv_pack")
+    return out
+
+
+def unpack(fmt, packed, n, k):
+    import torch
+    out = torch.empty((n, k), dtype=torch.float32, device=packed.device)
+    _check(unpack_raw(fmt, packed, out, n, k), "qgemv_unpack")
+    return out
+
+
+def qgemv(fmt, packed, x, n, k, y=None):
+    import torch
+    if y is None:
+        y = torch.empty(n, dtype=torch.float32, device=x.device)
+    _check(qgemv_raw(fmt, packed, x, y, n, k), "qgemv")
+    return y
+
+
+def qgemm(fmt, packed, x, n, k, y=None):
+    import torch
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    _check(qgemm_raw(fmt, packed, x, y, m, n, k), "qgemm")
+    return y
+
+
+def quantize_int8(x, group_size=0, dev_status=None):
+    import torch
+    rows, dim = x.shape
+    g = dim if group_size == 0 else group_size
+    codes = torch.empty((rows, dim), dtype=torch.int8, device=x.device)
+    scales = torch.empty((rows, dim // g), dtype=torch.float32, device=x.device)
+    _check(quantize_int8_raw(x, codes, scales, rows, dim, group_size, dev_status),
+           "quantize_int8")
+    return codes, scales
+
+
+def int8_gemm(w, x, ws, as_, row_sum=None, zp=None, asymmetric=False, dev_status=None, y=None):
+    import torch
+    m, k = x.shape
+    n = w.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    _check(int8_gemm_raw(w, x, ws, as_, row_sum, zp, y, m, n, k, asymmetric, dev_status),
+           "int8_gemm")
+    return y
+
+
+def int8_gemm_i32(w, x):
+    import torch
+    m, k = x.shape
+    n = w.shape[0]
+    acc = torch.empty((m, n), dtype=torch.int32, device=x.device)
+    _check(int8_gemm_i32_raw(w, x, acc, m, n, k), "int8_gemm_i32")
+    return acc
+
+
+def set_gemv_rows_per_wave(rows):
+    _check(lib.qc_hip_set_gemv_rows_per_wave(rows), "set_gemv_rows_per_wave")
+
+
+def qgemv_variant(fmt):
+    return lib.qc_hip_qgemv_variant(fmt).decode()
+
+
+def int8_gemm_variant():
+    return lib.qc_hip_int8_gemm_variant().decode()
+
+
+def version():
+    return lib.qc_hip_version().decode()

@@ -1,0 +1,86 @@
+"""CPU checks of the boundary: the library loads, exports every entry point
+include/quixicore_hip.h declares, and rejects invalid calls in the
+reference's validation order before touching the device (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "quixicore_hip.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(qc_hip_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    for required in ("qc_hip_qgemv", "qc_hip_qgemm", "qc_hip_quantize_int8", "qc_hip_int8_gemm",
+                     "qc_hip_qgemm_w8a8", "qc_hip_qgemv_pack", "qc_hip_qgemv_packed_size"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    import quixicore_hip as q
+    lib = ctypes.CDLL(q.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(declared()) == set(q.EXPORTED)
+
+
+def test_cpp_dropin_symbols_exported():
+    import subprocess
+    import quixicore_hip as q
+    out = subprocess.run(["nm", "-D", "-C", "--defined-only", q.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    for sym in ("quixicore_cpu::qgemv(", "quixicore_cpu::qgemm(", "quixicore_cpu::quantize_int8(",
+                "quixicore_cpu::int8_gemm(", "quixicore_cpu::qgemm_w8a8(",
+                "quixicore_cpu::qgemm_prepacked(", "quixicore_cpu::CpuPackedWeights::prepare(",
+                "quixicore_cpu::Workspace::allocate("):
+        assert sym in out, sym
+
+
+def test_packed_size_and_validation_without_device():
+    import quixicore_hip as q
+    assert q.packed_size(0, 4, 64) == (0, 4 * 2 * 34)
+    assert q.packed_size(1, 4, 64) == (0, 4 * 2 * 18)
+    assert q.packed_size(0, 4, 4096) == (0, 4 * 128 * 34)
+    assert q.packed_size(0, 4, 33)[0] == 1
+    assert q.packed_size(0, 0, 32)[0] == 1
+    assert q.packed_size(0, 1 << 62, 128)[0] == 1
+    assert q.packed_size(3, 4, 64)[0] == 2
+    assert q.lib.qc_hip_qgemv_packed_size(0, 1, 32, None) == 3
+    # qgemv: format, shape, then nulls -- all before any launch
+    assert q.lib.qc_hip_qgemv(7, None, None, None, 1, 32, None) == 2
+    assert q.lib.qc_hip_qgemv(0, None, None, None, 4, 33, None) == 1
+    assert q.lib.qc_hip_qgemv(0, None, None, None, 1, 32, None) == 3
+    # qgemm: products, nulls, then format
+    assert q.lib.qc_hip_qgemm(9, None, None, None, 0, 1, 32, None) == 1
+    assert q.lib.qc_hip_qgemm(9, None, None, None, 1, 1, 32, None) == 3
+    # quantize_int8: shape then nulls
+    assert q.lib.qc_hip_quantize_int8(None, None, None, 2, 6, 4, None, None) == 1
+    assert q.lib.qc_hip_quantize_int8(None, None, None, 2, 8, 4, None, None) == 3
+    # int8_gemm: shape then nulls (asymmetric needs row sums and zero points)
+    assert q.lib.qc_hip_int8_gemm(None, None, None, None, None, None, None, 0, 1, 1, 0, None,
+                                  None) == 1
+    assert q.lib.qc_hip_int8_gemm(None, None, None, None, None, None, None, 1, 1, 1, 0, None,
+                                  None) == 3
+    assert q.lib.qc_hip_int8_gemm_i32(None, None, None, 1, 1, 131072, None) == 1
+    assert q.qgemv_variant(0) == "hip_gfx950_q8_0" and q.qgemv_variant(5) == "unsupported"
+    assert q.lib.qc_hip_set_gemv_rows_per_wave(3) == 3
+
+
+def test_product_does_not_reference_oracle():
+    """The shipped library and binding never load or name the CPU oracle."""
+    import quixicore_hip as q
+    blob = open(q.LIB_PATH, "rb").read()
+    assert b"liboracle" not in blob and b"qco_" not in blob and b"qcref_" not in blob
+    pkg = os.path.join(ROOT, "quixicore-cpu_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h", ".c")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in text.replace("oracles", ""), f

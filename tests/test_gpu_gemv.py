@@ -1,0 +1,136 @@
+"""GPU parity: q8_0 / q4_0 GEMV and small-batch GEMM through the C ABI.
+
+Gate: per output |y - y64| <= 1e-4 * ||x||_2 * ||w_hat_row||_2
+against the f64 contract oracle over exactly dequantized weights.  Also the
+reference's own tolerance against its f32 route (atol 1e-5, rtol 1e-4 of the
+f64 value, tests/correctness/test_qgemv.cpp:291-295), bitwise determinism on
+rerun, and qgemm row m == qgemv of x[m] (kernels/quantization/qgemm_ref.cpp:156-162).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _case(oracle, synth, fmt, n, k, seed):
+    w = synth.normal_fast(seed, n * k, 0.02).reshape(n, k)
+    x = synth.normal_fast(seed + 1, k)
+    st, packed = oracle.pack(fmt, w)
+    assert st == 0
+    return packed, x
+
+
+def _check_rows(oracle, fmt, packed, x, y, n, k):
+    y64, wn = oracle.gemv_f64(fmt, packed, x, n, k)
+    ok, worst = oracle.within_contract(y, y64, wn, x, TOL)
+    assert ok, f"normalised error {worst:.3g} > {TOL}"
+    assert np.all(np.abs(y.astype(np.float64) - y64) <= 1e-5 + 1e-4 * np.abs(y64) +
+                  TOL * np.linalg.norm(x) * wn)
+
+
+SHAPES = [(1, 32), (3, 64), (5, 96), (33, 512), (129, 2048), (300, 4096), (64, 14336)]
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_qgemv_matches_oracle(qc, oracle, synth, dev, fmt, n, k):
+    import torch
+    print(f"qgemv fmt={fmt} n={n} k={k}", flush=True)
+    packed, x = _case(oracle, synth, fmt, n, k, 1000 + n + k)
+    P = torch.from_numpy(packed).to(dev)
+    X = torch.from_numpy(x).to(dev)
+    y = qc.qgemv(fmt, P, X, n, k)
+    y2 = qc.qgemv(fmt, P, X, n, k)
+    torch.cuda.synchronize()
+    yh = y.cpu().numpy()
+    _check_rows(oracle, fmt, packed, x, yh, n, k)
+    assert np.array_equal(yh.view(np.uint32), y2.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt,n,k", [(0, 4096, 4096), (1, 14336, 4096), (1, 4096, 14336)])
+def test_qgemv_baseline_configs(qc, oracle, synth, dev, fmt, n, k):
+    """BASELINE configs 0 and 1 at full size, seeded as the bench seeds them."""
+    import torch
+    print(f"qgemv config fmt={fmt} n={n} k={k}", flush=True)
+    cfg = 0 if fmt == 0 else 1
+    w = synth.weights(cfg, n, k)
+    x = synth.activations(cfg, 1, k)[0]
+    st, packed = oracle.pack(fmt, w)
+    y = qc.qgemv(fmt, torch.from_numpy(packed).to(dev), torch.from_numpy(x).to(dev), n, k)
+    _check_rows(oracle, fmt, packed, x, y.cpu().numpy(), n, k)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 8, 4])
+def test_rows_per_wave_variants(qc, oracle, synth, dev, rows):
+    import torch
+    print(f"rows_per_wave={rows}", flush=True)
+    qc.set_gemv_rows_per_wave(rows)
+    try:
+        for fmt in (0, 1):
+            n, k = 133, 2048
+            packed, x = _case(oracle, synth, fmt, n, k, 77)
+            y = qc.qgemv(fmt, torch.from_numpy(packed).to(dev), torch.from_numpy(x).to(dev), n, k)
+            _check_rows(oracle, fmt, packed, x, y.cpu().numpy(), n, k)
+    finally:
+        qc.set_gemv_rows_per_wave(4)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_qgemv_unaligned_weights(qc, oracle, synth, dev, fmt):
+    """Weights at a 2-byte offset take the byte-loading kernel."""
+    import torch
+    n, k = 40, 1024
+    packed, x = _case(oracle, synth, fmt, n, k, 5)
+    buf = torch.zeros(packed.size + 2, dtype=torch.uint8, device=dev)
+    buf[2:] = torch.from_numpy(packed).to(dev)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    st = qc.qgemv_raw(fmt, buf[2:], torch.from_numpy(x).to(dev), y, n, k)
+    assert st == 0
+    _check_rows(oracle, fmt, packed, x, y.cpu().numpy(), n, k)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16, 17, 32])
+def test_qgemm_small_batch(qc, oracle, synth, dev, fmt, m):
+    import torch
+    print(f"qgemm fmt={fmt} m={m}", flush=True)
+    n, k = 257, 4096
+    packed, _ = _case(oracle, synth, fmt, n, k, 31)
+    x = synth.normal_fast(4242 + m, m * k).reshape(m, k)
+    P = torch.from_numpy(packed).to(dev)
+    X = torch.from_numpy(x).to(dev)
+    Y = qc.qgemm(fmt, P, X, n, k).cpu().numpy()
+    for r in range(m):
+        _check_rows(oracle, fmt, packed, x[r], Y[r], n, k)
+    # each row is the GEMV of that row (the reference's qgemm definition)
+    for r in (0, m - 1):
+        yr = qc.qgemv(fmt, P, X[r].contiguous(), n, k).cpu().numpy()
+        assert np.array_equal(yr.view(np.uint32), Y[r].view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n", [(4, 4096), (32, 14336)])
+def test_qgemm_baseline_config2(qc, oracle, synth, dev, m, n):
+    """BASELINE config 2 (q8_0, K=4096) at two of its corners."""
+    import torch
+    print(f"qgemm config2 m={m} n={n}", flush=True)
+    k = 4096
+    w = synth.weights(2, n, k)
+    x = synth.activations(2, m, k)
+    st, packed = oracle.pack(0, w)
+    Y = qc.qgemm(0, torch.from_numpy(packed).to(dev), torch.from_numpy(x).to(dev), n, k)
+    Y = Y.cpu().numpy()
+    for r in (0, m // 2, m - 1):
+        _check_rows(oracle, 0, packed, x[r], Y[r], n, k)
+
+
+def test_qgemv_validation_order(qc, dev):
+    import torch
+    t = torch.zeros(64, dtype=torch.float32, device=dev)
+    # src/dispatch/qgemv.cpp:337-349: format, shape, then nulls
+    assert qc.qgemv_raw(7, t, t, t, 1, 32) == 2
+    assert qc.qgemv_raw(0, t, t, t, 4, 33) == 1
+    assert qc.qgemv_raw(0, None, t, t, 1, 32) == 3
+    assert qc.qgemm_raw(0, t, t, t, 0, 1, 32) == 1
+    assert qc.qgemm_raw(9, None, t, t, 1, 1, 32) == 3  # nulls before format in qgemm

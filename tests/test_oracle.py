@@ -1,0 +1,282 @@
+"""Pins the CPU oracle (oracle/qc_oracle.c) before anything is checked against it.
+
+Each oracle function is checked against at least one thing a plausible
+mistake would break:
+  * fp16 codec       -- exhaustive against numpy's IEEE float16 conversions and
+                        the reference's known answers (tests/correctness/
+                        test_qgemv.cpp:79-97).
+  * q8_0/q4_0 pack   -- byte-identical to the reference's own packers compiled
+                        from source (oracle/_ref), on random data and on the
+                        edge cases the reference tests (subnormal scale, zero
+                        block, non-finite rejection, rounding ties), and to the
+                        committed golden fixtures.
+  * unpack           -- exact products d*q checked against numpy.
+  * f32 GEMV orders  -- bit-identical to the reference's q8_0_gemv_ref, the
+                        AVX2 q4_rows route and the portable q4_0 kernel.
+  * f64 contract     -- against numpy float64 matmul of the unpacked weights.
+  * quantize_int8    -- bit-identical to the reference's quantize_int8 and its
+                        known answer (test_quantization.cpp:100-111).
+  * int8 GEMM        -- bit-identical to the reference's dispatched int8_gemm
+                        over its own test grid (test_int8_gemm.cpp:106-116),
+                        numpy int64 matmul, and the known answers
+                        {0, -1.5} / AZP {-5, -2} (test_projection_ops.cpp:81-97).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import xorshift32_unit
+
+
+# ------------------------------------------------------------------ fp16 ---
+
+def test_fp16_decode_exhaustive(oracle):
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = codes.view(np.float16).astype(np.float32)
+    got = np.array([oracle.fp16_to_fp32(int(c)) for c in codes], dtype=np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+
+
+def test_fp16_encode_matches_ieee(oracle):
+    rng = np.random.default_rng(7)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(1e-3),
+        (rng.standard_normal(20000) * 1e4).astype(np.float32),
+        np.ldexp(rng.uniform(1, 2, 20000), rng.integers(-30, 17, 20000)).astype(np.float32),
+        # halfway points between adjacent halves (ties to even)
+        ((np.arange(0, 4096, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -24)),
+        np.array([65504, 65519.996, 65520, 65536, 1e30, 2 ** -24, 2 ** -25, 3 * 2 ** -26,
+                  -0.0, 0.0, np.inf, -np.inf], dtype=np.float32),
+    ]).astype(np.float32)
+    want = vals.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.fp32_to_fp16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, want)
+    assert oracle.fp32_to_fp16(float("nan")) == 0x7E00
+
+
+def test_fp16_reference_known_answers(oracle):
+    # tests/correctness/test_qgemv.cpp:79-97
+    rt = lambda v: oracle.fp16_to_fp32(oracle.fp32_to_fp16(v))
+    assert rt(1.0) == 1.0 and rt(0.5) == 0.5 and rt(0.0) == 0.0 and rt(65504.0) == 65504.0
+    assert oracle.fp32_to_fp16(math.ldexp(1.0, -14)) == 0x0400
+    assert oracle.fp32_to_fp16(math.ldexp(1.0, -15)) == 0x0200
+    assert oracle.fp32_to_fp16(math.ldexp(1.0, -24)) == 0x0001
+    assert oracle.fp32_to_fp16(math.ldexp(1.0, -25)) == 0x0000
+    assert oracle.fp32_to_fp16(-math.ldexp(1.0, -24)) == 0x8001
+    v = np.float32(0.0123456)
+    assert abs(rt(float(v)) - v) / v < 1e-3
+
+
+# ------------------------------------------------------------------ pack ---
+
+def _edge_weights(k=32):
+    rows = [
+        np.full(k, 1e-3, np.float32),                     # fp16-subnormal scale
+        np.zeros(k, np.float32),                          # all-zero block
+        np.linspace(-1, 1, k, dtype=np.float32),
+        np.where(np.arange(k) % 2 == 0, 1.0, -1.0).astype(np.float32),
+        (np.arange(k, dtype=np.float32) - 16) * np.float32(0.5),  # many ties
+        np.full(k, -7.25, np.float32),
+        np.array([3.0e38] + [1.0] * (k - 1), np.float32),        # scale overflows fp16
+    ]
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_pack_matches_reference(oracle, ref, fmt):
+    for seed, (n, k) in enumerate([(1, 32), (3, 64), (5, 96), (33, 512), (17, 4096)]):
+        w = (np.random.default_rng(seed).standard_normal((n, k)) * 0.02).astype(np.float32)
+        st, got = oracle.pack(fmt, w)
+        rst, want = ref.pack(fmt, w)
+        assert st == 0 and rst == 0
+        assert np.array_equal(got, want), (fmt, n, k)
+    w = _edge_weights()
+    st, got = oracle.pack(fmt, w)
+    rst, want = ref.pack(fmt, w)
+    assert st == 0 and rst == 0 and np.array_equal(got, want)
+
+
+def test_pack_reference_edge_cases(oracle):
+    # sizes: 34 / 18 bytes per 32 weights (test_qgemv.cpp:116-122)
+    assert oracle.packed_size(0, 4, 64) == (0, 4 * 2 * 34)
+    assert oracle.packed_size(1, 4, 64) == (0, 4 * 2 * 18)
+    assert oracle.packed_size(0, 4, 33)[0] == 1
+    assert oracle.packed_size(0, 0, 32)[0] == 1
+    assert oracle.packed_size(0, 1 << 62, 128)[0] == 1
+    assert oracle.packed_size(5, 4, 64)[0] == 2
+    # non-finite rejection (test_qgemv.cpp:124-140)
+    for fmt in (0, 1):
+        for bad in (np.nan, np.inf):
+            w = np.ones((1, 32), np.float32)
+            w[0, 7] = bad
+            assert oracle.pack(fmt, w)[0] == 3
+    # subnormal fp16 scale keeps the block (test_qgemv.cpp:199-216)
+    st, p = oracle.pack(0, np.full((1, 32), 1e-3, np.float32))
+    dq = oracle.unpack(0, p, 1, 32)
+    assert dq[0, 0] != 0 and abs(dq[0, 0] - 1e-3) < 1e-5
+    # all-zero q4_0 block: d = -0.0 (0x8000) and every nibble 8
+    st, p = oracle.pack(1, np.zeros((1, 32), np.float32))
+    assert p[0] == 0x00 and p[1] == 0x80 and np.all(p[2:] == 0x88)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_unpack_is_exact_product(oracle, fmt):
+    w = (np.random.default_rng(3).standard_normal((7, 128)) * 0.02).astype(np.float32)
+    st, p = oracle.pack(fmt, w)
+    blocks = p.reshape(7, 4, 34 if fmt == 0 else 18)
+    d = blocks[:, :, :2].copy().view(np.float16)[:, :, 0].astype(np.float64)
+    if fmt == 0:
+        q = blocks[:, :, 2:].view(np.int8).astype(np.float64)
+    else:
+        b = blocks[:, :, 2:].astype(np.int64)
+        q = np.concatenate([(b & 15) - 8, (b >> 4) - 8], axis=2).astype(np.float64)
+    want = (d[:, :, None] * q).reshape(7, 128)
+    assert np.array_equal(oracle.unpack(fmt, p, 7, 128).astype(np.float64), want)
+
+
+# ------------------------------------------------------------------ GEMV ---
+
+def test_gemv_orders_match_reference(oracle, ref):
+    for fmt in (0, 1):
+        for seed, (n, k) in enumerate([(1, 32), (33, 512), (129, 2048), (64, 4096)]):
+            rng = np.random.default_rng(100 + seed)
+            w = rng.standard_normal((n, k)).astype(np.float32)
+            x = rng.standard_normal(k).astype(np.float32)
+            _, p = oracle.pack(fmt, w)
+            got = oracle.gemv(fmt, p, x, n, k)
+            want = ref.gemv(fmt, p, x, n, k)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (fmt, n, k)
+            if fmt == 1:
+                got = oracle.gemv(fmt, p, x, n, k, order="portable")
+                want = ref.gemv(fmt, p, x, n, k, portable=True)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemv_f64_contract_oracle(oracle):
+    for fmt in (0, 1):
+        rng = np.random.default_rng(11)
+        n, k = 33, 512
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        x = rng.standard_normal(k).astype(np.float32)
+        _, p = oracle.pack(fmt, w)
+        y64, wn = oracle.gemv_f64(fmt, p, x, n, k)
+        dq = oracle.unpack(fmt, p, n, k).astype(np.float64)
+        assert np.allclose(y64, dq @ x.astype(np.float64), rtol=1e-13, atol=1e-12)
+        assert np.allclose(wn, np.linalg.norm(dq, axis=1), rtol=1e-13)
+        # reference tolerance against the f32 route (test_qgemv.cpp:291-295)
+        y = oracle.gemv(fmt, p, x, n, k)
+        assert np.all(np.abs(y - y64) <= 1e-5 + 1e-4 * np.abs(y64))
+
+
+def test_reference_rng_shapes(oracle):
+    # the reference's own q4_0 contract case (test_qgemv.cpp:142-182)
+    n, k = 33, 512
+    vals = xorshift32_unit(0xD1B54A32, n * k + k)
+    w, x = vals[: n * k].reshape(n, k), vals[n * k:]
+    _, p = oracle.pack(1, w)
+    y = oracle.gemv(1, p, x, n, k)
+    y64, _ = oracle.gemv_f64(1, p, x, n, k)
+    assert np.all(np.abs(y - y64) <= 1e-5 + 1e-4 * np.abs(y64))
+
+
+# --------------------------------------------------------- quantize_int8 ---
+
+def test_quantize_int8_matches_reference(oracle, ref, synth):
+    cases = [
+        synth.activations_with_outliers(3, 16, 4096),
+        np.zeros((2, 64), np.float32),
+        (np.arange(-64, 64, dtype=np.float32) * np.float32(0.5)).reshape(2, 64),
+        np.random.default_rng(5).standard_normal((3, 96)).astype(np.float32) * np.float32(1e-30),
+    ]
+    for x in cases:
+        for group in (0, 32):
+            st, c, s = oracle.quantize_int8(x, group)
+            rst, rc, rs = ref.quantize_int8(x, group)
+            assert st == rst == 0
+            assert np.array_equal(c, rc) and np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+def test_quantize_int8_known_answers(oracle):
+    # test_quantization.cpp:100-111: group int8 endpoints
+    x = np.array([[-2.0, -0.5, 0.0, 2.0], [1.0, 2.0, 3.0, 4.0]], np.float32)
+    st, c, s = oracle.quantize_int8(x, 2)
+    assert st == 0 and c[0, 0] == -127 and c[0, 3] == 127 and c[1, 3] == 127
+    # closed form, by hand: row max 4 -> scale 4/127, codes rint(x*127/4)
+    st, c, s = oracle.quantize_int8(x, 0)
+    assert s[1, 0] == np.float32(4.0) / np.float32(127.0)
+    assert list(c[1]) == [32, 64, 95, 127]
+    # validation
+    assert oracle.quantize_int8(np.zeros((2, 6), np.float32), 4)[0] == 1
+    bad = np.ones((2, 4), np.float32)
+    bad[1, 2] = np.inf
+    assert oracle.quantize_int8(bad)[0] == 3
+
+
+# ------------------------------------------------------------- int8 GEMM ---
+
+def _ref_grid_case(m, n, k, asym, state):
+    def u32():
+        state[0] ^= (state[0] << 13) & 0xFFFFFFFF
+        state[0] ^= state[0] >> 17
+        state[0] ^= (state[0] << 5) & 0xFFFFFFFF
+        return state[0]
+    w = np.array([u32() & 255 for _ in range(n * k)], np.uint8).view(np.int8).reshape(n, k)
+    x = np.array([u32() & 255 for _ in range(m * k)], np.uint8).view(np.int8).reshape(m, k)
+    w[0, 0] = -1
+    x[0, 0] = -128
+    ws = (np.float32(0.001) * np.arange(1, n + 1, dtype=np.float32)).astype(np.float32)
+    as_ = (np.float32(0.002) * np.arange(1, m + 1, dtype=np.float32)).astype(np.float32)
+    rs = w.astype(np.int32).sum(axis=1).astype(np.int32)
+    zp = (np.arange(m, dtype=np.int32) - 2) if asym else np.zeros(m, np.int32)
+    return w, x, ws, as_, rs, zp.astype(np.int32)
+
+
+def test_int8_gemm_matches_reference_grid(oracle, ref):
+    # tests/correctness/test_int8_gemm.cpp:106-116
+    state = [0x9E3779B9]
+    for m in range(1, 6):
+        for n in range(1, 6):
+            for k in (1, 15, 16, 17, 63, 64, 65, 100, 1408):
+                for asym in (False, True):
+                    w, x, ws, as_, rs, zp = _ref_grid_case(m, n, k, asym, state)
+                    st, y = oracle.int8_gemm(w, x, ws, as_, rs, zp, asym)
+                    rst, ry = ref.int8_gemm(w, x, ws, as_, rs, zp, asym)
+                    assert st == rst == 0
+                    assert np.array_equal(y.view(np.uint32), ry.view(np.uint32)), (m, n, k, asym)
+                    acc = x.astype(np.int64) @ w.astype(np.int64).T
+                    if asym:
+                        acc -= zp[:, None].astype(np.int64) * rs[None, :]
+                    want = (acc.astype(np.float32) * ws[None, :]) * as_[:, None]
+                    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def test_int8_gemm_known_answers(oracle):
+    w = np.array([[1, 2, -1, 3], [-2, 1, 0, 2]], np.int8)
+    x = np.array([[2, -1, 3, 1]], np.int8)
+    ws = np.array([0.5, 0.25], np.float32)
+    as_ = np.array([2.0], np.float32)
+    st, y = oracle.int8_gemm(w, x, ws, as_)
+    assert st == 0 and abs(y[0, 0] - 0.0) < 1e-6 and abs(y[0, 1] + 1.5) < 1e-6
+    st, y = oracle.int8_gemm(w, x, ws, as_, np.array([5, 1], np.int32),
+                             np.array([1], np.int32), True)
+    assert st == 0 and abs(y[0, 0] + 5.0) < 1e-6 and abs(y[0, 1] + 2.0) < 1e-6
+    ws_bad = np.array([np.nan, 1.0], np.float32)
+    assert oracle.int8_gemm(w, x, ws_bad, as_)[0] == 3
+
+
+def test_int8_gemm_entries(oracle):
+    rng = np.random.default_rng(9)
+    w = rng.integers(-128, 128, (37, 200), dtype=np.int8)
+    x = rng.integers(-128, 128, (19, 200), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.01, 37).astype(np.float32)
+    as_ = rng.uniform(0.001, 0.01, 19).astype(np.float32)
+    st, y = oracle.int8_gemm(w, x, ws, as_)
+    rows = rng.integers(0, 19, 50)
+    cols = rng.integers(0, 37, 50)
+    acc, ye = oracle.int8_gemm_entries(w, x, ws, as_, rows, cols)
+    assert np.array_equal(acc, (x.astype(np.int64) @ w.astype(np.int64).T)[rows, cols])
+    assert np.array_equal(ye.view(np.uint32), y[rows, cols].view(np.uint32))
