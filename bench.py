@@ -182,8 +182,12 @@ def cpu_baseline(packed_dev, x_dev, y_dev, n, k, seconds):
     if not oracle.Reference.available():
         return None, None
     ref = oracle.Reference()
+    import quixicore_hip as qc
     packed = packed_dev.cpu().numpy()
     x = x_dev.cpu().numpy()
+    st = qc.qgemv_raw(qc.Q4_0, packed_dev, x_dev, y_dev, n, k)   # one fresh step on copy 0
+    if st:
+        raise RuntimeError(f"qgemv status {st}")
     y_gpu = y_dev.cpu().numpy()
     # correctness gate: GPU vs f64 contract oracle (1e-4 normalised) and vs
     # the reference's own f32 output

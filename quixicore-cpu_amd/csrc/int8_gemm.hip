@@ -116,6 +116,21 @@ __global__ __launch_bounds__(kThreads) void int8_gemm_mfma(
   }
 
   // C layout of a 16x16 tile: lane holds rows 4*(lane>>4)+e (n), column lane&15 (m).
+  if (acc_out != nullptr) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long long m = m0 + wm + 16 * j + (lane & 15);
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const long long nb = n0 + wn + 16 * i + 4 * (lane >> 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (nb + e < N) acc_out[m * N + nb + e] = acc[i][j][e];
+      }
+    }
+    return;
+  }
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -124,12 +139,6 @@ __global__ __launch_bounds__(kThreads) void int8_gemm_mfma(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const long long nb = n0 + wn + 16 * i + 4 * (lane >> 4);
-      if (acc_out != nullptr) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (nb + e < N) acc_out[m * N + nb + e] = acc[i][j][e];
-        continue;
-      }
       float out[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

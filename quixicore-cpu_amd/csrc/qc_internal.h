@@ -8,12 +8,16 @@
 namespace qc {
 
 struct GemvTuning {
-  int rows_per_wave = 4;  // rows each wavefront keeps in flight (1, 2, 4, 8)
+  int rows_per_wave = 0;  // GEMV rows per wavefront (1, 2, 4, 8; 0 = chosen from the shape)
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
 hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long long m,
                         long long n, long long k, hipStream_t s, const GemvTuning& t);
+
+// M = 1 GEMV with exact int8 digit dots (K % 64 == 0, W 4-byte aligned).
+hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, int n, int k,
+                            int rows_per_wave, hipStream_t s);
 
 // Per-group symmetric int8 quantization.  status == nullptr: caller has
 // already verified that x is finite.  Otherwise non-finite groups are left

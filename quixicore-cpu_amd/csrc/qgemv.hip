@@ -14,9 +14,10 @@
 // loads.  Lane l of a wavefront owns pairs l, l+64, ... of a row: one
 // load instruction of the wave covers a contiguous span of the row.
 //
-// x is staged once per workgroup into LDS (padded by 16 B every 64 floats so
-// the per-lane 256-B slices of consecutive lanes fall into different banks)
-// and each wave reuses its slice across RW rows held in flight.
+// M = 1 goes to the exact-int8-dot kernel of qgemv_dot.hip.  For M > 1, x is
+// staged per workgroup into LDS (padded by 16 B every 64 floats so the per-
+// lane 256-B slices of consecutive lanes fall into different banks) and every
+// decoded weight is reused for up to 8 activation rows.
 #include "qc_device.h"
 #include "qc_internal.h"
 
@@ -28,6 +29,13 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kLdsBudget = 64 * 1024;
 
 __device__ __forceinline__ int xpad(int j) { return j + ((j >> 6) << 2); }
+
+// Lane l always owns the pairs p with p % 64 == l, whatever the K chunking,
+// so every row is summed in the same order by the M = 1 and M > 1 kernels
+// (qgemm row m is bit-identical to qgemv of x[m], as in the reference).
+__device__ __forceinline__ int first_pair(int pbeg, int lane) {
+  return pbeg + ((lane - pbeg) & 63);
+}
 
 // Stage x[c0 : c0+clen] (clen a multiple of 64) of `mt` activation rows into
 // LDS; for q4_0 also the per-block sums used to fold the -8 nibble offset.
@@ -144,56 +152,6 @@ __device__ __forceinline__ float pair_dot(const uint32_t (&d)[Fmt<FMT>::pair_dwo
   return acc;
 }
 
-// M = 1 fast path: each wave holds RW rows in flight and reuses its x slice.
-template <int FMT, int RW>
-__global__ __launch_bounds__(kThreads) void qgemv_pairs_kernel(
-    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int n,
-    int k, int kc, int vec_ok) {
-  extern __shared__ float xs[];
-  constexpr int BB = Fmt<FMT>::block_bytes;
-  constexpr int PD = Fmt<FMT>::pair_dwords;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const long long row_bytes = static_cast<long long>(k >> 5) * BB;
-  const int row0 = (blockIdx.x * kWaves + wave) * RW;
-  float acc[RW];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) acc[r] = 0.f;
-
-  for (int c0 = 0; c0 < k; c0 += kc) {
-    const int clen = min(kc, k - c0);
-    if (c0) __syncthreads();
-    stage_x<FMT>(xs, x, 0, 1, c0, clen, kc, vec_ok != 0);
-    __syncthreads();
-    const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
-    const float* sums = xs + xpad(kc);
-    for (int p = pbeg + lane; p < pend; p += 64) {
-      uint32_t d[RW][PD];
-#pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        const int row = min(row0 + r, n - 1);
-        load_pair<FMT>(d[r], W + row * row_bytes + static_cast<long long>(p) * (2 * BB));
-      }
-      float xv[64];
-      const float* xsrc = xs + xpad((p - pbeg) * 64);
-#pragma unroll
-      for (int j = 0; j < 64; j += 4) *reinterpret_cast<float4*>(xv + j) = *reinterpret_cast<const float4*>(xsrc + j);
-      float xsum[2] = {0.f, 0.f};
-      if constexpr (FMT == kQ4_0) {
-        xsum[0] = sums[2 * (p - pbeg)];
-        xsum[1] = sums[2 * (p - pbeg) + 1];
-      }
-#pragma unroll
-      for (int r = 0; r < RW; ++r) acc[r] = pair_dot<FMT>(d[r], xv, xsum, acc[r]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const float t = wave_sum(acc[r]);
-    if (lane == 0 && row0 + r < n) y[row0 + r] = t;
-  }
-}
-
 // Small-batch path: MT activation rows per launch share every weight decode.
 template <int FMT, int MT>
 __global__ __launch_bounds__(kThreads) void qgemm_pairs_kernel(
@@ -219,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_pairs_kernel(
     __syncthreads();
     const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
     const float* sums = xs + mt * row_stride;
-    for (int p = pbeg + lane; p < pend; p += 64) {
+    for (int p = first_pair(pbeg, lane); p < pend; p += 64) {
       uint32_t d[PD];
       load_pair<FMT>(d, W + min(row, n - 1) * row_bytes + static_cast<long long>(p) * (2 * BB));
 #pragma unroll
@@ -306,20 +264,7 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, 
     return hipGetLastError();
   }
   const int vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (k % 4 == 0);
-  if (m == 1) {
-    const int kc = chunk_for(FMT, 1, k);
-    const size_t lds = lds_bytes(FMT, 1, kc);
-    const int rw = t.rows_per_wave;
-    const int rows_per_block = kWaves * rw;
-    const int grid = (n + rows_per_block - 1) / rows_per_block;
-    switch (rw) {
-      case 1: qgemv_pairs_kernel<FMT, 1><<<grid, kThreads, lds, s>>>(W, x, y, n, k, kc, vec); break;
-      case 2: qgemv_pairs_kernel<FMT, 2><<<grid, kThreads, lds, s>>>(W, x, y, n, k, kc, vec); break;
-      case 8: qgemv_pairs_kernel<FMT, 8><<<grid, kThreads, lds, s>>>(W, x, y, n, k, kc, vec); break;
-      default: qgemv_pairs_kernel<FMT, 4><<<grid, kThreads, lds, s>>>(W, x, y, n, k, kc, vec); break;
-    }
-    return hipGetLastError();
-  }
+  if (m == 1) return launch_qgemv_dot(FMT, W, x, y, n, k, t.rows_per_wave, s);
   const int grid = (n + kWaves - 1) / kWaves;
   for (int m0 = 0; m0 < m; m0 += 8) {
     const int mt = m - m0 < 8 ? m - m0 : 8;

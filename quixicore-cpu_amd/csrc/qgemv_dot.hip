@@ -1,0 +1,356 @@
+// q8_0 / q4_0 decode GEMV (M = 1) on gfx950 with exact int8 dot products.
+//
+// Semantics: y[n] = sum_k dequant(W)[n][k] * x[k] with f32 activations
+// (include/quixicore_cpu/qgemv.h:100-108, src/dispatch/qgemv.cpp:337-365 of
+// the reference), within the contract tolerance |y - y64| <= 1e-4 *
+// ||x||_2 * ||w_hat_row||_2 of the f64 oracle.
+//
+// Numerical method.  For every 32-element block b of x the workgroup picks the
+// power of two 2^e_b with max|x_b| < 2^(e_b + 21) (e_b = frexp exponent - 21)
+// and the integers q_j = rint(x_j * 2^-e_b), clamped to [-2^21, 2^21 - 1],
+// split into three int8 digits (floor division):
+//   q_j = 2^14 * d0_j + 2^7 * d1_j + d2_j,  d0 in [-128,127], d1, d2 in [0,127].
+// So x_j = 2^e_b * q_j + err_j with |err_j| <= 2^(e_b-1) <= max|x_b| * 2^-21:
+// a 22-bit fixed-point copy of the block whose error, after the contract's
+// normalisation by ||x||_2 ||w_hat_row||_2, is below 3e-6 in the worst case and
+// ~1e-8 typically.  Scaling by 2^-e_b is exact (v_ldexp), so subnormal and
+// huge activations keep their precision.  Each block dot is then three exact
+// int32 sums of int8 x int8 products (v_dot4_i32_i8, 4 MACs per instruction):
+//   sum_j w_j x_j ~= 2^e_b * d_w * (2^14 S0 + 2^7 S1 + S2),  S_t = sum_j c_j d_t,j
+// with c_j the q8_0 code, or the q4_0 nibble n_j with the -8 offset folded in
+// exactly as S_t -= 8 * sum_j d_t,j.  A block of x holding NaN or +-inf makes
+// every output NaN.  Blocks are accumulated in f32 in a fixed per-lane order
+// and reduced across the wave in a fixed butterfly, so results are
+// deterministic.
+//
+// Memory: W stays in the canonical GGUF layout.  Lane l owns the block pairs
+// p = l, l+64, ... of its wave's rows (a pair is 68 B for q8_0, 36 B for q4_0,
+// dword aligned when K/32 is even).  Each wave issues the loads for all of its
+// rows x pairs before anything else, so the whole weight stream is in flight
+// while the workgroup builds the digits of x in LDS; the barrier after the
+// digit build waits on LDS traffic only.
+#include "qc_device.h"
+#include "qc_internal.h"
+
+namespace qc {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRec = 208;  // LDS bytes per pair: 3 digit planes x 64 + 16 pad
+
+__device__ __forceinline__ int first_pair(int pbeg, int lane) {
+  return pbeg + ((lane - pbeg) & 63);
+}
+
+// Barrier that orders LDS traffic only: global loads already issued stay in
+// flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// LDS layout of one chunk of kc elements (kc a multiple of 64):
+//   [kc/64 pair records of kRec bytes][kc/32 int32 exponents e_b]
+//   [kc/32 f32 gates: 1, or NaN for a non-finite block][3 x kc/32 int32 digit sums]
+__host__ __device__ constexpr size_t exp_off(int kc) { return static_cast<size_t>(kc / 64) * kRec; }
+__host__ __device__ constexpr size_t gate_off(int kc) { return exp_off(kc) + 4 * static_cast<size_t>(kc / 32); }
+__host__ __device__ constexpr size_t dsum_off(int kc) { return gate_off(kc) + 4 * static_cast<size_t>(kc / 32); }
+__host__ __device__ constexpr size_t lds_size(int kc) { return dsum_off(kc) + 12 * static_cast<size_t>(kc / 32); }
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
+// Digits of x[0 : clen) into LDS.  Thread t handles half-blocks h = t, t+256, ...
+// of 16 elements; the two halves of a block sit in lanes t and t^1.
+template <bool WITH_SUMS>
+__device__ __forceinline__ void build_digits(uint8_t* lds, const float* __restrict__ x, int clen,
+                                             int kc, bool vec_ok) {
+  const int nh = clen >> 4;
+  for (int h = threadIdx.x; h < nh; h += kThreads) {
+    float v[16];
+    if (vec_ok) {
+      const float4* src = reinterpret_cast<const float4*>(x + 16 * h);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(v + 4 * i) = src[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = x[16 * h + i];
+    }
+    float m = 0.f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      m = fmaxf(m, fabsf(v[i]));
+      finite = finite && isfinite(v[i]);
+    }
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    finite = finite && (__shfl_xor(finite ? 1 : 0, 1, 64) != 0);
+    int ex = 0;
+    (void)frexpf(m, &ex);                            // m < 2^ex
+    const int e = finite ? ex - 21 : 0;
+    int d0[16], d1[16], d2[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      int q = finite ? __float2int_rn(ldexpf(v[i], -e)) : 0;   // |x * 2^-e| <= 2^21
+      q = q > 2097151 ? 2097151 : q;
+      d0[i] = q >> 14;                               // [-128, 127]
+      d1[i] = (q >> 7) & 127;                        // [0, 127]
+      d2[i] = q & 127;                               // [0, 127]
+    }
+    const int pair = h >> 2;
+    uint8_t* rec = lds + pair * kRec + (h & 3) * 16;
+    uint4 p0, p1, p2;
+    p0.x = pack4(d0[0], d0[1], d0[2], d0[3]);    p0.y = pack4(d0[4], d0[5], d0[6], d0[7]);
+    p0.z = pack4(d0[8], d0[9], d0[10], d0[11]);  p0.w = pack4(d0[12], d0[13], d0[14], d0[15]);
+    p1.x = pack4(d1[0], d1[1], d1[2], d1[3]);    p1.y = pack4(d1[4], d1[5], d1[6], d1[7]);
+    p1.z = pack4(d1[8], d1[9], d1[10], d1[11]);  p1.w = pack4(d1[12], d1[13], d1[14], d1[15]);
+    p2.x = pack4(d2[0], d2[1], d2[2], d2[3]);    p2.y = pack4(d2[4], d2[5], d2[6], d2[7]);
+    p2.z = pack4(d2[8], d2[9], d2[10], d2[11]);  p2.w = pack4(d2[12], d2[13], d2[14], d2[15]);
+    *reinterpret_cast<uint4*>(rec) = p0;
+    *reinterpret_cast<uint4*>(rec + 64) = p1;
+    *reinterpret_cast<uint4*>(rec + 128) = p2;
+    const int blk = h >> 1;
+    if constexpr (WITH_SUMS) {
+      int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s0 += d0[i];
+        s1 += d1[i];
+        s2 += d2[i];
+      }
+      s0 += __shfl_xor(s0, 1, 64);
+      s1 += __shfl_xor(s1, 1, 64);
+      s2 += __shfl_xor(s2, 1, 64);
+      if ((h & 1) == 0) {
+        int* sums = reinterpret_cast<int*>(lds + dsum_off(kc));
+        sums[blk] = s0;
+        sums[(kc >> 5) + blk] = s1;
+        sums[2 * (kc >> 5) + blk] = s2;
+      }
+    }
+    if ((h & 1) == 0) {
+      reinterpret_cast<int*>(lds + exp_off(kc))[blk] = e;
+      reinterpret_cast<float*>(lds + gate_off(kc))[blk] = finite ? 1.0f : __builtin_nanf("");
+    }
+  }
+}
+
+// The digits of one pair as seen by its owning lane.
+struct PairDigits {
+  uint32_t d[3][16];  // plane t, dword i = elements 4i..4i+3 of the pair
+  int e[2];           // block exponents e_b
+  float gate[2];      // 1, or NaN for a block of x holding a non-finite value
+  int off[2][3];      // q4_0: -8 * sum of plane t over block b
+};
+
+template <int FMT>
+__device__ __forceinline__ void read_digits(PairDigits& g, const uint8_t* lds, int pl, int kc) {
+  const uint8_t* rec = lds + pl * kRec;
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(rec + 64 * t + 16 * i);
+      g.d[t][4 * i] = v.x; g.d[t][4 * i + 1] = v.y; g.d[t][4 * i + 2] = v.z; g.d[t][4 * i + 3] = v.w;
+    }
+  const int2 ev = *reinterpret_cast<const int2*>(lds + exp_off(kc) + 8 * pl);
+  const float2 gv = *reinterpret_cast<const float2*>(lds + gate_off(kc) + 8 * pl);
+  g.e[0] = ev.x;
+  g.e[1] = ev.y;
+  g.gate[0] = gv.x;
+  g.gate[1] = gv.y;
+  if constexpr (FMT == kQ4_0) {
+    const int* sums = reinterpret_cast<const int*>(lds + dsum_off(kc));
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      const int2 v = *reinterpret_cast<const int2*>(sums + t * (kc >> 5) + 2 * pl);
+      g.off[0][t] = -8 * v.x;
+      g.off[1][t] = -8 * v.y;
+    }
+  }
+}
+
+__device__ __forceinline__ float combine(int s0, int s1, int s2) {
+  return fmaf(static_cast<float>(s0), 16384.f, fmaf(static_cast<float>(s1), 128.f, static_cast<float>(s2)));
+}
+
+// acc + 2^e * (d_w * gate) * (2^14 s0 + 2^7 s1 + s2)
+__device__ __forceinline__ float block_acc(float acc, uint32_t dbits, float gate, int e, int s0,
+                                           int s1, int s2) {
+  const float t = (half_bits_to_float(dbits) * gate) * combine(s0, s1, s2);
+  return acc + ldexpf(t, e);
+}
+
+// acc += contribution of one pair (two blocks) of one row.
+template <int FMT>
+__device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g, float acc) {
+  if constexpr (FMT == kQ8_0) {
+    int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = static_cast<int>(__builtin_amdgcn_alignbyte(w[i + 1], w[i], 2));
+      a0 = __builtin_amdgcn_sdot4(c, static_cast<int>(g.d[0][i]), a0, false);
+      a1 = __builtin_amdgcn_sdot4(c, static_cast<int>(g.d[1][i]), a1, false);
+      a2 = __builtin_amdgcn_sdot4(c, static_cast<int>(g.d[2][i]), a2, false);
+      const int e = static_cast<int>(w[9 + i]);
+      b0 = __builtin_amdgcn_sdot4(e, static_cast<int>(g.d[0][8 + i]), b0, false);
+      b1 = __builtin_amdgcn_sdot4(e, static_cast<int>(g.d[1][8 + i]), b1, false);
+      b2 = __builtin_amdgcn_sdot4(e, static_cast<int>(g.d[2][8 + i]), b2, false);
+    }
+    acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
+    acc = block_acc(acc, w[8] >> 16, g.gate[1], g.e[1], b0, b1, b2);
+  } else {
+    int a0 = g.off[0][0], a1 = g.off[0][1], a2 = g.off[0][2];
+    int b0 = g.off[1][0], b1 = g.off[1][1], b2 = g.off[1][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+      const int lo = static_cast<int>(q & 0x0F0F0F0Fu);
+      const int hi = static_cast<int>((q >> 4) & 0x0F0F0F0Fu);
+      a0 = __builtin_amdgcn_sdot4(lo, static_cast<int>(g.d[0][i]), a0, false);
+      a1 = __builtin_amdgcn_sdot4(lo, static_cast<int>(g.d[1][i]), a1, false);
+      a2 = __builtin_amdgcn_sdot4(lo, static_cast<int>(g.d[2][i]), a2, false);
+      a0 = __builtin_amdgcn_sdot4(hi, static_cast<int>(g.d[0][4 + i]), a0, false);
+      a1 = __builtin_amdgcn_sdot4(hi, static_cast<int>(g.d[1][4 + i]), a1, false);
+      a2 = __builtin_amdgcn_sdot4(hi, static_cast<int>(g.d[2][4 + i]), a2, false);
+      const uint32_t u = w[5 + i];
+      const int lo1 = static_cast<int>(u & 0x0F0F0F0Fu);
+      const int hi1 = static_cast<int>((u >> 4) & 0x0F0F0F0Fu);
+      b0 = __builtin_amdgcn_sdot4(lo1, static_cast<int>(g.d[0][8 + i]), b0, false);
+      b1 = __builtin_amdgcn_sdot4(lo1, static_cast<int>(g.d[1][8 + i]), b1, false);
+      b2 = __builtin_amdgcn_sdot4(lo1, static_cast<int>(g.d[2][8 + i]), b2, false);
+      b0 = __builtin_amdgcn_sdot4(hi1, static_cast<int>(g.d[0][12 + i]), b0, false);
+      b1 = __builtin_amdgcn_sdot4(hi1, static_cast<int>(g.d[1][12 + i]), b1, false);
+      b2 = __builtin_amdgcn_sdot4(hi1, static_cast<int>(g.d[2][12 + i]), b2, false);
+    }
+    acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
+    acc = block_acc(acc, w[4] >> 16, g.gate[1], g.e[1], b0, b1, b2);
+  }
+  return acc;
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_pair(uint32_t* d, const uint8_t* p) {
+  const u32x4_a4* v = reinterpret_cast<const u32x4_a4*>(p);
+  constexpr int NV = FMT == kQ8_0 ? 4 : 2;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const u32x4_a4 t = v[i];
+    d[4 * i] = t.x; d[4 * i + 1] = t.y; d[4 * i + 2] = t.z; d[4 * i + 3] = t.w;
+  }
+  d[4 * NV] = reinterpret_cast<const uint32_t*>(p)[4 * NV];
+}
+
+// RB rows per wave, up to NPM pairs per lane per K chunk.
+template <int FMT, int RB, int NPM>
+__global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __restrict__ W,
+                                                             const float* __restrict__ x,
+                                                             float* __restrict__ y, int n, int k,
+                                                             int kc, int vec_ok) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int BB = Fmt<FMT>::block_bytes;
+  constexpr int PD = Fmt<FMT>::pair_dwords;
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * RB;
+  const long long row_bytes = static_cast<long long>(k >> 5) * BB;
+  const uint8_t* wrow[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) wrow[r] = W + min(row0 + r, n - 1) * row_bytes;
+  float acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = 0.f;
+
+  for (int c0 = 0; c0 < k; c0 += kc) {
+    const int clen = min(kc, k - c0);
+    const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
+    const int p0 = first_pair(pbeg, lane);
+    // 1. every weight load of this chunk, issued before the digit build
+    uint32_t w[NPM][RB][PD];
+#pragma unroll
+    for (int j = 0; j < NPM; ++j) {
+      const int p = min(p0 + 64 * j, pend - 1);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) load_pair<FMT>(w[j][r], wrow[r] + static_cast<long long>(p) * (2 * BB));
+    }
+    // 2. digits of x for this chunk
+    if (c0) lds_barrier();
+    build_digits<FMT == kQ4_0>(lds, x + c0, clen, kc, vec_ok != 0);
+    lds_barrier();
+    // 3. exact block dots
+#pragma unroll
+    for (int j = 0; j < NPM; ++j) {
+      const int p = p0 + 64 * j;
+      if (p < pend) {
+        PairDigits g;
+        read_digits<FMT>(g, lds, p - pbeg, kc);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[r] = pair_dot<FMT>(w[j][r], g, acc[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const float t = wave_sum(acc[r]);
+    if (lane == 0 && row0 + r < n) y[row0 + r] = t;
+  }
+}
+
+template <int FMT, int RB, int NPM>
+hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, hipStream_t s) {
+  // weights held in flight per lane: RB * NPM * pair dwords (kept <= 144 VGPRs)
+  static_assert(RB * NPM * Fmt<FMT>::pair_dwords <= 144, "register budget");
+  const int kc = NPM * 4096 < k ? NPM * 4096 : k;
+  const int grid = (n + kWaves * RB - 1) / (kWaves * RB);
+  const int vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  qgemv_dot_kernel<FMT, RB, NPM><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc, vec);
+  return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, int rb,
+                      hipStream_t s) {
+  const int npairs = k >> 6;
+  const int npm = npairs <= 64 ? 1 : (npairs <= 128 ? 2 : 4);
+  // largest rows-per-wave allowed by the register budget for this K
+  const int cap = FMT == kQ8_0 ? (npm == 1 ? 8 : (npm == 2 ? 4 : 2)) : (npm == 1 ? 8 : 4);
+  if (rb == 0) rb = n >= 4 * 8 * 512 ? 8 : (n >= 4 * 4 * 256 ? 4 : (n >= 4 * 2 * 256 ? 2 : 1));
+  if (rb > cap) rb = cap;
+  if (npm == 1) {
+    switch (rb) {
+      case 1: return launch_one<FMT, 1, 1>(W, x, y, n, k, s);
+      case 2: return launch_one<FMT, 2, 1>(W, x, y, n, k, s);
+      case 4: return launch_one<FMT, 4, 1>(W, x, y, n, k, s);
+      default: return launch_one<FMT, 8, 1>(W, x, y, n, k, s);
+    }
+  }
+  if (npm == 2) {
+    switch (rb) {
+      case 1: return launch_one<FMT, 1, 2>(W, x, y, n, k, s);
+      case 2: return launch_one<FMT, 2, 2>(W, x, y, n, k, s);
+      default: return launch_one<FMT, 4, 2>(W, x, y, n, k, s);
+    }
+  }
+  switch (rb) {
+    case 1: return launch_one<FMT, 1, 4>(W, x, y, n, k, s);
+    case 2: return launch_one<FMT, 2, 4>(W, x, y, n, k, s);
+    default:
+      if constexpr (FMT == kQ4_0) return launch_one<FMT, 4, 4>(W, x, y, n, k, s);
+      return launch_one<FMT, 2, 4>(W, x, y, n, k, s);
+  }
+}
+
+}  // namespace
+
+// K % 64 == 0 and W 4-byte aligned (checked by the caller).  rows_per_wave:
+// 0 picks from the shape; otherwise 1, 2, 4 or 8, capped by the register budget.
+hipError_t launch_qgemv_dot(int fmt, const void* Wv, const float* x, float* y, int n, int k,
+                            int rows_per_wave, hipStream_t s) {
+  const auto* W = static_cast<const uint8_t*>(Wv);
+  return fmt == kQ8_0 ? launch_fmt<kQ8_0>(W, x, y, n, k, rows_per_wave, s)
+                      : launch_fmt<kQ4_0>(W, x, y, n, k, rows_per_wave, s);
+}
+
+}  // namespace qc

@@ -141,8 +141,13 @@ __global__ __launch_bounds__(kThreads) void nonfinite_scan(const float* __restri
 
 // ------------------------------------------------------- weight packing --
 
+// f32 -> f16 bits, round to nearest even (v_cvt_f16_f32).  The empty asm keeps
+// the compiler from fusing the conversion with the producing multiply into
+// v_fma_mix*_f16 with a +0 addend, which turns a -0 scale (all-zero q4_0
+// block, d = 0 / -8) into +0.
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
-  const _Float16 h = static_cast<_Float16>(f);  // v_cvt_f16_f32, round to nearest even
+  asm volatile("" : "+v"(f));
+  const _Float16 h = static_cast<_Float16>(f);
   return __builtin_bit_cast(uint16_t, h);
 }
 

@@ -79,8 +79,11 @@ def test_product_does_not_reference_oracle():
     blob = open(q.LIB_PATH, "rb").read()
     assert b"liboracle" not in blob and b"qco_" not in blob and b"qcref_" not in blob
     pkg = os.path.join(ROOT, "quixicore-cpu_amd")
+    needles = ("liboracle", "qco_", "qcref_", "import oracle", "oracle/", "oracle.py",
+               "_ref/libqcref")
     for dirpath, _, files in os.walk(pkg):
         for f in files:
-            if f.endswith((".py", ".cpp", ".hip", ".h", ".c")):
+            if f.endswith((".py", ".cpp", ".hip", ".h", ".c", "Makefile")):
                 text = open(os.path.join(dirpath, f)).read()
-                assert "oracle" not in text.replace("oracles", ""), f
+                for needle in needles:
+                    assert needle not in text, (f, needle)
