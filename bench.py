@@ -45,7 +45,12 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--rows-per-wave", type=int, default=0)
+    p.add_argument("--eager", action="store_true",
+                   help="time eager launches instead of one graph replay (for counter runs)")
     return p.parse_args()
+
+
+EAGER = False
 
 
 def rotation(footprint):
@@ -62,6 +67,17 @@ def time_steps(launch, steps, warmup):
         for i in range(warmup):
             launch(i)
     torch.cuda.synchronize()
+    if EAGER:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            t0 = time.perf_counter()
+            start.record(stream)
+            for i in range(steps):
+                launch(warmup + i)
+            end.record(stream)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+        return (t1 - t0) * 1e3 / steps, start.elapsed_time(end) / steps
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         for i in range(steps):
@@ -236,6 +252,8 @@ def cpu_baseline(packed_dev, x_dev, y_dev, n, k, seconds):
 
 def main():
     args = parse()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is design-only (see DESIGN.md).", file=sys.stderr)

@@ -120,8 +120,9 @@ int qc_hip_nonfinite_scan(const float* x, long long count, int* dev_flag, void* 
 const char* qc_hip_qgemv_variant(int format);
 const char* qc_hip_int8_gemm_variant(void);
 
-/* Rows each GEMV wavefront keeps in flight (1, 2, 4 or 8; default 4). Tuning
- * knob with no reference counterpart. */
+/* Rows each GEMV wavefront keeps in flight: 1, 2, 4, 7, 8 or 14 (capped by
+ * the register budget for K), or 0 (default) to choose from the shape.
+ * Tuning knob with no reference counterpart. */
 int qc_hip_set_gemv_rows_per_wave(int rows);
 
 #ifdef __cplusplus

@@ -253,7 +253,8 @@ const char* qc_hip_qgemv_variant(int format) {
 const char* qc_hip_int8_gemm_variant(void) { return "hip_gfx950_mfma_i8"; }
 
 int qc_hip_set_gemv_rows_per_wave(int rows) {
-  if (rows != 0 && rows != 1 && rows != 2 && rows != 4 && rows != 8) return QC_INVALID_ARGUMENT;
+  if (rows != 0 && rows != 1 && rows != 2 && rows != 4 && rows != 7 && rows != 8 && rows != 14)
+    return QC_INVALID_ARGUMENT;
   g_tuning.rows_per_wave = rows;
   return QC_OK;
 }

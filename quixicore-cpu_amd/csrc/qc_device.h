@@ -43,17 +43,54 @@ __device__ __forceinline__ float ubyte(uint32_t w) {
   return static_cast<float>(static_cast<uint8_t>(w >> (8 * B)));
 }
 
-// Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int offset = 32; offset >= 1; offset >>= 1) v += __shfl_xor(v, offset, 64);
-  return v;
+// Cross-lane moves with DPP (no LDS traffic).  Control words of the gfx9 DPP
+// encoding: row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143,
+// quad_perm [1,0,3,2] = 0xB1.  Lanes whose source is out of range, or that
+// the row/bank masks leave out, receive `old` (0 here).
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF, bool BOUND_ZERO = true>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK,
+                                                    BANK_MASK, BOUND_ZERO));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int offset = 32; offset >= 1; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
-  return v;
+// Value of the neighbouring lane l ^ 1.
+__device__ __forceinline__ float xor1_f32(float v) { return dpp_f32<0xB1>(v); }
+__device__ __forceinline__ int xor1_i32(int v) { return dpp_i32<0xB1>(v); }
+
+// Sum over the 64 lanes of a wavefront, valid in lane 63 only (the AMD DPP
+// reduction: partial sums within each 16-lane row, then row broadcasts).
+// Summation order is fixed, so results are deterministic.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  float t = v + dpp_f32<0x111>(v);       // + v[l-1]
+  t = t + dpp_f32<0x112>(v);             // + v[l-2]
+  t = t + dpp_f32<0x113>(v);             // + v[l-3]: sum of 4 lanes
+  t = t + dpp_f32<0x114, 0xF, 0xE, false>(t);   // lanes 4..15 of each row: sum of 8
+  t = t + dpp_f32<0x118, 0xF, 0xC, false>(t);   // lanes 8..15: lane 15 = row sum
+  t = t + dpp_f32<0x142, 0xA, 0xF, false>(t);   // rows 1, 3 += lane 15 of rows 0, 2
+  t = t + dpp_f32<0x143, 0xC, 0xF, false>(t);   // rows 2, 3 += lane 31: lane 63 = total
+  return t;
+}
+
+// Sum over the wavefront, returned to every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_lane63(v)), 63));
+}
+
+// Max over the wavefront of non-negative values (disabled DPP lanes read 0),
+// returned to every lane.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  float t = fmaxf(v, dpp_f32<0x111>(v));
+  t = fmaxf(t, dpp_f32<0x112>(v));
+  t = fmaxf(t, dpp_f32<0x113>(v));
+  t = fmaxf(t, dpp_f32<0x114, 0xF, 0xE, false>(t));
+  t = fmaxf(t, dpp_f32<0x118, 0xF, 0xC, false>(t));
+  t = fmaxf(t, dpp_f32<0x142, 0xA, 0xF, false>(t));
+  t = fmaxf(t, dpp_f32<0x143, 0xC, 0xF, false>(t));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 63));
 }
 
 // 4-byte-aligned 128-bit load (global_load_dwordx4 accepts dword alignment).

@@ -8,7 +8,7 @@
 namespace qc {
 
 struct GemvTuning {
-  int rows_per_wave = 0;  // GEMV rows per wavefront (1, 2, 4, 8; 0 = chosen from the shape)
+  int rows_per_wave = 0;  // GEMV rows per wavefront (1, 2, 4, 7, 8, 14; 0 = from the shape)
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).

@@ -63,22 +63,40 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | (static_cast<uint32_t>(d) << 24);
 }
 
-// Digits of x[0 : clen) into LDS.  Thread t handles half-blocks h = t, t+256, ...
-// of 16 elements; the two halves of a block sit in lanes t and t^1.
-template <bool WITH_SUMS>
-__device__ __forceinline__ void build_digits(uint8_t* lds, const float* __restrict__ x, int clen,
-                                             int kc, bool vec_ok) {
+// x values of this thread's half-blocks (16 elements each) of a chunk:
+// h = threadIdx.x + 256 j, j < NPM.  Issued before the weight loads so that
+// waiting for them does not wait for the weights (vmcnt retires in order).
+// Branch-free (an index past the chunk re-reads its last half-block, which
+// build_digits then skips): a branch around the loads would make the compiler
+// wait for them at the join, before the weight loads are issued.
+template <int NPM, bool VEC>
+__device__ __forceinline__ void load_x(float (&v)[NPM][16], const float* __restrict__ x, int clen) {
   const int nh = clen >> 4;
-  for (int h = threadIdx.x; h < nh; h += kThreads) {
-    float v[16];
-    if (vec_ok) {
+#pragma unroll
+  for (int j = 0; j < NPM; ++j) {
+    const int h = min(static_cast<int>(threadIdx.x) + kThreads * j, nh - 1);
+    if constexpr (VEC) {
       const float4* src = reinterpret_cast<const float4*>(x + 16 * h);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(v + 4 * i) = src[i];
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(&v[j][4 * i]) = src[i];
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = x[16 * h + i];
+      for (int i = 0; i < 16; ++i) v[j][i] = x[16 * h + i];
     }
+  }
+}
+
+// Digits of the loaded half-blocks into LDS; the two halves of a block sit
+// in lanes t and t^1.
+template <bool WITH_SUMS, int NPM>
+__device__ __forceinline__ void build_digits(uint8_t* lds, const float (&xv)[NPM][16], int clen,
+                                             int kc) {
+  const int nh = clen >> 4;
+#pragma unroll
+  for (int j = 0; j < NPM; ++j) {
+    const int h = threadIdx.x + kThreads * j;
+    if (h >= nh) break;
+    const float* v = xv[j];
     float m = 0.f;
     bool finite = true;
 #pragma unroll
@@ -86,8 +104,8 @@ __device__ __forceinline__ void build_digits(uint8_t* lds, const float* __restri
       m = fmaxf(m, fabsf(v[i]));
       finite = finite && isfinite(v[i]);
     }
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    finite = finite && (__shfl_xor(finite ? 1 : 0, 1, 64) != 0);
+    m = fmaxf(m, xor1_f32(m));
+    finite = finite && (xor1_i32(finite ? 1 : 0) != 0);
     int ex = 0;
     (void)frexpf(m, &ex);                            // m < 2^ex
     const int e = finite ? ex - 21 : 0;
@@ -121,9 +139,9 @@ __device__ __forceinline__ void build_digits(uint8_t* lds, const float* __restri
         s1 += d1[i];
         s2 += d2[i];
       }
-      s0 += __shfl_xor(s0, 1, 64);
-      s1 += __shfl_xor(s1, 1, 64);
-      s2 += __shfl_xor(s2, 1, 64);
+      s0 += xor1_i32(s0);
+      s1 += xor1_i32(s1);
+      s2 += xor1_i32(s2);
       if ((h & 1) == 0) {
         int* sums = reinterpret_cast<int*>(lds + dsum_off(kc));
         sums[blk] = s0;
@@ -245,11 +263,11 @@ __device__ __forceinline__ void load_pair(uint32_t* d, const uint8_t* p) {
 }
 
 // RB rows per wave, up to NPM pairs per lane per K chunk.
-template <int FMT, int RB, int NPM>
+template <int FMT, int RB, int NPM, bool VEC>
 __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __restrict__ W,
                                                              const float* __restrict__ x,
                                                              float* __restrict__ y, int n, int k,
-                                                             int kc, int vec_ok) {
+                                                             int kc) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int BB = Fmt<FMT>::block_bytes;
   constexpr int PD = Fmt<FMT>::pair_dwords;
@@ -267,7 +285,9 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
     const int clen = min(kc, k - c0);
     const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
     const int p0 = first_pair(pbeg, lane);
-    // 1. every weight load of this chunk, issued before the digit build
+    // 1. this thread's x values, then every weight load of this chunk
+    float xv[NPM][16];
+    load_x<NPM, VEC>(xv, x + c0, clen);
     uint32_t w[NPM][RB][PD];
 #pragma unroll
     for (int j = 0; j < NPM; ++j) {
@@ -277,7 +297,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
     }
     // 2. digits of x for this chunk
     if (c0) lds_barrier();
-    build_digits<FMT == kQ4_0>(lds, x + c0, clen, kc, vec_ok != 0);
+    build_digits<FMT == kQ4_0, NPM>(lds, xv, clen, kc);
     lds_barrier();
     // 3. exact block dots
 #pragma unroll
@@ -293,8 +313,8 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
   }
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    const float t = wave_sum(acc[r]);
-    if (lane == 0 && row0 + r < n) y[row0 + r] = t;
+    const float t = wave_sum_lane63(acc[r]);
+    if (lane == 63 && row0 + r < n) y[row0 + r] = t;
   }
 }
 
@@ -304,9 +324,47 @@ hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, 
   static_assert(RB * NPM * Fmt<FMT>::pair_dwords <= 144, "register budget");
   const int kc = NPM * 4096 < k ? NPM * 4096 : k;
   const int grid = (n + kWaves * RB - 1) / (kWaves * RB);
-  const int vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
-  qgemv_dot_kernel<FMT, RB, NPM><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc, vec);
+  if (reinterpret_cast<uintptr_t>(x) % 16 == 0)
+    qgemv_dot_kernel<FMT, RB, NPM, true><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
+  else
+    qgemv_dot_kernel<FMT, RB, NPM, false><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
   return hipGetLastError();
+}
+
+int cu_count() {
+  static int count = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return count;
+}
+
+// Rows per wave: the candidate that minimises the rows handled by the
+// busiest CU (all workgroups of a CU run together when there are at most two),
+// preferring two workgroups per CU, then one.
+int pick_rows(int n, const int* cand, int ncand) {
+  const int cus = cu_count();
+  int best = cand[0];
+  long long best_rows = -1;
+  int best_wpc = 0;
+  for (int i = 0; i < ncand; ++i) {
+    const int rb = cand[i];
+    const long long grid = (n + kWaves * rb - 1) / (kWaves * rb);
+    const long long wpc = (grid + cus - 1) / cus;
+    if (wpc > 2 && i + 1 < ncand) continue;
+    const long long rows = wpc * kWaves * rb;
+    const bool better = best_rows < 0 || rows < best_rows ||
+                        (rows == best_rows && wpc == 2 && best_wpc != 2);
+    if (better) {
+      best = rb;
+      best_rows = rows;
+      best_wpc = static_cast<int>(wpc);
+    }
+  }
+  return best;
 }
 
 template <int FMT>
@@ -314,25 +372,39 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, 
                       hipStream_t s) {
   const int npairs = k >> 6;
   const int npm = npairs <= 64 ? 1 : (npairs <= 128 ? 2 : 4);
-  // largest rows-per-wave allowed by the register budget for this K
-  const int cap = FMT == kQ8_0 ? (npm == 1 ? 8 : (npm == 2 ? 4 : 2)) : (npm == 1 ? 8 : 4);
-  if (rb == 0) rb = n >= 4 * 8 * 512 ? 8 : (n >= 4 * 4 * 256 ? 4 : (n >= 4 * 2 * 256 ? 2 : 1));
-  if (rb > cap) rb = cap;
   if (npm == 1) {
+    static const int q4c[] = {14, 7, 8, 4, 2, 1};
+    static const int q8c[] = {8, 7, 4, 2, 1};
+    if (rb == 0 || (FMT == kQ8_0 && rb > 8)) rb = FMT == kQ4_0 ? pick_rows(n, q4c, 6) : pick_rows(n, q8c, 5);
     switch (rb) {
       case 1: return launch_one<FMT, 1, 1>(W, x, y, n, k, s);
       case 2: return launch_one<FMT, 2, 1>(W, x, y, n, k, s);
       case 4: return launch_one<FMT, 4, 1>(W, x, y, n, k, s);
-      default: return launch_one<FMT, 8, 1>(W, x, y, n, k, s);
+      case 7: return launch_one<FMT, 7, 1>(W, x, y, n, k, s);
+      case 8: return launch_one<FMT, 8, 1>(W, x, y, n, k, s);
+      default:
+        if constexpr (FMT == kQ4_0) return launch_one<FMT, 14, 1>(W, x, y, n, k, s);
+        return launch_one<FMT, 8, 1>(W, x, y, n, k, s);
     }
   }
   if (npm == 2) {
+    static const int q4c[] = {7, 4, 2, 1};
+    static const int q8c[] = {4, 2, 1};
+    if (rb == 0 || rb > (FMT == kQ4_0 ? 7 : 4))
+      rb = FMT == kQ4_0 ? pick_rows(n, q4c, 4) : pick_rows(n, q8c, 3);
     switch (rb) {
       case 1: return launch_one<FMT, 1, 2>(W, x, y, n, k, s);
       case 2: return launch_one<FMT, 2, 2>(W, x, y, n, k, s);
-      default: return launch_one<FMT, 4, 2>(W, x, y, n, k, s);
+      case 4: return launch_one<FMT, 4, 2>(W, x, y, n, k, s);
+      default:
+        if constexpr (FMT == kQ4_0) return launch_one<FMT, 7, 2>(W, x, y, n, k, s);
+        return launch_one<FMT, 4, 2>(W, x, y, n, k, s);
     }
   }
+  static const int q4c[] = {4, 2, 1};
+  static const int q8c[] = {2, 1};
+  if (rb == 0 || rb > (FMT == kQ4_0 ? 4 : 2))
+    rb = FMT == kQ4_0 ? pick_rows(n, q4c, 3) : pick_rows(n, q8c, 2);
   switch (rb) {
     case 1: return launch_one<FMT, 1, 4>(W, x, y, n, k, s);
     case 2: return launch_one<FMT, 2, 4>(W, x, y, n, k, s);
@@ -345,7 +417,8 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, 
 }  // namespace
 
 // K % 64 == 0 and W 4-byte aligned (checked by the caller).  rows_per_wave:
-// 0 picks from the shape; otherwise 1, 2, 4 or 8, capped by the register budget.
+// 0 picks from the shape; otherwise 1, 2, 4, 7, 8 or 14, capped by the
+// register budget for K.
 hipError_t launch_qgemv_dot(int fmt, const void* Wv, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s) {
   const auto* W = static_cast<const uint8_t*>(Wv);

@@ -41,7 +41,7 @@ __device__ __forceinline__ float abs_max4(float4 v, float m) {
 __device__ __forceinline__ void block_max_or(float& m, int& bad) {
   __shared__ float smax[kThreads / 64];
   __shared__ int sbad[kThreads / 64];
-  m = wave_max(m);
+  m = wave_max_nonneg(m);
   bad = __any(bad) ? 1 : 0;
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void quantize_groups_generic(
     bad |= !isfinite(v);
     m = fmaxf(m, fabsf(v));
   }
-  m = wave_max(m);
+  m = wave_max_nonneg(m);
   if (__any(bad)) {
     if (status != nullptr) {
       if (lane == 0) *status = 3;

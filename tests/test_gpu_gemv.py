@@ -62,7 +62,7 @@ def test_qgemv_baseline_configs(qc, oracle, synth, dev, fmt, n, k):
     _check_rows(oracle, fmt, packed, x, y.cpu().numpy(), n, k)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 8, 4, 0])
+@pytest.mark.parametrize("rows", [1, 2, 7, 8, 14, 4, 0])
 def test_rows_per_wave_variants(qc, oracle, synth, dev, rows):
     import torch
     print(f"rows_per_wave={rows}", flush=True)
