@@ -41,7 +41,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=["headline", "all"], default="all")
+    p.add_argument("--only", choices=["headline", "all", "copy"], default="all",
+                   help="copy: a plain 64 MiB device copy, the calibration kernel for "
+                        "FETCH_SIZE / WRITE_SIZE counter runs")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--rows-per-wave", type=int, default=0)
@@ -190,6 +192,18 @@ def w8a8_case(qc, m, n, k, steps, warmup):
             "tops": ops / (wall * 1e-3) / 1e12, "kernel_tops": ops / (gpu * 1e-3) / 1e12}
 
 
+def profiled_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE runs,
+    scaled by the copy-kernel calibration, from the committed summary
+    profiles/<name>.txt (None if absent)."""
+    import re
+    path = os.path.join(ROOT, "profiles", name + ".txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
 def cpu_baseline(packed_dev, x_dev, y_dev, n, k, seconds):
     """Reference x86 q4_0 route (oracle/_ref) on this host: timing + gate."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -265,6 +279,14 @@ def main():
         sys.exit(1)
     if args.rows_per_wave:
         qc.set_gemv_rows_per_wave(args.rows_per_wave)
+    if args.only == "copy":
+        src = torch.randint(0, 255, (64 << 20,), dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 64 << 20, "launches": args.warmup + args.steps}))
+        return
     K, W = args.steps, args.warmup
     n, k = 14336, 4096
     head, packed, x, y = gemv_case(qc, 1, n, k, K, W, seed=1)
@@ -312,7 +334,7 @@ def main():
         "pct_hbm_peak": round(100.0 * head["gbs"] / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": profiled_traffic("q4_0_gemv_k4096_n14336"),
                      "kernel_us": round(head["gpu_ms"] * 1e3, 3)},
         "cpu_baseline": base,
         "check": gate,

@@ -10,9 +10,10 @@
 // and the integers q_j = rint(x_j * 2^-e_b), clamped to [-2^21, 2^21 - 1],
 // split into three int8 digits (floor division):
 //   q_j = 2^14 * d0_j + 2^7 * d1_j + d2_j,  d0 in [-128,127], d1, d2 in [0,127].
-// So x_j = 2^e_b * q_j + err_j with |err_j| <= 2^(e_b-1) <= max|x_b| * 2^-21:
-// a 22-bit fixed-point copy of the block whose error, after the contract's
-// normalisation by ||x||_2 ||w_hat_row||_2, is below 3e-6 in the worst case and
+// So x_j = 2^e_b * q_j + err_j with |err_j| <= 2^(e_b-1) <= max|x_b| * 2^-21
+// (2^-20 where the clamp applies): a 22-bit fixed-point copy of the block
+// whose error, after the contract's normalisation by ||x||_2 ||w_hat_row||_2
+// (Cauchy-Schwarz over blocks), is at most sqrt(32) * 2^-20 = 5.4e-6 and
 // ~1e-8 typically.  Scaling by 2^-e_b is exact (v_ldexp), so subnormal and
 // huge activations keep their precision.  Each block dot is then three exact
 // int32 sums of int8 x int8 products (v_dot4_i32_i8, 4 MACs per instruction):
