@@ -8,16 +8,19 @@
 //   y[m][n]   = (float(dot) * ws[n]) * as[m]     (two IEEE multiplies, no FMA)
 // W is [N][K] and X is token-major [M][K]: both operands are K-contiguous.
 //
-// Tiling: a 256-thread workgroup owns a 128(n) x 128(m) output tile; its
-// four wavefronts each own 64 x 64 as 4 x 4 MFMA tiles of 16 x 16.  Per
-// K step of 64 the workgroup stages W[128][64] and X[128][64] (8 KB each) in
-// LDS; a lane's 16-byte operand fragment is one row's 16-byte chunk, stored
-// with the chunk index XOR-swizzled by (row >> 2) & 3 so the 16 rows read by
-// one quarter-wave hit 16 distinct bank groups.  The next K step's global
-// loads are issued before the current step's MFMAs.
+// Tiling: a 256-thread workgroup owns a TN(n) x TM(m) output tile; its four
+// wavefronts form a 2 x 2 grid of (TN/2) x (TM/2) wave tiles made of 16 x 16
+// MFMA tiles.  The MFMA "A" operand is the W tile and "B" the X tile, so each
+// lane's four accumulators are 4 consecutive n of one m and the epilogue
+// stores 16 bytes.  Per K step of 64 the workgroup stages W[TN][64] and
+// X[TM][64] in LDS; a lane's 16-byte operand fragment is one row's 16-byte
+// chunk, stored with the chunk index XOR-swizzled by (row >> 2) & 3 so the 16
+// rows read by one quarter-wave hit 16 distinct bank groups.
 //
-// The MFMA's "A" operand is the W tile, "B" the X tile, so each lane's four
-// accumulators are 4 consecutive n of one m: the epilogue stores 16 bytes.
+// Pipeline: two LDS buffers and one register stage.  Iteration k stores the
+// registers holding step k+1 into the idle LDS buffer, issues the global loads
+// of step k+2, computes step k from the other buffer, then meets the
+// workgroup at a single barrier.
 #include "qc_device.h"
 #include "qc_internal.h"
 
@@ -27,8 +30,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kTileN = 128;
-constexpr int kTileM = 128;
 constexpr int kStepK = 64;
 // Largest K for which an int32 accumulator cannot overflow:
 // 131071 * 128 * 128 < 2^31.
@@ -38,11 +39,16 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return row * kStepK + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
+// Branch-free guarded 16-byte load: an out-of-range row or K chunk reads a
+// clamped in-range address; the caller zeroes it when it is staged into LDS
+// (one step later), so neither a branch nor the select forces a wait on the
+// load before the MFMAs of the current step.
 __device__ __forceinline__ v4i load16(const int8_t* base, long long rows, long long row,
-                                      long long ld, long long col, long long k) {
-  v4i v = {0, 0, 0, 0};
-  if (row < rows && col < k) v = *reinterpret_cast<const v4i*>(base + row * ld + col);
-  return v;
+                                      long long ld, long long col, long long k, bool& ok) {
+  ok = row < rows && col < k;
+  const long long r = row < rows ? row : rows - 1;
+  const long long c = col < k ? col : k - 16;
+  return *reinterpret_cast<const v4i*>(base + r * ld + c);
 }
 
 __device__ __forceinline__ float epilogue(int32_t acc, long long m, long long n, const float* ws,
@@ -55,74 +61,89 @@ __device__ __forceinline__ float epilogue(int32_t acc, long long m, long long n,
   return (static_cast<float>(acc) * ws[n]) * as[m];
 }
 
+template <int TN, int TM>
 __global__ __launch_bounds__(kThreads) void int8_gemm_mfma(
     const int8_t* __restrict__ W, const int8_t* __restrict__ X, const float* __restrict__ ws,
     const float* __restrict__ as, const int32_t* __restrict__ row_sum, const int* __restrict__ zp,
-    float* __restrict__ y, int32_t* __restrict__ acc_out, int M, int N, int K, int asym,
-    int* status) {
-  __shared__ __attribute__((aligned(16))) int8_t sW[kTileN * kStepK];
-  __shared__ __attribute__((aligned(16))) int8_t sX[kTileM * kStepK];
+    float* __restrict__ y, int32_t* __restrict__ acc_out, int M, int N, int K, int tiles_n,
+    int asym, int* status) {
+  constexpr int WN = TN / 2, WM = TM / 2;        // wave tile
+  constexpr int FN = WN / 16, FM = WM / 16;      // MFMA tiles per wave
+  constexpr int LW = TN * 4 / kThreads;          // 16-byte W chunks per thread per step
+  constexpr int LX = TM * 4 / kThreads;          // 16-byte X chunks per thread per step
+  __shared__ __attribute__((aligned(16))) int8_t sW[2][TN * kStepK];
+  __shared__ __attribute__((aligned(16))) int8_t sX[2][TM * kStepK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const long long n0 = static_cast<long long>(blockIdx.x) * kTileN;
-  const long long m0 = static_cast<long long>(blockIdx.y) * kTileM;
+  const long long n0 = static_cast<long long>(blockIdx.x % tiles_n) * TN;
+  const long long m0 = static_cast<long long>(blockIdx.x / tiles_n) * TM;
 
-  // global -> LDS mapping: two 16-byte chunks per thread per operand
-  const int lrow = tid >> 2;  // 0..63 (and +64)
+  // global -> LDS mapping: thread t moves chunk (t & 3) of rows (t >> 2) + 64 j
+  const int lrow = tid >> 2;
   const int lchunk = tid & 3;
-
-  v4i gw[2], gx[2];
+  v4i gw[LW], gx[LX];
+  bool okw[LW], okx[LX];
   auto fetch = [&](int k0) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      gw[h] = load16(W, N, n0 + lrow + 64 * h, K, k0 + 16 * lchunk, K);
-      gx[h] = load16(X, M, m0 + lrow + 64 * h, K, k0 + 16 * lchunk, K);
-    }
+    for (int j = 0; j < LW; ++j)
+      gw[j] = load16(W, N, n0 + lrow + 64 * j, K, k0 + 16 * lchunk, K, okw[j]);
+#pragma unroll
+    for (int j = 0; j < LX; ++j)
+      gx[j] = load16(X, M, m0 + lrow + 64 * j, K, k0 + 16 * lchunk, K, okx[j]);
+  };
+  const v4i zero = {0, 0, 0, 0};
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < LW; ++j)
+      *reinterpret_cast<v4i*>(&sW[buf][swz(lrow + 64 * j, lchunk)]) = okw[j] ? gw[j] : zero;
+#pragma unroll
+    for (int j = 0; j < LX; ++j)
+      *reinterpret_cast<v4i*>(&sX[buf][swz(lrow + 64 * j, lchunk)]) = okx[j] ? gx[j] : zero;
   };
 
-  v4i acc[4][4];
+  v4i acc[FN][FM];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  const int wn = (wave >> 1) * 64;  // wave's n offset inside the tile
-  const int wm = (wave & 1) * 64;   // wave's m offset inside the tile
+  const int wn = (wave >> 1) * WN;
+  const int wm = (wave & 1) * WM;
   const int frow = lane & 15;
   const int fchunk = lane >> 4;
+  const int nk = (K + kStepK - 1) / kStepK;
 
   fetch(0);
-  for (int k0 = 0; k0 < K; k0 += kStepK) {
-    __syncthreads();
+  stage(0);
+  if (nk > 1) fetch(kStepK);
+  __syncthreads();
+  for (int k = 0; k < nk; ++k) {
+    const int buf = k & 1;
+    if (k + 1 < nk) stage(buf ^ 1);
+    if (k + 2 < nk) fetch((k + 2) * kStepK);
+    v4i a[FN], b[FM];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      *reinterpret_cast<v4i*>(sW + swz(lrow + 64 * h, lchunk)) = gw[h];
-      *reinterpret_cast<v4i*>(sX + swz(lrow + 64 * h, lchunk)) = gx[h];
-    }
-    __syncthreads();
-    if (k0 + kStepK < K) fetch(k0 + kStepK);
-    v4i a[4], b[4];
+    for (int i = 0; i < FN; ++i) a[i] = *reinterpret_cast<const v4i*>(&sW[buf][swz(wn + 16 * i + frow, fchunk)]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4i*>(sW + swz(wn + 16 * i + frow, fchunk));
+    for (int j = 0; j < FM; ++j) b[j] = *reinterpret_cast<const v4i*>(&sX[buf][swz(wm + 16 * j + frow, fchunk)]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i*>(sX + swz(wm + 16 * j + frow, fchunk));
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < FM; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    __syncthreads();
   }
 
   // C layout of a 16x16 tile: lane holds rows 4*(lane>>4)+e (n), column lane&15 (m).
   if (acc_out != nullptr) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < FM; ++j) {
       const long long m = m0 + wm + 16 * j + (lane & 15);
       if (m >= M) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < FN; ++i) {
         const long long nb = n0 + wn + 16 * i + 4 * (lane >> 4);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -133,11 +154,13 @@ __global__ __launch_bounds__(kThreads) void int8_gemm_mfma(
   }
   bool bad = false;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < FM; ++j) {
     const long long m = m0 + wm + 16 * j + (lane & 15);
     if (m >= M) continue;
+    const float am = as[m];
+    bad |= !isfinite(am);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FN; ++i) {
       const long long nb = n0 + wn + 16 * i + 4 * (lane >> 4);
       float out[4];
 #pragma unroll
@@ -146,7 +169,6 @@ __global__ __launch_bounds__(kThreads) void int8_gemm_mfma(
         out[e] = epilogue(acc[i][j][e], m, n, ws, as, row_sum, zp, asym != 0);
         bad |= !isfinite(ws[n]);
       }
-      bad |= !isfinite(as[m]);
       float* dst = y + m * N + nb;
       if (nb + 3 < N && (N & 3) == 0) {
         *reinterpret_cast<float4*>(dst) = float4{out[0], out[1], out[2], out[3]};
@@ -183,6 +205,19 @@ __global__ __launch_bounds__(kThreads) void int8_gemm_simple(
   if (status != nullptr && !(isfinite(ws[n]) && isfinite(as[m]))) *status = 3;
 }
 
+template <int TN, int TM>
+hipError_t launch_tile(const int8_t* W, const int8_t* X, const float* ws, const float* as,
+                       const int32_t* row_sum, const int* zp, float* y, int32_t* acc_out,
+                       long long m, long long n, long long k, bool asymmetric, int* status,
+                       hipStream_t s) {
+  const long long tiles_n = (n + TN - 1) / TN;
+  const long long tiles_m = (m + TM - 1) / TM;
+  int8_gemm_mfma<TN, TM><<<static_cast<unsigned>(tiles_n * tiles_m), kThreads, 0, s>>>(
+      W, X, ws, as, row_sum, zp, y, acc_out, (int)m, (int)n, (int)k, (int)tiles_n,
+      asymmetric ? 1 : 0, status);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_int8_gemm(const int8_t* W, const int8_t* X, const float* ws, const float* as,
@@ -193,11 +228,11 @@ hipError_t launch_int8_gemm(const int8_t* W, const int8_t* X, const float* ws, c
                        reinterpret_cast<uintptr_t>(X) % 16 == 0 && k % 16 == 0;
   const bool fits = m <= 0x7FFFFFFFLL && n <= 0x7FFFFFFFLL && k <= kMaxK32;
   if (aligned && fits) {
-    const dim3 grid(static_cast<unsigned>((n + kTileN - 1) / kTileN),
-                    static_cast<unsigned>((m + kTileM - 1) / kTileM));
-    int8_gemm_mfma<<<grid, kThreads, 0, s>>>(W, X, ws, as, row_sum, zp, y, acc_out, (int)m,
-                                             (int)n, (int)k, asymmetric ? 1 : 0, status);
-    return hipGetLastError();
+    if (m >= 256)
+      return launch_tile<128, 256>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k, asymmetric,
+                                   status, s);
+    return launch_tile<128, 128>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k, asymmetric,
+                                 status, s);
   }
   const long long items = m * n;
   int8_gemm_simple<<<static_cast<unsigned>((items + kThreads - 1) / kThreads), kThreads, 0, s>>>(
