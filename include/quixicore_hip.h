@@ -125,6 +125,14 @@ const char* qc_hip_int8_gemm_variant(void);
  * Tuning knob with no reference counterpart. */
 int qc_hip_set_gemv_rows_per_wave(int rows);
 
+/* Kernel route of the int8 GEMM entry points (process-wide): 0 (default)
+ * chooses from the shape; 1 = full-line LDS ring (K % 32 == 0),
+ * 2 = 64-byte-step direct-to-LDS pipeline (K % 64 == 0), 3 = register-staged
+ * double buffer, 4 = one thread per output.  A route that cannot take a
+ * shape or alignment falls back to the default.  Every route returns the
+ * same bits.  Tuning and test knob with no reference counterpart. */
+int qc_hip_set_int8_gemm_route(int route);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,7 @@ namespace {
 
 thread_local std::string g_last_error;
 qc::GemvTuning g_tuning;
+int g_int8_route = qc::kInt8Auto;
 
 int device_error(hipError_t e) {
   g_last_error = hipGetErrorString(e);
@@ -210,7 +211,7 @@ int qc_hip_int8_gemm(const int8_t* w, const int8_t* x, const float* ws, const fl
   const hipStream_t s = as_stream(stream);
   if (dev_status != nullptr)
     return finish(qc::launch_int8_gemm(w, x, ws, as, row_sum, zp, y, nullptr, m, n, k,
-                                       asymmetric != 0, dev_status, s));
+                                       asymmetric != 0, dev_status, s, g_int8_route));
   bool finite = false;
   int st = all_finite(ws, n, s, &finite);
   if (st != QC_OK) return st;
@@ -219,7 +220,7 @@ int qc_hip_int8_gemm(const int8_t* w, const int8_t* x, const float* ws, const fl
   if (st != QC_OK) return st;
   if (!finite) return QC_INVALID_ARGUMENT;
   hipError_t e = qc::launch_int8_gemm(w, x, ws, as, row_sum, zp, y, nullptr, m, n, k,
-                                      asymmetric != 0, nullptr, s);
+                                      asymmetric != 0, nullptr, s, g_int8_route);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   return finish(e);
 }
@@ -236,7 +237,7 @@ int qc_hip_int8_gemm_i32(const int8_t* w, const int8_t* x, int32_t* acc, long lo
   if (k > 131071) return QC_INVALID_SHAPE;
   if (w == nullptr || x == nullptr || acc == nullptr) return QC_INVALID_ARGUMENT;
   return finish(qc::launch_int8_gemm(w, x, nullptr, nullptr, nullptr, nullptr, nullptr, acc, m,
-                                     n, k, false, nullptr, as_stream(stream)));
+                                     n, k, false, nullptr, as_stream(stream), g_int8_route));
 }
 
 int qc_hip_nonfinite_scan(const float* x, long long count, int* dev_flag, void* stream) {
@@ -256,6 +257,12 @@ int qc_hip_set_gemv_rows_per_wave(int rows) {
   if (rows != 0 && rows != 1 && rows != 2 && rows != 4 && rows != 7 && rows != 8 && rows != 14)
     return QC_INVALID_ARGUMENT;
   g_tuning.rows_per_wave = rows;
+  return QC_OK;
+}
+
+int qc_hip_set_int8_gemm_route(int route) {
+  if (route < qc::kInt8Auto || route > qc::kInt8Simple) return QC_INVALID_ARGUMENT;
+  g_int8_route = route;
   return QC_OK;
 }
 

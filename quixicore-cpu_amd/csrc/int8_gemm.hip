@@ -28,6 +28,9 @@ namespace qc {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+// 16-byte store that only assumes the 4-byte alignment of a float pointer
+// (global_store_dwordx4 accepts dword-aligned addresses).
+typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kThreads = 256;
 constexpr int kStepK = 64;
@@ -59,6 +62,468 @@ __device__ __forceinline__ float epilogue(int32_t acc, long long m, long long n,
     return (static_cast<float>(dot) * ws[n]) * as[m];
   }
   return (static_cast<float>(acc) * ws[n]) * as[m];
+}
+
+// Writes one wavefront's FN x FM grid of 16 x 16 accumulator tiles whose
+// origin is (mw, nw).  C layout of a 16x16 tile: the lane holds n rows
+// 4*(lane>>4)+e and m column lane&15.
+template <int FN, int FM>
+__device__ __forceinline__ void write_tile(const v4i (&acc)[FN][FM], long long mw, long long nw,
+                                           int lane, int M, int N, const float* ws,
+                                           const float* as, const int32_t* row_sum,
+                                           const int* zp, float* y, int32_t* acc_out, int asym,
+                                           int* status) {
+  if (acc_out != nullptr) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const long long m = mw + 16 * j + (lane & 15);
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const long long nb = nw + 16 * i + 4 * (lane >> 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (nb + e < N) acc_out[m * N + nb + e] = acc[i][j][e];
+      }
+    }
+    return;
+  }
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const long long m = mw + 16 * j + (lane & 15);
+    if (m >= M) continue;
+    const float am = as[m];
+    bad |= !isfinite(am);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const long long nb = nw + 16 * i + 4 * (lane >> 4);
+      float out[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const long long n = nb + e < N ? nb + e : N - 1;
+        out[e] = epilogue(acc[i][j][e], m, n, ws, as, row_sum, zp, asym != 0);
+        bad |= !isfinite(ws[n]);
+      }
+      float* dst = y + m * N + nb;
+      if (nb + 3 < N && (N & 3) == 0) {
+        *reinterpret_cast<f32x4_a4*>(dst) = f32x4_a4{out[0], out[1], out[2], out[3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (nb + e < N) dst[e] = out[e];
+      }
+    }
+  }
+  if (status != nullptr && __any(bad) && lane == 0) *status = 3;
+}
+
+// Output tile of workgroup `b` in an XCD-aware order.  Workgroups are handed
+// to the 8 XCDs round-robin (b % 8), each with its own L2, so the tiles one
+// XCD runs are made a contiguous range of a banded order (bands of kBandM
+// m-tiles, n-tiles within a band): an XCD then reads few W and X panels.
+constexpr int kXcds = 8;
+constexpr int kBandM = 4;
+__device__ __forceinline__ void tile_of(int b, int total, int tiles_n, int tiles_m, int& tn,
+                                        int& tm) {
+  const int q = total / kXcds, r = total % kXcds;
+  const int xcd = b % kXcds, idx = b / kXcds;
+  const int t = xcd * q + (xcd < r ? xcd : r) + idx;
+  const int band = t / (tiles_n * kBandM);
+  const int rem = t - band * tiles_n * kBandM;
+  const int left = tiles_m - band * kBandM;
+  const int gm = left < kBandM ? left : kBandM;
+  tn = rem / gm;
+  tm = band * kBandM + rem % gm;
+}
+
+// s_waitcnt vmcnt(N), leaving expcnt and lgkmcnt unconstrained (gfx9
+// encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Waits until at most G * min(D, ahead) loads are outstanding: the loads of
+// the `ahead` steps issued after the one needed now (at most D of them).
+template <int G, int D>
+__device__ __forceinline__ void wait_step(int ahead) {
+  if constexpr (D <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= D) wait_vmcnt<G * D>();
+    else wait_step<G, D - 1>(ahead);
+  }
+}
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+// global_load_lds_dwordx4: every lane sends 16 bytes from its own global
+// address to LDS byte lds + 16 * lane (`lds` is wave-uniform, passed in M0).
+// The address-space cast only exists in the device pass.
+__device__ __forceinline__ void load_lds16(const int8_t* g, int8_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+#endif
+}
+
+// Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() would
+// make the compiler drain every outstanding global->LDS load (vmcnt(0)) and
+// defeat the multi-stage prefetch; here the waits are explicit and the empty
+// asm statements only stop the compiler moving memory accesses across.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Direct-to-LDS pipelined kernel (K % 64 == 0).  An S-deep ring of LDS stages,
+// each holding W[TN][64] and X[TM][64] as 1 KB groups of 16 rows, is filled
+// with global_load_lds_dwordx4: one instruction moves a group, lane l writing
+// LDS bytes [16l, 16l+16) of it, i.e. row l>>2 at position l&3.  The lane
+// fetches logical chunk (l&3) ^ (l>>4), which realises the same XOR swizzle
+// as swz() for the fragment reads.  Loads run S-1 steps ahead of the MFMAs;
+// rows beyond M or N load a clamped in-range row whose products are never
+// stored.
+template <int TN, int TM, int S>
+__global__ __launch_bounds__(kThreads) void int8_gemm_dma(
+    const int8_t* __restrict__ W, const int8_t* __restrict__ X, const float* __restrict__ ws,
+    const float* __restrict__ as, const int32_t* __restrict__ row_sum, const int* __restrict__ zp,
+    float* __restrict__ y, int32_t* __restrict__ acc_out, int M, int N, int K, int tiles_n,
+    int tiles_m, int asym, int* status) {
+  constexpr int WN = TN / 2, WM = TM / 2;
+  constexpr int FN = WN / 16, FM = WM / 16;
+  constexpr int GW = TN / 16 / 4, GX = TM / 16 / 4;  // 1 KB groups per wave per step
+  constexpr int G = GW + GX;
+  constexpr int kStage = (TN + TM) * kStepK;
+  static_assert(GW >= 1 && GX >= 1 && S >= 2, "tile shape");
+  static_assert(G * (S - 2) < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) int8_t ring[S * kStage];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tn, tm;
+  tile_of(blockIdx.x, tiles_n * tiles_m, tiles_n, tiles_m, tn, tm);
+  const long long n0 = static_cast<long long>(tn) * TN;
+  const long long m0 = static_cast<long long>(tm) * TM;
+
+  // Source row pointers of this lane's groups, at logical chunk (l&3)^(l>>4).
+  const int chunk = ((lane & 3) ^ (lane >> 4)) * 16;
+  const int8_t* src[G];
+#pragma unroll
+  for (int j = 0; j < GW; ++j) {
+    long long r = n0 + 16 * (wave * GW + j) + (lane >> 2);
+    r = r < N ? r : N - 1;
+    src[j] = W + r * K + chunk;
+  }
+#pragma unroll
+  for (int j = 0; j < GX; ++j) {
+    long long r = m0 + 16 * (wave * GX + j) + (lane >> 2);
+    r = r < M ? r : M - 1;
+    src[GW + j] = X + r * K + chunk;
+  }
+  auto issue = [&](int step) {
+    int8_t* base = ring + (step % S) * kStage;
+    const int k0 = step * kStepK;
+#pragma unroll
+    for (int j = 0; j < GW; ++j) load_lds16(src[j] + k0, base + (wave * GW + j) * 1024);
+#pragma unroll
+    for (int j = 0; j < GX; ++j)
+      load_lds16(src[GW + j] + k0, base + TN * kStepK + (wave * GX + j) * 1024);
+  };
+
+  v4i acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  const int wn = (wave >> 1) * WN;
+  const int wm = (wave & 1) * WM;
+  const int frow = lane & 15;
+  const int fchunk = lane >> 4;
+  const int nk = K / kStepK;
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s);
+  for (int k = 0; k < nk; ++k) {
+    // Step k must have landed: the loads of the min(S-2, nk-1-k) later steps
+    // already issued may stay in flight.
+    wait_step<G, S - 2>(nk - 1 - k);
+    wait_lgkmcnt0();
+    // All waves' loads of step k are visible, and every wave is done reading
+    // the stage that the loads issued next will overwrite.
+    ring_barrier();
+    if (k + S - 1 < nk) issue(k + S - 1);
+    const int8_t* sw = ring + (k % S) * kStage;
+    const int8_t* sx = sw + TN * kStepK;
+    v4i a[FN], b[FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) a[i] = *reinterpret_cast<const v4i*>(&sw[swz(wn + 16 * i + frow, fchunk)]);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) b[j] = *reinterpret_cast<const v4i*>(&sx[swz(wm + 16 * j + frow, fchunk)]);
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+  write_tile<FN, FM>(acc, m0 + wm, n0 + wn, lane, M, N, ws, as, row_sum, zp, y, acc_out, asym,
+                     status);
+}
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Epilogue for 32 x 32 accumulator tiles (v_mfma_i32_32x32x32_i8 C layout:
+// the lane holds m column lane&31 and, in register e, n row
+// 8*(e>>2) + 4*(lane>>5) + (e&3): four runs of 4 consecutive n).  Every
+// scale (and zero-point term) the lane needs is loaded up front, so the
+// whole epilogue waits on memory once instead of once per output group.
+template <int FN, int FM>
+__device__ __forceinline__ void write_tile32(const v16i (&acc)[FN][FM], long long mw,
+                                             long long nw, int lane, int M, int N,
+                                             const float* ws, const float* as,
+                                             const int32_t* row_sum, const int* zp, float* y,
+                                             int32_t* acc_out, int asym, int* status) {
+  if (acc_out != nullptr) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const long long m = mw + 32 * j + (lane & 31);
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const long long nb = nw + 32 * i + 8 * g + 4 * (lane >> 5);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (nb + e < N) acc_out[m * N + nb + e] = acc[i][j][4 * g + e];
+        }
+    }
+    return;
+  }
+  float wsv[FN][16], asv[FM];
+  int32_t rsv[FN][16], zpv[FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      long long n = nw + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      n = n < N ? n : N - 1;
+      wsv[i][r] = ws[n];
+      rsv[i][r] = asym ? row_sum[n] : 0;
+    }
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    long long m = mw + 32 * j + (lane & 31);
+    m = m < M ? m : M - 1;
+    asv[j] = as[m];
+    zpv[j] = asym ? zp[m] : 0;
+  }
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const long long m = mw + 32 * j + (lane & 31);
+    if (m >= M) continue;
+    bad |= !isfinite(asv[j]);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const long long nb = nw + 32 * i + 8 * g + 4 * (lane >> 5);
+        float out[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          float d;
+          if (asym)
+            d = static_cast<float>(static_cast<long long>(acc[i][j][r]) -
+                                   static_cast<long long>(zpv[j]) * rsv[i][r]);
+          else
+            d = static_cast<float>(acc[i][j][r]);
+          out[e] = (d * wsv[i][r]) * asv[j];
+          bad |= nb + e < N && !isfinite(wsv[i][r]);
+        }
+        float* dst = y + m * N + nb;
+        if (nb + 3 < N && (N & 3) == 0) {
+          *reinterpret_cast<f32x4_a4*>(dst) = f32x4_a4{out[0], out[1], out[2], out[3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (nb + e < N) dst[e] = out[e];
+        }
+      }
+    }
+  }
+  if (status != nullptr && __any(bad) && lane == 0) *status = 3;
+}
+
+// Full-line ring kernel (K % 32 == 0).  Each K step covers 128 bytes of every
+// W and X row of the tile, i.e. whole 128-byte cache lines: the global->LDS
+// path delivers markedly more per CU for whole lines than for half lines.
+//
+// LDS: an S-deep ring of stages; a stage holds W[TN][128] then X[TM][128],
+// row-major, with the 16-byte chunk c of row r stored at position
+// c ^ ((r >> 1) & 7).  A global_load_lds_dwordx4 moves 8 rows (1 KB): lane l
+// writes position l&7 of row l>>3 and so fetches logical chunk
+// (l&7) ^ ((r >> 1) & 7).
+//
+// MFMA: v_mfma_i32_32x32x32_i8 (one wavefront sustains close to the CU's
+// int8 rate with it, unlike the 16x16x64 form).  A step is four K quarters
+// of 32; the operand of quarter q for a 32-row fragment is, in lane l,
+// row l&31, chunk 2q + (l>>5), the same lane->k map for W and X.  Those 64
+// reads fall on all 16 four-bank slots 4 times each under the swizzle above.
+//
+// Schedule (wavefront-uniform, branch-free in the steady state):
+//   prologue: issue the loads of steps 0..S-1 into stages 0..S-1;
+//   step k, quarter q = 0..2: read the fragments of quarter q+1 while the
+//     MFMAs of quarter q run;
+//   quarter 3: wait for this wave's loads of step k+1, barrier (all waves'
+//     loads are in and every wave has finished reading stage k), issue the
+//     loads of step k+S into stage k, read quarter 0 of step k+1, then the
+//     MFMAs of quarter 3.
+// Past the last step the loads repeat the last step into stages that are
+// never read again, which keeps every wait count a constant.  The last step
+// runs separately and, when K is not a multiple of 128, skips the quarters
+// past K (their loads read a clamped in-row address and are never used).
+template <int TN, int TM, int S, int WGN, int WGM>
+__global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
+    const int8_t* __restrict__ W, const int8_t* __restrict__ X, const float* __restrict__ ws,
+    const float* __restrict__ as, const int32_t* __restrict__ row_sum, const int* __restrict__ zp,
+    float* __restrict__ y, int32_t* __restrict__ acc_out, int M, int N, int K, int tiles_n,
+    int tiles_m, int asym, int* status) {
+  constexpr int kLine = 128;
+  constexpr int NW = WGN * WGM;                      // WGN x WGM grid of wavefronts
+  constexpr int WN = TN / WGN, WM = TM / WGM;        // wave tile
+  constexpr int FN = WN / 32, FM = WM / 32;          // 32 x 32 tiles per wave
+  constexpr int GW = TN / 8 / NW, GX = TM / 8 / NW;  // 8-row loads per wave per step
+  constexpr int G = GW + GX;
+  constexpr int kStage = (TN + TM) * kLine;
+  static_assert(FN >= 1 && FM >= 1 && GW >= 1 && GX >= 1 && S >= 2, "tile shape");
+  static_assert(GW % 2 == 0 && GX % 2 == 0, "8-row groups alternate swizzle parity");
+  static_assert(G * (S - 1) < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) int8_t ring[S * kStage];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tn, tm;
+  tile_of(blockIdx.x, tiles_n * tiles_m, tiles_n, tiles_m, tn, tm);
+  const long long n0 = static_cast<long long>(tn) * TN;
+  const long long m0 = static_cast<long long>(tm) * TM;
+
+  // Load j of a wave covers operand rows r = 8 * (wave * GW + j) + (lane >> 3)
+  // (W; likewise X with GX); its swizzle key (r >> 1) & 7 is
+  // 4 * (j & 1) + (lane >> 4), as GW and GX are even.
+  const int8_t* src[G];
+  int coff[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) coff[par] = ((lane & 7) ^ (4 * par + (lane >> 4))) * 16;
+#pragma unroll
+  for (int j = 0; j < GW; ++j) {
+    long long r = n0 + 8 * (wave * GW + j) + (lane >> 3);
+    r = r < N ? r : N - 1;
+    src[j] = W + r * K;
+  }
+#pragma unroll
+  for (int j = 0; j < GX; ++j) {
+    long long r = m0 + 8 * (wave * GX + j) + (lane >> 3);
+    r = r < M ? r : M - 1;
+    src[GW + j] = X + r * K;
+  }
+  auto issue = [&](int step, int stage) {
+    int8_t* base = ring + stage * kStage;
+    const int k0 = step * kLine;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      int off = k0 + coff[j & 1];
+      off = off < K - 16 ? off : K - 16;
+      int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
+                           : base + TN * kLine + (wave * GX + (j - GW)) * 1024;
+      load_lds16(src[j] + off, dst);
+    }
+  };
+
+  // Fragment offsets of quarter q within a 32-row block: row lane&31,
+  // position (2q + (lane>>5)) ^ ((row>>1)&7) = 2q ^ t.
+  const int t = (lane >> 5) ^ ((lane >> 1) & 7);
+  int foff[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) foff[q] = (lane & 31) * kLine + ((2 * q) ^ t) * 16;
+
+  v16i acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+  const int wn = (wave / WGM) * WN;
+  const int wm = (wave % WGM) * WM;
+  const int nq = K / 32;                 // K quarters in total
+  const int nk = (nq + 3) / 4;           // steps
+
+  v4i fa[2][FN], fb[2][FM];
+  auto read_frags = [&](int stage, int q, int slot) {
+    const int8_t* sw = ring + stage * kStage + wn * kLine + foff[q];
+    const int8_t* sx = ring + stage * kStage + (TN + wm) * kLine + foff[q];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) fa[slot][i] = *reinterpret_cast<const v4i*>(sw + 32 * i * kLine);
+#pragma unroll
+    for (int j = 0; j < FM; ++j) fb[slot][j] = *reinterpret_cast<const v4i*>(sx + 32 * j * kLine);
+  };
+  auto mfmas = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot][i], fb[slot][j], acc[i][j],
+                                                          0, 0, 0);
+  };
+
+#pragma unroll
+  for (int st = 0; st < S; ++st) issue(st < nk ? st : nk - 1, st);
+  wait_vmcnt<G * (S - 1)>();
+  ring_barrier();
+  read_frags(0, 0, 0);
+  int stage = 0;
+  for (int k = 0; k + 1 < nk; ++k) {
+    read_frags(stage, 1, 1);
+    mfmas(0);
+    read_frags(stage, 2, 0);
+    mfmas(1);
+    read_frags(stage, 3, 1);
+    mfmas(0);
+    // Loads issued: steps up to k+S-1; step k+1 must be in.
+    wait_vmcnt<G * (S - 2)>();
+    wait_lgkmcnt0();
+    ring_barrier();
+    issue(k + S < nk ? k + S : nk - 1, stage);
+    stage = stage + 1 < S ? stage + 1 : 0;
+    read_frags(stage, 0, 0);
+    mfmas(1);
+  }
+  {
+    const int qn = nq - 4 * (nk - 1);    // 1..4 quarters in the last step
+    if (qn > 1) read_frags(stage, 1, 1);
+    mfmas(0);
+    if (qn > 1) {
+      if (qn > 2) read_frags(stage, 2, 0);
+      mfmas(1);
+      if (qn > 2) {
+        if (qn > 3) read_frags(stage, 3, 1);
+        mfmas(0);
+        if (qn > 3) mfmas(1);
+      }
+    }
+  }
+  // No global->LDS load may still be in flight when the workgroup's LDS is
+  // released.
+  wait_vmcnt<0>();
+  write_tile32<FN, FM>(acc, m0 + wm, n0 + wn, lane, M, N, ws, as, row_sum, zp, y, acc_out, asym,
+                       status);
 }
 
 template <int TN, int TM>
@@ -136,50 +601,8 @@ __global__ __launch_bounds__(kThreads) void int8_gemm_mfma(
     __syncthreads();
   }
 
-  // C layout of a 16x16 tile: lane holds rows 4*(lane>>4)+e (n), column lane&15 (m).
-  if (acc_out != nullptr) {
-#pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const long long m = m0 + wm + 16 * j + (lane & 15);
-      if (m >= M) continue;
-#pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        const long long nb = n0 + wn + 16 * i + 4 * (lane >> 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (nb + e < N) acc_out[m * N + nb + e] = acc[i][j][e];
-      }
-    }
-    return;
-  }
-  bool bad = false;
-#pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const long long m = m0 + wm + 16 * j + (lane & 15);
-    if (m >= M) continue;
-    const float am = as[m];
-    bad |= !isfinite(am);
-#pragma unroll
-    for (int i = 0; i < FN; ++i) {
-      const long long nb = n0 + wn + 16 * i + 4 * (lane >> 4);
-      float out[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const long long n = nb + e < N ? nb + e : N - 1;
-        out[e] = epilogue(acc[i][j][e], m, n, ws, as, row_sum, zp, asym != 0);
-        bad |= !isfinite(ws[n]);
-      }
-      float* dst = y + m * N + nb;
-      if (nb + 3 < N && (N & 3) == 0) {
-        *reinterpret_cast<float4*>(dst) = float4{out[0], out[1], out[2], out[3]};
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (nb + e < N) dst[e] = out[e];
-      }
-    }
-  }
-  if (status != nullptr && __any(bad) && lane == 0) *status = 3;
+  write_tile<FN, FM>(acc, m0 + wm, n0 + wn, lane, M, N, ws, as, row_sum, zp, y, acc_out, asym,
+                     status);
 }
 
 // Exact fallback for any shape/alignment and for K beyond the int32 bound:
@@ -218,21 +641,84 @@ hipError_t launch_tile(const int8_t* W, const int8_t* X, const float* ws, const 
   return hipGetLastError();
 }
 
+template <int TN, int TM, int S, int WGN, int WGM>
+hipError_t launch_ring(const int8_t* W, const int8_t* X, const float* ws, const float* as,
+                       const int32_t* row_sum, const int* zp, float* y, int32_t* acc_out,
+                       long long m, long long n, long long k, bool asymmetric, int* status,
+                       hipStream_t s) {
+  const long long tiles_n = (n + TN - 1) / TN;
+  const long long tiles_m = (m + TM - 1) / TM;
+  int8_gemm_ring<TN, TM, S, WGN, WGM>
+      <<<static_cast<unsigned>(tiles_n * tiles_m), 64 * WGN * WGM, 0, s>>>(
+      W, X, ws, as, row_sum, zp, y, acc_out, (int)m, (int)n, (int)k, (int)tiles_n, (int)tiles_m,
+      asymmetric ? 1 : 0, status);
+  return hipGetLastError();
+}
+
+template <int TN, int TM, int S>
+hipError_t launch_dma(const int8_t* W, const int8_t* X, const float* ws, const float* as,
+                      const int32_t* row_sum, const int* zp, float* y, int32_t* acc_out,
+                      long long m, long long n, long long k, bool asymmetric, int* status,
+                      hipStream_t s) {
+  const long long tiles_n = (n + TN - 1) / TN;
+  const long long tiles_m = (m + TM - 1) / TM;
+  int8_gemm_dma<TN, TM, S><<<static_cast<unsigned>(tiles_n * tiles_m), kThreads, 0, s>>>(
+      W, X, ws, as, row_sum, zp, y, acc_out, (int)m, (int)n, (int)k, (int)tiles_n, (int)tiles_m,
+      asymmetric ? 1 : 0, status);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_int8_gemm(const int8_t* W, const int8_t* X, const float* ws, const float* as,
                             const int32_t* row_sum, const int* zp, float* y, int32_t* acc_out,
                             long long m, long long n, long long k, bool asymmetric, int* status,
-                            hipStream_t s) {
+                            hipStream_t s, int route) {
   const bool aligned = reinterpret_cast<uintptr_t>(W) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(X) % 16 == 0 && k % 16 == 0;
   const bool fits = m <= 0x7FFFFFFFLL && n <= 0x7FFFFFFFLL && k <= kMaxK32;
-  if (aligned && fits) {
-    if (m >= 256)
-      return launch_tile<128, 256>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k, asymmetric,
+  const bool can_ring = aligned && fits && k % 32 == 0;
+  const bool can_dma = aligned && fits && k % kStepK == 0;
+  const bool can_staged = aligned && fits;
+  if (route == kInt8Ring && !can_ring) route = kInt8Auto;
+  if (route == kInt8Dma && !can_dma) route = kInt8Auto;
+  if (route == kInt8Staged && !can_staged) route = kInt8Auto;
+  if (route == kInt8Auto)
+    route = can_ring ? kInt8Ring : can_staged ? kInt8Staged : kInt8Simple;
+  const bool wide = m >= 256;
+  switch (route) {
+    case kInt8Ring: {
+      // Largest tile that still gives (about) every CU a workgroup: the
+      // bytes moved per MFMA through a CU's global->LDS path bound this
+      // kernel, and a 256 x 256 tile moves 2/3 of what 128 x 256 does.
+      auto tiles = [&](long long tn, long long tm) { return ((n + tn - 1) / tn) * ((m + tm - 1) / tm); };
+      const long long cus = 256;
+      if (wide && tiles(256, 256) >= cus * 3 / 4)
+        return launch_ring<256, 256, 2, 4, 2>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k,
+                                              asymmetric, status, s);
+      if (wide && tiles(128, 256) >= cus * 3 / 4)
+        return launch_ring<128, 256, 3, 2, 4>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k,
+                                              asymmetric, status, s);
+      if (tiles(128, 128) >= cus * 3 / 4)
+        return launch_ring<128, 128, 4, 2, 4>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k,
+                                              asymmetric, status, s);
+      return launch_ring<64, 128, 4, 2, 2>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k,
+                                           asymmetric, status, s);
+    }
+    case kInt8Dma:
+      if (wide)
+        return launch_dma<128, 256, 4>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k,
+                                       asymmetric, status, s);
+      return launch_dma<128, 128, 4>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k, asymmetric,
+                                     status, s);
+    case kInt8Staged:
+      if (wide)
+        return launch_tile<128, 256>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k, asymmetric,
+                                     status, s);
+      return launch_tile<128, 128>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k, asymmetric,
                                    status, s);
-    return launch_tile<128, 128>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k, asymmetric,
-                                 status, s);
+    default:
+      break;
   }
   const long long items = m * n;
   int8_gemm_simple<<<static_cast<unsigned>((items + kThreads - 1) / kThreads), kThreads, 0, s>>>(

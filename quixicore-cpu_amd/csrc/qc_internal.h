@@ -32,10 +32,15 @@ hipError_t launch_nonfinite_scan(const float* x, long long count, int* flag, hip
 // acc_out (optional, test seam) receives the exact accumulators as int32
 // instead of y when non-null.  status (optional): set to 3 when a scale is
 // non-finite.
+// route: 0 = from the shape; 1 = full-line ring (K % 32 == 0), 2 = 64-byte
+// step direct-to-LDS (K % 64 == 0), 3 = register-staged (K % 16 == 0),
+// 4 = one thread per output.  Routes 1-3 also need 16-byte aligned W and X;
+// a route that cannot take the shape falls back to the default.
+enum Int8Route { kInt8Auto = 0, kInt8Ring = 1, kInt8Dma = 2, kInt8Staged = 3, kInt8Simple = 4 };
 hipError_t launch_int8_gemm(const int8_t* W, const int8_t* X, const float* ws, const float* as,
                             const int32_t* row_sum, const int* zp, float* y, int32_t* acc_out,
                             long long m, long long n, long long k, bool asymmetric,
-                            int* status, hipStream_t s);
+                            int* status, hipStream_t s, int route = kInt8Auto);
 
 // Weight packing / unpacking on the device (bit-exact with the reference
 // packers).  status: set to 3 on a non-finite weight (block left unwritten).

@@ -46,6 +46,7 @@ _SIGS = {
     "qc_hip_qgemv_variant": ([_I], ctypes.c_char_p),
     "qc_hip_int8_gemm_variant": ([], ctypes.c_char_p),
     "qc_hip_set_gemv_rows_per_wave": ([_I], _I),
+    "qc_hip_set_int8_gemm_route": ([_I], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -186,6 +187,12 @@ def int8_gemm_i32(w, x):
 
 def set_gemv_rows_per_wave(rows):
     _check(lib.qc_hip_set_gemv_rows_per_wave(rows), "set_gemv_rows_per_wave")
+
+
+def set_int8_gemm_route(route):
+    """0 = from the shape, 1 = full-line ring, 2 = 64-byte-step DMA,
+    3 = register-staged, 4 = one thread per output."""
+    _check(lib.qc_hip_set_int8_gemm_route(route), "set_int8_gemm_route")
 
 
 def qgemv_variant(fmt):

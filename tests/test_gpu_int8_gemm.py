@@ -34,18 +34,49 @@ def test_reference_grid_bit_exact(qc, oracle, dev):
                     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, n, k, asym)
 
 
+@pytest.fixture(params=[0, 1, 2, 3], ids=["auto", "ring", "dma", "staged"])
+def route(request, qc):
+    qc.set_int8_gemm_route(request.param)
+    yield request.param
+    qc.set_int8_gemm_route(0)
+
+
 @pytest.mark.parametrize("m,n,k", [(128, 128, 64), (200, 136, 1408), (37, 301, 4096),
-                                   (256, 512, 4160), (5, 4096, 4096)])
-def test_accumulators_exact(qc, dev, m, n, k):
-    print(f"int8 acc m={m} n={n} k={k}", flush=True)
+                                   (256, 512, 4160), (5, 4096, 4096), (257, 129, 64),
+                                   (300, 200, 128), (520, 130, 192), (1100, 390, 320),
+                                   (64, 96, 32), (513, 257, 96), (260, 140, 4128),
+                                   (33, 4100, 160), (1030, 6150, 96), (200, 16400, 64),
+                                   (1030, 9990, 96)])
+def test_accumulators_exact(qc, dev, route, m, n, k):
+    print(f"int8 acc route={route} m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(m * n + k)
     w = rng.integers(-128, 128, (n, k), dtype=np.int8)
     x = rng.integers(-128, 128, (m, k), dtype=np.int8)
     w[0, :] = -128
     x[0, :] = -128  # the largest products
     acc = qc.int8_gemm_i32(_t(w, dev), _t(x, dev)).cpu().numpy()
-    want = x.astype(np.int64) @ w.astype(np.int64).T
+    # float64 BLAS is exact here: every partial sum is an integer below 2^53
+    want = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64)
     assert np.array_equal(acc.astype(np.int64), want)
+
+
+@pytest.mark.parametrize("asym", [False, True])
+@pytest.mark.parametrize("m,n,k", [(300, 200, 4096), (700, 390, 1376)])
+def test_epilogue_bit_exact(qc, oracle, dev, route, m, n, k, asym):
+    """Full f32 epilogue (with and without the zero-point correction) on every
+    kernel route, bit-exact against the oracle over the whole matrix."""
+    print(f"int8 epilogue route={route} m={m} n={n} k={k} asym={asym}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    x = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    ws = rng.uniform(1e-4, 1e-2, n).astype(np.float32)
+    as_ = rng.uniform(1e-3, 1e-1, m).astype(np.float32)
+    rs = w.astype(np.int32).sum(axis=1).astype(np.int32) if asym else None
+    zp = rng.integers(-128, 128, m).astype(np.int32) if asym else None
+    st, want = oracle.int8_gemm(w, x, ws, as_, rs, zp, asym)
+    y = qc.int8_gemm(_t(w, dev), _t(x, dev), _t(ws, dev), _t(as_, dev),
+                     _t(rs, dev) if asym else None, _t(zp, dev) if asym else None, asym)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 def test_config3_sampled_bit_exact(qc, oracle, synth, dev):
