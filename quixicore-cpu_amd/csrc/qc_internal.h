@@ -19,6 +19,10 @@ hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long l
 hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s);
 
+// Small-batch GEMM on bf16 MFMA (m >= 2, K % 64 == 0, W 4-byte aligned).
+hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
+                             int k, hipStream_t s);
+
 // Per-group symmetric int8 quantization.  status == nullptr: caller has
 // already verified that x is finite.  Otherwise non-finite groups are left
 // unwritten and *status is set to 3 (kInvalidArgument).

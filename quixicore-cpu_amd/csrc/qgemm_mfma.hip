@@ -1,0 +1,564 @@
+// Small-batch q8_0 / q4_0 GEMM (2 <= M, in tiles of 16 activation rows) on
+// gfx950 bf16 MFMA.
+//
+// Semantics as the reference's qgemm (kernels/quantization/qgemm_ref.cpp:
+// 156-162, one qgemv per activation row: y[m][n] = sum_b d[n][b] *
+// sum_{k in b} q[n][k] * x[m][k]); the f32 outputs are held to the contract
+// bound |y - y_exact| <= 1e-4 * ||x_m|| * ||w_n|| like the M = 1 path.
+//
+// Numerics.  Each activation is split into two bf16 values, hi = bf16(x) and
+// lo = bf16(x - hi), so x - hi - lo is within 2^-17 |x|; the q8_0 codes
+// (|q| <= 127) and the q4_0 nibbles (0..15) are exact in bf16.  One
+// v_mfma_f32_16x16x32_bf16 covers exactly one 32-element block, so the block
+// dot sum_k q*hi + sum_k q*lo comes out of two MFMAs with f32 accumulation
+// and is then scaled by the block's fp16 d with one FMA per output.  For
+// q4_0 the -8 offset enters through the MFMA's C input: the block starts from
+// bias = -8 * sum_k (hi + lo), precomputed per activation row and block.
+// Worst-case error, normalised by ||x_m|| * ||w_n||: 2^-17 from the split,
+// about 32 * 2^-24 * 15/8 * sqrt(32) ~ 2e-5 from the f32 accumulation of the
+// q4 block sums, plus 2^-24 per block for the scaled accumulation -- well
+// inside 1e-4.
+//
+// Data flow.  A prep kernel writes the activation fragments in the MFMA
+// operand layout ([block][m-tile][hi | lo][64 lanes][16 B]) plus the q4 bias,
+// and zeroes y when two K halves will add into it.  The GEMM workgroup (8
+// wavefronts, 16 weight rows each = 128 rows) runs a ring of LDS stages, each
+// holding 4 block pairs (256 K) of its 128 weight rows -- whole row segments,
+// copied with global_load_lds_dwordx4, so every weight byte crosses the
+// memory system once in full cache lines -- and the activation fragments of
+// those blocks, which all 8 wavefronts share.  Each lane then picks its
+// codes and scales out of LDS.  The ring is 3 stages deep where LDS allows
+// (2 for q8_0 with 32 activation rows).
+//
+// K is split over `ks` workgroups per 128-row slab when N alone gives too
+// few workgroups.  With ks = 2 both halves add atomically into a y that the
+// prep kernel zeroed (two addends onto zero: order-independent); with
+// ks > 2 the partial sums go to a workspace and a small kernel adds them in
+// index order.  Results are deterministic either way.  (A per-workgroup
+// device-scope fence, as a "last workgroup reduces" scheme needs, writes
+// back the XCD's whole L2 and costs far more than the extra launch.)
+#include <mutex>
+#include <vector>
+
+#include "qc_device.h"
+#include "qc_internal.h"
+
+namespace qc {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kSlab = 16 * kWaves;       // weight rows per workgroup
+constexpr int kStagePairs = 4;           // block pairs per ring stage
+constexpr int kStageBlocks = 2 * kStagePairs;
+
+// Bytes of activation fragments per block and m-tile: hi and lo, 64 lanes x 16 B.
+constexpr int kFragBytes = 2048;
+
+template <int FMT>
+struct PairLayout;
+// q8_0 pair (68 B): d0 @0, q0 @2..33, d1 @34, q1 @36..67.  Lane group j
+// (lane >> 4) needs codes 8j..8j+7 of each block.
+template <>
+struct PairLayout<kQ8_0> {
+  static constexpr int bytes = 68;
+  __device__ static int blk0_dword(int j) { return 2 * j; }   // 3 dwords, bytes 2.. of them
+  __device__ static int blk1_dword(int j) { return 9 + 2 * j; }
+  static constexpr int scale1_dword = 8;                       // d1 in the high half
+};
+// q4_0 pair (36 B): d0 @0, nibbles @2..17, d1 @18, nibbles @20..35.  Byte i of
+// a block holds code i (low nibble) and code i+16 (high nibble), so lane
+// groups j and j+2 read the same 8 bytes.
+template <>
+struct PairLayout<kQ4_0> {
+  static constexpr int bytes = 36;
+  __device__ static int blk0_dword(int j) { return 2 * (j & 1); }
+  __device__ static int blk1_dword(int j) { return 5 + 2 * (j & 1); }
+  static constexpr int scale1_dword = 4;
+};
+
+typedef uint32_t u32x3_a4 __attribute__((ext_vector_type(3), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+// Eight codes of this lane for one block as a bf16 MFMA operand.
+template <int FMT>
+__device__ __forceinline__ bf16x8 codes_bf16(uint32_t lo, uint32_t hi, int j) {
+  bf16x8 v;
+  if constexpr (FMT == kQ8_0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>(lo >> (8 * i))));
+      v[4 + i] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>(hi >> (8 * i))));
+    }
+  } else {
+    const int sh = (j >> 1) * 4;          // lane groups 2, 3 take the high nibbles
+    const uint32_t a = (lo >> sh) & 0x0F0F0F0Fu, b = (hi >> sh) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = static_cast<__bf16>(static_cast<float>((a >> (8 * i)) & 0xFFu));
+      v[4 + i] = static_cast<__bf16>(static_cast<float>((b >> (8 * i)) & 0xFFu));
+    }
+  }
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Waits until at most G * min(D, ahead) loads are outstanding (`ahead` is a
+// constant once the stage loop is unrolled).
+template <int G, int D>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if constexpr (D <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= D) wait_vmcnt<G * D>();
+    else wait_stages<G, D - 1>(ahead);
+  }
+}
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+// Barrier that neither drains outstanding global->LDS loads (the waits are
+// explicit) nor lets the compiler move memory accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+#endif
+}
+
+// global_load_lds_dwordx4 from a wave-uniform base (scalar registers) plus a
+// per-lane byte offset, to LDS byte lds + 16 * lane (lds wave-uniform, in
+// M0).  Written as inline assembly so the compiler, which cannot see that
+// the ring slots read next are not the ones being filled, adds no waits of
+// its own: the kernels wait for these loads explicitly (wait_vmcnt) before
+// any read of the data and before the workgroup ends.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, const void* lds) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));  // LDS offset
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory", "m0");
+}
+
+// Same with a per-lane 64-bit address (used only for a short last stage).
+__device__ __forceinline__ void dma16_addr(const void* addr, const void* lds) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(addr), "s"(m0)
+      : "memory", "m0");
+}
+
+// Activation fragments: one 64-thread workgroup per (block b, m-tile t).
+// Lane l covers row 16t + (l & 15), codes 8(l >> 4) .. +7 of the block.
+// Block 0 also copies the weights' last row's short final stage (`tail`
+// bytes from `tail_src`) into the zero-padded `tail_pad` (pad_bytes), which
+// the GEMM reads instead of running past the end of W.
+template <int T, bool BIAS>
+__global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, int M, int K,
+                                                 uint8_t* __restrict__ xf,
+                                                 float* __restrict__ bias, float* zero_y,
+                                                 long long zero_count,
+                                                 const uint8_t* __restrict__ tail_src, int tail,
+                                                 uint8_t* __restrict__ tail_pad, int pad_bytes) {
+  if (blockIdx.x == 0 && tail > 0)
+    for (int i = threadIdx.x; i < pad_bytes; i += 64) tail_pad[i] = i < tail ? tail_src[i] : 0;
+  const int b = blockIdx.x / T, t = blockIdx.x % T;
+  const int l = threadIdx.x;
+  const int m = 16 * t + (l & 15), j = l >> 4;
+  const int nb = K / 32;
+  float v[8];
+  const bool live = m < M && b < nb;
+  const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * b : 0) + 8 * j;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = live ? src[i] : 0.0f;
+  bf16x8 hi, lo;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    hi[i] = static_cast<__bf16>(v[i]);
+    const float h = static_cast<float>(hi[i]);
+    lo[i] = static_cast<__bf16>(v[i] - h);
+    s += h + static_cast<float>(lo[i]);
+  }
+  uint8_t* dst = xf + (static_cast<long long>(b) * T + t) * kFragBytes + 16 * l;
+  *reinterpret_cast<bf16x8*>(dst) = hi;
+  *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
+  if constexpr (BIAS) {
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    if (j == 0) bias[(static_cast<long long>(b) * T + t) * 16 + (l & 15)] = -8.0f * s;
+  }
+  // y is accumulated with two atomic adds when K is split in two: clear it.
+  for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
+       i += static_cast<long long>(gridDim.x) * 64)
+    zero_y[i] = 0.0f;
+}
+
+// Sum of the ks partial results in index order (K split more than twice).
+__global__ __launch_bounds__(256) void qgemm_reduce(const float* __restrict__ partial,
+                                                    float* __restrict__ y, long long count,
+                                                    int ks) {
+  for (long long o = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; o < count;
+       o += static_cast<long long>(gridDim.x) * 256) {
+    float sum = partial[o];
+    for (int q = 1; q < ks; ++q) sum += partial[static_cast<long long>(q) * count + o];
+    y[o] = sum;
+  }
+}
+
+// Weight rows of one ring stage (4 block pairs): whole 16-byte chunks, so a
+// wavefront's 16 rows are copied to LDS with global_load_lds_dwordx4 as
+// contiguous row segments (every byte read once, full cache lines).
+template <int FMT>
+struct WStage {
+  static constexpr int row_bytes = kStagePairs * PairLayout<FMT>::bytes;  // 272 / 144
+  static constexpr int chunks = row_bytes / 16;                          // 17 / 9
+  static_assert(row_bytes % 16 == 0, "stage rows must be whole chunks");
+  static constexpr int wave_chunks = 16 * chunks;
+  static constexpr int loads = (wave_chunks + 63) / 64;                   // per wave per stage
+  static constexpr int last_lanes = wave_chunks - 64 * (loads - 1);      // active in the last
+  static constexpr int wave_bytes = 16 * row_bytes;
+};
+
+template <int FMT, int T>
+struct StageLayout {
+  static constexpr bool bias = FMT == kQ4_0;
+  static constexpr int w_bytes = kWaves * WStage<FMT>::wave_bytes;
+  static constexpr int x_bytes = kStageBlocks * T * kFragBytes;
+  static constexpr int bias_bytes = bias ? kStageBlocks * T * 64 : 0;
+  static constexpr int bytes = w_bytes + x_bytes + bias_bytes;
+  // Ring depth: three stages when they fit the 160 KB LDS, else two.
+  static constexpr int ring = 3 * bytes <= 160 * 1024 ? 3 : 2;
+  static constexpr int gx = x_bytes / 1024 / kWaves;
+  static constexpr int g = WStage<FMT>::loads + gx + (bias ? 1 : 0);  // loads per wave per stage
+};
+
+template <int FMT, int T, int NST>
+__global__ __launch_bounds__(kThreads) void qgemm_mfma(
+    const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
+    float* __restrict__ y, float* __restrict__ partial, const uint8_t* __restrict__ tail_pad,
+    int M, int N, int K, int nslabs, int ks_count, int nstages) {
+  using L = StageLayout<FMT, T>;
+  using WS = WStage<FMT>;
+  constexpr int S = L::ring;
+  constexpr int G = L::g;
+  constexpr int kBiasPerWave = L::bias_bytes / kWaves;
+  static_assert(L::bias_bytes % (16 * kWaves) == 0, "bias split");
+  static_assert(L::gx >= 1 && L::x_bytes % (1024 * kWaves) == 0, "stage split");
+  static_assert(G * (S - 1) < 64, "vmcnt range");
+  // One LDS array per ring slot: slot indices are compile-time after
+  // unrolling, so the compiler can tell the reads of one slot from the
+  // global->LDS writes into another and adds no waits of its own.
+  __shared__ __attribute__((aligned(1024))) uint8_t ring0[L::bytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring1[L::bytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring2[S > 2 ? L::bytes : 16];
+  auto slot_base = [&](int slot) -> uint8_t* { return slot == 0 ? ring0 : slot == 1 ? ring1 : ring2; };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane >> 4;
+  const int slab = blockIdx.x % nslabs;
+  const int ks = blockIdx.x / nslabs;
+  // NST stages per workgroup (the last K range may hold fewer).
+  const int st0 = ks * NST;
+  const int st1 = st0 + NST < nstages ? st0 + NST : nstages;
+  const int npairs = K / 64;
+  const long long row_bytes = static_cast<long long>(K / 32) * (PairLayout<FMT>::bytes / 2);
+  const int n = slab * kSlab + wave * 16 + (lane & 15);
+
+  // Every global->LDS load addresses a wave-uniform base (scalar registers)
+  // plus a per-lane 32-bit offset that never changes, so no register holding
+  // an in-flight load's address is ever reused (which would make the
+  // compiler wait for that load).  W must therefore span < 4 GiB.
+  // Weight chunk c = 64 q + lane of the wave's 16 stage rows is row
+  // c / chunks, bytes 16 (c % chunks) of the row's stage segment.
+  uint32_t wrow_off[WS::loads], wchunk[WS::loads];
+  bool wlast[WS::loads];   // chunk of W's last row
+#pragma unroll
+  for (int q = 0; q < WS::loads; ++q) {
+    int c = 64 * q + lane;
+    c = c < WS::wave_chunks ? c : WS::wave_chunks - 1;
+    int r = slab * kSlab + wave * 16 + c / WS::chunks;
+    r = r < N ? r : N - 1;
+    wrow_off[q] = static_cast<uint32_t>(static_cast<long long>(r) * row_bytes);
+    wchunk[q] = static_cast<uint32_t>(16 * (c % WS::chunks));
+    wlast[q] = r == N - 1;
+  }
+  // A last stage with fewer than 4 pairs runs past each row's end into the
+  // following rows; those bytes belong to skipped pairs.  W's last row takes
+  // its final stage from the zero-padded copy, and any chunk that would run
+  // past the end of W (holding skipped bytes only) reads the copy as well.
+  const bool short_tail = npairs % kStagePairs != 0;
+  const unsigned long long w_end = static_cast<unsigned long long>(N) * row_bytes;
+  const uint32_t xoff = static_cast<uint32_t>(wave * L::gx * 1024 + lane * 16);
+  const uint32_t boff = static_cast<uint32_t>(wave * kBiasPerWave + lane * 16);
+  auto issue = [&](int stage, int slot) {
+    const int st = stage < st1 ? stage : st1 - 1;
+    const uint8_t* base = slot_base(slot);
+    const uint32_t seg = static_cast<uint32_t>(st) * WS::row_bytes;
+    if (short_tail && st == nstages - 1) {
+#pragma unroll
+      for (int q = 0; q < WS::loads; ++q) {
+        const unsigned long long a = static_cast<unsigned long long>(wrow_off[q]) + seg + wchunk[q];
+        const uint8_t* src = wlast[q] || a + 16 > w_end ? tail_pad + wchunk[q] : W + a;
+        const uint8_t* dst = base + wave * WS::wave_bytes + q * 1024;
+        if (q + 1 < WS::loads || lane < WS::last_lanes) dma16_addr(src, dst);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < WS::loads; ++q) {
+        const uint8_t* dst = base + wave * WS::wave_bytes + q * 1024;
+        if (q + 1 < WS::loads || lane < WS::last_lanes) dma16(W, wrow_off[q] + seg + wchunk[q], dst);
+      }
+    }
+    const uint8_t* xs = xf + static_cast<long long>(st) * L::x_bytes;
+#pragma unroll
+    for (int i = 0; i < L::gx; ++i)
+      dma16(xs, xoff + i * 1024, base + L::w_bytes + (wave * L::gx + i) * 1024);
+    if constexpr (L::bias) {
+      // Wave w moves bias bytes [w, w+1) * kBiasPerWave of the stage with
+      // its first kBiasPerWave / 16 lanes.
+      const uint8_t* bs = reinterpret_cast<const uint8_t*>(bias) +
+                          static_cast<long long>(st) * L::bias_bytes;
+      if (lane < kBiasPerWave / 16)
+        dma16(bs, boff, base + L::w_bytes + L::x_bytes + wave * kBiasPerWave);
+    }
+  };
+
+  f32x4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int stage, int slot) {
+    const uint8_t* base = slot_base(slot);
+    const uint8_t* row = base + wave * WS::wave_bytes + (lane & 15) * WS::row_bytes;
+    const uint8_t* xs = base + L::w_bytes;
+#pragma unroll
+    for (int pp = 0; pp < kStagePairs; ++pp) {
+      if (stage * kStagePairs + pp >= npairs) break;   // wave-uniform
+      const uint32_t* pr = reinterpret_cast<const uint32_t*>(row + pp * PairLayout<FMT>::bytes);
+      const u32x3_a4 b0 = *reinterpret_cast<const u32x3_a4*>(pr + PairLayout<FMT>::blk0_dword(j));
+      const u32x2_a4 b1 = *reinterpret_cast<const u32x2_a4*>(pr + PairLayout<FMT>::blk1_dword(j));
+      const uint32_t s0 = pr[0], s1 = pr[PairLayout<FMT>::scale1_dword];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t c0 = h == 0 ? __builtin_amdgcn_alignbyte(b0.y, b0.x, 2) : b1.x;
+        const uint32_t c1 = h == 0 ? __builtin_amdgcn_alignbyte(b0.z, b0.y, 2) : b1.y;
+        const bf16x8 wv = codes_bf16<FMT>(c0, c1, j);
+        const float d = half_bits_to_float(h == 0 ? (s0 & 0xFFFFu) : (s1 >> 16));
+        const int blk = 2 * pp + h;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint8_t* f = xs + (blk * T + t) * kFragBytes + lane * 16;
+          const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
+          const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+          f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (L::bias)
+            c = *reinterpret_cast<const f32x4*>(xs + L::x_bytes + (blk * T + t) * 64 + 16 * j);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv, c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv, c, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(c[e], d, acc[t][e]);
+        }
+      }
+    }
+  };
+
+  // Fully unrolled over the workgroup's NST stages (straight-line code).
+  // Each step waits for its stage, meets the workgroup (so the slot the
+  // next issue overwrites is no longer read), issues the loads S-1 stages
+  // ahead and then computes, so S-1 stages are in flight during the
+  // compute.  Stages past st1 only issue (clamped) loads.
+#pragma unroll
+  for (int i = 0; i < S - 1; ++i)
+    if (i < NST) issue(st0 + i, i);
+#pragma unroll
+  for (int i = 0; i < NST; ++i) {
+    const int cur = st0 + i;
+    // Stage `cur` has landed; the issues of min(S-2, NST-1-i) later stages
+    // may still be in flight.
+    wait_stages<G, S - 2>(NST - 1 - i);
+    wait_lgkmcnt0();
+    ring_barrier();
+    if (i + S - 1 < NST) issue(cur + S - 1, (i + S - 1) % S);
+    if (cur < st1) compute(cur, i % S);
+  }
+  wait_vmcnt<0>();   // no global->LDS load may outlive the workgroup's LDS
+
+  // acc[t][e] is output (m = 16t + 4j + e, n).  One K range: store.  Two:
+  // both add into the zeroed y (0 + a + b == 0 + b + a, so the result does
+  // not depend on which finishes first).  More: partial sums for the
+  // reduction kernel.
+  if (n >= N) return;
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 16 * t + 4 * j + e;
+      if (m >= M) continue;
+      const long long o = static_cast<long long>(m) * N + n;
+      if (ks_count == 1) y[o] = acc[t][e];
+      else if (ks_count == 2) atomicAdd(y + o, acc[t][e]);
+      else partial[static_cast<long long>(ks) * M * N + o] = acc[t][e];
+    }
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  return cus;
+}
+
+// Workspace (activation fragments and partial sums) kept per
+// (device, stream) and reused by every call on that stream: stream order
+// keeps successive calls from overlapping, and calls on different streams
+// never share a buffer.  A buffer only grows; the one it replaces is freed
+// after the stream drains (or, under graph capture, kept until exit).
+struct StreamWorkspace {
+  int device;
+  hipStream_t stream;
+  void* ptr;
+  size_t bytes;
+};
+
+hipError_t workspace_for(hipStream_t s, size_t bytes, void** out) {
+  static std::mutex mu;
+  static std::vector<StreamWorkspace> table;
+  static std::vector<void*> retired;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  for (auto& w : table) {
+    if (w.device != dev || w.stream != s) continue;
+    if (w.bytes >= bytes) {
+      *out = w.ptr;
+      return hipSuccess;
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(s, &cap);
+    if (e != hipSuccess) return e;
+    if (cap == hipStreamCaptureStatusNone) {
+      e = hipStreamSynchronize(s);
+      if (e != hipSuccess) return e;
+      e = hipFree(w.ptr);
+      if (e != hipSuccess) return e;
+    } else {
+      retired.push_back(w.ptr);   // may still be used by the captured work
+    }
+    w.ptr = nullptr;
+    w.bytes = 0;
+    e = hipMalloc(&w.ptr, bytes);
+    if (e != hipSuccess) return e;
+    w.bytes = bytes;
+    *out = w.ptr;
+    return hipSuccess;
+  }
+  void* p = nullptr;
+  e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return e;
+  table.push_back({dev, s, p, bytes});
+  *out = p;
+  return hipSuccess;
+}
+
+template <int FMT, int T, int NST>
+hipError_t launch_nst(const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
+                      float* partial, const uint8_t* tail_pad, int m, int n, int k, int nslabs,
+                      int ks, int nstages, hipStream_t s) {
+  qgemm_mfma<FMT, T, NST><<<nslabs * ks, kThreads, 0, s>>>(W, xf, bias, y, partial, tail_pad, m,
+                                                            n, k, nslabs, ks, nstages);
+  return hipGetLastError();
+}
+
+template <int FMT, int T>
+hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, hipStream_t s) {
+  const int nb = k / 32;
+  const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
+  const int nbp = nstages * kStageBlocks;
+  const int nslabs = (n + kSlab - 1) / kSlab;
+  // One workgroup per CU at a time (LDS ring + 8 wavefronts).  Each
+  // workgroup takes NST consecutive stages (fully unrolled); NST is the
+  // largest of 16, 8, 4, 2, 1 that still gives about 3/4 of the CUs a
+  // workgroup, which keeps K split as few ways as possible.
+  const int cus = device_cus();
+  int nst = 16;
+  while (nst > 1 && static_cast<long long>(nslabs) * ((nstages + nst - 1) / nst) * 4 < 3LL * cus)
+    nst /= 2;
+  const int ks = (nstages + nst - 1) / nst;
+  const size_t xf_bytes = static_cast<size_t>(nbp) * T * kFragBytes;
+  const size_t bias_bytes = FMT == kQ4_0 ? static_cast<size_t>(nbp) * T * 64 : 0;
+  const size_t part_bytes = ks > 2 ? static_cast<size_t>(ks) * m * n * sizeof(float) : 0;
+  const size_t pad_bytes = WStage<FMT>::row_bytes;
+  const size_t total = xf_bytes + bias_bytes + part_bytes + pad_bytes + 256;
+  void* ws = nullptr;
+  hipError_t e = workspace_for(s, total, &ws);
+  if (e != hipSuccess) return e;
+  uint8_t* xf = static_cast<uint8_t*>(ws);
+  float* bias = reinterpret_cast<float*>(xf + xf_bytes);
+  float* partial = reinterpret_cast<float*>(xf + xf_bytes + bias_bytes);
+  uint8_t* tail_pad = xf + xf_bytes + bias_bytes + part_bytes;
+  const long long outs = static_cast<long long>(m) * n;
+  const long long row_bytes = static_cast<long long>(nb) * PairLayout<FMT>::bytes / 2;
+  const int tail = (k / 64) % kStagePairs * PairLayout<FMT>::bytes;
+  const uint8_t* tail_src = W + (n - 1) * row_bytes + static_cast<long long>(nstages - 1) * WStage<FMT>::row_bytes;
+  qgemm_prep<T, FMT == kQ4_0><<<nbp * T, 64, 0, s>>>(x, m, k, xf, bias, y, ks == 2 ? outs : 0,
+                                                     tail_src, tail, tail_pad,
+                                                     static_cast<int>(pad_bytes));
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  switch (nst) {
+    case 16: e = launch_nst<FMT, T, 16>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
+    case 8: e = launch_nst<FMT, T, 8>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
+    case 4: e = launch_nst<FMT, T, 4>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
+    case 2: e = launch_nst<FMT, T, 2>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
+    default: e = launch_nst<FMT, T, 1>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
+  }
+  if (e != hipSuccess || ks <= 2) return e;
+  const long long blocks = (outs + 255) / 256;
+  qgemm_reduce<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(partial, y, outs, ks);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
+                             int k, hipStream_t s) {
+  const auto* w = static_cast<const uint8_t*>(W);
+  for (int m0 = 0; m0 < m; m0 += 32) {
+    const int mt = m - m0 < 32 ? m - m0 : 32;
+    const float* xm = x + static_cast<long long>(m0) * k;
+    float* ym = y + static_cast<long long>(m0) * n;
+    hipError_t e;
+    if (fmt == kQ8_0)
+      e = mt <= 16 ? run<kQ8_0, 1>(w, xm, ym, mt, n, k, s) : run<kQ8_0, 2>(w, xm, ym, mt, n, k, s);
+    else
+      e = mt <= 16 ? run<kQ4_0, 1>(w, xm, ym, mt, n, k, s) : run<kQ4_0, 2>(w, xm, ym, mt, n, k, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace qc

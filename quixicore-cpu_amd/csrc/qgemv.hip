@@ -265,6 +265,11 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, 
   }
   const int vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (k % 4 == 0);
   if (m == 1) return launch_qgemv_dot(FMT, W, x, y, n, k, t.rows_per_wave, s);
+  // The MFMA path addresses W with 32-bit offsets from its base (plus up to
+  // one stage of row overrun).
+  const long long w_bytes = static_cast<long long>(n) * (k / 32) * Fmt<FMT>::block_bytes;
+  if (k % 64 == 0 && w_bytes + 4096 < (1LL << 32))
+    return launch_qgemm_mfma(FMT, W, x, y, m, n, k, s);
   const int grid = (n + kWaves - 1) / kWaves;
   for (int m0 = 0; m0 < m; m0 += 8) {
     const int mt = m - m0 < 8 ? m - m0 : 8;

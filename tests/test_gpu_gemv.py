@@ -113,6 +113,25 @@ def test_qgemm_small_batch(qc, oracle, synth, dev, fmt, m):
         assert ok, worst
 
 
+@pytest.mark.parametrize("fmt,m,n,k", [(0, 33, 300, 192), (1, 40, 129, 64), (0, 5, 2000, 4160),
+                                        (1, 32, 4096, 1408), (0, 17, 1000, 14336),
+                                        (1, 2, 14336, 4096), (0, 64, 520, 256),
+                                        (0, 3, 5, 64), (1, 7, 3, 128), (0, 20, 130, 320)])
+def test_qgemm_mfma_shapes(qc, oracle, synth, dev, fmt, m, n, k):
+    """Small-batch GEMM shapes that exercise M beyond one 32-row launch,
+    partial last K stages, ragged N and split-K partial sums."""
+    import torch
+    print(f"qgemm shapes fmt={fmt} m={m} n={n} k={k}", flush=True)
+    packed, _ = _case(oracle, synth, fmt, n, k, 77 + m)
+    x = synth.normal_fast(900 + m + k, m * k).reshape(m, k)
+    Y = qc.qgemm(fmt, torch.from_numpy(packed).to(dev), torch.from_numpy(x).to(dev), n, k)
+    Y = Y.cpu().numpy()
+    for r in sorted({0, m // 2, m - 1}):
+        _check_rows(oracle, fmt, packed, x[r], Y[r], n, k)
+    Y2 = qc.qgemm(fmt, torch.from_numpy(packed).to(dev), torch.from_numpy(x).to(dev), n, k)
+    assert np.array_equal(Y2.cpu().numpy().view(np.uint32), Y.view(np.uint32))  # deterministic
+
+
 @pytest.mark.parametrize("m,n", [(4, 4096), (32, 14336)])
 def test_qgemm_baseline_config2(qc, oracle, synth, dev, m, n):
     """BASELINE config 2 (q8_0, K=4096) at two of its corners."""
