@@ -11,7 +11,8 @@ so that every step streams from HBM, not from the 256 MB Infinity Cache.
 
 Secondary lines (same discipline) cover the other BASELINE configs: q8_0 GEMV
 (config 0), q4_0 K=14336 -> N=4096, the q8_0 small-batch GEMM (config 2), the
-activation quantizer and the W8A8 GEMM at M=2048 (config 3).
+activation quantizer and the W8A8 GEMM at M=2048 (config 3), and the per-layer
+sums of the 32-layer decoder sweep (config 4).
 
 cpu_baseline: the reference's own x86 route for the headline op (AVX2
 q4_rows, compiled from the reference sources into oracle/_ref by
@@ -128,18 +129,18 @@ def gemv_case(qc, fmt, n, k, steps, warmup, seed):
             "kernel_gbs": alg / (gpu * 1e-3) / 1e9}, packs[0], x, y
 
 
-def qgemm_case(qc, n, k, m, steps, warmup, seed):
+def qgemm_case(qc, n, k, m, steps, warmup, seed, fmt=0):
     import torch
     dev = torch.device("cuda:0")
-    wbytes = n * (k // 32) * 34
+    wbytes = n * (k // 32) * qc.BLOCK_BYTES[fmt]
     copies = rotation(wbytes + 4 * m * k)
     g = torch.Generator(device=dev).manual_seed(seed)
-    packs = [qc.pack(0, torch.randn((n, k), generator=g, device=dev) * 0.02) for _ in range(copies)]
+    packs = [qc.pack(fmt, torch.randn((n, k), generator=g, device=dev) * 0.02) for _ in range(copies)]
     x = torch.randn((m, k), generator=g, device=dev)
     y = torch.empty((m, n), dtype=torch.float32, device=dev)
 
     def launch(i):
-        st = qc.qgemm_raw(0, packs[i % copies], x, y, m, n, k)
+        st = qc.qgemm_raw(fmt, packs[i % copies], x, y, m, n, k)
         if st:
             raise RuntimeError(f"qgemm status {st}")
 
@@ -190,6 +191,40 @@ def w8a8_case(qc, m, n, k, steps, warmup):
     ops = 2.0 * m * n * k
     return {"m": m, "n": n, "k": k, "ops": ops, "wall_ms": wall, "gpu_ms": gpu,
             "tops": ops / (wall * 1e-3) / 1e12, "kernel_tops": ops / (gpu * 1e-3) / 1e12}
+
+
+# the matmuls of one layer of a synthetic 32-layer,
+# 4096-hidden / 14336-FFN decoder, as (count, N, K).
+LAYER = [(4, 4096, 4096), (2, 14336, 4096), (1, 4096, 14336)]
+
+
+def layer_sweep(qc, steps, warmup):
+    """Per-layer sum of kernel times for each regime of config 4: q4_0 weights
+    at M=1 (GEMV) and M=8 (small-batch GEMM); W8A8 at M=512 and M=2048
+    (per-token activation quantization + int8 GEMM).  Each matmul is timed on
+    its own (same graph discipline, rotated weight copies)."""
+    out = {}
+    for m in (1, 8):
+        us, wbytes = 0.0, 0
+        for cnt, n, k in LAYER:
+            if m == 1:
+                r, *_ = gemv_case(qc, 1, n, k, steps, warmup, seed=100 + n + k)
+            else:
+                r = qgemm_case(qc, n, k, m, steps, warmup, seed=200 + n + k, fmt=1)
+            us += cnt * r["gpu_ms"] * 1e3
+            wbytes += cnt * n * (k // 32) * 18
+        out[f"q4_0_m{m}"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
+                             "weight_gbs": wbytes / (us * 1e-6) / 1e9}
+    for m in (512, 2048):
+        us, ops = 0.0, 0.0
+        for cnt, n, k in LAYER:
+            q = quant_case(qc, m, k, steps, warmup)
+            g = w8a8_case(qc, m, n, k, max(10, steps // 4), warmup)
+            us += cnt * (q["gpu_ms"] + g["gpu_ms"]) * 1e3
+            ops += cnt * 2.0 * m * n * k
+        out[f"w8a8_m{m}"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
+                             "tops": ops / (us * 1e-6) / 1e12}
+    return out
 
 
 def profiled_traffic(name):
@@ -305,6 +340,8 @@ def main():
         s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
         s["w8a8_m2048_k4096_n4096"] = w8a8_case(qc, 2048, 4096, 4096, max(20, K // 4), W)
         s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, max(20, K // 4), W)
+        for key, r in layer_sweep(qc, max(20, K // 4), W).items():
+            s[f"decoder_layer_{key}"] = r
         for key, r in s.items():
             print(f"# {key}: " + ", ".join(f"{a}={b:.4g}" if isinstance(b, float) else f"{a}={b}"
                                           for a, b in r.items()), file=sys.stderr, flush=True)
