@@ -21,22 +21,23 @@
 //
 // Data flow.  A prep kernel writes the activation fragments in the MFMA
 // operand layout ([block][m-tile][hi | lo][64 lanes][16 B]) plus the q4 bias,
-// and zeroes y when two K halves will add into it.  The GEMM workgroup (8
-// wavefronts, 16 weight rows each = 128 rows) runs a ring of LDS stages, each
-// holding 4 block pairs (256 K) of its 128 weight rows -- whole row segments,
+// and zeroes y when two K halves will add into it.  The GEMM workgroup (4 or
+// 8 wavefronts, 16 weight rows each) runs a ring of LDS stages, each
+// holding 4 block pairs (256 K) of its weight rows -- whole row segments,
 // copied with global_load_lds_dwordx4, so every weight byte crosses the
 // memory system once in full cache lines -- and the activation fragments of
-// those blocks, which all 8 wavefronts share.  Each lane then picks its
+// those blocks, which all its wavefronts share.  Each lane then picks its
 // codes and scales out of LDS.  The ring is 3 stages deep where LDS allows
 // (2 for q8_0 with 32 activation rows).
 //
-// K is split over `ks` workgroups per 128-row slab when N alone gives too
+// K is split over `ks` workgroups per row slab when N alone gives too
 // few workgroups.  With ks = 2 both halves add atomically into a y that the
 // prep kernel zeroed (two addends onto zero: order-independent); with
 // ks > 2 the partial sums go to a workspace and a small kernel adds them in
 // index order.  Results are deterministic either way.  (A per-workgroup
 // device-scope fence, as a "last workgroup reduces" scheme needs, writes
 // back the XCD's whole L2 and costs far more than the extra launch.)
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -50,9 +51,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kSlab = 16 * kWaves;       // weight rows per workgroup
 constexpr int kStagePairs = 4;           // block pairs per ring stage
 constexpr int kStageBlocks = 2 * kStagePairs;
 
@@ -98,9 +96,9 @@ __device__ __forceinline__ bf16x8 codes_bf16(uint32_t lo, uint32_t hi, int j) {
     const int sh = (j >> 1) * 4;          // lane groups 2, 3 take the high nibbles
     const uint32_t a = (lo >> sh) & 0x0F0F0F0Fu, b = (hi >> sh) & 0x0F0F0F0Fu;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = static_cast<__bf16>(static_cast<float>((a >> (8 * i)) & 0xFFu));
-      v[4 + i] = static_cast<__bf16>(static_cast<float>((b >> (8 * i)) & 0xFFu));
+    for (int i = 0; i < 4; ++i) {   // v_cvt_f32_ubyte{0..3}
+      v[i] = static_cast<__bf16>(static_cast<float>(static_cast<uint8_t>(a >> (8 * i))));
+      v[4 + i] = static_cast<__bf16>(static_cast<float>(static_cast<uint8_t>(b >> (8 * i))));
     }
   }
   return v;
@@ -129,7 +127,9 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 // explicit) nor lets the compiler move memory accesses across it.
 __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
 }
 __device__ __forceinline__ void load_lds16(const void* g, void* lds) {
@@ -239,31 +239,33 @@ struct WStage {
   static constexpr int wave_bytes = 16 * row_bytes;
 };
 
-template <int FMT, int T>
+template <int FMT, int T, int NW>
 struct StageLayout {
   static constexpr bool bias = FMT == kQ4_0;
-  static constexpr int w_bytes = kWaves * WStage<FMT>::wave_bytes;
+  static constexpr int w_bytes = NW * WStage<FMT>::wave_bytes;
   static constexpr int x_bytes = kStageBlocks * T * kFragBytes;
   static constexpr int bias_bytes = bias ? kStageBlocks * T * 64 : 0;
   static constexpr int bytes = w_bytes + x_bytes + bias_bytes;
   // Ring depth: three stages when they fit the 160 KB LDS, else two.
   static constexpr int ring = 3 * bytes <= 160 * 1024 ? 3 : 2;
-  static constexpr int gx = x_bytes / 1024 / kWaves;
+  static constexpr int gx = x_bytes / 1024 / NW;
   static constexpr int g = WStage<FMT>::loads + gx + (bias ? 1 : 0);  // loads per wave per stage
 };
 
-template <int FMT, int T, int NST>
-__global__ __launch_bounds__(kThreads) void qgemm_mfma(
+// NW wavefronts per workgroup, 16 weight rows each.
+template <int FMT, int T, int NW, int NST>
+__global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
     float* __restrict__ y, float* __restrict__ partial, const uint8_t* __restrict__ tail_pad,
     int M, int N, int K, int nslabs, int ks_count, int nstages) {
-  using L = StageLayout<FMT, T>;
+  using L = StageLayout<FMT, T, NW>;
   using WS = WStage<FMT>;
+  constexpr int kSlab = 16 * NW;
   constexpr int S = L::ring;
   constexpr int G = L::g;
-  constexpr int kBiasPerWave = L::bias_bytes / kWaves;
-  static_assert(L::bias_bytes % (16 * kWaves) == 0, "bias split");
-  static_assert(L::gx >= 1 && L::x_bytes % (1024 * kWaves) == 0, "stage split");
+  constexpr int kBiasPerWave = L::bias_bytes / NW;
+  static_assert(L::bias_bytes % (16 * NW) == 0, "bias split");
+  static_assert(L::gx >= 1 && L::x_bytes % (1024 * NW) == 0, "stage split");
   static_assert(G * (S - 1) < 64, "vmcnt range");
   // One LDS array per ring slot: slot indices are compile-time after
   // unrolling, so the compiler can tell the reads of one slot from the
@@ -348,13 +350,17 @@ __global__ __launch_bounds__(kThreads) void qgemm_mfma(
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int stage, int slot) {
+  // Branch-free, so the compiler can overlap the pairs' LDS reads, code
+  // conversions and MFMAs.  A pair past K or a stage past st1 (clamped
+  // reloads) adds c * 0: its codes are finite integers and its activation
+  // fragments zero or finite, so c is finite, and its scale is replaced by 0.
+  auto compute = [&](int stage, int slot, bool live) {
     const uint8_t* base = slot_base(slot);
     const uint8_t* row = base + wave * WS::wave_bytes + (lane & 15) * WS::row_bytes;
     const uint8_t* xs = base + L::w_bytes;
 #pragma unroll
     for (int pp = 0; pp < kStagePairs; ++pp) {
-      if (stage * kStagePairs + pp >= npairs) break;   // wave-uniform
+      const bool valid = live && stage * kStagePairs + pp < npairs;   // wave-uniform
       const uint32_t* pr = reinterpret_cast<const uint32_t*>(row + pp * PairLayout<FMT>::bytes);
       const u32x3_a4 b0 = *reinterpret_cast<const u32x3_a4*>(pr + PairLayout<FMT>::blk0_dword(j));
       const u32x2_a4 b1 = *reinterpret_cast<const u32x2_a4*>(pr + PairLayout<FMT>::blk1_dword(j));
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_mfma(
         const uint32_t c0 = h == 0 ? __builtin_amdgcn_alignbyte(b0.y, b0.x, 2) : b1.x;
         const uint32_t c1 = h == 0 ? __builtin_amdgcn_alignbyte(b0.z, b0.y, 2) : b1.y;
         const bf16x8 wv = codes_bf16<FMT>(c0, c1, j);
-        const float d = half_bits_to_float(h == 0 ? (s0 & 0xFFFFu) : (s1 >> 16));
+        const float d = valid ? half_bits_to_float(h == 0 ? (s0 & 0xFFFFu) : (s1 >> 16)) : 0.0f;
         const int blk = 2 * pp + h;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -400,7 +406,12 @@ __global__ __launch_bounds__(kThreads) void qgemm_mfma(
     wait_lgkmcnt0();
     ring_barrier();
     if (i + S - 1 < NST) issue(cur + S - 1, (i + S - 1) % S);
-    if (cur < st1) compute(cur, i % S);
+    compute(cur, i % S, cur < st1);
+    // Materialise the accumulators here: otherwise the compiler sinks the
+    // scale FMAs of every stage into the (conditional) store block and keeps
+    // all MFMA results of the workgroup live until then.
+#pragma unroll
+    for (int t = 0; t < T; ++t) asm volatile("" : "+v"(acc[t]));
   }
   wait_vmcnt<0>();   // no global->LDS load may outlive the workgroup's LDS
 
@@ -484,13 +495,58 @@ hipError_t workspace_for(hipStream_t s, size_t bytes, void** out) {
   return hipSuccess;
 }
 
-template <int FMT, int T, int NST>
+template <int FMT, int T, int NW, int NST>
 hipError_t launch_nst(const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
                       float* partial, const uint8_t* tail_pad, int m, int n, int k, int nslabs,
                       int ks, int nstages, hipStream_t s) {
-  qgemm_mfma<FMT, T, NST><<<nslabs * ks, kThreads, 0, s>>>(W, xf, bias, y, partial, tail_pad, m,
-                                                            n, k, nslabs, ks, nstages);
+  qgemm_mfma<FMT, T, NW, NST><<<nslabs * ks, 64 * NW, 0, s>>>(W, xf, bias, y, partial, tail_pad,
+                                                              m, n, k, nslabs, ks, nstages);
   return hipGetLastError();
+}
+
+template <int FMT, int T, int NW>
+hipError_t launch_nw(int nst, const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
+                     float* partial, const uint8_t* tail_pad, int m, int n, int k, int nslabs,
+                     int ks, int nstages, hipStream_t s) {
+  switch (nst) {
+    case 16: return launch_nst<FMT, T, NW, 16>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 8: return launch_nst<FMT, T, NW, 8>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 4: return launch_nst<FMT, T, NW, 4>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 2: return launch_nst<FMT, T, NW, 2>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    default: return launch_nst<FMT, T, NW, 1>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+  }
+}
+
+// Workgroup width (NW wavefronts = 16 NW rows) and stages per workgroup
+// (NST; K is split ceil(nstages / NST) ways) from a simple cost model of
+// this kernel on gfx950: one workgroup per CU at a time (LDS), a CU streams
+// at most ~37 GB/s on its own and the chip ~5.2 TB/s, a workgroup costs
+// ~1.5 us of latency, and a K split beyond two ways costs a reduction kernel
+// (~3.5 us).
+struct Plan {
+  int nw, nst, ks;
+};
+template <int FMT>
+Plan plan_for(int n, int nstages, int cus) {
+  Plan best{8, 1, nstages};
+  double best_t = 1e30;
+  for (int nw : {8, 4}) {
+    const int nslabs = (n + 16 * nw - 1) / (16 * nw);
+    for (int nst : {16, 8, 4, 2, 1}) {
+      const int ks = (nstages + nst - 1) / nst;
+      const long long wgs = static_cast<long long>(nslabs) * ks;
+      const long long active = wgs < cus ? wgs : cus;
+      const long long rounds = (wgs + cus - 1) / cus;
+      const double rate = std::min(37e9, 5.2e12 / static_cast<double>(active));
+      const double wg_bytes = 16.0 * nw * nst * kStagePairs * PairLayout<FMT>::bytes;
+      const double t = rounds * (wg_bytes / rate + 1.5e-6) + (ks > 2 ? 3.5e-6 : 0.0);
+      if (t < best_t * 0.999) {
+        best_t = t;
+        best = Plan{nw, nst, ks};
+      }
+    }
+  }
+  return best;
 }
 
 template <int FMT, int T>
@@ -498,16 +554,9 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
-  const int nslabs = (n + kSlab - 1) / kSlab;
-  // One workgroup per CU at a time (LDS ring + 8 wavefronts).  Each
-  // workgroup takes NST consecutive stages (fully unrolled); NST is the
-  // largest of 16, 8, 4, 2, 1 that still gives about 3/4 of the CUs a
-  // workgroup, which keeps K split as few ways as possible.
-  const int cus = device_cus();
-  int nst = 16;
-  while (nst > 1 && static_cast<long long>(nslabs) * ((nstages + nst - 1) / nst) * 4 < 3LL * cus)
-    nst /= 2;
-  const int ks = (nstages + nst - 1) / nst;
+  const Plan plan = plan_for<FMT>(n, nstages, device_cus());
+  const int nslabs = (n + 16 * plan.nw - 1) / (16 * plan.nw);
+  const int ks = plan.ks;
   const size_t xf_bytes = static_cast<size_t>(nbp) * T * kFragBytes;
   const size_t bias_bytes = FMT == kQ4_0 ? static_cast<size_t>(nbp) * T * 64 : 0;
   const size_t part_bytes = ks > 2 ? static_cast<size_t>(ks) * m * n * sizeof(float) : 0;
@@ -529,13 +578,10 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
                                                      static_cast<int>(pad_bytes));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  switch (nst) {
-    case 16: e = launch_nst<FMT, T, 16>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
-    case 8: e = launch_nst<FMT, T, 8>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
-    case 4: e = launch_nst<FMT, T, 4>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
-    case 2: e = launch_nst<FMT, T, 2>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
-    default: e = launch_nst<FMT, T, 1>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s); break;
-  }
+  if (plan.nw == 8)
+    e = launch_nw<FMT, T, 8>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+  else
+    e = launch_nw<FMT, T, 4>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
   if (e != hipSuccess || ks <= 2) return e;
   const long long blocks = (outs + 255) / 256;
   qgemm_reduce<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(partial, y, outs, ks);
