@@ -26,10 +26,11 @@
 //
 // Memory: W stays in the canonical GGUF layout.  Lane l owns the block pairs
 // p = l, l+64, ... of its wave's rows (a pair is 68 B for q8_0, 36 B for q4_0,
-// dword aligned when K/32 is even).  Each wave issues the loads for all of its
-// rows x pairs before anything else, so the whole weight stream is in flight
-// while the workgroup builds the digits of x in LDS; the barrier after the
-// digit build waits on LDS traffic only.
+// dword aligned when K/32 is even).  Each wave issues its first weight loads
+// before anything else, so they are in flight while the workgroup builds the
+// digits of x in LDS (the barrier after the digit build waits on LDS traffic
+// only), and then keeps a small window of (pair, row) items in flight ahead
+// of the one it computes.
 #include "qc_device.h"
 #include "qc_internal.h"
 
@@ -263,8 +264,14 @@ __device__ __forceinline__ void load_pair(uint32_t* d, const uint8_t* p) {
   d[4 * NV] = reinterpret_cast<const uint32_t*>(p)[4 * NV];
 }
 
-// RB rows per wave, up to NPM pairs per lane per K chunk.
-template <int FMT, int RB, int NPM, bool VEC>
+// RB rows per wave, up to NPM pairs per lane per K chunk.  The (pair j,
+// row r) items of a chunk are loaded in j-major order with at most WIN items
+// in flight: item t + WIN is issued just before item t is computed, so the
+// data arrive roughly in the order they are used (all at once, when WIN >=
+// NPM * RB).  A bounded window keeps a wave from waiting on its first rows
+// while the memory system still returns the others, which for several rows
+// per wave leaves less compute after the last byte lands.
+template <int FMT, int RB, int NPM, int WIN, bool VEC>
 __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __restrict__ W,
                                                              const float* __restrict__ x,
                                                              float* __restrict__ y, int n, int k,
@@ -272,6 +279,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int BB = Fmt<FMT>::block_bytes;
   constexpr int PD = Fmt<FMT>::pair_dwords;
+  constexpr int T = NPM * RB;
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * RB;
   const long long row_bytes = static_cast<long long>(k >> 5) * BB;
@@ -286,29 +294,32 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
     const int clen = min(kc, k - c0);
     const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
     const int p0 = first_pair(pbeg, lane);
-    // 1. this thread's x values, then every weight load of this chunk
+    // 1. this thread's x values, then the first WIN weight items
     float xv[NPM][16];
     load_x<NPM, VEC>(xv, x + c0, clen);
-    uint32_t w[NPM][RB][PD];
-#pragma unroll
-    for (int j = 0; j < NPM; ++j) {
+    uint32_t w[T][PD];
+    auto issue = [&](int t) {
+      const int j = t / RB, r = t % RB;
       const int p = min(p0 + 64 * j, pend - 1);
+      load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
+    };
 #pragma unroll
-      for (int r = 0; r < RB; ++r) load_pair<FMT>(w[j][r], wrow[r] + static_cast<long long>(p) * (2 * BB));
-    }
+    for (int t = 0; t < T && t < WIN; ++t) issue(t);
     // 2. digits of x for this chunk
     if (c0) lds_barrier();
     build_digits<FMT == kQ4_0, NPM>(lds, xv, clen, kc);
     lds_barrier();
-    // 3. exact block dots
+    // 3. exact block dots, issuing the window's next item before each
 #pragma unroll
     for (int j = 0; j < NPM; ++j) {
       const int p = p0 + 64 * j;
-      if (p < pend) {
-        PairDigits g;
-        read_digits<FMT>(g, lds, p - pbeg, kc);
+      PairDigits g;
+      read_digits<FMT>(g, lds, min(p, pend - 1) - pbeg, kc);
 #pragma unroll
-        for (int r = 0; r < RB; ++r) acc[r] = pair_dot<FMT>(w[j][r], g, acc[r]);
+      for (int r = 0; r < RB; ++r) {
+        const int t = j * RB + r;
+        if (t + WIN < T) issue(t + WIN);
+        if (p < pend) acc[r] = pair_dot<FMT>(w[t], g, acc[r]);
       }
     }
   }
@@ -319,16 +330,24 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
   }
 }
 
+// Load window: a wave with 7 or more rows keeps 2 items (q4_0) or 1 item
+// (q8_0) in flight beyond the one it computes; smaller waves issue all.
+template <int FMT, int RB, int NPM>
+constexpr int window() {
+  return RB >= 7 ? (FMT == kQ4_0 ? 2 : 1) : NPM * RB;
+}
+
 template <int FMT, int RB, int NPM>
 hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, hipStream_t s) {
-  // weights held in flight per lane: RB * NPM * pair dwords (kept <= 144 VGPRs)
+  // weights held in flight per lane: at most RB * NPM * pair dwords (<= 144 VGPRs)
   static_assert(RB * NPM * Fmt<FMT>::pair_dwords <= 144, "register budget");
+  constexpr int WIN = window<FMT, RB, NPM>();
   const int kc = NPM * 4096 < k ? NPM * 4096 : k;
   const int grid = (n + kWaves * RB - 1) / (kWaves * RB);
   if (reinterpret_cast<uintptr_t>(x) % 16 == 0)
-    qgemv_dot_kernel<FMT, RB, NPM, true><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
+    qgemv_dot_kernel<FMT, RB, NPM, WIN, true><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
   else
-    qgemv_dot_kernel<FMT, RB, NPM, false><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
+    qgemv_dot_kernel<FMT, RB, NPM, WIN, false><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
   return hipGetLastError();
 }
 
