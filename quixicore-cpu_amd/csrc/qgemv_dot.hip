@@ -37,8 +37,6 @@
 namespace qc {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
 constexpr int kRec = 208;  // LDS bytes per pair: 3 digit planes x 64 + 16 pad
 
 __device__ __forceinline__ int first_pair(int pbeg, int lane) {
@@ -66,17 +64,17 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 }
 
 // x values of this thread's half-blocks (16 elements each) of a chunk:
-// h = threadIdx.x + 256 j, j < NPM.  Issued before the weight loads so that
+// h = threadIdx.x + NT j, j < HPT.  Issued before the weight loads so that
 // waiting for them does not wait for the weights (vmcnt retires in order).
 // Branch-free (an index past the chunk re-reads its last half-block, which
 // build_digits then skips): a branch around the loads would make the compiler
 // wait for them at the join, before the weight loads are issued.
-template <int NPM, bool VEC>
-__device__ __forceinline__ void load_x(float (&v)[NPM][16], const float* __restrict__ x, int clen) {
+template <int HPT, int NT, bool VEC>
+__device__ __forceinline__ void load_x(float (&v)[HPT][16], const float* __restrict__ x, int clen) {
   const int nh = clen >> 4;
 #pragma unroll
-  for (int j = 0; j < NPM; ++j) {
-    const int h = min(static_cast<int>(threadIdx.x) + kThreads * j, nh - 1);
+  for (int j = 0; j < HPT; ++j) {
+    const int h = min(static_cast<int>(threadIdx.x) + NT * j, nh - 1);
     if constexpr (VEC) {
       const float4* src = reinterpret_cast<const float4*>(x + 16 * h);
 #pragma unroll
@@ -90,13 +88,13 @@ __device__ __forceinline__ void load_x(float (&v)[NPM][16], const float* __restr
 
 // Digits of the loaded half-blocks into LDS; the two halves of a block sit
 // in lanes t and t^1.
-template <bool WITH_SUMS, int NPM>
-__device__ __forceinline__ void build_digits(uint8_t* lds, const float (&xv)[NPM][16], int clen,
+template <bool WITH_SUMS, int HPT, int NT>
+__device__ __forceinline__ void build_digits(uint8_t* lds, const float (&xv)[HPT][16], int clen,
                                              int kc) {
   const int nh = clen >> 4;
 #pragma unroll
-  for (int j = 0; j < NPM; ++j) {
-    const int h = threadIdx.x + kThreads * j;
+  for (int j = 0; j < HPT; ++j) {
+    const int h = threadIdx.x + NT * j;
     if (h >= nh) break;
     const float* v = xv[j];
     float m = 0.f;
@@ -264,15 +262,15 @@ __device__ __forceinline__ void load_pair(uint32_t* d, const uint8_t* p) {
   d[4 * NV] = reinterpret_cast<const uint32_t*>(p)[4 * NV];
 }
 
-// RB rows per wave, up to NPM pairs per lane per K chunk.  The (pair j,
+// NW wavefronts of RB rows each, up to NPM pairs per lane per K chunk.  The (pair j,
 // row r) items of a chunk are loaded in j-major order with at most WIN items
 // in flight: item t + WIN is issued just before item t is computed, so the
 // data arrive roughly in the order they are used (all at once, when WIN >=
 // NPM * RB).  A bounded window keeps a wave from waiting on its first rows
 // while the memory system still returns the others, which for several rows
 // per wave leaves less compute after the last byte lands.
-template <int FMT, int RB, int NPM, int WIN, bool VEC>
-__global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __restrict__ W,
+template <int FMT, int NW, int RB, int NPM, int WIN, bool VEC>
+__global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const uint8_t* __restrict__ W,
                                                              const float* __restrict__ x,
                                                              float* __restrict__ y, int n, int k,
                                                              int kc) {
@@ -280,8 +278,10 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
   constexpr int BB = Fmt<FMT>::block_bytes;
   constexpr int PD = Fmt<FMT>::pair_dwords;
   constexpr int T = NPM * RB;
+  constexpr int NT = 64 * NW;
+  constexpr int HPT = (NPM * 256 + NT - 1) / NT;   // half-blocks of x per thread
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * RB;
+  const int row0 = (blockIdx.x * NW + (threadIdx.x >> 6)) * RB;
   const long long row_bytes = static_cast<long long>(k >> 5) * BB;
   const uint8_t* wrow[RB];
 #pragma unroll
@@ -295,8 +295,8 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
     const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
     const int p0 = first_pair(pbeg, lane);
     // 1. this thread's x values, then the first WIN weight items
-    float xv[NPM][16];
-    load_x<NPM, VEC>(xv, x + c0, clen);
+    float xv[HPT][16];
+    load_x<HPT, NT, VEC>(xv, x + c0, clen);
     uint32_t w[T][PD];
     auto issue = [&](int t) {
       const int j = t / RB, r = t % RB;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
     for (int t = 0; t < T && t < WIN; ++t) issue(t);
     // 2. digits of x for this chunk
     if (c0) lds_barrier();
-    build_digits<FMT == kQ4_0, NPM>(lds, xv, clen, kc);
+    build_digits<FMT == kQ4_0, HPT, NT>(lds, xv, clen, kc);
     lds_barrier();
     // 3. exact block dots, issuing the window's next item before each
 #pragma unroll
@@ -330,24 +330,26 @@ __global__ __launch_bounds__(kThreads) void qgemv_dot_kernel(const uint8_t* __re
   }
 }
 
-// Load window: a wave with 7 or more rows keeps 2 items (q4_0) or 1 item
-// (q8_0) in flight beyond the one it computes; smaller waves issue all.
-template <int FMT, int RB, int NPM>
+// Load window (items in flight beyond the one being computed) by items per
+// wave, T = NPM * RB, as measured on MI355X: enough to cover the load latency
+// while keeping the arrival order close to the compute order.
+template <int FMT, int T>
 constexpr int window() {
-  return RB >= 7 ? (FMT == kQ4_0 ? 2 : 1) : NPM * RB;
+  if constexpr (FMT == kQ4_0) return T >= 8 ? 3 : (T >= 4 ? 2 : 1);
+  return T >= 8 ? 2 : 1;
 }
 
-template <int FMT, int RB, int NPM>
+template <int FMT, int NW, int RB, int NPM>
 hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, hipStream_t s) {
-  // weights held in flight per lane: at most RB * NPM * pair dwords (<= 144 VGPRs)
+  // weights held per lane: at most RB * NPM * pair dwords (<= 144 VGPRs)
   static_assert(RB * NPM * Fmt<FMT>::pair_dwords <= 144, "register budget");
-  constexpr int WIN = window<FMT, RB, NPM>();
+  constexpr int WIN = window<FMT, NPM * RB>();
   const int kc = NPM * 4096 < k ? NPM * 4096 : k;
-  const int grid = (n + kWaves * RB - 1) / (kWaves * RB);
+  const int grid = (n + NW * RB - 1) / (NW * RB);
   if (reinterpret_cast<uintptr_t>(x) % 16 == 0)
-    qgemv_dot_kernel<FMT, RB, NPM, WIN, true><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
+    qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
   else
-    qgemv_dot_kernel<FMT, RB, NPM, WIN, false><<<grid, kThreads, lds_size(kc), s>>>(W, x, y, n, k, kc);
+    qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, false><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
   return hipGetLastError();
 }
 
@@ -362,83 +364,116 @@ int cu_count() {
   return count;
 }
 
-// Rows per wave: the candidate that minimises the rows handled by the
-// busiest CU (all workgroups of a CU run together when there are at most two),
-// preferring two workgroups per CU, then one.
-int pick_rows(int n, const int* cand, int ncand) {
+struct Shape {
+  int nw, rb;
+};
+
+// Workgroup width (8 or 4 waves) and rows per wave: the candidate that
+// minimises the rows handled by the busiest CU, among those with at most two
+// workgroups per CU (which then all run together) when there are any; ties go
+// to 8 waves per CU (one 8-wave or two 4-wave workgroups), then to 8-wave
+// workgroups for fewer than 7 rows per wave (one digit build of x shared by
+// twice the rows) and to 4-wave ones otherwise (two workgroups per CU overlap
+// one's digit build with the other's loads), then to the earlier candidate.
+// `forced_rb` (non-zero) restricts the choice to that many rows per wave.
+Shape pick_shape(int n, const int* cand, int ncand, int forced_rb) {
   const int cus = cu_count();
-  int best = cand[0];
-  long long best_rows = -1;
-  int best_wpc = 0;
-  for (int i = 0; i < ncand; ++i) {
-    const int rb = cand[i];
-    const long long grid = (n + kWaves * rb - 1) / (kWaves * rb);
-    const long long wpc = (grid + cus - 1) / cus;
-    if (wpc > 2 && i + 1 < ncand) continue;
-    const long long rows = wpc * kWaves * rb;
-    const bool better = best_rows < 0 || rows < best_rows ||
-                        (rows == best_rows && wpc == 2 && best_wpc != 2);
-    if (better) {
-      best = rb;
-      best_rows = rows;
-      best_wpc = static_cast<int>(wpc);
+  Shape best{8, forced_rb ? forced_rb : cand[0]};
+  for (int pass = 0; pass < 2; ++pass) {
+    long long best_score = -1;
+    for (int nw : {8, 4}) {
+      for (int i = 0; i < ncand; ++i) {
+        const int rb = cand[i];
+        if (forced_rb && rb != forced_rb) continue;
+        const long long grid = (n + nw * rb - 1) / (nw * rb);
+        const long long wpc = (grid + cus - 1) / cus;
+        if (pass == 0 && wpc > 2) continue;
+        const long long rows = wpc * nw * rb;
+        const int not_eight = wpc * nw == 8 ? 0 : 1;
+        const int not_pref = (rb >= 7) == (nw == 4) ? 0 : 1;
+        const long long score = rows * 4 + not_eight * 2 + not_pref;
+        if (best_score < 0 || score < best_score) {
+          best = Shape{nw, rb};
+          best_score = score;
+        }
+      }
     }
+    if (best_score >= 0) break;
   }
   return best;
+}
+
+template <int FMT, int NW, int NPM>
+hipError_t launch_rb(int rb, const uint8_t* W, const float* x, float* y, int n, int k,
+                     hipStream_t s) {
+  if constexpr (NPM == 1) {
+    switch (rb) {
+      case 1: return launch_one<FMT, NW, 1, 1>(W, x, y, n, k, s);
+      case 2: return launch_one<FMT, NW, 2, 1>(W, x, y, n, k, s);
+      case 4: return launch_one<FMT, NW, 4, 1>(W, x, y, n, k, s);
+      case 7: return launch_one<FMT, NW, 7, 1>(W, x, y, n, k, s);
+      case 8: return launch_one<FMT, NW, 8, 1>(W, x, y, n, k, s);
+      default:
+        if constexpr (FMT == kQ4_0) return launch_one<FMT, NW, 14, 1>(W, x, y, n, k, s);
+        return launch_one<FMT, NW, 8, 1>(W, x, y, n, k, s);
+    }
+  } else if constexpr (NPM == 2) {
+    switch (rb) {
+      case 1: return launch_one<FMT, NW, 1, 2>(W, x, y, n, k, s);
+      case 2: return launch_one<FMT, NW, 2, 2>(W, x, y, n, k, s);
+      case 4: return launch_one<FMT, NW, 4, 2>(W, x, y, n, k, s);
+      default:
+        if constexpr (FMT == kQ4_0) return launch_one<FMT, NW, 7, 2>(W, x, y, n, k, s);
+        return launch_one<FMT, NW, 4, 2>(W, x, y, n, k, s);
+    }
+  } else {
+    switch (rb) {
+      case 1: return launch_one<FMT, NW, 1, 4>(W, x, y, n, k, s);
+      case 2: return launch_one<FMT, NW, 2, 4>(W, x, y, n, k, s);
+      default:
+        if constexpr (FMT == kQ4_0) return launch_one<FMT, NW, 4, 4>(W, x, y, n, k, s);
+        return launch_one<FMT, NW, 2, 4>(W, x, y, n, k, s);
+    }
+  }
+}
+
+template <int FMT, int NPM>
+hipError_t launch_npm(const int* cand, int ncand, const uint8_t* W, const float* x, float* y,
+                      int n, int k, int rb, hipStream_t s) {
+  bool listed = false;
+  for (int i = 0; i < ncand; ++i) listed = listed || cand[i] == rb;
+  const Shape sh = pick_shape(n, cand, ncand, listed ? rb : 0);
+  return sh.nw == 8 ? launch_rb<FMT, 8, NPM>(sh.rb, W, x, y, n, k, s)
+                    : launch_rb<FMT, 4, NPM>(sh.rb, W, x, y, n, k, s);
 }
 
 template <int FMT>
 hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, int rb,
                       hipStream_t s) {
   const int npairs = k >> 6;
-  const int npm = npairs <= 64 ? 1 : (npairs <= 128 ? 2 : 4);
-  if (npm == 1) {
+  if (npairs <= 64) {
     static const int q4c[] = {14, 7, 8, 4, 2, 1};
     static const int q8c[] = {8, 7, 4, 2, 1};
-    if (rb == 0 || (FMT == kQ8_0 && rb > 8)) rb = FMT == kQ4_0 ? pick_rows(n, q4c, 6) : pick_rows(n, q8c, 5);
-    switch (rb) {
-      case 1: return launch_one<FMT, 1, 1>(W, x, y, n, k, s);
-      case 2: return launch_one<FMT, 2, 1>(W, x, y, n, k, s);
-      case 4: return launch_one<FMT, 4, 1>(W, x, y, n, k, s);
-      case 7: return launch_one<FMT, 7, 1>(W, x, y, n, k, s);
-      case 8: return launch_one<FMT, 8, 1>(W, x, y, n, k, s);
-      default:
-        if constexpr (FMT == kQ4_0) return launch_one<FMT, 14, 1>(W, x, y, n, k, s);
-        return launch_one<FMT, 8, 1>(W, x, y, n, k, s);
-    }
+    return FMT == kQ4_0 ? launch_npm<FMT, 1>(q4c, 6, W, x, y, n, k, rb, s)
+                        : launch_npm<FMT, 1>(q8c, 5, W, x, y, n, k, rb, s);
   }
-  if (npm == 2) {
+  if (npairs <= 128) {
     static const int q4c[] = {7, 4, 2, 1};
     static const int q8c[] = {4, 2, 1};
-    if (rb == 0 || rb > (FMT == kQ4_0 ? 7 : 4))
-      rb = FMT == kQ4_0 ? pick_rows(n, q4c, 4) : pick_rows(n, q8c, 3);
-    switch (rb) {
-      case 1: return launch_one<FMT, 1, 2>(W, x, y, n, k, s);
-      case 2: return launch_one<FMT, 2, 2>(W, x, y, n, k, s);
-      case 4: return launch_one<FMT, 4, 2>(W, x, y, n, k, s);
-      default:
-        if constexpr (FMT == kQ4_0) return launch_one<FMT, 7, 2>(W, x, y, n, k, s);
-        return launch_one<FMT, 4, 2>(W, x, y, n, k, s);
-    }
+    return FMT == kQ4_0 ? launch_npm<FMT, 2>(q4c, 4, W, x, y, n, k, rb, s)
+                        : launch_npm<FMT, 2>(q8c, 3, W, x, y, n, k, rb, s);
   }
   static const int q4c[] = {4, 2, 1};
   static const int q8c[] = {2, 1};
-  if (rb == 0 || rb > (FMT == kQ4_0 ? 4 : 2))
-    rb = FMT == kQ4_0 ? pick_rows(n, q4c, 3) : pick_rows(n, q8c, 2);
-  switch (rb) {
-    case 1: return launch_one<FMT, 1, 4>(W, x, y, n, k, s);
-    case 2: return launch_one<FMT, 2, 4>(W, x, y, n, k, s);
-    default:
-      if constexpr (FMT == kQ4_0) return launch_one<FMT, 4, 4>(W, x, y, n, k, s);
-      return launch_one<FMT, 2, 4>(W, x, y, n, k, s);
-  }
+  return FMT == kQ4_0 ? launch_npm<FMT, 4>(q4c, 3, W, x, y, n, k, rb, s)
+                      : launch_npm<FMT, 4>(q8c, 2, W, x, y, n, k, rb, s);
 }
 
 }  // namespace
 
 // K % 64 == 0 and W 4-byte aligned (checked by the caller).  rows_per_wave:
-// 0 picks from the shape; otherwise 1, 2, 4, 7, 8 or 14, capped by the
-// register budget for K.
+// 0, or a count the register budget for K does not allow, picks from the
+// shape; otherwise 1, 2, 4, 7, 8 or 14 (q4_0) rows per wave.
 hipError_t launch_qgemv_dot(int fmt, const void* Wv, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s) {
   const auto* W = static_cast<const uint8_t*>(Wv);
