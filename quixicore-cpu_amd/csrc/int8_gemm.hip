@@ -388,21 +388,25 @@ __device__ __forceinline__ void write_tile32(const v16i (&acc)[FN][FM], long lon
 // never read again, which keeps every wait count a constant.  The last step
 // runs separately and, when K is not a multiple of 128, skips the quarters
 // past K (their loads read a clamped in-row address and are never used).
-template <int TN, int TM, int S, int WGN, int WGM>
+template <int TN, int TM, int S, int WGN, int WGM, int KL>
 __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
     const int8_t* __restrict__ W, const int8_t* __restrict__ X, const float* __restrict__ ws,
     const float* __restrict__ as, const int32_t* __restrict__ row_sum, const int* __restrict__ zp,
     float* __restrict__ y, int32_t* __restrict__ acc_out, int M, int N, int K, int tiles_n,
     int tiles_m, int asym, int* status) {
-  constexpr int kLine = 128;
+  static_assert(KL == 128 || KL == 64, "K step is a whole or a half cache line");
+  constexpr int kLine = KL;
+  constexpr int QPS = KL / 32;                       // K quarters per step
+  constexpr int RPL = 1024 / KL;                     // rows per 1 KB load
+  constexpr int CPR = KL / 16;                       // 16-byte chunks per row
   constexpr int NW = WGN * WGM;                      // WGN x WGM grid of wavefronts
   constexpr int WN = TN / WGN, WM = TM / WGM;        // wave tile
   constexpr int FN = WN / 32, FM = WM / 32;          // 32 x 32 tiles per wave
-  constexpr int GW = TN / 8 / NW, GX = TM / 8 / NW;  // 8-row loads per wave per step
+  constexpr int GW = TN / RPL / NW, GX = TM / RPL / NW;  // 1 KB loads per wave per step
   constexpr int G = GW + GX;
   constexpr int kStage = (TN + TM) * kLine;
   static_assert(FN >= 1 && FM >= 1 && GW >= 1 && GX >= 1 && S >= 2, "tile shape");
-  static_assert(GW % 2 == 0 && GX % 2 == 0, "8-row groups alternate swizzle parity");
+  static_assert(KL == 64 || (GW % 2 == 0 && GX % 2 == 0), "8-row groups alternate swizzle parity");
   static_assert(G * (S - 1) < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) int8_t ring[S * kStage];
 
@@ -413,22 +417,25 @@ __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
   const long long n0 = static_cast<long long>(tn) * TN;
   const long long m0 = static_cast<long long>(tm) * TM;
 
-  // Load j of a wave covers operand rows r = 8 * (wave * GW + j) + (lane >> 3)
-  // (W; likewise X with GX); its swizzle key (r >> 1) & 7 is
-  // 4 * (j & 1) + (lane >> 4), as GW and GX are even.
+  // Load j of a wave covers operand rows r = RPL * (wave * GW + j) + lane / CPR
+  // (W; likewise X with GX), lane writing slot lane % CPR of its row.  Swizzle
+  // key of row r: (r >> 1) & (CPR - 1).  128-byte lines: 4 * (j & 1) +
+  // (lane >> 4), as GW and GX are even; 64-byte halves: (lane >> 3) & 3.
   const int8_t* src[G];
   int coff[2];
 #pragma unroll
-  for (int par = 0; par < 2; ++par) coff[par] = ((lane & 7) ^ (4 * par + (lane >> 4))) * 16;
+  for (int par = 0; par < 2; ++par)
+    coff[par] = KL == 128 ? ((lane & 7) ^ (4 * par + (lane >> 4))) * 16
+                          : ((lane & 3) ^ ((lane >> 3) & 3)) * 16;
 #pragma unroll
   for (int j = 0; j < GW; ++j) {
-    long long r = n0 + 8 * (wave * GW + j) + (lane >> 3);
+    long long r = n0 + RPL * (wave * GW + j) + lane / CPR;
     r = r < N ? r : N - 1;
     src[j] = W + r * K;
   }
 #pragma unroll
   for (int j = 0; j < GX; ++j) {
-    long long r = m0 + 8 * (wave * GX + j) + (lane >> 3);
+    long long r = m0 + RPL * (wave * GX + j) + lane / CPR;
     r = r < M ? r : M - 1;
     src[GW + j] = X + r * K;
   }
@@ -446,11 +453,11 @@ __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
   };
 
   // Fragment offsets of quarter q within a 32-row block: row lane&31,
-  // position (2q + (lane>>5)) ^ ((row>>1)&7) = 2q ^ t.
-  const int t = (lane >> 5) ^ ((lane >> 1) & 7);
-  int foff[4];
+  // logical chunk 2q + (lane>>5), stored at that chunk ^ key(row).
+  const int t = KL == 128 ? (lane >> 5) ^ ((lane >> 1) & 7) : (lane >> 5) ^ ((lane >> 1) & 3);
+  int foff[QPS];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) foff[q] = (lane & 31) * kLine + ((2 * q) ^ t) * 16;
+  for (int q = 0; q < QPS; ++q) foff[q] = (lane & 31) * kLine + ((2 * q) ^ t) * 16;
 
   v16i acc[FN][FM];
 #pragma unroll
@@ -462,8 +469,8 @@ __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
 
   const int wn = (wave / WGM) * WN;
   const int wm = (wave % WGM) * WM;
-  const int nq = K / 32;                 // K quarters in total
-  const int nk = (nq + 3) / 4;           // steps
+  const int nq = K / 32;                    // K quarters in total
+  const int nk = (nq + QPS - 1) / QPS;      // steps
 
   v4i fa[2][FN], fb[2][FM];
   auto read_frags = [&](int stage, int q, int slot) {
@@ -490,12 +497,11 @@ __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
   read_frags(0, 0, 0);
   int stage = 0;
   for (int k = 0; k + 1 < nk; ++k) {
-    read_frags(stage, 1, 1);
-    mfmas(0);
-    read_frags(stage, 2, 0);
-    mfmas(1);
-    read_frags(stage, 3, 1);
-    mfmas(0);
+#pragma unroll
+    for (int q = 1; q < QPS; ++q) {
+      read_frags(stage, q, q & 1);
+      mfmas((q - 1) & 1);
+    }
     // Loads issued: steps up to k+S-1; step k+1 must be in.
     wait_vmcnt<G * (S - 2)>();
     wait_lgkmcnt0();
@@ -503,21 +509,16 @@ __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
     issue(k + S < nk ? k + S : nk - 1, stage);
     stage = stage + 1 < S ? stage + 1 : 0;
     read_frags(stage, 0, 0);
-    mfmas(1);
+    mfmas((QPS - 1) & 1);
   }
   {
-    const int qn = nq - 4 * (nk - 1);    // 1..4 quarters in the last step
-    if (qn > 1) read_frags(stage, 1, 1);
-    mfmas(0);
-    if (qn > 1) {
-      if (qn > 2) read_frags(stage, 2, 0);
-      mfmas(1);
-      if (qn > 2) {
-        if (qn > 3) read_frags(stage, 3, 1);
-        mfmas(0);
-        if (qn > 3) mfmas(1);
-      }
+    const int qn = nq - QPS * (nk - 1);    // 1..QPS quarters in the last step
+#pragma unroll
+    for (int q = 1; q < QPS; ++q) {
+      if (q < qn) read_frags(stage, q, q & 1);
+      if (q - 1 < qn) mfmas((q - 1) & 1);
     }
+    if (QPS - 1 < qn) mfmas((QPS - 1) & 1);
   }
   // No global->LDS load may still be in flight when the workgroup's LDS is
   // released.
@@ -641,14 +642,14 @@ hipError_t launch_tile(const int8_t* W, const int8_t* X, const float* ws, const 
   return hipGetLastError();
 }
 
-template <int TN, int TM, int S, int WGN, int WGM>
+template <int TN, int TM, int S, int WGN, int WGM, int KL = 128>
 hipError_t launch_ring(const int8_t* W, const int8_t* X, const float* ws, const float* as,
                        const int32_t* row_sum, const int* zp, float* y, int32_t* acc_out,
                        long long m, long long n, long long k, bool asymmetric, int* status,
                        hipStream_t s) {
   const long long tiles_n = (n + TN - 1) / TN;
   const long long tiles_m = (m + TM - 1) / TM;
-  int8_gemm_ring<TN, TM, S, WGN, WGM>
+  int8_gemm_ring<TN, TM, S, WGN, WGM, KL>
       <<<static_cast<unsigned>(tiles_n * tiles_m), 64 * WGN * WGM, 0, s>>>(
       W, X, ws, as, row_sum, zp, y, acc_out, (int)m, (int)n, (int)k, (int)tiles_n, (int)tiles_m,
       asymmetric ? 1 : 0, status);
