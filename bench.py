@@ -42,9 +42,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=["headline", "all", "copy"], default="all",
+    p.add_argument("--only", choices=["headline", "all", "copy", "w8a8", "qgemm"], default="all",
                    help="copy: a plain 64 MiB device copy, the calibration kernel for "
-                        "FETCH_SIZE / WRITE_SIZE counter runs")
+                        "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm: only those "
+                        "secondary cases (for profiling), no JSON line")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--rows-per-wave", type=int, default=0)
@@ -299,6 +300,12 @@ def cpu_baseline(packed_dev, x_dev, y_dev, n, k, seconds):
     return base, gate
 
 
+def print_cases(cases):
+    for key, r in cases.items():
+        print(f"# {key}: " + ", ".join(f"{a}={b:.4g}" if isinstance(b, float) else f"{a}={b}"
+                                      for a, b in r.items()), file=sys.stderr, flush=True)
+
+
 def main():
     args = parse()
     global EAGER
@@ -323,6 +330,20 @@ def main():
         print(json.dumps({"copy_bytes": 64 << 20, "launches": args.warmup + args.steps}))
         return
     K, W = args.steps, args.warmup
+    if args.only in ("w8a8", "qgemm"):
+        s = {}
+        if args.only == "w8a8":
+            s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
+            s["w8a8_m2048_k4096_n4096"] = w8a8_case(qc, 2048, 4096, 4096, K, W)
+            s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, K, W)
+        else:
+            for fmt, name in ((0, "q8_0"), (1, "q4_0")):
+                for n_ in (4096, 14336):
+                    for m in (4, 8, 16, 32):
+                        s[f"{name}_qgemm_m{m}_k4096_n{n_}"] = qgemm_case(qc, n_, 4096, m, K, W,
+                                                                        seed=4 + m, fmt=fmt)
+        print_cases(s)
+        return
     n, k = 14336, 4096
     head, packed, x, y = gemv_case(qc, 1, n, k, K, W, seed=1)
     print(f"# headline q4_0 GEMV K={k} N={n}: {head['gbs']:.1f} GB/s wall, "
@@ -342,9 +363,7 @@ def main():
         s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, max(20, K // 4), W)
         for key, r in layer_sweep(qc, max(20, K // 4), W).items():
             s[f"decoder_layer_{key}"] = r
-        for key, r in s.items():
-            print(f"# {key}: " + ", ".join(f"{a}={b:.4g}" if isinstance(b, float) else f"{a}={b}"
-                                          for a, b in r.items()), file=sys.stderr, flush=True)
+        print_cases(s)
         secondary = s
     base, gate = (None, None)
     if not args.no_cpu:
