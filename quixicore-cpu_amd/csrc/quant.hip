@@ -37,10 +37,11 @@ __device__ __forceinline__ float abs_max4(float4 v, float m) {
   return fmaxf(fmaxf(fmaxf(m, fabsf(v.x)), fmaxf(fabsf(v.y), fabsf(v.z))), fabsf(v.w));
 }
 
-// Workgroup-wide max of a per-thread value and OR of a per-thread flag.
+// Workgroup-wide (NT threads) max of a per-thread value and OR of a per-thread flag.
+template <int NT>
 __device__ __forceinline__ void block_max_or(float& m, int& bad) {
-  __shared__ float smax[kThreads / 64];
-  __shared__ int sbad[kThreads / 64];
+  __shared__ float smax[NT / 64];
+  __shared__ int sbad[NT / 64];
   m = wave_max_nonneg(m);
   bad = __any(bad) ? 1 : 0;
   const int wave = threadIdx.x >> 6;
@@ -52,17 +53,17 @@ __device__ __forceinline__ void block_max_or(float& m, int& bad) {
   m = smax[0];
   bad = sbad[0];
 #pragma unroll
-  for (int w = 1; w < kThreads / 64; ++w) {
+  for (int w = 1; w < NT / 64; ++w) {
     m = fmaxf(m, smax[w]);
     bad |= sbad[w];
   }
 }
 
-// One workgroup per row, the row held in registers: V float4 per thread.
-// Requires dim % 4 == 0, x 16-byte aligned, codes 4-byte aligned and
-// dim <= 1024 * V.
-template <int V>
-__global__ __launch_bounds__(kThreads) void quantize_rows_regs(const float* __restrict__ x,
+// One workgroup of NT threads per row, the row held in registers: V float4
+// per thread.  Requires dim % 4 == 0, x 16-byte aligned, codes 4-byte
+// aligned and dim <= 4 * NT * V.
+template <int V, int NT>
+__global__ __launch_bounds__(NT) void quantize_rows_regs(const float* __restrict__ x,
                                                                int8_t* __restrict__ codes,
                                                                float* __restrict__ scales,
                                                                int dim, int* status) {
@@ -75,14 +76,14 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_regs(const float* __re
   int bad = 0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    const int idx = threadIdx.x + i * kThreads;
+    const int idx = threadIdx.x + i * NT;
     if (idx < n4) {
       v[i] = xr[idx];
       bad |= !finite4(v[i]);
       m = abs_max4(v[i], m);
     }
   }
-  block_max_or(m, bad);
+  block_max_or<NT>(m, bad);
   if (bad && status != nullptr) {
     if (threadIdx.x == 0) *status = 3;
     return;
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_regs(const float* __re
   const float inv = scale > 0.f ? 1.0f / scale : 0.f;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    const int idx = threadIdx.x + i * kThreads;
+    const int idx = threadIdx.x + i * NT;
     if (idx < n4) cr[idx] = quant4(v[i], inv);
   }
   if (threadIdx.x == 0) scales[row] = scale;
@@ -242,16 +243,20 @@ hipError_t launch_quantize_int8(const float* x, int8_t* codes, float* scales, lo
   const bool per_row = group == dim;
   const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(codes) % 4 == 0 && dim % 4 == 0;
-  if (per_row && aligned && dim <= 8192 && rows <= 0x7FFFFFFFLL) {
+  if (per_row && aligned && dim <= 32768 && rows <= 0x7FFFFFFFLL) {
     const unsigned grid = static_cast<unsigned>(rows);
     if (dim <= 1024)
-      quantize_rows_regs<1><<<grid, kThreads, 0, s>>>(x, codes, scales, (int)dim, status);
+      quantize_rows_regs<1, 256><<<grid, 256, 0, s>>>(x, codes, scales, (int)dim, status);
     else if (dim <= 2048)
-      quantize_rows_regs<2><<<grid, kThreads, 0, s>>>(x, codes, scales, (int)dim, status);
+      quantize_rows_regs<2, 256><<<grid, 256, 0, s>>>(x, codes, scales, (int)dim, status);
     else if (dim <= 4096)
-      quantize_rows_regs<4><<<grid, kThreads, 0, s>>>(x, codes, scales, (int)dim, status);
+      quantize_rows_regs<4, 256><<<grid, 256, 0, s>>>(x, codes, scales, (int)dim, status);
+    else if (dim <= 8192)
+      quantize_rows_regs<8, 256><<<grid, 256, 0, s>>>(x, codes, scales, (int)dim, status);
+    else if (dim <= 16384)
+      quantize_rows_regs<8, 512><<<grid, 512, 0, s>>>(x, codes, scales, (int)dim, status);
     else
-      quantize_rows_regs<8><<<grid, kThreads, 0, s>>>(x, codes, scales, (int)dim, status);
+      quantize_rows_regs<8, 1024><<<grid, 1024, 0, s>>>(x, codes, scales, (int)dim, status);
     return hipGetLastError();
   }
   const long long ngroups = rows * (dim / group);

@@ -25,12 +25,22 @@ def test_quantize_int8_config3(qc, oracle, synth, dev):
 
 @pytest.mark.parametrize("rows,dim,group", [(1, 4, 0), (3, 100, 0), (5, 1024, 0), (7, 2048, 0),
                                             (3, 8192, 0), (2, 12288, 0), (4, 4096, 128),
-                                            (2, 4, 2), (3, 96, 32)])
+                                            (2, 4, 2), (3, 96, 32), (5, 14336, 0), (2, 16384, 0),
+                                            (3, 16388, 0), (2, 32768, 0), (2, 32772, 0),
+                                            (3, 14338, 0)])
 def test_quantize_int8_shapes(qc, oracle, dev, rows, dim, group):
     rng = np.random.default_rng(rows * 1000 + dim)
     x = rng.standard_normal((rows, dim)).astype(np.float32)
     x[0, : min(dim, 8)] = 0.0
     _quant_check(qc, oracle, dev, x, group)
+
+
+def test_quantize_int8_down_proj(qc, oracle, synth, dev):
+    """Config 4's down projection input: 512 x 14336 with outliers (a 512-thread
+    workgroup per row)."""
+    print("quantize_int8 512x14336", flush=True)
+    x = synth.activations_outliers_fast(4, 512, 14336)
+    _quant_check(qc, oracle, dev, x)
 
 
 def test_quantize_int8_edges(qc, oracle, dev):
