@@ -54,8 +54,28 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kStagePairs = 4;           // block pairs per ring stage
 constexpr int kStageBlocks = 2 * kStagePairs;
 
-// Bytes of activation fragments per block and m-tile: hi and lo, 64 lanes x 16 B.
+// Bytes of activation fragments per block and dense m-tile: hi and lo, 64
+// lanes x 16 B.
 constexpr int kFragBytes = 2048;
+
+// Activation layout per 32-element block, by XL:
+//  * XL = 16 / 32 (dense, T = XL / 16 m-tiles): [m-tile][hi | lo][64 lanes][16 B],
+//    exactly the MFMA operand registers, plus (q4_0) a separate bias array
+//    [block][m-tile][16 rows] of f32;
+//  * XL = 4 / 8 (compact, for M <= XL): only XL rows, [hi: XL rows x 80 B]
+//    [lo: XL rows x 80 B] with 16 B of padding per row (so the rows a lane
+//    group reads fall on distinct LDS bank groups), then (q4_0) the XL bias
+//    floats; lanes of rows >= XL use zero operands.
+template <int XL, bool BIAS>
+struct XBlock {
+  static constexpr bool compact = XL <= 8;
+  static constexpr int T = compact ? 1 : XL / 16;        // m-tiles of 16 rows
+  static constexpr int row_stride = 80;
+  static constexpr int bytes = compact ? 2 * XL * row_stride + (BIAS ? 4 * XL : 0)
+                                       : T * kFragBytes;
+  static constexpr int bias_bytes = compact || !BIAS ? 0 : T * 64;   // separate array
+  static_assert(bytes % 16 == 0, "whole 16-byte chunks");
+};
 
 template <int FMT>
 struct PairLayout;
@@ -132,11 +152,6 @@ __device__ __forceinline__ void ring_barrier() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
 }
-__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-#endif
-}
 
 // global_load_lds_dwordx4 from a wave-uniform base (scalar registers) plus a
 // per-lane byte offset, to LDS byte lds + 16 * lane (lds wave-uniform, in
@@ -172,7 +187,7 @@ __device__ __forceinline__ void dma16_addr(const void* addr, const void* lds) {
 // Block 0 also copies the weights' last row's short final stage (`tail`
 // bytes from `tail_src`) into the zero-padded `tail_pad` (pad_bytes), which
 // the GEMM reads instead of running past the end of W.
-template <int T, bool BIAS>
+template <int XL, bool BIAS>
 __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, int M, int K,
                                                  uint8_t* __restrict__ xf,
                                                  float* __restrict__ bias, float* zero_y,
@@ -181,6 +196,8 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
                                                  uint8_t* __restrict__ tail_pad, int pad_bytes) {
   if (blockIdx.x == 0 && tail > 0)
     for (int i = threadIdx.x; i < pad_bytes; i += 64) tail_pad[i] = i < tail ? tail_src[i] : 0;
+  using XB = XBlock<XL, BIAS>;
+  constexpr int T = XB::T;
   const int b = blockIdx.x / T, t = blockIdx.x % T;
   const int l = threadIdx.x;
   const int m = 16 * t + (l & 15), j = l >> 4;
@@ -199,13 +216,23 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
     lo[i] = static_cast<__bf16>(v[i] - h);
     s += h + static_cast<float>(lo[i]);
   }
-  uint8_t* dst = xf + (static_cast<long long>(b) * T + t) * kFragBytes + 16 * l;
-  *reinterpret_cast<bf16x8*>(dst) = hi;
-  *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
   if constexpr (BIAS) {
     s += __shfl_xor(s, 16);
     s += __shfl_xor(s, 32);
-    if (j == 0) bias[(static_cast<long long>(b) * T + t) * 16 + (l & 15)] = -8.0f * s;
+  }
+  if constexpr (XB::compact) {
+    uint8_t* rec = xf + static_cast<long long>(b) * XB::bytes;
+    const int r = l & 15;
+    if (r < XL) {
+      *reinterpret_cast<bf16x8*>(rec + r * XB::row_stride + 16 * j) = hi;
+      *reinterpret_cast<bf16x8*>(rec + (XL + r) * XB::row_stride + 16 * j) = lo;
+      if (BIAS && j == 0) reinterpret_cast<float*>(rec + 2 * XL * XB::row_stride)[r] = -8.0f * s;
+    }
+  } else {
+    uint8_t* dst = xf + (static_cast<long long>(b) * T + t) * kFragBytes + 16 * l;
+    *reinterpret_cast<bf16x8*>(dst) = hi;
+    *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
+    if (BIAS && j == 0) bias[(static_cast<long long>(b) * T + t) * 16 + (l & 15)] = -8.0f * s;
   }
   // y is accumulated with two atomic adds when K is split in two: clear it.
   for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
@@ -239,33 +266,41 @@ struct WStage {
   static constexpr int wave_bytes = 16 * row_bytes;
 };
 
-template <int FMT, int T, int NW>
+template <int FMT, int XL, int NW>
 struct StageLayout {
+  using XB = XBlock<XL, FMT == kQ4_0>;
   static constexpr bool bias = FMT == kQ4_0;
   static constexpr int w_bytes = NW * WStage<FMT>::wave_bytes;
-  static constexpr int x_bytes = kStageBlocks * T * kFragBytes;
-  static constexpr int bias_bytes = bias ? kStageBlocks * T * 64 : 0;
+  static constexpr int x_bytes = kStageBlocks * XB::bytes;
+  static constexpr int bias_bytes = kStageBlocks * XB::bias_bytes;   // dense q4_0 only
   static constexpr int bytes = w_bytes + x_bytes + bias_bytes;
-  // Ring depth: three stages when they fit the 160 KB LDS, else two.
+  // Ring depth: three stages when they fit the 160 KB LDS, else two (deeper
+  // rings measured slower on MI355X).
   static constexpr int ring = 3 * bytes <= 160 * 1024 ? 3 : 2;
-  static constexpr int gx = x_bytes / 1024 / NW;
-  static constexpr int g = WStage<FMT>::loads + gx + (bias ? 1 : 0);  // loads per wave per stage
+  // The x bytes of a stage are xc 16-byte chunks; wave w copies chunks
+  // [w * cpw, (w + 1) * cpw) with gx loads (the last ones partial).
+  static constexpr int xc = x_bytes / 16;
+  static constexpr int cpw = (xc + NW - 1) / NW;
+  static constexpr int gx = (cpw + 63) / 64;
+  static_assert((NW - 1) * cpw + 64 * (gx - 1) < xc, "every x load keeps an active lane");
+  static constexpr int g = WStage<FMT>::loads + gx + (bias_bytes ? 1 : 0);  // loads per wave per stage
 };
 
 // NW wavefronts per workgroup, 16 weight rows each.
-template <int FMT, int T, int NW, int NST>
+template <int FMT, int XL, int NW, int NST>
 __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
     float* __restrict__ y, float* __restrict__ partial, const uint8_t* __restrict__ tail_pad,
     int M, int N, int K, int nslabs, int ks_count, int nstages) {
-  using L = StageLayout<FMT, T, NW>;
+  using L = StageLayout<FMT, XL, NW>;
+  using XB = typename L::XB;
   using WS = WStage<FMT>;
+  constexpr int T = XB::T;
   constexpr int kSlab = 16 * NW;
   constexpr int S = L::ring;
   constexpr int G = L::g;
   constexpr int kBiasPerWave = L::bias_bytes / NW;
   static_assert(L::bias_bytes % (16 * NW) == 0, "bias split");
-  static_assert(L::gx >= 1 && L::x_bytes % (1024 * NW) == 0, "stage split");
   static_assert(G * (S - 1) < 64, "vmcnt range");
   // One LDS array per ring slot: slot indices are compile-time after
   // unrolling, so the compiler can tell the reads of one slot from the
@@ -311,7 +346,7 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
   // past the end of W (holding skipped bytes only) reads the copy as well.
   const bool short_tail = npairs % kStagePairs != 0;
   const unsigned long long w_end = static_cast<unsigned long long>(N) * row_bytes;
-  const uint32_t xoff = static_cast<uint32_t>(wave * L::gx * 1024 + lane * 16);
+  const uint32_t xoff = static_cast<uint32_t>(16 * (wave * L::cpw + lane));
   const uint32_t boff = static_cast<uint32_t>(wave * kBiasPerWave + lane * 16);
   auto issue = [&](int stage, int slot) {
     const int st = stage < st1 ? stage : st1 - 1;
@@ -334,9 +369,12 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     }
     const uint8_t* xs = xf + static_cast<long long>(st) * L::x_bytes;
 #pragma unroll
-    for (int i = 0; i < L::gx; ++i)
-      dma16(xs, xoff + i * 1024, base + L::w_bytes + (wave * L::gx + i) * 1024);
-    if constexpr (L::bias) {
+    for (int i = 0; i < L::gx; ++i) {
+      const int c = 64 * i + lane;   // chunk wave * cpw + c of the stage
+      if (c < L::cpw && wave * L::cpw + c < L::xc)
+        dma16(xs, xoff + i * 1024, base + L::w_bytes + 16 * (wave * L::cpw + 64 * i));
+    }
+    if constexpr (L::bias_bytes > 0) {
       // Wave w moves bias bytes [w, w+1) * kBiasPerWave of the stage with
       // its first kBiasPerWave / 16 lanes.
       const uint8_t* bs = reinterpret_cast<const uint8_t*>(bias) +
@@ -374,12 +412,26 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
         const int blk = 2 * pp + h;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-          const uint8_t* f = xs + (blk * T + t) * kFragBytes + lane * 16;
-          const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
-          const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+          bf16x8 xh, xl;
           f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
-          if constexpr (L::bias)
-            c = *reinterpret_cast<const f32x4*>(xs + L::x_bytes + (blk * T + t) * 64 + 16 * j);
+          if constexpr (XB::compact) {
+            // rows >= XL: zero operands (their outputs are never stored)
+            const int r = lane & 15;
+            const uint8_t* rec = xs + blk * XB::bytes;
+            const uint8_t* fh = rec + (r < XL ? r : XL - 1) * XB::row_stride + 16 * j;
+            const bf16x8 zero = {};
+            xh = r < XL ? *reinterpret_cast<const bf16x8*>(fh) : zero;
+            xl = r < XL ? *reinterpret_cast<const bf16x8*>(fh + XL * XB::row_stride) : zero;
+            if constexpr (L::bias)
+              if (4 * j < XL)
+                c = *reinterpret_cast<const f32x4*>(rec + 2 * XL * XB::row_stride + 16 * j);
+          } else {
+            const uint8_t* f = xs + (blk * T + t) * kFragBytes + lane * 16;
+            xh = *reinterpret_cast<const bf16x8*>(f);
+            xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+            if constexpr (L::bias)
+              c = *reinterpret_cast<const f32x4*>(xs + L::x_bytes + (blk * T + t) * 64 + 16 * j);
+          }
           c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv, c, 0, 0, 0);
           c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv, c, 0, 0, 0);
 #pragma unroll
@@ -495,25 +547,25 @@ hipError_t workspace_for(hipStream_t s, size_t bytes, void** out) {
   return hipSuccess;
 }
 
-template <int FMT, int T, int NW, int NST>
+template <int FMT, int XL, int NW, int NST>
 hipError_t launch_nst(const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
                       float* partial, const uint8_t* tail_pad, int m, int n, int k, int nslabs,
                       int ks, int nstages, hipStream_t s) {
-  qgemm_mfma<FMT, T, NW, NST><<<nslabs * ks, 64 * NW, 0, s>>>(W, xf, bias, y, partial, tail_pad,
+  qgemm_mfma<FMT, XL, NW, NST><<<nslabs * ks, 64 * NW, 0, s>>>(W, xf, bias, y, partial, tail_pad,
                                                               m, n, k, nslabs, ks, nstages);
   return hipGetLastError();
 }
 
-template <int FMT, int T, int NW>
+template <int FMT, int XL, int NW>
 hipError_t launch_nw(int nst, const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
                      float* partial, const uint8_t* tail_pad, int m, int n, int k, int nslabs,
                      int ks, int nstages, hipStream_t s) {
   switch (nst) {
-    case 16: return launch_nst<FMT, T, NW, 16>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    case 8: return launch_nst<FMT, T, NW, 8>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    case 4: return launch_nst<FMT, T, NW, 4>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    case 2: return launch_nst<FMT, T, NW, 2>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    default: return launch_nst<FMT, T, NW, 1>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 16: return launch_nst<FMT, XL, NW, 16>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 8: return launch_nst<FMT, XL, NW, 8>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 4: return launch_nst<FMT, XL, NW, 4>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 2: return launch_nst<FMT, XL, NW, 2>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    default: return launch_nst<FMT, XL, NW, 1>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
   }
 }
 
@@ -549,7 +601,7 @@ Plan plan_for(int n, int nstages, int cus) {
   return best;
 }
 
-template <int FMT, int T>
+template <int FMT, int XL>
 hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, hipStream_t s) {
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
@@ -557,8 +609,9 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const Plan plan = plan_for<FMT>(n, nstages, device_cus());
   const int nslabs = (n + 16 * plan.nw - 1) / (16 * plan.nw);
   const int ks = plan.ks;
-  const size_t xf_bytes = static_cast<size_t>(nbp) * T * kFragBytes;
-  const size_t bias_bytes = FMT == kQ4_0 ? static_cast<size_t>(nbp) * T * 64 : 0;
+  using XB = XBlock<XL, FMT == kQ4_0>;
+  const size_t xf_bytes = static_cast<size_t>(nbp) * XB::bytes;
+  const size_t bias_bytes = static_cast<size_t>(nbp) * XB::bias_bytes;
   const size_t part_bytes = ks > 2 ? static_cast<size_t>(ks) * m * n * sizeof(float) : 0;
   const size_t pad_bytes = WStage<FMT>::row_bytes;
   const size_t total = xf_bytes + bias_bytes + part_bytes + pad_bytes + 256;
@@ -573,15 +626,15 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const long long row_bytes = static_cast<long long>(nb) * PairLayout<FMT>::bytes / 2;
   const int tail = (k / 64) % kStagePairs * PairLayout<FMT>::bytes;
   const uint8_t* tail_src = W + (n - 1) * row_bytes + static_cast<long long>(nstages - 1) * WStage<FMT>::row_bytes;
-  qgemm_prep<T, FMT == kQ4_0><<<nbp * T, 64, 0, s>>>(x, m, k, xf, bias, y, ks == 2 ? outs : 0,
+  qgemm_prep<XL, FMT == kQ4_0><<<nbp * XB::T, 64, 0, s>>>(x, m, k, xf, bias, y, ks == 2 ? outs : 0,
                                                      tail_src, tail, tail_pad,
                                                      static_cast<int>(pad_bytes));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (plan.nw == 8)
-    e = launch_nw<FMT, T, 8>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    e = launch_nw<FMT, XL, 8>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
   else
-    e = launch_nw<FMT, T, 4>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    e = launch_nw<FMT, XL, 4>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
   if (e != hipSuccess || ks <= 2) return e;
   const long long blocks = (outs + 255) / 256;
   qgemm_reduce<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(partial, y, outs, ks);
@@ -597,11 +650,16 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
     const int mt = m - m0 < 32 ? m - m0 : 32;
     const float* xm = x + static_cast<long long>(m0) * k;
     float* ym = y + static_cast<long long>(m0) * n;
+    // activation layout: compact rows for M <= 4 / 8, dense 16-row tiles above
     hipError_t e;
     if (fmt == kQ8_0)
-      e = mt <= 16 ? run<kQ8_0, 1>(w, xm, ym, mt, n, k, s) : run<kQ8_0, 2>(w, xm, ym, mt, n, k, s);
+      e = mt <= 4 ? run<kQ8_0, 4>(w, xm, ym, mt, n, k, s)
+        : mt <= 8 ? run<kQ8_0, 8>(w, xm, ym, mt, n, k, s)
+        : mt <= 16 ? run<kQ8_0, 16>(w, xm, ym, mt, n, k, s) : run<kQ8_0, 32>(w, xm, ym, mt, n, k, s);
     else
-      e = mt <= 16 ? run<kQ4_0, 1>(w, xm, ym, mt, n, k, s) : run<kQ4_0, 2>(w, xm, ym, mt, n, k, s);
+      e = mt <= 4 ? run<kQ4_0, 4>(w, xm, ym, mt, n, k, s)
+        : mt <= 8 ? run<kQ4_0, 8>(w, xm, ym, mt, n, k, s)
+        : mt <= 16 ? run<kQ4_0, 16>(w, xm, ym, mt, n, k, s) : run<kQ4_0, 32>(w, xm, ym, mt, n, k, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

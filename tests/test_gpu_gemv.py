@@ -116,7 +116,10 @@ def test_qgemm_small_batch(qc, oracle, synth, dev, fmt, m):
 @pytest.mark.parametrize("fmt,m,n,k", [(0, 33, 300, 192), (1, 40, 129, 64), (0, 5, 2000, 4160),
                                         (1, 32, 4096, 1408), (0, 17, 1000, 14336),
                                         (1, 2, 14336, 4096), (0, 64, 520, 256),
-                                        (0, 3, 5, 64), (1, 7, 3, 128), (0, 20, 130, 320)])
+                                        (0, 3, 5, 64), (1, 7, 3, 128), (0, 20, 130, 320),
+                                        (1, 4, 14336, 4096), (0, 8, 4096, 4096),
+                                        (1, 6, 1000, 14336), (0, 4, 700, 8256),
+                                        (1, 9, 260, 4096), (0, 12, 4096, 448)])
 def test_qgemm_mfma_shapes(qc, oracle, synth, dev, fmt, m, n, k):
     """Small-batch GEMM shapes that exercise M beyond one 32-row launch,
     partial last K stages, ragged N and split-K partial sums."""
