@@ -50,6 +50,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kStagePairs = 4;           // block pairs per ring stage
 constexpr int kStageBlocks = 2 * kStagePairs;
@@ -58,22 +59,24 @@ constexpr int kStageBlocks = 2 * kStagePairs;
 // lanes x 16 B.
 constexpr int kFragBytes = 2048;
 
-// Activation layout per 32-element block, by XL:
-//  * XL = 16 / 32 (dense, T = XL / 16 m-tiles): [m-tile][hi | lo][64 lanes][16 B],
-//    exactly the MFMA operand registers, plus (q4_0) a separate bias array
-//    [block][m-tile][16 rows] of f32;
-//  * XL = 4 / 8 (compact, for M <= XL): only XL rows, [hi: XL rows x 80 B]
-//    [lo: XL rows x 80 B] with 16 B of padding per row (so the rows a lane
-//    group reads fall on distinct LDS bank groups), then (q4_0) the XL bias
-//    floats; lanes of rows >= XL use zero operands.
+// Activation layout per 32-element block, by XL (rows per pass, M <= XL):
+//  * XL = 16 / 32, bf16 mode (T = XL / 16 m-tiles): [m-tile][hi | lo][64
+//    lanes][16 B], exactly the MFMA operand registers, plus (q4_0) a separate
+//    bias array [block][m-tile][16 rows] of f32;
+//  * XL = 4 / 8, digit mode (T = XL / 4 tiles of 4 rows): the int8 digit
+//    planes of each row as v_mfma_i32_16x16x32_i8 A operands, [tile][64
+//    lanes][8 B] with operand row 4 (m & 3) + d holding digit d of row m (d = 3
+//    is zero); then per row {int32 e, f32 gate}; then (q4_0) per row the
+//    int32 C input {-8 sum_k digit_d, d = 0..3}.
 template <int XL, bool BIAS>
 struct XBlock {
-  static constexpr bool compact = XL <= 8;
-  static constexpr int T = compact ? 1 : XL / 16;        // m-tiles of 16 rows
-  static constexpr int row_stride = 80;
-  static constexpr int bytes = compact ? 2 * XL * row_stride + (BIAS ? 4 * XL : 0)
-                                       : T * kFragBytes;
-  static constexpr int bias_bytes = compact || !BIAS ? 0 : T * 64;   // separate array
+  static constexpr bool digits = XL <= 8;
+  static constexpr int T = digits ? XL / 4 : XL / 16;   // operand tiles
+  static constexpr int meta_off = digits ? T * 512 : 0;
+  static constexpr int bias_off = meta_off + 8 * XL;
+  static constexpr int bytes = digits ? bias_off + (BIAS ? 16 * XL : 0) : T * kFragBytes;
+  static constexpr int bias_bytes = digits || !BIAS ? 0 : T * 64;    // separate array
+  static constexpr int prep_groups = digits ? 1 : T;                 // prep workgroups per block
   static_assert(bytes % 16 == 0, "whole 16-byte chunks");
 };
 
@@ -197,42 +200,101 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
   if (blockIdx.x == 0 && tail > 0)
     for (int i = threadIdx.x; i < pad_bytes; i += 64) tail_pad[i] = i < tail ? tail_src[i] : 0;
   using XB = XBlock<XL, BIAS>;
-  constexpr int T = XB::T;
-  const int b = blockIdx.x / T, t = blockIdx.x % T;
   const int l = threadIdx.x;
-  const int m = 16 * t + (l & 15), j = l >> 4;
   const int nb = K / 32;
-  float v[8];
-  const bool live = m < M && b < nb;
-  const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * b : 0) + 8 * j;
+  if constexpr (XB::digits) {
+    // Thread l: row m = l >> 3, elements 4 (l & 7) .. +3 of block b.  The
+    // digits are those of the M = 1 path: e = frexp exponent of max|x_b| - 21,
+    // q = rint(x * 2^-e) clamped to [-2^21, 2^21), q = 2^14 d0 + 2^7 d1 + d2.
+    const int b = blockIdx.x;
+    const int m = l >> 3, part = l & 7;
+    const bool row_ok = m < XL;
+    const bool live = row_ok && m < M && b < nb;
+    const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * b : 0) + 4 * part;
+    float v[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = live ? src[i] : 0.0f;
-  bf16x8 hi, lo;
-  float s = 0.0f;
+    for (int i = 0; i < 4; ++i) v[i] = live ? src[i] : 0.0f;
+    float mx = 0.f;
+    int fin = 1;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    hi[i] = static_cast<__bf16>(v[i]);
-    const float h = static_cast<float>(hi[i]);
-    lo[i] = static_cast<__bf16>(v[i] - h);
-    s += h + static_cast<float>(lo[i]);
-  }
-  if constexpr (BIAS) {
-    s += __shfl_xor(s, 16);
-    s += __shfl_xor(s, 32);
-  }
-  if constexpr (XB::compact) {
+    for (int i = 0; i < 4; ++i) {
+      mx = fmaxf(mx, fabsf(v[i]));
+      fin &= isfinite(v[i]) ? 1 : 0;
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+      mx = fmaxf(mx, __shfl_xor(mx, o));
+      fin &= __shfl_xor(fin, o);
+    }
+    int ex = 0;
+    (void)frexpf(mx, &ex);                           // mx < 2^ex
+    const int e = fin ? ex - 21 : 0;
+    uint32_t pk[3] = {0u, 0u, 0u};
+    int sum[3] = {0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int q = fin ? __float2int_rn(ldexpf(v[i], -e)) : 0;   // |x * 2^-e| <= 2^21
+      q = q > 2097151 ? 2097151 : q;
+      const int dg[3] = {q >> 14, (q >> 7) & 127, q & 127};
+#pragma unroll
+      for (int d = 0; d < 3; ++d) {
+        pk[d] |= static_cast<uint32_t>(dg[d] & 0xFF) << (8 * i);
+        sum[d] += dg[d];
+      }
+    }
     uint8_t* rec = xf + static_cast<long long>(b) * XB::bytes;
-    const int r = l & 15;
-    if (r < XL) {
-      *reinterpret_cast<bf16x8*>(rec + r * XB::row_stride + 16 * j) = hi;
-      *reinterpret_cast<bf16x8*>(rec + (XL + r) * XB::row_stride + 16 * j) = lo;
-      if (BIAS && j == 0) reinterpret_cast<float*>(rec + 2 * XL * XB::row_stride)[r] = -8.0f * s;
+    if (row_ok) {
+      // operand row r = 4 (m & 3) + d, k = 4 part + i: lane r + 16 (part >> 1),
+      // bytes 4 (part & 1) .. +3 of its 8
+      uint8_t* a = rec + (m >> 2) * 512 + 4 * (part & 1);
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        *reinterpret_cast<uint32_t*>(a + 8 * (4 * (m & 3) + d + 16 * (part >> 1))) = d < 3 ? pk[d] : 0u;
+    }
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) sum[d] += __shfl_xor(sum[d], o);
+    }
+    if (row_ok && part == 0) {
+      int* meta = reinterpret_cast<int*>(rec + XB::meta_off) + 2 * m;
+      meta[0] = e;
+      meta[1] = __float_as_int(fin ? 1.0f : __builtin_nanf(""));
+      if constexpr (BIAS) {
+        int* c = reinterpret_cast<int*>(rec + XB::bias_off) + 4 * m;
+        c[0] = -8 * sum[0];
+        c[1] = -8 * sum[1];
+        c[2] = -8 * sum[2];
+        c[3] = 0;
+      }
     }
   } else {
+    constexpr int T = XB::T;
+    const int b = blockIdx.x / T, t = blockIdx.x % T;
+    const int m = 16 * t + (l & 15), j = l >> 4;
+    float v[8];
+    const bool live = m < M && b < nb;
+    const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * b : 0) + 8 * j;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = live ? src[i] : 0.0f;
+    bf16x8 hi, lo;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      hi[i] = static_cast<__bf16>(v[i]);
+      const float h = static_cast<float>(hi[i]);
+      lo[i] = static_cast<__bf16>(v[i] - h);
+      s += h + static_cast<float>(lo[i]);
+    }
     uint8_t* dst = xf + (static_cast<long long>(b) * T + t) * kFragBytes + 16 * l;
     *reinterpret_cast<bf16x8*>(dst) = hi;
     *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
-    if (BIAS && j == 0) bias[(static_cast<long long>(b) * T + t) * 16 + (l & 15)] = -8.0f * s;
+    if constexpr (BIAS) {
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      if (j == 0) bias[(static_cast<long long>(b) * T + t) * 16 + (l & 15)] = -8.0f * s;
+    }
   }
   // y is accumulated with two atomic adds when K is split in two: clear it.
   for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
@@ -384,9 +446,13 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     }
   };
 
-  f32x4 acc[T];
+  f32x4 acc[T];     // bf16 mode: output (m = 16t + 4j + e, n)
+  float accd[T];    // digit mode: output (m = 4t + j, n)
 #pragma unroll
-  for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < T; ++t) {
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accd[t] = 0.f;
+  }
 
   // Branch-free, so the compiler can overlap the pairs' LDS reads, code
   // conversions and MFMAs.  A pair past K or a stage past st1 (clamped
@@ -407,35 +473,50 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
       for (int h = 0; h < 2; ++h) {
         const uint32_t c0 = h == 0 ? __builtin_amdgcn_alignbyte(b0.y, b0.x, 2) : b1.x;
         const uint32_t c1 = h == 0 ? __builtin_amdgcn_alignbyte(b0.z, b0.y, 2) : b1.y;
-        const bf16x8 wv = codes_bf16<FMT>(c0, c1, j);
-        const float d = valid ? half_bits_to_float(h == 0 ? (s0 & 0xFFFFu) : (s1 >> 16)) : 0.0f;
+        const uint32_t dbits = h == 0 ? (s0 & 0xFFFFu) : (s1 >> 16);
         const int blk = 2 * pp + h;
+        if constexpr (XB::digits) {
+          // B operand: the lane's 8 codes as int8 (q8_0 as stored; q4_0
+          // nibbles 0..15, the -8 entering through the C input).
+          uint32_t w0 = c0, w1 = c1;
+          if constexpr (FMT == kQ4_0) {
+            const int sh = (j >> 1) * 4;
+            w0 = (c0 >> sh) & 0x0F0F0F0Fu;
+            w1 = (c1 >> sh) & 0x0F0F0F0Fu;
+          }
+          const long wq = static_cast<long>(w0) | (static_cast<long>(w1) << 32);
+          const float dw = half_bits_to_float(dbits);
+          const uint8_t* rec = xs + blk * XB::bytes;
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          bf16x8 xh, xl;
-          f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
-          if constexpr (XB::compact) {
-            // rows >= XL: zero operands (their outputs are never stored)
-            const int r = lane & 15;
-            const uint8_t* rec = xs + blk * XB::bytes;
-            const uint8_t* fh = rec + (r < XL ? r : XL - 1) * XB::row_stride + 16 * j;
-            const bf16x8 zero = {};
-            xh = r < XL ? *reinterpret_cast<const bf16x8*>(fh) : zero;
-            xl = r < XL ? *reinterpret_cast<const bf16x8*>(fh + XL * XB::row_stride) : zero;
+          for (int t = 0; t < T; ++t) {
+            const long a = *reinterpret_cast<const long*>(rec + t * 512 + 8 * lane);
+            i32x4 c = {0, 0, 0, 0};
             if constexpr (L::bias)
-              if (4 * j < XL)
-                c = *reinterpret_cast<const f32x4*>(rec + 2 * XL * XB::row_stride + 16 * j);
-          } else {
+              c = *reinterpret_cast<const i32x4*>(rec + XB::bias_off + 16 * (4 * t + j));
+            // D lane (n, j): digit sums S_0..S_3 of row m = 4t + j (S_3 = 0)
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wq, c, 0, 0, 0);
+            const int2 me = *reinterpret_cast<const int2*>(rec + XB::meta_off + 8 * (4 * t + j));
+            const float f = fmaf(static_cast<float>(c[0]), 16384.f,
+                                 fmaf(static_cast<float>(c[1]), 128.f, static_cast<float>(c[2])));
+            const float blk_dot = ldexpf((dw * __int_as_float(me.y)) * f, me.x);
+            accd[t] += valid ? blk_dot : 0.0f;
+          }
+        } else {
+          const bf16x8 wv = codes_bf16<FMT>(c0, c1, j);
+          const float d = valid ? half_bits_to_float(dbits) : 0.0f;
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
             const uint8_t* f = xs + (blk * T + t) * kFragBytes + lane * 16;
-            xh = *reinterpret_cast<const bf16x8*>(f);
-            xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+            const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
+            const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+            f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
             if constexpr (L::bias)
               c = *reinterpret_cast<const f32x4*>(xs + L::x_bytes + (blk * T + t) * 64 + 16 * j);
-          }
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv, c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv, c, 0, 0, 0);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(c[e], d, acc[t][e]);
+            for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(c[e], d, acc[t][e]);
+          }
         }
       }
     }
@@ -463,7 +544,10 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     // scale FMAs of every stage into the (conditional) store block and keeps
     // all MFMA results of the workgroup live until then.
 #pragma unroll
-    for (int t = 0; t < T; ++t) asm volatile("" : "+v"(acc[t]));
+    for (int t = 0; t < T; ++t) {
+      if constexpr (XB::digits) asm volatile("" : "+v"(accd[t]));
+      else asm volatile("" : "+v"(acc[t]));
+    }
   }
   wait_vmcnt<0>();   // no global->LDS load may outlive the workgroup's LDS
 
@@ -472,17 +556,22 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
   // not depend on which finishes first).  More: partial sums for the
   // reduction kernel.
   if (n >= N) return;
+  auto put = [&](int m, float v) {
+    if (m >= M) return;
+    const long long o = static_cast<long long>(m) * N + n;
+    if (ks_count == 1) y[o] = v;
+    else if (ks_count == 2) atomicAdd(y + o, v);
+    else partial[static_cast<long long>(ks) * M * N + o] = v;
+  };
 #pragma unroll
-  for (int t = 0; t < T; ++t)
+  for (int t = 0; t < T; ++t) {
+    if constexpr (XB::digits) {
+      put(4 * t + j, accd[t]);
+    } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = 16 * t + 4 * j + e;
-      if (m >= M) continue;
-      const long long o = static_cast<long long>(m) * N + n;
-      if (ks_count == 1) y[o] = acc[t][e];
-      else if (ks_count == 2) atomicAdd(y + o, acc[t][e]);
-      else partial[static_cast<long long>(ks) * M * N + o] = acc[t][e];
+      for (int e = 0; e < 4; ++e) put(16 * t + 4 * j + e, acc[t][e]);
     }
+  }
 }
 
 int device_cus() {
@@ -626,7 +715,7 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const long long row_bytes = static_cast<long long>(nb) * PairLayout<FMT>::bytes / 2;
   const int tail = (k / 64) % kStagePairs * PairLayout<FMT>::bytes;
   const uint8_t* tail_src = W + (n - 1) * row_bytes + static_cast<long long>(nstages - 1) * WStage<FMT>::row_bytes;
-  qgemm_prep<XL, FMT == kQ4_0><<<nbp * XB::T, 64, 0, s>>>(x, m, k, xf, bias, y, ks == 2 ? outs : 0,
+  qgemm_prep<XL, FMT == kQ4_0><<<nbp * XB::prep_groups, 64, 0, s>>>(x, m, k, xf, bias, y, ks == 2 ? outs : 0,
                                                      tail_src, tail, tail_pad,
                                                      static_cast<int>(pad_bytes));
   e = hipGetLastError();
