@@ -133,6 +133,14 @@ int qc_hip_set_gemv_rows_per_wave(int rows);
  * same bits.  Tuning and test knob with no reference counterpart. */
 int qc_hip_set_int8_gemm_route(int route);
 
+/* Work split of the small-batch GEMM (qc_hip_qgemm with M >= 2, K % 64 == 0;
+ * process-wide): waves per workgroup (4 or 8) and 256-element K stages per
+ * workgroup (1, 2, 4, 8 or 16; K is split into ceil(K / 256 / stages)
+ * ranges); 0 leaves a field to the shape-based planner.  Results stay within
+ * the contract tolerance for every split, and reruns with one split are
+ * bit-identical.  Tuning and test knob with no reference counterpart. */
+int qc_hip_set_qgemm_plan(int waves, int stages);
+
 #ifdef __cplusplus
 }
 #endif

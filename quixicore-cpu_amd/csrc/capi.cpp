@@ -260,6 +260,15 @@ int qc_hip_set_gemv_rows_per_wave(int rows) {
   return QC_OK;
 }
 
+int qc_hip_set_qgemm_plan(int waves, int stages) {
+  if (waves != 0 && waves != 4 && waves != 8) return QC_INVALID_ARGUMENT;
+  if (stages != 0 && stages != 1 && stages != 2 && stages != 4 && stages != 8 && stages != 16)
+    return QC_INVALID_ARGUMENT;
+  g_tuning.qgemm_waves = waves;
+  g_tuning.qgemm_stages = stages;
+  return QC_OK;
+}
+
 int qc_hip_set_int8_gemm_route(int route) {
   if (route < qc::kInt8Auto || route > qc::kInt8Simple) return QC_INVALID_ARGUMENT;
   g_int8_route = route;

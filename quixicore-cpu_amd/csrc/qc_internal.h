@@ -9,6 +9,8 @@ namespace qc {
 
 struct GemvTuning {
   int rows_per_wave = 0;  // GEMV rows per wavefront (1, 2, 4, 7, 8, 14; 0 = from the shape)
+  int qgemm_waves = 0;    // small-batch GEMM waves per workgroup (4, 8; 0 = from the shape)
+  int qgemm_stages = 0;   // small-batch GEMM K stages per workgroup (1..16; 0 = from the shape)
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
@@ -19,9 +21,11 @@ hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long l
 hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s);
 
-// Small-batch GEMM on bf16 MFMA (m >= 2, K % 64 == 0, W 4-byte aligned).
+// Small-batch GEMM on MFMA (m >= 2, K % 64 == 0, W 4-byte aligned): int8
+// digit planes for up to 8 rows per pass, bf16 hi/lo above.  waves / stages:
+// plan override (0 = from the shape).
 hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
-                             int k, hipStream_t s);
+                             int k, hipStream_t s, int waves = 0, int stages = 0);
 
 // Per-group symmetric int8 quantization.  status == nullptr: caller has
 // already verified that x is finite.  Otherwise non-finite groups are left

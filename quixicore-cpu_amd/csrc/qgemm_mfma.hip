@@ -691,11 +691,17 @@ Plan plan_for(int n, int nstages, int cus) {
 }
 
 template <int FMT, int XL>
-hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, hipStream_t s) {
+hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, hipStream_t s,
+               int waves, int stages) {
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
-  const Plan plan = plan_for<FMT>(n, nstages, device_cus());
+  Plan plan = plan_for<FMT>(n, nstages, device_cus());
+  if (waves) plan.nw = waves;                      // test / tuning overrides
+  if (stages) {
+    plan.nst = stages;
+    plan.ks = (nstages + stages - 1) / stages;
+  }
   const int nslabs = (n + 16 * plan.nw - 1) / (16 * plan.nw);
   const int ks = plan.ks;
   using XB = XBlock<XL, FMT == kQ4_0>;
@@ -733,7 +739,7 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
 }  // namespace
 
 hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
-                             int k, hipStream_t s) {
+                             int k, hipStream_t s, int waves, int stages) {
   const auto* w = static_cast<const uint8_t*>(W);
   for (int m0 = 0; m0 < m; m0 += 32) {
     const int mt = m - m0 < 32 ? m - m0 : 32;
@@ -742,13 +748,13 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
     // activation layout: compact rows for M <= 4 / 8, dense 16-row tiles above
     hipError_t e;
     if (fmt == kQ8_0)
-      e = mt <= 4 ? run<kQ8_0, 4>(w, xm, ym, mt, n, k, s)
-        : mt <= 8 ? run<kQ8_0, 8>(w, xm, ym, mt, n, k, s)
-        : mt <= 16 ? run<kQ8_0, 16>(w, xm, ym, mt, n, k, s) : run<kQ8_0, 32>(w, xm, ym, mt, n, k, s);
+      e = mt <= 4 ? run<kQ8_0, 4>(w, xm, ym, mt, n, k, s, waves, stages)
+        : mt <= 8 ? run<kQ8_0, 8>(w, xm, ym, mt, n, k, s, waves, stages)
+        : mt <= 16 ? run<kQ8_0, 16>(w, xm, ym, mt, n, k, s, waves, stages) : run<kQ8_0, 32>(w, xm, ym, mt, n, k, s, waves, stages);
     else
-      e = mt <= 4 ? run<kQ4_0, 4>(w, xm, ym, mt, n, k, s)
-        : mt <= 8 ? run<kQ4_0, 8>(w, xm, ym, mt, n, k, s)
-        : mt <= 16 ? run<kQ4_0, 16>(w, xm, ym, mt, n, k, s) : run<kQ4_0, 32>(w, xm, ym, mt, n, k, s);
+      e = mt <= 4 ? run<kQ4_0, 4>(w, xm, ym, mt, n, k, s, waves, stages)
+        : mt <= 8 ? run<kQ4_0, 8>(w, xm, ym, mt, n, k, s, waves, stages)
+        : mt <= 16 ? run<kQ4_0, 16>(w, xm, ym, mt, n, k, s, waves, stages) : run<kQ4_0, 32>(w, xm, ym, mt, n, k, s, waves, stages);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -47,6 +47,7 @@ _SIGS = {
     "qc_hip_int8_gemm_variant": ([], ctypes.c_char_p),
     "qc_hip_set_gemv_rows_per_wave": ([_I], _I),
     "qc_hip_set_int8_gemm_route": ([_I], _I),
+    "qc_hip_set_qgemm_plan": ([_I, _I], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -187,6 +188,12 @@ def int8_gemm_i32(w, x):
 
 def set_gemv_rows_per_wave(rows):
     _check(lib.qc_hip_set_gemv_rows_per_wave(rows), "set_gemv_rows_per_wave")
+
+
+def set_qgemm_plan(waves=0, stages=0):
+    """Small-batch GEMM work split: waves per workgroup (4/8) and K stages
+    per workgroup (1/2/4/8/16); 0 = from the shape."""
+    _check(lib.qc_hip_set_qgemm_plan(waves, stages), "set_qgemm_plan")
 
 
 def set_int8_gemm_route(route):

@@ -135,6 +135,29 @@ def test_qgemm_mfma_shapes(qc, oracle, synth, dev, fmt, m, n, k):
     assert np.array_equal(Y2.cpu().numpy().view(np.uint32), Y.view(np.uint32))  # deterministic
 
 
+@pytest.mark.parametrize("fmt,m", [(0, 3), (1, 7), (1, 12), (0, 20)])
+def test_qgemm_every_plan(qc, oracle, synth, dev, fmt, m):
+    """Every forced work split (4/8 waves, 1..16 K stages per workgroup, i.e.
+    one K range, two atomically added ranges, or partial sums reduced in
+    index order) stays within the contract; the digit (m <= 8) and bf16
+    activation layouts both."""
+    import torch
+    n, k = 300, 2304                      # 9 stages: ragged K splits
+    packed, _ = _case(oracle, synth, fmt, n, k, 91 + m)
+    x = synth.normal_fast(950 + m, m * k).reshape(m, k)
+    P, X = torch.from_numpy(packed).to(dev), torch.from_numpy(x).to(dev)
+    try:
+        for waves in (4, 8):
+            for stages in (1, 2, 4, 8, 16):
+                print(f"qgemm plan fmt={fmt} m={m} waves={waves} stages={stages}", flush=True)
+                qc.set_qgemm_plan(waves, stages)
+                Y = qc.qgemm(fmt, P, X, n, k).cpu().numpy()
+                for r in (0, m - 1):
+                    _check_rows(oracle, fmt, packed, x[r], Y[r], n, k)
+    finally:
+        qc.set_qgemm_plan(0, 0)
+
+
 @pytest.mark.parametrize("m,n", [(4, 4096), (32, 14336)])
 def test_qgemm_baseline_config2(qc, oracle, synth, dev, m, n):
     """BASELINE config 2 (q8_0, K=4096) at two of its corners."""
