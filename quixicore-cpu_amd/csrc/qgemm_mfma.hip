@@ -156,6 +156,12 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The two helpers below load M0 (the LDS base of global_load_lds) and list it
+// as clobbered; clang warns for any clobber of M0 as a reserved register,
+// which is the intent here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+
 // global_load_lds_dwordx4 from a wave-uniform base (scalar registers) plus a
 // per-lane byte offset, to LDS byte lds + 16 * lane (lds wave-uniform, in
 // M0).  Written as inline assembly so the compiler, which cannot see that
@@ -184,6 +190,7 @@ __device__ __forceinline__ void dma16_addr(const void* addr, const void* lds) {
       : "v"(addr), "s"(m0)
       : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Activation fragments: one 64-thread workgroup per (block b, m-tile t).
 // Lane l covers row 16t + (l & 15), codes 8(l >> 4) .. +7 of the block.
