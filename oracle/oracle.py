@@ -50,6 +50,7 @@ def _load():
     lib.qco_q4_0_gemv_avx2order.restype = None
     lib.qco_qgemv_f64.argtypes = [ctypes.c_int, _P, _P, _P, _P, _LL, _LL]
     lib.qco_quantize_int8.argtypes = [_P, _P, _P, _LL, _LL, _LL]
+    lib.qco_qgemv_w8a8.argtypes = [ctypes.c_int, _P, _P, _P, _LL, _LL]
     lib.qco_int8_gemm.argtypes = [_P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, ctypes.c_int]
     lib.qco_int8_gemm_entries.argtypes = [_P, _P, _P, _P, _P, _P, _LL, _LL, _P, _P]
     lib.qco_int8_gemm_entries.restype = None
@@ -143,6 +144,27 @@ def quantize_int8(x: np.ndarray, group_size=0):
     return st, codes, scales
 
 
+def gemv_w8a8(fmt, packed, x, n, k):
+    """qgemv_w8a8: per-32-block int8 activations, integer block dots,
+    y = sum_b (float(dot) * d_w) * d_x in block order.  Returns (status, y)."""
+    x = None if x is None else np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros(max(n, 0), dtype=np.float32)
+    st = lib.qco_qgemv_w8a8(fmt, _ptr(packed), _ptr(x), _ptr(y), n, k)
+    return st, y
+
+
+def gemv_w8a8_f64(fmt, packed, x, n, k):
+    """The reference test's tight oracle (tests/correctness/test_qgemv_w8a8.cpp:
+    65-98): dequantized weights times dequantized blockwise-int8 activations in
+    f64."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    st, codes, scales = quantize_int8(x.reshape(1, k), 32)
+    assert st == 0, st
+    xq = codes.reshape(-1, 32).astype(np.float64) * scales.reshape(-1, 1).astype(np.float64)
+    w = unpack(fmt, packed, n, k).astype(np.float64)
+    return w @ xq.reshape(k)
+
+
 def int8_gemm(w, x, ws, as_, row_sum=None, zp=None, asymmetric=False):
     m, k = x.shape
     n = w.shape[0]
@@ -189,6 +211,9 @@ class Reference:
         L.qcref_quantize_int8.argtypes = [_P, _P, _P, _LL, _LL, _LL]
         L.qcref_int8_gemm.argtypes = [_P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, ctypes.c_int]
         L.qcref_int8_gemm_variant.restype = ctypes.c_char_p
+        for name in ("qcref_q4_0_gemv_w8a8", "qcref_q8_0_gemv_w8a8"):
+            getattr(L, name).argtypes = [_P, _P, _P, _LL, _LL]
+            getattr(L, name).restype = None
         L.qcref_set_num_threads.argtypes = [ctypes.c_int]
         L.qcref_set_num_threads.restype = None
 
@@ -238,6 +263,13 @@ class Reference:
         st = self.lib.qcref_int8_gemm(_ptr(w), _ptr(x), _ptr(ws), _ptr(as_), _ptr(row_sum),
                                       _ptr(zp), _ptr(y), m, n, k, int(asymmetric))
         return st, y
+
+    def gemv_w8a8(self, fmt, packed, x, n, k):
+        y = np.empty(n, dtype=np.float32)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        fn = self.lib.qcref_q8_0_gemv_w8a8 if fmt == Q8_0 else self.lib.qcref_q4_0_gemv_w8a8
+        fn(_ptr(packed), _ptr(x), _ptr(y), n, k)
+        return y
 
     def variant(self):
         return self.lib.qcref_int8_gemm_variant().decode()

@@ -11,6 +11,7 @@
 #include <limits.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ---------------------------------------------------------------- fp16 --- */
@@ -339,6 +340,73 @@ int qco_quantize_int8(const float* x, int8_t* codes, float* scales, long long ro
       }
     }
   }
+  return QCO_OK;
+}
+
+/* ------------------------------------------------------- qgemv_w8a8 --- */
+
+/* Per-32-block int8 activations: kernels/quantization/qgemv_w8a8_ref.cpp:18-41
+ * (max = fmax(max, |x|), scale = max / 127, inverse = scale != 0 ? 1/scale
+ * : 0, code = clamp(nearbyint(x * inverse), -127, 127)); x is finite here. */
+static void quantize_blocks32(const float* x, long long k, int8_t* qx, float* dx) {
+  for (long long b = 0; b < k / 32; ++b) {
+    const float* in = x + b * 32;
+    float maximum = 0.0f;
+    for (int e = 0; e < 32; ++e) maximum = fmaxf(maximum, fabsf(in[e]));
+    const float scale = maximum / 127.0f;
+    const float inverse = scale != 0.0f ? 1.0f / scale : 0.0f;
+    dx[b] = scale;
+    for (int e = 0; e < 32; ++e) {
+      const float v = nearbyintf(in[e] * inverse);
+      qx[b * 32 + e] = (int8_t)(v < -127.0f ? -127.0f : (v > 127.0f ? 127.0f : v));
+    }
+  }
+}
+
+/* qgemv_w8a8: validation src/dispatch/qgemv_w8a8.cpp:99-105,130-143 (format,
+ * then shape, then nulls, then a non-finite x); rows
+ * kernels/quantization/qgemv_w8a8_ref.cpp:120-145 (q4_0: integer dot of
+ * (nibble - 8) with the codes, low nibbles against elements 0..15 and high
+ * against 16..31) and 147-177 (q8_0).  Per row, in block order:
+ * sum = sum + (float(dot) * d_w) * d_x. */
+int qco_qgemv_w8a8(int format, const void* packed, const float* x, float* y, long long n,
+                   long long k) {
+  const int status = validate_shape(format, n, k);
+  if (status != QCO_OK) return status;
+  if (packed == NULL || x == NULL || y == NULL) return QCO_INVALID_ARGUMENT;
+  for (long long e = 0; e < k; ++e)
+    if (!isfinite(x[e])) return QCO_INVALID_ARGUMENT;
+  const long long nb = k / 32;
+  int8_t* qx = (int8_t*)malloc((size_t)k);
+  float* dx = (float*)malloc((size_t)nb * sizeof(float));
+  if (qx == NULL || dx == NULL) {
+    free(qx);
+    free(dx);
+    return QCO_OUT_OF_MEMORY;
+  }
+  quantize_blocks32(x, k, qx, dx);
+  const uint8_t* p = (const uint8_t*)packed;
+  const int bb = block_bytes_of(format);
+  for (long long r = 0; r < n; ++r) {
+    float sum = 0.0f;
+    for (long long b = 0; b < nb; ++b) {
+      const uint8_t* blk = p + (r * nb + b) * bb;
+      const int8_t* in = qx + b * 32;
+      int dot = 0;
+      if (format == QCO_Q4_0) {
+        for (int j = 0; j < 16; ++j) {
+          dot += ((blk[2 + j] & 0x0F) - 8) * in[j];
+          dot += ((blk[2 + j] >> 4) - 8) * in[j + 16];
+        }
+      } else {
+        for (int e = 0; e < 32; ++e) dot += (int)(int8_t)blk[2 + e] * in[e];
+      }
+      sum += (float)dot * block_scale(blk) * dx[b];
+    }
+    y[r] = sum;
+  }
+  free(qx);
+  free(dx);
   return QCO_OK;
 }
 

@@ -57,6 +57,11 @@ int qco_qgemv_f64(int format, const void* packed, const float* x, double* y64,
 int qco_quantize_int8(const float* x, int8_t* codes, float* scales, long long rows,
                       long long dim, long long group_size);
 
+/* Activation-quantizing GEMV: x quantized per 32-element block to int8, integer
+ * block dots, y[r] = sum_b (float(dot) * d_w) * d_x in block order. */
+int qco_qgemv_w8a8(int format, const void* packed, const float* x, float* y, long long n,
+                   long long k);
+
 int qco_int8_gemm(const int8_t* w, const int8_t* x, const float* ws, const float* as,
                   const int32_t* row_sum, const int* zp, float* y, long long m,
                   long long n, long long k, int asymmetric);

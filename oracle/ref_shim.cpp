@@ -9,6 +9,7 @@
 //   qgemm       -> one qgemv per row        (kernels/quantization/qgemm_ref.cpp:156-162)
 //   int8_gemm   -> the public dispatcher    (src/dispatch/int8_gemm.cpp:67-94)
 //   quantize_int8 -> the public function    (kernels/quantization/quantization_ref.cpp:143-168)
+//   qgemv_w8a8  -> quant::q{4,8}_0_gemv_w8a8_ref (src/dispatch/qgemv_w8a8.cpp:27-34,66-73)
 #include <cstddef>
 #include <cstdint>
 
@@ -67,6 +68,18 @@ int qcref_int8_gemm(const std::int8_t* w, const std::int8_t* x, const float* ws,
                     long long m, long long n, long long k, int asymmetric) {
   return static_cast<int>(
       qc::int8_gemm(w, x, ws, as, row_sum, zp, y, m, n, k, asymmetric != 0));
+}
+
+// qgemv_w8a8 -> the x86 variant the dispatcher resolves, the portable ref
+// (src/dispatch/qgemv_w8a8.cpp:27-34,66-73; the dotprod variants are aarch64).
+void qcref_q4_0_gemv_w8a8(const void* packed, const float* x, float* y, long long n,
+                          long long k) {
+  qc::quant::q4_0_gemv_w8a8_ref(static_cast<const qc::quant::BlockQ4_0*>(packed), x, y, n, k);
+}
+
+void qcref_q8_0_gemv_w8a8(const void* packed, const float* x, float* y, long long n,
+                          long long k) {
+  qc::quant::q8_0_gemv_w8a8_ref(static_cast<const qc::quant::BlockQ8_0*>(packed), x, y, n, k);
 }
 
 const char* qcref_int8_gemm_variant() { return qc::int8_gemm_variant(); }

@@ -16,6 +16,13 @@ mistake would break:
   * f64 contract     -- against numpy float64 matmul of the unpacked weights.
   * quantize_int8    -- bit-identical to the reference's quantize_int8 and its
                         known answer (test_quantization.cpp:100-111).
+  * qgemv_w8a8       -- bit-identical to the reference's q4_0/q8_0
+                        gemv_w8a8_ref (oracle/_ref); the reference test's own
+                        xorshift case within its tight f64 oracle
+                        (test_qgemv_w8a8.cpp:57-116); a numpy float32
+                        restatement of the per-block order; the codes equal
+                        quantize_int8 with 32-element groups; validation order
+                        (test_qgemv_w8a8.cpp:126-134).
   * int8 GEMM        -- bit-identical to the reference's dispatched int8_gemm
                         over its own test grid (test_int8_gemm.cpp:106-116),
                         numpy int64 matmul, and the known answers
@@ -181,6 +188,88 @@ def test_reference_rng_shapes(oracle):
     y = oracle.gemv(1, p, x, n, k)
     y64, _ = oracle.gemv_f64(1, p, x, n, k)
     assert np.all(np.abs(y - y64) <= 1e-5 + 1e-4 * np.abs(y64))
+
+
+# ------------------------------------------------------------ qgemv_w8a8 ---
+
+def _w8a8_cases():
+    rng = np.random.default_rng(21)
+    for fmt in (0, 1):
+        for n, k in ((1, 32), (17, 256), (40, 4096), (3, 14336)):
+            w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+            x = rng.standard_normal(k).astype(np.float32)
+            if k >= 64:
+                x[:32] = 0.0                                       # all-zero block
+                x[32:64] = (np.arange(32, dtype=np.float32) - 16) * np.float32(0.5)   # ties
+            if k >= 128:
+                x[64:96] *= np.float32(1e-30)                       # tiny block
+                x[96:128] *= np.float32(1e20)                       # huge block
+            yield fmt, n, k, w, x
+
+
+def test_gemv_w8a8_matches_reference(oracle, ref):
+    for fmt, n, k, w, x in _w8a8_cases():
+        st, p = oracle.pack(fmt, w)
+        assert st == 0
+        st, got = oracle.gemv_w8a8(fmt, p, x, n, k)
+        assert st == 0
+        want = ref.gemv_w8a8(fmt, p, x, n, k)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (fmt, n, k)
+
+
+def test_gemv_w8a8_numpy_restatement(oracle):
+    """Independent float32 restatement: codes from quantize_int8 with 32-element
+    groups, exact integer block dots, then sum = sum + (dot * d_w) * d_x in
+    block order."""
+    for fmt, n, k, w, x in _w8a8_cases():
+        if k > 4096:
+            continue
+        _, p = oracle.pack(fmt, w)
+        st, codes, scales = oracle.quantize_int8(x.reshape(1, k), 32)
+        assert st == 0
+        nb = k // 32
+        blocks = p.reshape(n, nb, oracle.BLOCK_BYTES[fmt])
+        d = blocks[:, :, 0:2].copy().view(np.float16).astype(np.float32).reshape(n, nb)
+        if fmt == 0:
+            q = blocks[:, :, 2:].view(np.int8).astype(np.int64)
+        else:
+            nib = blocks[:, :, 2:].astype(np.int64)
+            q = np.concatenate([(nib & 15) - 8, (nib >> 4) - 8], axis=2)
+        dots = np.einsum("nbj,bj->nb", q, codes.reshape(nb, 32).astype(np.int64))
+        y = np.zeros(n, dtype=np.float32)
+        for b in range(nb):
+            y = y + (dots[:, b].astype(np.float32) * d[:, b]) * scales[0, b]
+        st, got = oracle.gemv_w8a8(fmt, p, x, n, k)
+        assert np.array_equal(got.view(np.uint32), y.view(np.uint32)), (fmt, n, k)
+
+
+def test_gemv_w8a8_reference_test_case(oracle):
+    """tests/correctness/test_qgemv_w8a8.cpp:57-116: Rng(1234) weights then x,
+    n=96, k=256, within atol 1e-4 + rtol 1e-4 of the dequantized f64 oracle."""
+    n, k = 96, 256
+    vals = xorshift32_unit(1234, n * k + k)
+    w, x = vals[: n * k].reshape(n, k), vals[n * k:]
+    for fmt in (1, 0):
+        _, p = oracle.pack(fmt, w)
+        st, y = oracle.gemv_w8a8(fmt, p, x, n, k)
+        assert st == 0
+        ref64 = oracle.gemv_w8a8_f64(fmt, p, x, n, k)
+        assert np.all(np.abs(y.astype(np.float64) - ref64) <= 1e-4 + 1e-4 * np.abs(ref64))
+
+
+def test_gemv_w8a8_validation(oracle):
+    """Status order of src/dispatch/qgemv_w8a8.cpp:99-105,130-143 and the
+    reference test's cases (test_qgemv_w8a8.cpp:126-134)."""
+    n, k = 96, 256
+    vals = xorshift32_unit(1234, n * k + k)
+    w, x = vals[: n * k].reshape(n, k), vals[n * k:].copy()
+    _, p = oracle.pack(1, w)
+    assert oracle.gemv_w8a8(1, p, x, n, k + 1)[0] == 1
+    assert oracle.gemv_w8a8(1, None, x, n, k)[0] == 3
+    assert oracle.gemv_w8a8(7, p, x, n, k)[0] == 2
+    assert oracle.gemv_w8a8(7, p, x, n, k + 1)[0] == 2      # format before shape
+    x[7] = np.nan
+    assert oracle.gemv_w8a8(1, p, x, n, k)[0] == 3
 
 
 # --------------------------------------------------------- quantize_int8 ---
