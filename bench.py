@@ -130,6 +130,35 @@ def gemv_case(qc, fmt, n, k, steps, warmup, seed):
             "kernel_gbs": alg / (gpu * 1e-3) / 1e9}, packs[0], x, y
 
 
+def gemv_w8a8_case(qc, fmt, n, k, steps, warmup, seed):
+    """qgemv_w8a8 (per-block int8 activations) on rotated weight copies; the
+    asynchronous form (device status word), as a decode loop would call it."""
+    import torch
+    dev = torch.device("cuda:0")
+    wbytes = n * (k // 32) * qc.BLOCK_BYTES[fmt]
+    copies = rotation(wbytes)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    packs = []
+    for c in range(copies):
+        w = torch.randn((n, k), generator=g, device=dev) * 0.02
+        packs.append(qc.pack(fmt, w))
+        del w
+    x = torch.randn(k, generator=g, device=dev)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def launch(i):
+        st = qc.qgemv_w8a8_raw(fmt, packs[i % copies], x, y, n, k, status)
+        if st:
+            raise RuntimeError(f"qgemv_w8a8 status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    alg = wbytes + 4 * k + 4 * n
+    return {"bytes": alg, "weight_bytes": wbytes, "copies": copies, "wall_ms": wall,
+            "gpu_ms": gpu, "gbs": alg / (wall * 1e-3) / 1e9,
+            "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
+
+
 def qgemm_case(qc, n, k, m, steps, warmup, seed, fmt=0):
     import torch
     dev = torch.device("cuda:0")
@@ -356,6 +385,8 @@ def main():
         s["q8_0_gemv_k4096_n4096"] = r
         r, *_ = gemv_case(qc, 1, 4096, 14336, K, W, seed=3)
         s["q4_0_gemv_k14336_n4096"] = r
+        s["q4_0_gemv_w8a8_k4096_n14336"] = gemv_w8a8_case(qc, 1, 14336, 4096, K, W, seed=11)
+        s["q8_0_gemv_w8a8_k4096_n4096"] = gemv_w8a8_case(qc, 0, 4096, 4096, K, W, seed=12)
         for m in (4, 8, 16, 32):
             s[f"q8_0_qgemm_m{m}_k4096_n14336"] = qgemm_case(qc, 14336, 4096, m, K, W, seed=4 + m)
         s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)

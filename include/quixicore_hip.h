@@ -80,6 +80,27 @@ int qc_hip_qgemv(int format, const void* packed, const float* x, float* y, long 
 int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long long m,
                  long long n, long long k, void* stream);
 
+/* Activation-quantizing GEMV: x is quantized per 32-element block to int8
+ * (scale = max|x_b| / 127, round half to even, clamp +-127), each block dot is
+ * an exact integer sum, and y[r] = sum_b (float(dot) * d_w) * d_x in block
+ * order -- bit-identical to the reference.  Replaces qgemv_w8a8
+ * (include/quixicore_cpu/qgemv_w8a8.h:16; src/dispatch/qgemv_w8a8.cpp:130-153;
+ * kernels/quantization/qgemv_w8a8_ref.cpp:18-41,120-177).  dev_status NULL:
+ * a non-finite x returns 3 before any work (the call blocks).  Otherwise the
+ * call is asynchronous, *dev_status is set to 3 and the affected outputs are
+ * NaN. */
+int qc_hip_qgemv_w8a8(int format, const void* packed, const float* x, float* y, long long n,
+                      long long k, int* dev_status, void* stream);
+
+/* Packed weight bytes for qgemv_w8a8 (the qgemv q8_0 / q4_0 layouts).
+ * Replaces qgemv_w8a8_packed_size (include/quixicore_cpu/qgemv_w8a8.h:23;
+ * src/dispatch/qgemv_w8a8.cpp:108-125). */
+int qc_hip_qgemv_w8a8_packed_size(int format, long long n, long long k, long long* bytes);
+
+/* Name of the route qgemv_w8a8 takes for a format.  Replaces
+ * qgemv_w8a8_variant (include/quixicore_cpu/qgemv_w8a8.h:29). */
+const char* qc_hip_qgemv_w8a8_variant(int format);
+
 /* Per-group symmetric int8 quantization; group_size 0 means one group per
  * row.  Bit-identical codes and scales.  Replaces quantize_int8
  * (include/quixicore_cpu/quantization.h:42;

@@ -260,6 +260,45 @@ int qc_hip_set_gemv_rows_per_wave(int rows) {
   return QC_OK;
 }
 
+// src/dispatch/qgemv_w8a8.cpp:108-125 (qgemv_w8a8_packed_size).
+int qc_hip_qgemv_w8a8_packed_size(int format, long long n, long long k, long long* bytes) {
+  size_t size = 0;
+  const int st = qc_hip_qgemv_packed_size(format, n, k, &size);
+  if (st != QC_OK) return st;
+  if (bytes == nullptr) return QC_INVALID_ARGUMENT;
+  if (size > static_cast<size_t>(LLONG_MAX)) return QC_INVALID_SHAPE;
+  *bytes = static_cast<long long>(size);
+  return QC_OK;
+}
+
+// src/dispatch/qgemv_w8a8.cpp:130-153: format and shape (99-105), nulls, then a
+// non-finite x, all before any work.
+int qc_hip_qgemv_w8a8(int format, const void* packed, const float* x, float* y, long long n,
+                      long long k, int* dev_status, void* stream) {
+  const int st = validate(format, n, k);
+  if (st != QC_OK) return st;
+  size_t ignored = 0;
+  if (packed_bytes(format, n, k, &ignored) != QC_OK) return QC_INVALID_SHAPE;
+  if (packed == nullptr || x == nullptr || y == nullptr) return QC_INVALID_ARGUMENT;
+  const hipStream_t s = as_stream(stream);
+  if (dev_status != nullptr)
+    return finish(qc::launch_qgemv_w8a8(format, packed, x, y, n, k, g_tuning.rows_per_wave,
+                                        dev_status, s));
+  bool finite = false;
+  const int fst = all_finite(x, k, s, &finite);
+  if (fst != QC_OK) return fst;
+  if (!finite) return QC_INVALID_ARGUMENT;
+  hipError_t e = qc::launch_qgemv_w8a8(format, packed, x, y, n, k, g_tuning.rows_per_wave,
+                                       nullptr, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return finish(e);
+}
+
+const char* qc_hip_qgemv_w8a8_variant(int format) {
+  if (block_bytes(format) == 0) return "unsupported";
+  return format == QC_Q8_0 ? "hip_gfx950_w8a8_q8_0" : "hip_gfx950_w8a8_q4_0";
+}
+
 int qc_hip_set_qgemm_plan(int waves, int stages) {
   if (waves != 0 && waves != 4 && waves != 8) return QC_INVALID_ARGUMENT;
   if (stages != 0 && stages != 1 && stages != 2 && stages != 4 && stages != 8 && stages != 16)

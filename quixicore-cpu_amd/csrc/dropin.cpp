@@ -14,6 +14,7 @@
 
 #include "quixicore_cpu/qgemm.h"
 #include "quixicore_cpu/qgemv.h"
+#include "quixicore_cpu/qgemv_w8a8.h"
 #include "quixicore_cpu/quantization.h"
 #include "quixicore_hip.h"
 #include "qc_dropin.h"
@@ -160,6 +161,33 @@ Status qgemv(QuantFormat format, const void* packed, const float* x, float* y, l
 }
 
 const char* qgemv_variant(QuantFormat format) { return qc_hip_qgemv_variant(fmt_id(format)); }
+
+Status qgemv_w8a8(QuantFormat format, const void* packed_weights, const float* x, float* y,
+                  long long n, long long k) {
+  const size_t bytes = packed_or_zero(format, n, k);
+  if (bytes == 0 || packed_weights == nullptr || x == nullptr || y == nullptr)
+    return static_cast<Status>(
+        qc_hip_qgemv_w8a8(fmt_id(format), packed_weights, x, y, n, k, nullptr, nullptr));
+  Staging g(nullptr);
+  const void* p = g.in(packed_weights, bytes);
+  const float* xd = static_cast<const float*>(g.in(x, sizeof(float) * k));
+  float* yd = static_cast<float*>(g.out(y, sizeof(float) * n));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(qc_hip_qgemv_w8a8(fmt_id(format), p, xd, yd, n, k, nullptr, g.stream()));
+}
+
+Status qgemv_w8a8_packed_size(QuantFormat format, long long n, long long k, long long* bytes) {
+  return static_cast<Status>(qc_hip_qgemv_w8a8_packed_size(fmt_id(format), n, k, bytes));
+}
+
+Status qgemv_w8a8_pack(QuantFormat format, const float* weights, long long n, long long k,
+                       void* packed) {
+  return qgemv_pack(format, weights, n, k, packed);
+}
+
+const char* qgemv_w8a8_variant(QuantFormat format) {
+  return qc_hip_qgemv_w8a8_variant(fmt_id(format));
+}
 
 Status qgemm(QuantFormat format, const void* packed_weights, const float* x, float* y,
              long long m, long long n, long long k) {

@@ -21,6 +21,12 @@ hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long l
 hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s);
 
+// qgemv_w8a8: x quantized per 32-element block to int8, exact integer block
+// dots, y bit-identical to the reference.  status (optional): set to 3 when x
+// holds a non-finite value (the affected outputs are NaN).
+hipError_t launch_qgemv_w8a8(int fmt, const void* W, const float* x, float* y, long long n,
+                             long long k, int rows_per_wave, int* status, hipStream_t s);
+
 // Small-batch GEMM on MFMA (m >= 2, K % 64 == 0, W 4-byte aligned): int8
 // digit planes for up to 8 rows per pass, bf16 hi/lo above.  waves / stages:
 // plan override (0 = from the shape).

@@ -330,6 +330,255 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const uint8_t* __res
   }
 }
 
+// ------------------------------------------------------------ qgemv_w8a8
+// Activation-quantizing GEMV (src/dispatch/qgemv_w8a8.cpp:130-153;
+// kernels/quantization/qgemv_w8a8_ref.cpp:18-41,120-177).  The workgroup
+// quantizes each 32-element block of x exactly as the reference does
+// (max = fmax(max, |x|), scale = max / 127, inverse = scale != 0 ? 1 / scale
+// : 0, code = clamp(rint(x * inverse), -127, 127)) into LDS; each block dot
+// is an exact int32 sum of v_dot4_i32_i8 (q4_0: nibbles, with the -8 folded
+// in as -8 * the block's code sum); each block's term (float(dot) * d_w) *
+// d_x goes to LDS, and one lane per row adds the terms in block order,
+// sum = sum + term, as the reference's row loop does -- so y is bit-identical
+// to the reference's.  Weights are read with the GEMV's pair-per-lane loads
+// and load window.
+
+constexpr int kW8Rec = 80;   // LDS bytes per pair: 64 codes, then {d_x0, d_x1, s_0, s_1}
+
+// LDS layout of one chunk of kc elements: [kc/64 pair records]
+// [NW waves][RB rows][kc/32 f32 block terms].
+__host__ __device__ constexpr size_t w8_terms_off(int kc) {
+  return static_cast<size_t>(kc / 64) * kW8Rec;
+}
+__host__ __device__ constexpr size_t w8_lds_size(int kc, int nw, int rb) {
+  return w8_terms_off(kc) + static_cast<size_t>(nw) * rb * (kc / 32) * 4;
+}
+
+// Codes, scales and (q4_0) code sums of the loaded half-blocks into LDS; the
+// two halves of a block sit in lanes t and t^1.  A block holding NaN or
+// +-inf gets d_x = NaN (its terms, hence its rows, become NaN) and sets
+// *status = 3.
+template <bool WITH_SUMS, int HPT, int NT>
+__device__ __forceinline__ void build_codes(uint8_t* lds, const float (&xv)[HPT][16], int clen,
+                                            int* status) {
+  const int nh = clen >> 4;
+#pragma unroll
+  for (int j = 0; j < HPT; ++j) {
+    const int h = threadIdx.x + NT * j;
+    if (h >= nh) break;
+    const float* v = xv[j];
+    float m = 0.f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      m = fmaxf(m, fabsf(v[i]));
+      finite = finite && isfinite(v[i]);
+    }
+    m = fmaxf(m, xor1_f32(m));
+    finite = finite && (xor1_i32(finite ? 1 : 0) != 0);
+    const float scale = m / 127.0f;
+    const float inverse = scale != 0.0f ? 1.0f / scale : 0.0f;
+    int c[16];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float r = rintf(v[i] * inverse);
+      r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+      c[i] = finite ? static_cast<int>(r) : 0;
+      sum += c[i];
+    }
+    uint8_t* rec = lds + (h >> 2) * kW8Rec;
+    uint4 q;
+    q.x = pack4(c[0], c[1], c[2], c[3]);    q.y = pack4(c[4], c[5], c[6], c[7]);
+    q.z = pack4(c[8], c[9], c[10], c[11]);  q.w = pack4(c[12], c[13], c[14], c[15]);
+    *reinterpret_cast<uint4*>(rec + (h & 3) * 16) = q;
+    if constexpr (WITH_SUMS) sum += xor1_i32(sum);
+    if ((h & 1) == 0) {
+      const int blk = (h >> 1) & 1;
+      reinterpret_cast<float*>(rec + 64)[blk] = finite ? scale : __builtin_nanf("");
+      if constexpr (WITH_SUMS) reinterpret_cast<int*>(rec + 72)[blk] = sum;
+    }
+    if (!finite && status != nullptr) *status = 3;
+  }
+}
+
+// The two block terms (float(dot) * d_w) * d_x of one pair of one row.
+template <int FMT>
+__device__ __forceinline__ void pair_terms(const uint32_t* w, const uint32_t (&cx)[16],
+                                           const float4& meta, float& t0, float& t1) {
+  int a, b;
+  if constexpr (FMT == kQ8_0) {
+    a = 0;
+    b = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = static_cast<int>(__builtin_amdgcn_alignbyte(w[i + 1], w[i], 2));
+      a = __builtin_amdgcn_sdot4(c, static_cast<int>(cx[i]), a, false);
+      b = __builtin_amdgcn_sdot4(static_cast<int>(w[9 + i]), static_cast<int>(cx[8 + i]), b, false);
+    }
+  } else {
+    a = -8 * __float_as_int(meta.z);
+    b = -8 * __float_as_int(meta.w);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+      a = __builtin_amdgcn_sdot4(static_cast<int>(q & 0x0F0F0F0Fu), static_cast<int>(cx[i]), a, false);
+      a = __builtin_amdgcn_sdot4(static_cast<int>((q >> 4) & 0x0F0F0F0Fu), static_cast<int>(cx[4 + i]), a, false);
+      const uint32_t u = w[5 + i];
+      b = __builtin_amdgcn_sdot4(static_cast<int>(u & 0x0F0F0F0Fu), static_cast<int>(cx[8 + i]), b, false);
+      b = __builtin_amdgcn_sdot4(static_cast<int>((u >> 4) & 0x0F0F0F0Fu), static_cast<int>(cx[12 + i]), b, false);
+    }
+  }
+  const uint32_t d1 = FMT == kQ8_0 ? (w[8] >> 16) : (w[4] >> 16);
+  t0 = (static_cast<float>(a) * half_bits_to_float(w[0] & 0xFFFFu)) * meta.x;
+  t1 = (static_cast<float>(b) * half_bits_to_float(d1)) * meta.y;
+}
+
+template <int FMT, int NW, int RB, int NPM, int WIN, bool VEC>
+__global__ __launch_bounds__(64 * NW) void qgemv_w8a8_kernel(const uint8_t* __restrict__ W,
+                                                             const float* __restrict__ x,
+                                                             float* __restrict__ y, int n, int k,
+                                                             int kc, int* status) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int BB = Fmt<FMT>::block_bytes;
+  constexpr int PD = Fmt<FMT>::pair_dwords;
+  constexpr int T = NPM * RB;
+  constexpr int NT = 64 * NW;
+  constexpr int HPT = (NPM * 256 + NT - 1) / NT;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * NW + wave) * RB;
+  const long long row_bytes = static_cast<long long>(k >> 5) * BB;
+  const uint8_t* wrow[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) wrow[r] = W + min(row0 + r, n - 1) * row_bytes;
+  float* terms = reinterpret_cast<float*>(lds + w8_terms_off(kc)) + wave * RB * (kc >> 5);
+  float total = 0.f;   // lane r < RB: the block-order sum of row row0 + r
+
+  for (int c0 = 0; c0 < k; c0 += kc) {
+    const int clen = min(kc, k - c0);
+    const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
+    const int p0 = first_pair(pbeg, lane);
+    float xv[HPT][16];
+    load_x<HPT, NT, VEC>(xv, x + c0, clen);
+    uint32_t w[T][PD];
+    auto issue = [&](int t) {
+      const int j = t / RB, r = t % RB;
+      const int p = min(p0 + 64 * j, pend - 1);
+      load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
+    };
+#pragma unroll
+    for (int t = 0; t < T && t < WIN; ++t) issue(t);
+    if (c0) lds_barrier();
+    build_codes<FMT == kQ4_0, HPT, NT>(lds, xv, clen, status);
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < NPM; ++j) {
+      const int p = p0 + 64 * j;
+      const uint8_t* rec = lds + (min(p, pend - 1) - pbeg) * kW8Rec;
+      uint32_t cx[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 v = reinterpret_cast<const uint4*>(rec)[i];
+        cx[4 * i] = v.x; cx[4 * i + 1] = v.y; cx[4 * i + 2] = v.z; cx[4 * i + 3] = v.w;
+      }
+      const float4 meta = *reinterpret_cast<const float4*>(rec + 64);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int t = j * RB + r;
+        if (t + WIN < T) issue(t + WIN);
+        if (p < pend) {
+          float t0, t1;
+          pair_terms<FMT>(w[t], cx, meta, t0, t1);
+          *reinterpret_cast<float2*>(terms + r * (kc >> 5) + 2 * (p - pbeg)) = make_float2(t0, t1);
+        }
+      }
+    }
+    // Block-order sum of this chunk's terms (the wave's own LDS writes above
+    // precede these reads in its instruction stream): fully unrolled over
+    // the at most NPM * 128 terms, in groups of 16 behind a uniform guard.
+    if (lane < RB) {
+      const float* tr = terms + lane * (kc >> 5);
+      const int nbc = clen >> 5;                  // even, <= NPM * 128
+#pragma unroll
+      for (int g = 0; g < NPM * 8; ++g) {
+        if (16 * g + 16 <= nbc) {
+          float4 v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = reinterpret_cast<const float4*>(tr + 16 * g)[i];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            total += v[i].x;
+            total += v[i].y;
+            total += v[i].z;
+            total += v[i].w;
+          }
+        } else {
+          for (int b = 16 * g; b < nbc; b += 2) {
+            const float2 v = *reinterpret_cast<const float2*>(tr + b);
+            total += v.x;
+            total += v.y;
+          }
+          break;
+        }
+      }
+    }
+  }
+  if (lane < RB && row0 + lane < n) y[row0 + lane] = total;
+}
+
+// Any K / alignment: one wavefront per row, lanes take blocks lane, lane +
+// 64, ...; lane 0 adds the terms in block order.
+template <int FMT>
+__global__ __launch_bounds__(256) void qgemv_w8a8_generic(const uint8_t* __restrict__ W,
+                                                          const float* __restrict__ x,
+                                                          float* __restrict__ y, long long n,
+                                                          long long k, int* status) {
+  __shared__ float terms[4][64];
+  constexpr int BB = Fmt<FMT>::block_bytes;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long long row = static_cast<long long>(blockIdx.x) * 4 + wave;
+  const bool live = row < n;                       // wave-uniform
+  const long long nb = k / 32;
+  float total = 0.f;
+  for (long long b0 = 0; b0 < nb; b0 += 64) {
+    const long long b = b0 + lane;
+    float t = 0.f;
+    if (live && b < nb) {
+      const float* xb = x + b * 32;
+      float v[32];
+      float m = 0.f;
+      bool finite = true;
+      for (int e = 0; e < 32; ++e) {
+        v[e] = xb[e];
+        m = fmaxf(m, fabsf(v[e]));
+        finite = finite && isfinite(v[e]);
+      }
+      const float scale = m / 127.0f;
+      const float inverse = scale != 0.0f ? 1.0f / scale : 0.0f;
+      const uint8_t* blk = W + (row * nb + b) * BB;
+      int dot = 0;
+      for (int e = 0; e < 32; ++e) {
+        float r = rintf(v[e] * inverse);
+        r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+        const int c = finite ? static_cast<int>(r) : 0;
+        const int q = FMT == kQ8_0 ? static_cast<int>(static_cast<int8_t>(blk[2 + e]))
+                                   : (e < 16 ? (blk[2 + e] & 15) : (blk[2 + e - 16] >> 4)) - 8;
+        dot += q * c;
+      }
+      const float d = half_bits_to_float(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
+      t = (static_cast<float>(dot) * d) * (finite ? scale : __builtin_nanf(""));
+      if (!finite && status != nullptr) *status = 3;
+    }
+    terms[wave][lane] = t;
+    if (lane == 0) {
+      const long long cnt = nb - b0 < 64 ? nb - b0 : 64;
+      for (int i = 0; i < cnt; ++i) total += terms[wave][i];
+    }
+  }
+  if (live && lane == 0) y[row] = total;
+}
+
 // Load window (items in flight beyond the one being computed) by items per
 // wave, T = NPM * RB, as measured on MI355X: enough to cover the load latency
 // while keeping the arrival order close to the compute order.
@@ -339,17 +588,28 @@ constexpr int window() {
   return T >= 8 ? 2 : 1;
 }
 
-template <int FMT, int NW, int RB, int NPM>
-hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, hipStream_t s) {
+// KIND 0: qgemv (f32 activations, exact digit dots); KIND 1: qgemv_w8a8.
+template <int KIND, int FMT, int NW, int RB, int NPM>
+hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, int* status,
+                      hipStream_t s) {
   // weights held per lane: at most RB * NPM * pair dwords (<= 144 VGPRs)
   static_assert(RB * NPM * Fmt<FMT>::pair_dwords <= 144, "register budget");
   constexpr int WIN = window<FMT, NPM * RB>();
   const int kc = NPM * 4096 < k ? NPM * 4096 : k;
   const int grid = (n + NW * RB - 1) / (NW * RB);
-  if (reinterpret_cast<uintptr_t>(x) % 16 == 0)
-    qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
-  else
-    qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, false><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
+  const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  if constexpr (KIND == 0) {
+    if (vec)
+      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
+    else
+      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, false><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
+  } else {
+    const size_t lds = w8_lds_size(kc, NW, RB);
+    if (vec)
+      qgemv_w8a8_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds, s>>>(W, x, y, n, k, kc, status);
+    else
+      qgemv_w8a8_kernel<FMT, NW, RB, NPM, WIN, false><<<grid, 64 * NW, lds, s>>>(W, x, y, n, k, kc, status);
+  }
   return hipGetLastError();
 }
 
@@ -403,70 +663,70 @@ Shape pick_shape(int n, const int* cand, int ncand, int forced_rb) {
   return best;
 }
 
-template <int FMT, int NW, int NPM>
+template <int KIND, int FMT, int NW, int NPM>
 hipError_t launch_rb(int rb, const uint8_t* W, const float* x, float* y, int n, int k,
-                     hipStream_t s) {
+                     int* status, hipStream_t s) {
   if constexpr (NPM == 1) {
     switch (rb) {
-      case 1: return launch_one<FMT, NW, 1, 1>(W, x, y, n, k, s);
-      case 2: return launch_one<FMT, NW, 2, 1>(W, x, y, n, k, s);
-      case 4: return launch_one<FMT, NW, 4, 1>(W, x, y, n, k, s);
-      case 7: return launch_one<FMT, NW, 7, 1>(W, x, y, n, k, s);
-      case 8: return launch_one<FMT, NW, 8, 1>(W, x, y, n, k, s);
+      case 1: return launch_one<KIND, FMT, NW, 1, 1>(W, x, y, n, k, status, s);
+      case 2: return launch_one<KIND, FMT, NW, 2, 1>(W, x, y, n, k, status, s);
+      case 4: return launch_one<KIND, FMT, NW, 4, 1>(W, x, y, n, k, status, s);
+      case 7: return launch_one<KIND, FMT, NW, 7, 1>(W, x, y, n, k, status, s);
+      case 8: return launch_one<KIND, FMT, NW, 8, 1>(W, x, y, n, k, status, s);
       default:
-        if constexpr (FMT == kQ4_0) return launch_one<FMT, NW, 14, 1>(W, x, y, n, k, s);
-        return launch_one<FMT, NW, 8, 1>(W, x, y, n, k, s);
+        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 14, 1>(W, x, y, n, k, status, s);
+        return launch_one<KIND, FMT, NW, 8, 1>(W, x, y, n, k, status, s);
     }
   } else if constexpr (NPM == 2) {
     switch (rb) {
-      case 1: return launch_one<FMT, NW, 1, 2>(W, x, y, n, k, s);
-      case 2: return launch_one<FMT, NW, 2, 2>(W, x, y, n, k, s);
-      case 4: return launch_one<FMT, NW, 4, 2>(W, x, y, n, k, s);
+      case 1: return launch_one<KIND, FMT, NW, 1, 2>(W, x, y, n, k, status, s);
+      case 2: return launch_one<KIND, FMT, NW, 2, 2>(W, x, y, n, k, status, s);
+      case 4: return launch_one<KIND, FMT, NW, 4, 2>(W, x, y, n, k, status, s);
       default:
-        if constexpr (FMT == kQ4_0) return launch_one<FMT, NW, 7, 2>(W, x, y, n, k, s);
-        return launch_one<FMT, NW, 4, 2>(W, x, y, n, k, s);
+        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 7, 2>(W, x, y, n, k, status, s);
+        return launch_one<KIND, FMT, NW, 4, 2>(W, x, y, n, k, status, s);
     }
   } else {
     switch (rb) {
-      case 1: return launch_one<FMT, NW, 1, 4>(W, x, y, n, k, s);
-      case 2: return launch_one<FMT, NW, 2, 4>(W, x, y, n, k, s);
+      case 1: return launch_one<KIND, FMT, NW, 1, 4>(W, x, y, n, k, status, s);
+      case 2: return launch_one<KIND, FMT, NW, 2, 4>(W, x, y, n, k, status, s);
       default:
-        if constexpr (FMT == kQ4_0) return launch_one<FMT, NW, 4, 4>(W, x, y, n, k, s);
-        return launch_one<FMT, NW, 2, 4>(W, x, y, n, k, s);
+        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 4, 4>(W, x, y, n, k, status, s);
+        return launch_one<KIND, FMT, NW, 2, 4>(W, x, y, n, k, status, s);
     }
   }
 }
 
-template <int FMT, int NPM>
+template <int KIND, int FMT, int NPM>
 hipError_t launch_npm(const int* cand, int ncand, const uint8_t* W, const float* x, float* y,
-                      int n, int k, int rb, hipStream_t s) {
+                      int n, int k, int rb, int* status, hipStream_t s) {
   bool listed = false;
   for (int i = 0; i < ncand; ++i) listed = listed || cand[i] == rb;
   const Shape sh = pick_shape(n, cand, ncand, listed ? rb : 0);
-  return sh.nw == 8 ? launch_rb<FMT, 8, NPM>(sh.rb, W, x, y, n, k, s)
-                    : launch_rb<FMT, 4, NPM>(sh.rb, W, x, y, n, k, s);
+  return sh.nw == 8 ? launch_rb<KIND, FMT, 8, NPM>(sh.rb, W, x, y, n, k, status, s)
+                    : launch_rb<KIND, FMT, 4, NPM>(sh.rb, W, x, y, n, k, status, s);
 }
 
-template <int FMT>
+template <int KIND, int FMT>
 hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, int rb,
-                      hipStream_t s) {
+                      int* status, hipStream_t s) {
   const int npairs = k >> 6;
   if (npairs <= 64) {
     static const int q4c[] = {14, 7, 8, 4, 2, 1};
     static const int q8c[] = {8, 7, 4, 2, 1};
-    return FMT == kQ4_0 ? launch_npm<FMT, 1>(q4c, 6, W, x, y, n, k, rb, s)
-                        : launch_npm<FMT, 1>(q8c, 5, W, x, y, n, k, rb, s);
+    return FMT == kQ4_0 ? launch_npm<KIND, FMT, 1>(q4c, 6, W, x, y, n, k, rb, status, s)
+                        : launch_npm<KIND, FMT, 1>(q8c, 5, W, x, y, n, k, rb, status, s);
   }
   if (npairs <= 128) {
     static const int q4c[] = {7, 4, 2, 1};
     static const int q8c[] = {4, 2, 1};
-    return FMT == kQ4_0 ? launch_npm<FMT, 2>(q4c, 4, W, x, y, n, k, rb, s)
-                        : launch_npm<FMT, 2>(q8c, 3, W, x, y, n, k, rb, s);
+    return FMT == kQ4_0 ? launch_npm<KIND, FMT, 2>(q4c, 4, W, x, y, n, k, rb, status, s)
+                        : launch_npm<KIND, FMT, 2>(q8c, 3, W, x, y, n, k, rb, status, s);
   }
   static const int q4c[] = {4, 2, 1};
   static const int q8c[] = {2, 1};
-  return FMT == kQ4_0 ? launch_npm<FMT, 4>(q4c, 3, W, x, y, n, k, rb, s)
-                      : launch_npm<FMT, 4>(q8c, 2, W, x, y, n, k, rb, s);
+  return FMT == kQ4_0 ? launch_npm<KIND, FMT, 4>(q4c, 3, W, x, y, n, k, rb, status, s)
+                      : launch_npm<KIND, FMT, 4>(q8c, 2, W, x, y, n, k, rb, status, s);
 }
 
 }  // namespace
@@ -477,8 +737,26 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, 
 hipError_t launch_qgemv_dot(int fmt, const void* Wv, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s) {
   const auto* W = static_cast<const uint8_t*>(Wv);
-  return fmt == kQ8_0 ? launch_fmt<kQ8_0>(W, x, y, n, k, rows_per_wave, s)
-                      : launch_fmt<kQ4_0>(W, x, y, n, k, rows_per_wave, s);
+  return fmt == kQ8_0 ? launch_fmt<0, kQ8_0>(W, x, y, n, k, rows_per_wave, nullptr, s)
+                      : launch_fmt<0, kQ4_0>(W, x, y, n, k, rows_per_wave, nullptr, s);
+}
+
+// qgemv_w8a8: the fast kernel when K/32 is even, W is 4-byte aligned and the
+// sizes fit 32-bit indexing; the one-wave-per-row kernel otherwise.
+hipError_t launch_qgemv_w8a8(int fmt, const void* Wv, const float* x, float* y, long long n,
+                             long long k, int rows_per_wave, int* status, hipStream_t s) {
+  const auto* W = static_cast<const uint8_t*>(Wv);
+  const bool fast = (k >> 5) % 2 == 0 && reinterpret_cast<uintptr_t>(W) % 4 == 0 &&
+                    n < (1LL << 31) && k < (1LL << 31);
+  if (fast)
+    return fmt == kQ8_0 ? launch_fmt<1, kQ8_0>(W, x, y, (int)n, (int)k, rows_per_wave, status, s)
+                        : launch_fmt<1, kQ4_0>(W, x, y, (int)n, (int)k, rows_per_wave, status, s);
+  const long long grid = (n + 3) / 4;
+  if (fmt == kQ8_0)
+    qgemv_w8a8_generic<kQ8_0><<<static_cast<unsigned>(grid), 256, 0, s>>>(W, x, y, n, k, status);
+  else
+    qgemv_w8a8_generic<kQ4_0><<<static_cast<unsigned>(grid), 256, 0, s>>>(W, x, y, n, k, status);
+  return hipGetLastError();
 }
 
 }  // namespace qc

@@ -38,6 +38,9 @@ _SIGS = {
     "qc_hip_qgemv_unpack": ([_I, _P, _LL, _LL, _P, _P], _I),
     "qc_hip_qgemv": ([_I, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_qgemm": ([_I, _P, _P, _P, _LL, _LL, _LL, _P], _I),
+    "qc_hip_qgemv_w8a8": ([_I, _P, _P, _P, _LL, _LL, _P, _P], _I),
+    "qc_hip_qgemv_w8a8_packed_size": ([_I, _LL, _LL, _P], _I),
+    "qc_hip_qgemv_w8a8_variant": ([_I], ctypes.c_char_p),
     "qc_hip_quantize_int8": ([_P, _P, _P, _LL, _LL, _LL, _P, _P], _I),
     "qc_hip_int8_gemm": ([_P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _I, _P, _P], _I),
     "qc_hip_qgemm_w8a8": ([_P, _P, _P, _P, _P, _LL, _LL, _LL, _P, _P], _I),
@@ -89,6 +92,11 @@ def packed_size(fmt, n, k):
 # Raw entry points: return the status integer (tests exercise error paths).
 def qgemv_raw(fmt, packed, x, y, n, k, stream=None):
     return lib.qc_hip_qgemv(fmt, _ptr(packed), _ptr(x), _ptr(y), n, k, _stream(stream))
+
+
+def qgemv_w8a8_raw(fmt, packed, x, y, n, k, dev_status=None, stream=None):
+    return lib.qc_hip_qgemv_w8a8(fmt, _ptr(packed), _ptr(x), _ptr(y), n, k, _ptr(dev_status),
+                                 _stream(stream))
 
 
 def qgemm_raw(fmt, packed, x, y, m, n, k, stream=None):
@@ -143,6 +151,14 @@ def qgemv(fmt, packed, x, n, k, y=None):
     if y is None:
         y = torch.empty(n, dtype=torch.float32, device=x.device)
     _check(qgemv_raw(fmt, packed, x, y, n, k), "qgemv")
+    return y
+
+
+def qgemv_w8a8(fmt, packed, x, n, k, y=None):
+    import torch
+    if y is None:
+        y = torch.empty(n, dtype=torch.float32, device=x.device)
+    _check(qgemv_w8a8_raw(fmt, packed, x, y, n, k), "qgemv_w8a8")
     return y
 
 
@@ -204,6 +220,10 @@ def set_int8_gemm_route(route):
 
 def qgemv_variant(fmt):
     return lib.qc_hip_qgemv_variant(fmt).decode()
+
+
+def qgemv_w8a8_variant(fmt):
+    return lib.qc_hip_qgemv_w8a8_variant(fmt).decode()
 
 
 def int8_gemm_variant():

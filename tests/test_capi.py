@@ -38,6 +38,7 @@ def test_cpp_dropin_symbols_exported():
                          text=True, check=True).stdout
     for sym in ("quixicore_cpu::qgemv(", "quixicore_cpu::qgemm(", "quixicore_cpu::quantize_int8(",
                 "quixicore_cpu::int8_gemm(", "quixicore_cpu::qgemm_w8a8(",
+                "quixicore_cpu::qgemv_w8a8(", "quixicore_cpu::qgemv_w8a8_packed_size(",
                 "quixicore_cpu::qgemm_prepacked(", "quixicore_cpu::CpuPackedWeights::prepare(",
                 "quixicore_cpu::Workspace::allocate("):
         assert sym in out, sym
@@ -69,6 +70,18 @@ def test_packed_size_and_validation_without_device():
     assert q.lib.qc_hip_int8_gemm(None, None, None, None, None, None, None, 1, 1, 1, 0, None,
                                   None) == 3
     assert q.lib.qc_hip_int8_gemm_i32(None, None, None, 1, 1, 131072, None) == 1
+    # qgemv_w8a8 (src/dispatch/qgemv_w8a8.cpp:99-105,130-143): format, shape, nulls
+    assert q.lib.qc_hip_qgemv_w8a8(7, None, None, None, 1, 32, None, None) == 2
+    assert q.lib.qc_hip_qgemv_w8a8(7, None, None, None, 1, 33, None, None) == 2
+    assert q.lib.qc_hip_qgemv_w8a8(1, None, None, None, 96, 257, None, None) == 1
+    assert q.lib.qc_hip_qgemv_w8a8(1, None, None, None, 96, 256, None, None) == 3
+    nbytes = ctypes.c_longlong(0)
+    assert q.lib.qc_hip_qgemv_w8a8_packed_size(1, 96, 256, ctypes.byref(nbytes)) == 0
+    assert nbytes.value == 96 * 8 * 18
+    assert q.lib.qc_hip_qgemv_w8a8_packed_size(0, 96, 256, None) == 3
+    assert q.lib.qc_hip_qgemv_w8a8_packed_size(2, 96, 256, ctypes.byref(nbytes)) == 2
+    assert q.qgemv_w8a8_variant(1) == "hip_gfx950_w8a8_q4_0"
+    assert q.qgemv_w8a8_variant(3) == "unsupported"
     assert q.qgemv_variant(0) == "hip_gfx950_q8_0" and q.qgemv_variant(5) == "unsupported"
     assert q.lib.qc_hip_set_gemv_rows_per_wave(3) == 3
 
