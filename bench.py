@@ -159,6 +159,41 @@ def gemv_w8a8_case(qc, fmt, n, k, steps, warmup, seed):
             "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
 
 
+def fused_case(qc, kind, fmt, rows, k, steps, warmup, seed):
+    """One fused decode launch over one x: kind "up_gate" (rows = (n, n)) or
+    "qkv" (rows = (q, kv, kv)), rotated weight copies."""
+    import torch
+    dev = torch.device("cuda:0")
+    bb = qc.BLOCK_BYTES[fmt]
+    wbytes = sum(r * (k // 32) * bb for r in rows)
+    copies = rotation(wbytes)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    sets = []
+    for c in range(copies):
+        mats = []
+        for r in rows:
+            w = torch.randn((r, k), generator=g, device=dev) * 0.02
+            mats.append(qc.pack(fmt, w))
+            del w
+        sets.append(mats)
+    x = torch.randn(k, generator=g, device=dev)
+    ys = [torch.empty(r, dtype=torch.float32, device=dev) for r in rows]
+
+    def launch(i):
+        m = sets[i % copies]
+        if kind == "up_gate":
+            st = qc.qgemv_up_gate_raw(fmt, m[0], m[1], x, ys[0], ys[1], rows[0], k)
+        else:
+            st = qc.qgemv_qkv_raw(fmt, m[0], m[1], m[2], x, ys[0], ys[1], ys[2], rows[0], rows[1], k)
+        if st:
+            raise RuntimeError(f"{kind} status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    alg = wbytes + 4 * k + 4 * sum(rows)
+    return {"bytes": alg, "copies": copies, "wall_ms": wall, "gpu_ms": gpu,
+            "gbs": alg / (wall * 1e-3) / 1e9, "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
+
+
 def qgemm_case(qc, n, k, m, steps, warmup, seed, fmt=0):
     import torch
     dev = torch.device("cuda:0")
@@ -245,6 +280,20 @@ def layer_sweep(qc, steps, warmup):
             wbytes += cnt * n * (k // 32) * 18
         out[f"q4_0_m{m}"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
                              "weight_gbs": wbytes / (us * 1e-6) / 1e9}
+    # M = 1 with the fused decode seams: Q/K/V in one launch (4096 x 3 rows),
+    # O alone, gate/up in one launch, down alone.
+    us, wbytes = 0.0, 0
+    r = fused_case(qc, "qkv", 1, (4096, 4096, 4096), 4096, steps, warmup, seed=301)
+    us += r["gpu_ms"] * 1e3
+    r, *_ = gemv_case(qc, 1, 4096, 4096, steps, warmup, seed=302)
+    us += r["gpu_ms"] * 1e3
+    r = fused_case(qc, "up_gate", 1, (14336, 14336), 4096, steps, warmup, seed=303)
+    us += r["gpu_ms"] * 1e3
+    r, *_ = gemv_case(qc, 1, 4096, 14336, steps, warmup, seed=304)
+    us += r["gpu_ms"] * 1e3
+    wbytes = sum(cnt * n * (k // 32) * 18 for cnt, n, k in LAYER)
+    out["q4_0_m1_fused"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
+                            "weight_gbs": wbytes / (us * 1e-6) / 1e9}
     for m in (512, 2048):
         us, ops = 0.0, 0.0
         for cnt, n, k in LAYER:
@@ -387,6 +436,8 @@ def main():
         s["q4_0_gemv_k14336_n4096"] = r
         s["q4_0_gemv_w8a8_k4096_n14336"] = gemv_w8a8_case(qc, 1, 14336, 4096, K, W, seed=11)
         s["q8_0_gemv_w8a8_k4096_n4096"] = gemv_w8a8_case(qc, 0, 4096, 4096, K, W, seed=12)
+        s["q4_0_up_gate_k4096_n2x14336"] = fused_case(qc, "up_gate", 1, (14336, 14336), 4096, K, W,
+                                                      seed=13)
         for m in (4, 8, 16, 32):
             s[f"q8_0_qgemm_m{m}_k4096_n14336"] = qgemm_case(qc, 14336, 4096, m, K, W, seed=4 + m)
         s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)

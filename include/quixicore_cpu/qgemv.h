@@ -68,4 +68,18 @@ Status qgemv(QuantFormat format, const void* packed, const float* x, float* y, l
 // include/quixicore_cpu/qgemv.h:166
 const char* qgemv_variant(QuantFormat format);
 
+// Fused decode projections over one x (include/quixicore_cpu/qgemv.h:143-153
+// of the reference), one GPU launch: up/gate [n][k] each; the activation form
+// stores out = activation(gate) * up (GELU-tanh or SiLU) without storing either
+// projection; Q [query_dim][input_dim], K and V [kv_dim][input_dim].  q8_0 and
+// q4_0 only (other formats return kUnsupportedFormat).
+Status qgemv_up_gate(QuantFormat format, const void* packed_up, const void* packed_gate,
+                     const float* x, float* up, float* gate, long long n, long long k);
+Status qgemv_up_gate_activation(QuantFormat format, const void* packed_up,
+                                const void* packed_gate, const float* x, float* out,
+                                long long n, long long k, bool gelu_tanh = true);
+Status qgemv_qkv(QuantFormat format, const void* packed_q, const void* packed_k,
+                 const void* packed_v, const float* x, float* q, float* k_out, float* v_out,
+                 long long query_dim, long long kv_dim, long long input_dim);
+
 }  // namespace quixicore_cpu

@@ -80,6 +80,32 @@ int qc_hip_qgemv(int format, const void* packed, const float* x, float* y, long 
 int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long long m,
                  long long n, long long k, void* stream);
 
+/* Fused decode projections over one x, one launch where the shapes allow:
+ * up = W_up . x and gate = W_gate . x ([n][k] each).  Same numerics as
+ * qc_hip_qgemv per matrix.  Replaces qgemv_up_gate
+ * (include/quixicore_cpu/qgemv.h:144; kernels/quantization/
+ * qgemv_fused_ref.cpp:194-229).  Formats other than q8_0 / q4_0 return 2. */
+int qc_hip_qgemv_up_gate(int format, const void* packed_up, const void* packed_gate,
+                         const float* x, float* up, float* gate, long long n, long long k,
+                         void* stream);
+
+/* out = activation(W_gate . x) * (W_up . x), activation GELU-tanh
+ * (gelu_tanh != 0) or SiLU; the two projections are never stored.  Replaces
+ * qgemv_up_gate_activation (include/quixicore_cpu/qgemv.h:147;
+ * kernels/quantization/qgemv_fused_ref.cpp:184-192,231-273). */
+int qc_hip_qgemv_up_gate_activation(int format, const void* packed_up, const void* packed_gate,
+                                    const float* x, float* out, long long n, long long k,
+                                    int gelu_tanh, void* stream);
+
+/* q = W_q . x ([query_dim][input_dim]), k_out = W_k . x and v_out = W_v . x
+ * ([kv_dim][input_dim] each) in one launch.  Replaces qgemv_qkv
+ * (include/quixicore_cpu/qgemv.h:151; kernels/quantization/
+ * qgemv_fused_ref.cpp:275-327). */
+int qc_hip_qgemv_qkv(int format, const void* packed_q, const void* packed_k,
+                     const void* packed_v, const float* x, float* q, float* k_out,
+                     float* v_out, long long query_dim, long long kv_dim, long long input_dim,
+                     void* stream);
+
 /* Activation-quantizing GEMV: x is quantized per 32-element block to int8
  * (scale = max|x_b| / 127, round half to even, clamp +-127), each block dot is
  * an exact integer sum, and y[r] = sum_b (float(dot) * d_w) * d_x in block

@@ -260,6 +260,113 @@ int qc_hip_set_gemv_rows_per_wave(int rows) {
   return QC_OK;
 }
 
+// Fused GEMVs over one x.  One launch when every matrix takes the M = 1
+// kernel (K/32 even, 4-byte aligned W, 32-bit row counts); otherwise one
+// qgemv per matrix, and for the activation form an elementwise pass over a
+// temporary up vector.
+namespace {
+
+__global__ void fused_activation_kernel(float* out, const float* up, long long n, int act) {
+  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = out[i];
+  constexpr float kSqrt2OverPi = 0.7978845608028654f;
+  const float a = act == 1 ? 0.5f * v * (1.0f + tanhf(kSqrt2OverPi * (v + 0.044715f * v * v * v)))
+                           : v / (1.0f + expf(-v));
+  out[i] = a * up[i];
+}
+
+int fused_gemv(int format, int nseg, const void* const* w, float* const* y,
+               const long long* rows, int act, const float* x, long long k, hipStream_t s) {
+  bool fast = (k >> 5) % 2 == 0 && k < (1LL << 31) && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  long long total = 0;
+  for (int i = 0; i < nseg; ++i) {
+    fast = fast && reinterpret_cast<uintptr_t>(w[i]) % 4 == 0;
+    total += rows[i];
+  }
+  fast = fast && total < (1LL << 30);
+  if (fast) {
+    int r[3] = {0, 0, 0};
+    for (int i = 0; i < nseg; ++i) r[i] = static_cast<int>(rows[i]);
+    return finish(qc::launch_qgemv_multi(format, nseg, w, y, r, act, x, static_cast<int>(k), s));
+  }
+  if (act < 0) {
+    for (int i = 0; i < nseg; ++i) {
+      const hipError_t e = qc::launch_qgemm(format, w[i], x, y[i], 1, rows[i], k, s, g_tuning);
+      if (e != hipSuccess) return device_error(e);
+    }
+    return QC_OK;
+  }
+  float* up = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&up), sizeof(float) * rows[0], s);
+  if (e != hipSuccess) return device_error(e);
+  e = qc::launch_qgemm(format, w[0], x, up, 1, rows[0], k, s, g_tuning);
+  if (e == hipSuccess) e = qc::launch_qgemm(format, w[1], x, y[0], 1, rows[0], k, s, g_tuning);
+  if (e == hipSuccess) {
+    fused_activation_kernel<<<static_cast<unsigned>((rows[0] + 255) / 256), 256, 0, s>>>(
+        y[0], up, rows[0], act);
+    e = hipGetLastError();
+  }
+  const hipError_t f = hipFreeAsync(up, s);
+  return finish(e != hipSuccess ? e : f);
+}
+
+}  // namespace
+
+// kernels/quantization/qgemv_fused_ref.cpp:194-229 (qgemv_up_gate): shape
+// product, nulls, then the packed layout (format, K).
+int qc_hip_qgemv_up_gate(int format, const void* packed_up, const void* packed_gate,
+                         const float* x, float* up, float* gate, long long n, long long k,
+                         void* stream) {
+  if (!valid_product({n, k})) return QC_INVALID_SHAPE;
+  if (!packed_up || !packed_gate || !x || !up || !gate) return QC_INVALID_ARGUMENT;
+  size_t bytes = 0;
+  const int st = qc_hip_qgemv_packed_size(format, n, k, &bytes);
+  if (st != QC_OK) return st;
+  const void* w[2] = {packed_up, packed_gate};
+  float* y[2] = {up, gate};
+  const long long rows[2] = {n, n};
+  return fused_gemv(format, 2, w, y, rows, -1, x, k, as_stream(stream));
+}
+
+// kernels/quantization/qgemv_fused_ref.cpp:184-192,231-273
+// (qgemv_up_gate_activation): out = activation(gate) * up, GELU-tanh or SiLU.
+int qc_hip_qgemv_up_gate_activation(int format, const void* packed_up, const void* packed_gate,
+                                    const float* x, float* out, long long n, long long k,
+                                    int gelu_tanh, void* stream) {
+  if (!valid_product({n, k})) return QC_INVALID_SHAPE;
+  if (!packed_up || !packed_gate || !x || !out) return QC_INVALID_ARGUMENT;
+  size_t bytes = 0;
+  const int st = qc_hip_qgemv_packed_size(format, n, k, &bytes);
+  if (st != QC_OK) return st;
+  const void* w[2] = {packed_up, packed_gate};
+  float* y[1] = {out};
+  const long long rows[2] = {n, n};
+  return fused_gemv(format, 2, w, y, rows, gelu_tanh ? 1 : 0, x, k, as_stream(stream));
+}
+
+// kernels/quantization/qgemv_fused_ref.cpp:275-327 (qgemv_qkv): products and
+// the 2 * kv_dim overflow check, nulls, the Q layout (format, K), then the KV
+// layout (shape).
+int qc_hip_qgemv_qkv(int format, const void* packed_q, const void* packed_k,
+                     const void* packed_v, const float* x, float* q, float* k_out,
+                     float* v_out, long long query_dim, long long kv_dim, long long input_dim,
+                     void* stream) {
+  if (!valid_product({query_dim, kv_dim, input_dim})) return QC_INVALID_SHAPE;
+  if (kv_dim > (LLONG_MAX - query_dim) / 2) return QC_INVALID_SHAPE;
+  if (!packed_q || !packed_k || !packed_v || !x || !q || !k_out || !v_out)
+    return QC_INVALID_ARGUMENT;
+  size_t bytes = 0;
+  const int st = qc_hip_qgemv_packed_size(format, query_dim, input_dim, &bytes);
+  if (st != QC_OK) return st;
+  if (qc_hip_qgemv_packed_size(format, kv_dim, input_dim, &bytes) != QC_OK)
+    return QC_INVALID_SHAPE;
+  const void* w[3] = {packed_q, packed_k, packed_v};
+  float* y[3] = {q, k_out, v_out};
+  const long long rows[3] = {query_dim, kv_dim, kv_dim};
+  return fused_gemv(format, 3, w, y, rows, -1, x, input_dim, as_stream(stream));
+}
+
 // src/dispatch/qgemv_w8a8.cpp:108-125 (qgemv_w8a8_packed_size).
 int qc_hip_qgemv_w8a8_packed_size(int format, long long n, long long k, long long* bytes) {
   size_t size = 0;

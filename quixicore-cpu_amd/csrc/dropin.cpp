@@ -162,6 +162,74 @@ Status qgemv(QuantFormat format, const void* packed, const float* x, float* y, l
 
 const char* qgemv_variant(QuantFormat format) { return qc_hip_qgemv_variant(fmt_id(format)); }
 
+Status qgemv_up_gate(QuantFormat format, const void* packed_up, const void* packed_gate,
+                     const float* x, float* up, float* gate, long long n, long long k) {
+  const int pre = qc_hip_qgemv_up_gate(fmt_id(format), nullptr, nullptr, nullptr, nullptr,
+                                       nullptr, n, k, nullptr);
+  if (pre == QC_INVALID_SHAPE) return Status::kInvalidShape;
+  if (!packed_up || !packed_gate || !x || !up || !gate) return Status::kInvalidArgument;
+  const size_t bytes = packed_or_zero(format, n, k);
+  if (bytes == 0)
+    return static_cast<Status>(
+        qc_hip_qgemv_up_gate(fmt_id(format), packed_up, packed_gate, x, up, gate, n, k, nullptr));
+  Staging g(nullptr);
+  const void* pu = g.in(packed_up, bytes);
+  const void* pg = g.in(packed_gate, bytes);
+  const float* xd = static_cast<const float*>(g.in(x, sizeof(float) * k));
+  float* ud = static_cast<float*>(g.out(up, sizeof(float) * n));
+  float* gd = static_cast<float*>(g.out(gate, sizeof(float) * n));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(qc_hip_qgemv_up_gate(fmt_id(format), pu, pg, xd, ud, gd, n, k, g.stream()));
+}
+
+Status qgemv_up_gate_activation(QuantFormat format, const void* packed_up,
+                                const void* packed_gate, const float* x, float* out,
+                                long long n, long long k, bool gelu_tanh) {
+  const int pre = qc_hip_qgemv_up_gate_activation(fmt_id(format), nullptr, nullptr, nullptr,
+                                                  nullptr, n, k, gelu_tanh, nullptr);
+  if (pre == QC_INVALID_SHAPE) return Status::kInvalidShape;
+  if (!packed_up || !packed_gate || !x || !out) return Status::kInvalidArgument;
+  const size_t bytes = packed_or_zero(format, n, k);
+  if (bytes == 0)
+    return static_cast<Status>(qc_hip_qgemv_up_gate_activation(
+        fmt_id(format), packed_up, packed_gate, x, out, n, k, gelu_tanh, nullptr));
+  Staging g(nullptr);
+  const void* pu = g.in(packed_up, bytes);
+  const void* pg = g.in(packed_gate, bytes);
+  const float* xd = static_cast<const float*>(g.in(x, sizeof(float) * k));
+  float* od = static_cast<float*>(g.out(out, sizeof(float) * n));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(qc_hip_qgemv_up_gate_activation(fmt_id(format), pu, pg, xd, od, n, k,
+                                                  gelu_tanh, g.stream()));
+}
+
+Status qgemv_qkv(QuantFormat format, const void* packed_q, const void* packed_k,
+                 const void* packed_v, const float* x, float* q, float* k_out, float* v_out,
+                 long long query_dim, long long kv_dim, long long input_dim) {
+  const int pre = qc_hip_qgemv_qkv(fmt_id(format), nullptr, nullptr, nullptr, nullptr, nullptr,
+                                   nullptr, nullptr, query_dim, kv_dim, input_dim, nullptr);
+  if (pre == QC_INVALID_SHAPE) return Status::kInvalidShape;
+  if (!packed_q || !packed_k || !packed_v || !x || !q || !k_out || !v_out)
+    return Status::kInvalidArgument;
+  const size_t qb = packed_or_zero(format, query_dim, input_dim);
+  const size_t kb = packed_or_zero(format, kv_dim, input_dim);
+  if (qb == 0 || kb == 0)
+    return static_cast<Status>(qc_hip_qgemv_qkv(fmt_id(format), packed_q, packed_k, packed_v, x,
+                                                q, k_out, v_out, query_dim, kv_dim, input_dim,
+                                                nullptr));
+  Staging g(nullptr);
+  const void* pq = g.in(packed_q, qb);
+  const void* pk = g.in(packed_k, kb);
+  const void* pv = g.in(packed_v, kb);
+  const float* xd = static_cast<const float*>(g.in(x, sizeof(float) * input_dim));
+  float* qd = static_cast<float*>(g.out(q, sizeof(float) * query_dim));
+  float* kd = static_cast<float*>(g.out(k_out, sizeof(float) * kv_dim));
+  float* vd = static_cast<float*>(g.out(v_out, sizeof(float) * kv_dim));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(qc_hip_qgemv_qkv(fmt_id(format), pq, pk, pv, xd, qd, kd, vd, query_dim, kv_dim,
+                                   input_dim, g.stream()));
+}
+
 Status qgemv_w8a8(QuantFormat format, const void* packed_weights, const float* x, float* y,
                   long long n, long long k) {
   const size_t bytes = packed_or_zero(format, n, k);

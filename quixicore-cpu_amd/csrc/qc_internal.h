@@ -21,6 +21,13 @@ hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long l
 hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s);
 
+// Fused GEMVs over one x in a single launch (K % 64 == 0, every W 4-byte
+// aligned, x 16-byte aligned): nseg matrices W[i] of rows[i] rows into y[i] (act = -1), or up
+// (W[0]) and gate (W[1]) of rows[0] rows into y[0] = activation(gate) * up
+// (act 0: SiLU, 1: GELU-tanh).  Same numerics as launch_qgemm with m = 1.
+hipError_t launch_qgemv_multi(int fmt, int nseg, const void* const* W, float* const* y,
+                              const int* rows, int act, const float* x, int k, hipStream_t s);
+
 // qgemv_w8a8: x quantized per 32-element block to int8, exact integer block
 // dots, y bit-identical to the reference.  status (optional): set to 3 when x
 // holds a non-finite value (the affected outputs are NaN).

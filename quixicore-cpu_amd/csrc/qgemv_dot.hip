@@ -262,6 +262,26 @@ __device__ __forceinline__ void load_pair(uint32_t* d, const uint8_t* p) {
   d[4 * NV] = reinterpret_cast<const uint32_t*>(p)[4 * NV];
 }
 
+// Row space of one launch: up to three weight matrices with their outputs,
+// concatenated (logical row g of segment s is row g - start[s] of w[s]), or,
+// with act >= 0, up (even logical rows) and gate (odd) of one row index
+// interleaved, stored as out[i] = activation(gate[i]) * up[i] (act 0: SiLU,
+// 1: GELU-tanh; kernels/quantization/qgemv_fused_ref.cpp:184-192).  The same
+// x is shared by every row.
+struct GemvSegs {
+  const uint8_t* w[3];
+  float* y[3];
+  int start[4];    // start[nseg] = total logical rows
+  int nseg;
+  int act;         // -1: plain segments
+};
+
+__device__ __forceinline__ float fused_activation(float v, int act) {
+  constexpr float kSqrt2OverPi = 0.7978845608028654f;
+  return act == 1 ? 0.5f * v * (1.0f + tanhf(kSqrt2OverPi * (v + 0.044715f * v * v * v)))
+                  : v / (1.0f + expf(-v));
+}
+
 // NW wavefronts of RB rows each, up to NPM pairs per lane per K chunk.  The (pair j,
 // row r) items of a chunk are loaded in j-major order with at most WIN items
 // in flight: item t + WIN is issued just before item t is computed, so the
@@ -269,10 +289,14 @@ __device__ __forceinline__ void load_pair(uint32_t* d, const uint8_t* p) {
 // NPM * RB).  A bounded window keeps a wave from waiting on its first rows
 // while the memory system still returns the others, which for several rows
 // per wave leaves less compute after the last byte lands.
-template <int FMT, int NW, int RB, int NPM, int WIN, bool VEC>
-__global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const uint8_t* __restrict__ W,
-                                                             const float* __restrict__ x,
-                                                             float* __restrict__ y, int n, int k,
+//
+// MULTI false: one matrix (segs.w[0], segs.y[0], segs.start[1] rows).  MULTI
+// true: the whole segment table, with the activation epilogue when act >= 0;
+// the selection is kept out of the one-matrix kernel, whose prologue and
+// epilogue it would lengthen.
+template <int FMT, int NW, int RB, int NPM, int WIN, bool VEC, bool MULTI>
+__global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
+                                                             const float* __restrict__ x, int k,
                                                              int kc) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int BB = Fmt<FMT>::block_bytes;
@@ -281,11 +305,36 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const uint8_t* __res
   constexpr int NT = 64 * NW;
   constexpr int HPT = (NPM * 256 + NT - 1) / NT;   // half-blocks of x per thread
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * NW + (threadIdx.x >> 6)) * RB;
   const long long row_bytes = static_cast<long long>(k >> 5) * BB;
   const uint8_t* wrow[RB];
+  int row0, total;
+  if constexpr (!MULTI) {
+    total = segs.start[1];
+    row0 = (blockIdx.x * NW + (threadIdx.x >> 6)) * RB;
 #pragma unroll
-  for (int r = 0; r < RB; ++r) wrow[r] = W + min(row0 + r, n - 1) * row_bytes;
+    for (int r = 0; r < RB; ++r) wrow[r] = segs.w[0] + min(row0 + r, total - 1) * row_bytes;
+  } else {
+    // the wave index is uniform; saying so keeps the row and segment
+    // selection in scalar registers (a per-lane selection indexes the kernel
+    // arguments with vector loads, serialised before the first weight load).
+    // The table is read into locals and selected by value: indexing the
+    // argument array, or taking its address, moves it to scratch.
+    row0 = (blockIdx.x * NW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RB;
+    const uint8_t* const w0 = segs.w[0];
+    const uint8_t* const w1 = segs.w[1];
+    const uint8_t* const w2 = segs.w[2];
+    const int s1 = segs.start[1], s2 = segs.start[2], nseg = segs.nseg, act = segs.act;
+    total = nseg == 1 ? s1 : nseg == 2 ? s2 : segs.start[3];
+    const bool three = nseg > 2;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int g = min(row0 + r, total - 1);
+      const bool in2 = three && g >= s2, in1 = g >= s1;
+      const uint8_t* const base = act >= 0 ? ((g & 1) ? w1 : w0) : in2 ? w2 : in1 ? w1 : w0;
+      const int local = act >= 0 ? g >> 1 : g - (in2 ? s2 : in1 ? s1 : 0);
+      wrow[r] = base + static_cast<long long>(local) * row_bytes;
+    }
+  }
   float acc[RB];
 #pragma unroll
   for (int r = 0; r < RB; ++r) acc[r] = 0.f;
@@ -323,10 +372,37 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const uint8_t* __res
       }
     }
   }
+  if constexpr (!MULTI) {
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const float t = wave_sum_lane63(acc[r]);
-    if (lane == 63 && row0 + r < n) y[row0 + r] = t;
+    for (int r = 0; r < RB; ++r) {
+      const float t = wave_sum_lane63(acc[r]);
+      if (lane == 63 && row0 + r < total) segs.y[0][row0 + r] = t;
+    }
+  } else {
+    float t[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) t[r] = wave_sum_lane63(acc[r]);
+    if (lane != 63) return;
+    const int s1 = segs.start[1], s2 = segs.start[2], act = segs.act;
+    const bool three = segs.nseg > 2;
+    float* const y0 = segs.y[0];
+    float* const y1 = segs.y[1];
+    float* const y2 = segs.y[2];
+    if (act >= 0) {
+      // RB is even and row0 even: rows (2i, 2i+1) = (up, gate) of row index i
+#pragma unroll
+      for (int r = 0; r + 1 < RB; r += 2)
+        if (row0 + r < total) y0[(row0 + r) >> 1] = fused_activation(t[r + 1], act) * t[r];
+      return;
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int g = row0 + r;
+      if (g >= total) continue;
+      const bool in2 = three && g >= s2, in1 = g >= s1;
+      float* const out = in2 ? y2 : in1 ? y1 : y0;
+      out[g - (in2 ? s2 : in1 ? s1 : 0)] = t[r];
+    }
   }
 }
 
@@ -588,10 +664,12 @@ constexpr int window() {
   return T >= 8 ? 2 : 1;
 }
 
-// KIND 0: qgemv (f32 activations, exact digit dots); KIND 1: qgemv_w8a8.
+// KIND 0: qgemv (f32 activations, exact digit dots); KIND 1: qgemv_w8a8;
+// KIND 2: qgemv over a segment table (several matrices, or up/gate with the
+// activation epilogue), x 16-byte aligned.
 template <int KIND, int FMT, int NW, int RB, int NPM>
-hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, int* status,
-                      hipStream_t s) {
+hipError_t launch_one(const GemvSegs& sg, const float* x, int k, int* status, hipStream_t s) {
+  const int n = sg.start[sg.nseg];
   // weights held per lane: at most RB * NPM * pair dwords (<= 144 VGPRs)
   static_assert(RB * NPM * Fmt<FMT>::pair_dwords <= 144, "register budget");
   constexpr int WIN = window<FMT, NPM * RB>();
@@ -600,15 +678,18 @@ hipError_t launch_one(const uint8_t* W, const float* x, float* y, int n, int k, 
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if constexpr (KIND == 0) {
     if (vec)
-      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
+      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true, false><<<grid, 64 * NW, lds_size(kc), s>>>(sg, x, k, kc);
     else
-      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, false><<<grid, 64 * NW, lds_size(kc), s>>>(W, x, y, n, k, kc);
+      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, false, false><<<grid, 64 * NW, lds_size(kc), s>>>(sg, x, k, kc);
+  } else if constexpr (KIND == 2) {
+    // the caller guarantees a 16-byte aligned x
+    qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true, true><<<grid, 64 * NW, lds_size(kc), s>>>(sg, x, k, kc);
   } else {
     const size_t lds = w8_lds_size(kc, NW, RB);
     if (vec)
-      qgemv_w8a8_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds, s>>>(W, x, y, n, k, kc, status);
+      qgemv_w8a8_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds, s>>>(sg.w[0], x, sg.y[0], n, k, kc, status);
     else
-      qgemv_w8a8_kernel<FMT, NW, RB, NPM, WIN, false><<<grid, 64 * NW, lds, s>>>(W, x, y, n, k, kc, status);
+      qgemv_w8a8_kernel<FMT, NW, RB, NPM, WIN, false><<<grid, 64 * NW, lds, s>>>(sg.w[0], x, sg.y[0], n, k, kc, status);
   }
   return hipGetLastError();
 }
@@ -664,69 +745,75 @@ Shape pick_shape(int n, const int* cand, int ncand, int forced_rb) {
 }
 
 template <int KIND, int FMT, int NW, int NPM>
-hipError_t launch_rb(int rb, const uint8_t* W, const float* x, float* y, int n, int k,
-                     int* status, hipStream_t s) {
+hipError_t launch_rb(int rb, const GemvSegs& sg, const float* x, int k, int* status,
+                     hipStream_t s) {
   if constexpr (NPM == 1) {
     switch (rb) {
-      case 1: return launch_one<KIND, FMT, NW, 1, 1>(W, x, y, n, k, status, s);
-      case 2: return launch_one<KIND, FMT, NW, 2, 1>(W, x, y, n, k, status, s);
-      case 4: return launch_one<KIND, FMT, NW, 4, 1>(W, x, y, n, k, status, s);
-      case 7: return launch_one<KIND, FMT, NW, 7, 1>(W, x, y, n, k, status, s);
-      case 8: return launch_one<KIND, FMT, NW, 8, 1>(W, x, y, n, k, status, s);
+      case 1: return launch_one<KIND, FMT, NW, 1, 1>(sg, x, k, status, s);
+      case 2: return launch_one<KIND, FMT, NW, 2, 1>(sg, x, k, status, s);
+      case 4: return launch_one<KIND, FMT, NW, 4, 1>(sg, x, k, status, s);
+      case 7: return launch_one<KIND, FMT, NW, 7, 1>(sg, x, k, status, s);
+      case 8: return launch_one<KIND, FMT, NW, 8, 1>(sg, x, k, status, s);
       default:
-        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 14, 1>(W, x, y, n, k, status, s);
-        return launch_one<KIND, FMT, NW, 8, 1>(W, x, y, n, k, status, s);
+        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 14, 1>(sg, x, k, status, s);
+        return launch_one<KIND, FMT, NW, 8, 1>(sg, x, k, status, s);
     }
   } else if constexpr (NPM == 2) {
     switch (rb) {
-      case 1: return launch_one<KIND, FMT, NW, 1, 2>(W, x, y, n, k, status, s);
-      case 2: return launch_one<KIND, FMT, NW, 2, 2>(W, x, y, n, k, status, s);
-      case 4: return launch_one<KIND, FMT, NW, 4, 2>(W, x, y, n, k, status, s);
+      case 1: return launch_one<KIND, FMT, NW, 1, 2>(sg, x, k, status, s);
+      case 2: return launch_one<KIND, FMT, NW, 2, 2>(sg, x, k, status, s);
+      case 4: return launch_one<KIND, FMT, NW, 4, 2>(sg, x, k, status, s);
       default:
-        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 7, 2>(W, x, y, n, k, status, s);
-        return launch_one<KIND, FMT, NW, 4, 2>(W, x, y, n, k, status, s);
+        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 7, 2>(sg, x, k, status, s);
+        return launch_one<KIND, FMT, NW, 4, 2>(sg, x, k, status, s);
     }
   } else {
     switch (rb) {
-      case 1: return launch_one<KIND, FMT, NW, 1, 4>(W, x, y, n, k, status, s);
-      case 2: return launch_one<KIND, FMT, NW, 2, 4>(W, x, y, n, k, status, s);
+      case 1: return launch_one<KIND, FMT, NW, 1, 4>(sg, x, k, status, s);
+      case 2: return launch_one<KIND, FMT, NW, 2, 4>(sg, x, k, status, s);
       default:
-        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 4, 4>(W, x, y, n, k, status, s);
-        return launch_one<KIND, FMT, NW, 2, 4>(W, x, y, n, k, status, s);
+        if constexpr (FMT == kQ4_0) return launch_one<KIND, FMT, NW, 4, 4>(sg, x, k, status, s);
+        return launch_one<KIND, FMT, NW, 2, 4>(sg, x, k, status, s);
     }
   }
 }
 
+// Candidates of rows per wave: with an activation epilogue only even counts
+// (each wave holds whole (up, gate) row pairs).
 template <int KIND, int FMT, int NPM>
-hipError_t launch_npm(const int* cand, int ncand, const uint8_t* W, const float* x, float* y,
-                      int n, int k, int rb, int* status, hipStream_t s) {
+hipError_t launch_npm(const int* cand_all, int ncand_all, const GemvSegs& sg, const float* x,
+                      int k, int rb, int* status, hipStream_t s) {
+  int cand[8];
+  int ncand = 0;
+  for (int i = 0; i < ncand_all; ++i)
+    if (sg.act < 0 || cand_all[i] % 2 == 0) cand[ncand++] = cand_all[i];
   bool listed = false;
   for (int i = 0; i < ncand; ++i) listed = listed || cand[i] == rb;
-  const Shape sh = pick_shape(n, cand, ncand, listed ? rb : 0);
-  return sh.nw == 8 ? launch_rb<KIND, FMT, 8, NPM>(sh.rb, W, x, y, n, k, status, s)
-                    : launch_rb<KIND, FMT, 4, NPM>(sh.rb, W, x, y, n, k, status, s);
+  const Shape sh = pick_shape(sg.start[sg.nseg], cand, ncand, listed ? rb : 0);
+  return sh.nw == 8 ? launch_rb<KIND, FMT, 8, NPM>(sh.rb, sg, x, k, status, s)
+                    : launch_rb<KIND, FMT, 4, NPM>(sh.rb, sg, x, k, status, s);
 }
 
 template <int KIND, int FMT>
-hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, int rb,
-                      int* status, hipStream_t s) {
+hipError_t launch_fmt(const GemvSegs& sg, const float* x, int k, int rb, int* status,
+                      hipStream_t s) {
   const int npairs = k >> 6;
   if (npairs <= 64) {
     static const int q4c[] = {14, 7, 8, 4, 2, 1};
     static const int q8c[] = {8, 7, 4, 2, 1};
-    return FMT == kQ4_0 ? launch_npm<KIND, FMT, 1>(q4c, 6, W, x, y, n, k, rb, status, s)
-                        : launch_npm<KIND, FMT, 1>(q8c, 5, W, x, y, n, k, rb, status, s);
+    return FMT == kQ4_0 ? launch_npm<KIND, FMT, 1>(q4c, 6, sg, x, k, rb, status, s)
+                        : launch_npm<KIND, FMT, 1>(q8c, 5, sg, x, k, rb, status, s);
   }
   if (npairs <= 128) {
     static const int q4c[] = {7, 4, 2, 1};
     static const int q8c[] = {4, 2, 1};
-    return FMT == kQ4_0 ? launch_npm<KIND, FMT, 2>(q4c, 4, W, x, y, n, k, rb, status, s)
-                        : launch_npm<KIND, FMT, 2>(q8c, 3, W, x, y, n, k, rb, status, s);
+    return FMT == kQ4_0 ? launch_npm<KIND, FMT, 2>(q4c, 4, sg, x, k, rb, status, s)
+                        : launch_npm<KIND, FMT, 2>(q8c, 3, sg, x, k, rb, status, s);
   }
   static const int q4c[] = {4, 2, 1};
   static const int q8c[] = {2, 1};
-  return FMT == kQ4_0 ? launch_npm<KIND, FMT, 4>(q4c, 3, W, x, y, n, k, rb, status, s)
-                      : launch_npm<KIND, FMT, 4>(q8c, 2, W, x, y, n, k, rb, status, s);
+  return FMT == kQ4_0 ? launch_npm<KIND, FMT, 4>(q4c, 3, sg, x, k, rb, status, s)
+                      : launch_npm<KIND, FMT, 4>(q8c, 2, sg, x, k, rb, status, s);
 }
 
 }  // namespace
@@ -736,9 +823,40 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int n, int k, 
 // shape; otherwise 1, 2, 4, 7, 8 or 14 (q4_0) rows per wave.
 hipError_t launch_qgemv_dot(int fmt, const void* Wv, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s) {
-  const auto* W = static_cast<const uint8_t*>(Wv);
-  return fmt == kQ8_0 ? launch_fmt<0, kQ8_0>(W, x, y, n, k, rows_per_wave, nullptr, s)
-                      : launch_fmt<0, kQ4_0>(W, x, y, n, k, rows_per_wave, nullptr, s);
+  GemvSegs sg{};
+  sg.w[0] = static_cast<const uint8_t*>(Wv);
+  sg.y[0] = y;
+  sg.start[0] = 0;
+  sg.start[1] = n;
+  sg.nseg = 1;
+  sg.act = -1;
+  return fmt == kQ8_0 ? launch_fmt<0, kQ8_0>(sg, x, k, rows_per_wave, nullptr, s)
+                      : launch_fmt<0, kQ4_0>(sg, x, k, rows_per_wave, nullptr, s);
+}
+
+// Several matrices over one x in one launch (K % 64 == 0, every W 4-byte
+// aligned, x 16-byte aligned, checked by the caller): nseg plain segments, or
+// (act >= 0) up and gate with out = activation(gate) * up.
+hipError_t launch_qgemv_multi(int fmt, int nseg, const void* const* W, float* const* y,
+                              const int* rows, int act, const float* x, int k, hipStream_t s) {
+  GemvSegs sg{};
+  sg.nseg = act >= 0 ? 1 : nseg;
+  sg.act = act;
+  sg.start[0] = 0;
+  if (act >= 0) {
+    sg.w[0] = static_cast<const uint8_t*>(W[0]);
+    sg.w[1] = static_cast<const uint8_t*>(W[1]);
+    sg.y[0] = y[0];
+    sg.start[1] = 2 * rows[0];
+  } else {
+    for (int i = 0; i < nseg; ++i) {
+      sg.w[i] = static_cast<const uint8_t*>(W[i]);
+      sg.y[i] = y[i];
+      sg.start[i + 1] = sg.start[i] + rows[i];
+    }
+  }
+  return fmt == kQ8_0 ? launch_fmt<2, kQ8_0>(sg, x, k, 0, nullptr, s)
+                      : launch_fmt<2, kQ4_0>(sg, x, k, 0, nullptr, s);
 }
 
 // qgemv_w8a8: the fast kernel when K/32 is even, W is 4-byte aligned and the
@@ -748,9 +866,17 @@ hipError_t launch_qgemv_w8a8(int fmt, const void* Wv, const float* x, float* y, 
   const auto* W = static_cast<const uint8_t*>(Wv);
   const bool fast = (k >> 5) % 2 == 0 && reinterpret_cast<uintptr_t>(W) % 4 == 0 &&
                     n < (1LL << 31) && k < (1LL << 31);
-  if (fast)
-    return fmt == kQ8_0 ? launch_fmt<1, kQ8_0>(W, x, y, (int)n, (int)k, rows_per_wave, status, s)
-                        : launch_fmt<1, kQ4_0>(W, x, y, (int)n, (int)k, rows_per_wave, status, s);
+  if (fast) {
+    GemvSegs sg{};
+    sg.w[0] = W;
+    sg.y[0] = y;
+    sg.start[0] = 0;
+    sg.start[1] = static_cast<int>(n);
+    sg.nseg = 1;
+    sg.act = -1;
+    return fmt == kQ8_0 ? launch_fmt<1, kQ8_0>(sg, x, (int)k, rows_per_wave, status, s)
+                        : launch_fmt<1, kQ4_0>(sg, x, (int)k, rows_per_wave, status, s);
+  }
   const long long grid = (n + 3) / 4;
   if (fmt == kQ8_0)
     qgemv_w8a8_generic<kQ8_0><<<static_cast<unsigned>(grid), 256, 0, s>>>(W, x, y, n, k, status);

@@ -39,6 +39,9 @@ _SIGS = {
     "qc_hip_qgemv": ([_I, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_qgemm": ([_I, _P, _P, _P, _LL, _LL, _LL, _P], _I),
     "qc_hip_qgemv_w8a8": ([_I, _P, _P, _P, _LL, _LL, _P, _P], _I),
+    "qc_hip_qgemv_up_gate": ([_I, _P, _P, _P, _P, _P, _LL, _LL, _P], _I),
+    "qc_hip_qgemv_up_gate_activation": ([_I, _P, _P, _P, _P, _LL, _LL, _I, _P], _I),
+    "qc_hip_qgemv_qkv": ([_I, _P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _P], _I),
     "qc_hip_qgemv_w8a8_packed_size": ([_I, _LL, _LL, _P], _I),
     "qc_hip_qgemv_w8a8_variant": ([_I], ctypes.c_char_p),
     "qc_hip_quantize_int8": ([_P, _P, _P, _LL, _LL, _LL, _P, _P], _I),
@@ -97,6 +100,21 @@ def qgemv_raw(fmt, packed, x, y, n, k, stream=None):
 def qgemv_w8a8_raw(fmt, packed, x, y, n, k, dev_status=None, stream=None):
     return lib.qc_hip_qgemv_w8a8(fmt, _ptr(packed), _ptr(x), _ptr(y), n, k, _ptr(dev_status),
                                  _stream(stream))
+
+
+def qgemv_up_gate_raw(fmt, p_up, p_gate, x, up, gate, n, k, stream=None):
+    return lib.qc_hip_qgemv_up_gate(fmt, _ptr(p_up), _ptr(p_gate), _ptr(x), _ptr(up), _ptr(gate),
+                                    n, k, _stream(stream))
+
+
+def qgemv_up_gate_activation_raw(fmt, p_up, p_gate, x, out, n, k, gelu_tanh=True, stream=None):
+    return lib.qc_hip_qgemv_up_gate_activation(fmt, _ptr(p_up), _ptr(p_gate), _ptr(x), _ptr(out),
+                                               n, k, int(bool(gelu_tanh)), _stream(stream))
+
+
+def qgemv_qkv_raw(fmt, pq, pk, pv, x, q, k_out, v_out, query_dim, kv_dim, input_dim, stream=None):
+    return lib.qc_hip_qgemv_qkv(fmt, _ptr(pq), _ptr(pk), _ptr(pv), _ptr(x), _ptr(q), _ptr(k_out),
+                                _ptr(v_out), query_dim, kv_dim, input_dim, _stream(stream))
 
 
 def qgemm_raw(fmt, packed, x, y, m, n, k, stream=None):

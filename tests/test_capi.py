@@ -70,6 +70,16 @@ def test_packed_size_and_validation_without_device():
     assert q.lib.qc_hip_int8_gemm(None, None, None, None, None, None, None, 1, 1, 1, 0, None,
                                   None) == 3
     assert q.lib.qc_hip_int8_gemm_i32(None, None, None, 1, 1, 131072, None) == 1
+    # fused projections (kernels/quantization/qgemv_fused_ref.cpp:194-327):
+    # shape products, nulls, then the packed layout (format, K)
+    L = q.lib
+    assert L.qc_hip_qgemv_up_gate(1, None, None, None, None, None, 0, 64, None) == 1
+    assert L.qc_hip_qgemv_up_gate(9, None, None, None, None, None, 4, 64, None) == 3
+    assert L.qc_hip_qgemv_up_gate_activation(1, None, None, None, None, 4, -1, 1, None) == 1
+    assert L.qc_hip_qgemv_qkv(1, None, None, None, None, None, None, None, 4, 0, 64, None) == 1
+    assert L.qc_hip_qgemv_qkv(1, None, None, None, None, None, None, None,
+                              2, (1 << 62), 1, None) == 1
+    assert L.qc_hip_qgemv_qkv(1, None, None, None, None, None, None, None, 4, 4, 64, None) == 3
     # qgemv_w8a8 (src/dispatch/qgemv_w8a8.cpp:99-105,130-143): format, shape, nulls
     assert q.lib.qc_hip_qgemv_w8a8(7, None, None, None, 1, 32, None, None) == 2
     assert q.lib.qc_hip_qgemv_w8a8(7, None, None, None, 1, 33, None, None) == 2

@@ -1,0 +1,115 @@
+"""GPU parity: fused decode projections (qgemv_up_gate, qgemv_up_gate_activation,
+qgemv_qkv; kernels/quantization/qgemv_fused_ref.cpp:184-327) through the C ABI.
+
+Each projection of the fused launch uses the GEMV's per-row arithmetic, so it
+is bit-identical to qc_hip_qgemv of that matrix (itself held to the 1e-4
+contract against the f64 oracle in test_gpu_gemv.py), and also checked against
+the f64 oracle here.  The activation form is checked against
+activation(gate) * up evaluated in f64 from the plain fused projections.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _packed(oracle, synth, fmt, n, k, seed):
+    w = synth.normal_fast(seed, n * k, 0.02).reshape(n, k)
+    st, p = oracle.pack(fmt, w)
+    assert st == 0
+    return p
+
+
+def _dev(arr, dev, offset=0):
+    import torch
+    t = torch.zeros(arr.size + offset, dtype=torch.uint8 if arr.dtype == np.uint8 else torch.float32,
+                    device=dev)
+    t[offset:] = torch.from_numpy(arr).to(dev)
+    return t[offset:]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def _check_contract(oracle, fmt, packed, x, y, n, k):
+    y64, wn = oracle.gemv_f64(fmt, packed, x, n, k)
+    ok, worst = oracle.within_contract(y, y64, wn, x, TOL)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("fmt,n,k,w_off", [(1, 14336, 4096, 0), (0, 4096, 4096, 0),
+                                           (1, 300, 64, 0), (0, 1000, 96, 0), (1, 257, 4096, 2),
+                                           (0, 70, 14336, 0)])
+def test_up_gate(qc, oracle, synth, dev, fmt, n, k, w_off):
+    import torch
+    print(f"up_gate fmt={fmt} n={n} k={k} w_off={w_off}", flush=True)
+    pu = _packed(oracle, synth, fmt, n, k, 10 + n)
+    pg = _packed(oracle, synth, fmt, n, k, 20 + n)
+    x = synth.normal_fast(30 + k, k)
+    PU, PG, X = _dev(pu, dev, w_off), _dev(pg, dev, w_off), _dev(x, dev)
+    up = torch.empty(n, dtype=torch.float32, device=dev)
+    gate = torch.empty(n, dtype=torch.float32, device=dev)
+    assert qc.qgemv_up_gate_raw(fmt, PU, PG, X, up, gate, n, k) == 0
+    up, gate = up.cpu().numpy(), gate.cpu().numpy()
+    assert np.array_equal(_bits(up), _bits(qc.qgemv(fmt, PU, X, n, k).cpu().numpy()))
+    assert np.array_equal(_bits(gate), _bits(qc.qgemv(fmt, PG, X, n, k).cpu().numpy()))
+    for p, y in ((pu, up), (pg, gate)):
+        _check_contract(oracle, fmt, p, x, y, n, k)
+
+
+def _act64(v, gelu):
+    v = v.astype(np.float64)
+    if gelu:
+        return 0.5 * v * (1.0 + np.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))
+    return v / (1.0 + np.exp(-v))
+
+
+@pytest.mark.parametrize("fmt,n,k", [(1, 14336, 4096), (0, 512, 4096), (1, 130, 96)])
+@pytest.mark.parametrize("gelu", [True, False])
+def test_up_gate_activation(qc, oracle, synth, dev, fmt, n, k, gelu):
+    import torch
+    print(f"up_gate_activation fmt={fmt} n={n} k={k} gelu={gelu}", flush=True)
+    pu = _packed(oracle, synth, fmt, n, k, 40 + n)
+    pg = _packed(oracle, synth, fmt, n, k, 50 + n)
+    x = synth.normal_fast(60 + k, k) * np.float32(3.0)     # gate values over several units
+    PU, PG, X = _dev(pu, dev), _dev(pg, dev), _dev(x, dev)
+    up = torch.empty(n, dtype=torch.float32, device=dev)
+    gate = torch.empty(n, dtype=torch.float32, device=dev)
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    assert qc.qgemv_up_gate_raw(fmt, PU, PG, X, up, gate, n, k) == 0
+    assert qc.qgemv_up_gate_activation_raw(fmt, PU, PG, X, out, n, k, gelu) == 0
+    up, gate, out = (t.cpu().numpy() for t in (up, gate, out))
+    want = _act64(gate, gelu) * up.astype(np.float64)
+    # f32 activation rounding (a few ulp) plus, for GELU-tanh, the cancellation
+    # in 1 + tanh(z) for negative gates (~ulp(1) * |gate|)
+    bound = 1e-5 * np.abs(gate.astype(np.float64) * up) + 2e-6 * np.abs(want) + 1e-30
+    assert np.all(np.abs(out - want) <= bound)
+    # and against the f64 oracle's projections
+    g64, _ = oracle.gemv_f64(fmt, pg, x, n, k)
+    u64, _ = oracle.gemv_f64(fmt, pu, x, n, k)
+    ref = _act64(g64, gelu) * u64
+    scale = np.max(np.abs(ref)) + 1e-30
+    assert np.max(np.abs(out - ref)) <= 1e-3 * scale
+
+
+@pytest.mark.parametrize("fmt,qd,kvd,k", [(1, 4096, 1024, 4096), (0, 300, 64, 256),
+                                          (1, 96, 32, 160), (0, 2048, 512, 8192)])
+def test_qkv(qc, oracle, synth, dev, fmt, qd, kvd, k):
+    import torch
+    print(f"qkv fmt={fmt} q={qd} kv={kvd} k={k}", flush=True)
+    pq = _packed(oracle, synth, fmt, qd, k, 70)
+    pk = _packed(oracle, synth, fmt, kvd, k, 71)
+    pv = _packed(oracle, synth, fmt, kvd, k, 72)
+    x = synth.normal_fast(73 + k, k)
+    PQ, PK, PV, X = _dev(pq, dev), _dev(pk, dev), _dev(pv, dev), _dev(x, dev)
+    q = torch.empty(qd, dtype=torch.float32, device=dev)
+    ko = torch.empty(kvd, dtype=torch.float32, device=dev)
+    vo = torch.empty(kvd, dtype=torch.float32, device=dev)
+    assert qc.qgemv_qkv_raw(fmt, PQ, PK, PV, X, q, ko, vo, qd, kvd, k) == 0
+    for P, p, y, n in ((PQ, pq, q, qd), (PK, pk, ko, kvd), (PV, pv, vo, kvd)):
+        y = y.cpu().numpy()
+        assert np.array_equal(_bits(y), _bits(qc.qgemv(fmt, P, X, n, k).cpu().numpy()))
+        _check_contract(oracle, fmt, p, x, y, n, k)
