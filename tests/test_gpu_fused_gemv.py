@@ -40,16 +40,19 @@ def _check_contract(oracle, fmt, packed, x, y, n, k):
     assert ok, worst
 
 
-@pytest.mark.parametrize("fmt,n,k,w_off", [(1, 14336, 4096, 0), (0, 4096, 4096, 0),
-                                           (1, 300, 64, 0), (0, 1000, 96, 0), (1, 257, 4096, 2),
-                                           (0, 70, 14336, 0)])
-def test_up_gate(qc, oracle, synth, dev, fmt, n, k, w_off):
+# w_off: weights 2 bytes off 4-byte alignment; x_off: x one or three floats
+# off 16-byte alignment (both take the per-matrix route)
+@pytest.mark.parametrize("fmt,n,k,w_off,x_off", [(1, 14336, 4096, 0, 0), (0, 4096, 4096, 0, 0),
+                                                 (1, 300, 64, 0, 0), (0, 1000, 96, 0, 0),
+                                                 (1, 257, 4096, 2, 0), (0, 70, 14336, 0, 0),
+                                                 (1, 1024, 4096, 0, 1), (0, 300, 96, 0, 3)])
+def test_up_gate(qc, oracle, synth, dev, fmt, n, k, w_off, x_off):
     import torch
-    print(f"up_gate fmt={fmt} n={n} k={k} w_off={w_off}", flush=True)
+    print(f"up_gate fmt={fmt} n={n} k={k} w_off={w_off} x_off={x_off}", flush=True)
     pu = _packed(oracle, synth, fmt, n, k, 10 + n)
     pg = _packed(oracle, synth, fmt, n, k, 20 + n)
     x = synth.normal_fast(30 + k, k)
-    PU, PG, X = _dev(pu, dev, w_off), _dev(pg, dev, w_off), _dev(x, dev)
+    PU, PG, X = _dev(pu, dev, w_off), _dev(pg, dev, w_off), _dev(x, dev, x_off)
     up = torch.empty(n, dtype=torch.float32, device=dev)
     gate = torch.empty(n, dtype=torch.float32, device=dev)
     assert qc.qgemv_up_gate_raw(fmt, PU, PG, X, up, gate, n, k) == 0
@@ -67,15 +70,16 @@ def _act64(v, gelu):
     return v / (1.0 + np.exp(-v))
 
 
-@pytest.mark.parametrize("fmt,n,k", [(1, 14336, 4096), (0, 512, 4096), (1, 130, 96)])
+@pytest.mark.parametrize("fmt,n,k,x_off", [(1, 14336, 4096, 0), (0, 512, 4096, 0),
+                                           (1, 130, 96, 0), (0, 700, 4096, 1), (1, 96, 160, 2)])
 @pytest.mark.parametrize("gelu", [True, False])
-def test_up_gate_activation(qc, oracle, synth, dev, fmt, n, k, gelu):
+def test_up_gate_activation(qc, oracle, synth, dev, fmt, n, k, x_off, gelu):
     import torch
-    print(f"up_gate_activation fmt={fmt} n={n} k={k} gelu={gelu}", flush=True)
+    print(f"up_gate_activation fmt={fmt} n={n} k={k} x_off={x_off} gelu={gelu}", flush=True)
     pu = _packed(oracle, synth, fmt, n, k, 40 + n)
     pg = _packed(oracle, synth, fmt, n, k, 50 + n)
     x = synth.normal_fast(60 + k, k) * np.float32(3.0)     # gate values over several units
-    PU, PG, X = _dev(pu, dev), _dev(pg, dev), _dev(x, dev)
+    PU, PG, X = _dev(pu, dev), _dev(pg, dev), _dev(x, dev, x_off)
     up = torch.empty(n, dtype=torch.float32, device=dev)
     gate = torch.empty(n, dtype=torch.float32, device=dev)
     out = torch.empty(n, dtype=torch.float32, device=dev)
@@ -95,16 +99,17 @@ def test_up_gate_activation(qc, oracle, synth, dev, fmt, n, k, gelu):
     assert np.max(np.abs(out - ref)) <= 1e-3 * scale
 
 
-@pytest.mark.parametrize("fmt,qd,kvd,k", [(1, 4096, 1024, 4096), (0, 300, 64, 256),
-                                          (1, 96, 32, 160), (0, 2048, 512, 8192)])
-def test_qkv(qc, oracle, synth, dev, fmt, qd, kvd, k):
+@pytest.mark.parametrize("fmt,qd,kvd,k,x_off", [(1, 4096, 1024, 4096, 0), (0, 300, 64, 256, 0),
+                                                (1, 96, 32, 160, 0), (0, 2048, 512, 8192, 0),
+                                                (1, 512, 128, 4096, 1)])
+def test_qkv(qc, oracle, synth, dev, fmt, qd, kvd, k, x_off):
     import torch
-    print(f"qkv fmt={fmt} q={qd} kv={kvd} k={k}", flush=True)
+    print(f"qkv fmt={fmt} q={qd} kv={kvd} k={k} x_off={x_off}", flush=True)
     pq = _packed(oracle, synth, fmt, qd, k, 70)
     pk = _packed(oracle, synth, fmt, kvd, k, 71)
     pv = _packed(oracle, synth, fmt, kvd, k, 72)
     x = synth.normal_fast(73 + k, k)
-    PQ, PK, PV, X = _dev(pq, dev), _dev(pk, dev), _dev(pv, dev), _dev(x, dev)
+    PQ, PK, PV, X = _dev(pq, dev), _dev(pk, dev), _dev(pv, dev), _dev(x, dev, x_off)
     q = torch.empty(qd, dtype=torch.float32, device=dev)
     ko = torch.empty(kvd, dtype=torch.float32, device=dev)
     vo = torch.empty(kvd, dtype=torch.float32, device=dev)
