@@ -53,6 +53,10 @@ def _load():
     lib.qco_qgemv_w8a8.argtypes = [ctypes.c_int, _P, _P, _P, _LL, _LL]
     lib.qco_int8_gemm.argtypes = [_P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, ctypes.c_int]
     lib.qco_int8_gemm_entries.argtypes = [_P, _P, _P, _P, _P, _P, _LL, _LL, _P, _P]
+    lib.qco_rms_norm_add_quant_int8.argtypes = [_P, _P, _P, _P, _P, _P, _LL, _LL,
+                                                ctypes.c_float, _LL]
+    lib.qco_quantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
+    lib.qco_dequantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
     lib.qco_int8_gemm_entries.restype = None
     return lib
 
@@ -144,6 +148,55 @@ def quantize_int8(x: np.ndarray, group_size=0):
     return st, codes, scales
 
 
+# Sentinels for outputs a call may leave unwritten (invalid groups).
+CODE_SENTINEL = 0x5A
+SCALE_SENTINEL = -7.0
+
+
+def _norm_outputs(rows, hidden, group_size):
+    g = hidden if group_size == 0 else group_size
+    groups = hidden // g if g > 0 and hidden % g == 0 else 1
+    codes = np.full((rows, hidden), CODE_SENTINEL, dtype=np.int8)
+    resid = np.zeros((rows, hidden), dtype=np.float32)
+    scales = np.full((rows, groups), SCALE_SENTINEL, dtype=np.float32)
+    return codes, resid, scales
+
+
+def rms_norm_add_quant_int8(x, residual, weight, eps=1e-5, group_size=0):
+    """Residual add + RMSNorm + dynamic int8 quantization.  Returns (status,
+    codes, residual_out, scales); unwritten outputs keep the sentinels."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    residual = np.ascontiguousarray(residual, dtype=np.float32)
+    weight = np.ascontiguousarray(weight, dtype=np.float32)
+    rows, hidden = x.shape
+    codes, resid, scales = _norm_outputs(rows, hidden, group_size)
+    st = lib.qco_rms_norm_add_quant_int8(_ptr(x), _ptr(residual), _ptr(weight), _ptr(codes),
+                                         _ptr(resid), _ptr(scales), rows, hidden, eps,
+                                         group_size)
+    return st, codes, resid, scales
+
+
+def quantize_int8_asymmetric(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, dim = x.shape
+    codes = np.zeros((rows, dim), dtype=np.int8)
+    scales = np.zeros(rows, dtype=np.float32)
+    zps = np.zeros(rows, dtype=np.int32)
+    st = lib.qco_quantize_int8_asymmetric(_ptr(x), _ptr(codes), _ptr(scales), _ptr(zps), rows,
+                                          dim)
+    return st, codes, scales, zps
+
+
+def dequantize_int8_asymmetric(codes, scales, zps):
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    rows, dim = codes.shape
+    out = np.zeros((rows, dim), dtype=np.float32)
+    st = lib.qco_dequantize_int8_asymmetric(_ptr(codes), _ptr(np.ascontiguousarray(scales, np.float32)),
+                                            _ptr(np.ascontiguousarray(zps, np.int32)), _ptr(out),
+                                            rows, dim)
+    return st, out
+
+
 def gemv_w8a8(fmt, packed, x, n, k):
     """qgemv_w8a8: per-32-block int8 activations, integer block dots,
     y = sum_b (float(dot) * d_w) * d_x in block order.  Returns (status, y)."""
@@ -215,6 +268,10 @@ class Reference:
             getattr(L, name).argtypes = [_P, _P, _P, _LL, _LL]
             getattr(L, name).restype = None
         L.qcref_set_num_threads.argtypes = [ctypes.c_int]
+        L.qcref_rms_norm_add_quant_int8.argtypes = [_P, _P, _P, _P, _P, _P, _LL, _LL,
+                                                    ctypes.c_float, _LL]
+        L.qcref_quantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
+        L.qcref_dequantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
         L.qcref_set_num_threads.restype = None
 
     @staticmethod
@@ -270,6 +327,36 @@ class Reference:
         fn = self.lib.qcref_q8_0_gemv_w8a8 if fmt == Q8_0 else self.lib.qcref_q4_0_gemv_w8a8
         fn(_ptr(packed), _ptr(x), _ptr(y), n, k)
         return y
+
+    def rms_norm_add_quant_int8(self, x, residual, weight, eps=1e-5, group_size=0):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        residual = np.ascontiguousarray(residual, dtype=np.float32)
+        weight = np.ascontiguousarray(weight, dtype=np.float32)
+        rows, hidden = x.shape
+        codes, resid, scales = _norm_outputs(rows, hidden, group_size)
+        st = self.lib.qcref_rms_norm_add_quant_int8(_ptr(x), _ptr(residual), _ptr(weight),
+                                                    _ptr(codes), _ptr(resid), _ptr(scales),
+                                                    rows, hidden, eps, group_size)
+        return st, codes, resid, scales
+
+    def quantize_int8_asymmetric(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, dim = x.shape
+        codes = np.zeros((rows, dim), dtype=np.int8)
+        scales = np.zeros(rows, dtype=np.float32)
+        zps = np.zeros(rows, dtype=np.int32)
+        st = self.lib.qcref_quantize_int8_asymmetric(_ptr(x), _ptr(codes), _ptr(scales),
+                                                     _ptr(zps), rows, dim)
+        return st, codes, scales, zps
+
+    def dequantize_int8_asymmetric(self, codes, scales, zps):
+        codes = np.ascontiguousarray(codes, dtype=np.int8)
+        rows, dim = codes.shape
+        out = np.zeros((rows, dim), dtype=np.float32)
+        st = self.lib.qcref_dequantize_int8_asymmetric(
+            _ptr(codes), _ptr(np.ascontiguousarray(scales, np.float32)),
+            _ptr(np.ascontiguousarray(zps, np.int32)), _ptr(out), rows, dim)
+        return st, out
 
     def variant(self):
         return self.lib.qcref_int8_gemm_variant().decode()

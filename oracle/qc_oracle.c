@@ -448,3 +448,133 @@ void qco_int8_gemm_entries(const int8_t* w, const int8_t* x, const float* ws,
     y[e] = (float)dot * ws[c] * as[r];
   }
 }
+
+/* ------------------------------------------- rms_norm_add_quant_int8 --- */
+
+/* kernels/norms/norm_quant_ref.cpp:106-114 (valid_dynamic_shape: rows x
+ * hidden product, finite eps >= 0, group 0 -> hidden, hidden % group == 0),
+ * 117-130 (shape, then nulls), 33-92 (add_and_measure, RMS branch; the
+ * x86-64 build runs the plain loop at 82-89: value = x + residual stored to
+ * residual_out, sumsq += double(value) * value in element order, inverse =
+ * float(1 / sqrt(sumsq / hidden + eps)) in double), 94-104 (normalized_at:
+ * (residual_out * inverse) * weight in f32), 150-168 and 224-290 (per group:
+ * maximum = max(maximum, |value|), a non-finite value marks the group
+ * invalid and skips it; scale = maximum / 127, inverse = scale > 0 ? 1 /
+ * scale : 0, code = clamp(nearbyint(value * inverse), -127, 127)).  Every
+ * row is processed; an invalid group leaves its scale and codes unwritten
+ * and the call returns kInvalidArgument at the end. */
+int qco_rms_norm_add_quant_int8(const float* x, const float* residual, const float* weight,
+                                int8_t* codes, float* residual_out, float* scales,
+                                long long rows, long long hidden, float eps,
+                                long long group_size) {
+  if (rows <= 0 || hidden <= 0 || rows > LLONG_MAX / hidden || !isfinite(eps) || eps < 0.0f)
+    return QCO_INVALID_SHAPE;
+  if (group_size == 0) group_size = hidden;
+  if (group_size <= 0 || hidden % group_size != 0) return QCO_INVALID_SHAPE;
+  if (!x || !residual || !weight || !codes || !residual_out || !scales)
+    return QCO_INVALID_ARGUMENT;
+  float* values = (float*)malloc((size_t)group_size * sizeof(float));
+  if (values == NULL) return QCO_OUT_OF_MEMORY;
+  const long long groups = hidden / group_size;
+  int invalid = 0;
+  for (long long r = 0; r < rows; ++r) {
+    const long long base = r * hidden;
+    double sumsq = 0.0;
+    for (long long i = 0; i < hidden; ++i) {
+      const float value = x[base + i] + residual[base + i];
+      residual_out[base + i] = value;
+      sumsq += (double)value * value;
+    }
+    const float inverse = (float)(1.0 / sqrt(sumsq / (double)hidden + (double)eps));
+    for (long long g = 0; g < groups; ++g) {
+      float maximum = 0.0f;
+      int bad = 0;
+      for (long long i = 0; i < group_size; ++i) {
+        const long long col = g * group_size + i;
+        const float value = (residual_out[base + col] * inverse) * weight[col];
+        values[i] = value;
+        if (!isfinite(value)) bad = 1;
+        const float a = fabsf(value);
+        if (maximum < a) maximum = a;
+      }
+      if (bad) {
+        invalid = 1;
+        continue;
+      }
+      const float scale = maximum / 127.0f;
+      scales[r * groups + g] = scale;
+      const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+      for (long long i = 0; i < group_size; ++i) {
+        int q = (int)nearbyintf(values[i] * inv);
+        q = q < -127 ? -127 : (q > 127 ? 127 : q);
+        codes[base + g * group_size + i] = (int8_t)q;
+      }
+    }
+  }
+  free(values);
+  return invalid ? QCO_INVALID_ARGUMENT : QCO_OK;
+}
+
+/* ------------------------------------------ quantize_int8_asymmetric --- */
+
+/* static_cast<int>(double) as the reference's x86-64 build executes it
+ * (cvttsd2si / cvttpd2dq): truncation toward zero, and INT_MIN for NaN or a
+ * value outside the int range.  int + int and int - int wrap. */
+static int x86_double_to_int(double d) {
+  if (!(d > -2147483649.0 && d < 2147483648.0)) return INT_MIN;
+  return (int)d;
+}
+static int wrap_add(int a, int b) { return (int)((uint32_t)a + (uint32_t)b); }
+static int wrap_sub(int a, int b) { return (int)((uint32_t)a - (uint32_t)b); }
+
+/* kernels/quantization/quantization_ref.cpp:190-226.  Whole-input finite
+ * check first; per row, in double: range = max - min, scale_value = range > 0
+ * ? range / 255 : max(|min| / 127, 1e-7), scale = float(scale_value), zero =
+ * int(nearbyint(-128 - min / scale_value)), code = clamp(int(nearbyint(x /
+ * scale_value)) + zero, -128, 127). */
+int qco_quantize_int8_asymmetric(const float* x, int8_t* codes, float* scales,
+                                 int* zero_points, long long rows, long long dim) {
+  if (rows <= 0 || dim <= 0 || rows > LLONG_MAX / dim) return QCO_INVALID_SHAPE;
+  if (!x || !codes || !scales || !zero_points) return QCO_INVALID_ARGUMENT;
+  for (long long i = 0; i < rows * dim; ++i)
+    if (!isfinite(x[i])) return QCO_INVALID_ARGUMENT;
+  for (long long r = 0; r < rows; ++r) {
+    const float* in = x + r * dim;
+    float lo = in[0], hi = in[0];
+    for (long long i = 1; i < dim; ++i) {
+      if (in[i] < lo) lo = in[i];
+      if (hi < in[i]) hi = in[i];
+    }
+    const double minimum = (double)lo, maximum = (double)hi;
+    const double range = maximum - minimum;
+    double scale_value;
+    if (range > 0.0) {
+      scale_value = range / 255.0;
+    } else {
+      const double a = fabs(minimum) / 127.0;
+      scale_value = a < 1e-7 ? 1e-7 : a;
+    }
+    const int zero = x86_double_to_int(nearbyint(-128.0 - minimum / scale_value));
+    scales[r] = (float)scale_value;
+    zero_points[r] = zero;
+    for (long long i = 0; i < dim; ++i) {
+      int q = wrap_add(x86_double_to_int(nearbyint((double)in[i] / scale_value)), zero);
+      q = q < -128 ? -128 : (q > 127 ? 127 : q);
+      codes[r * dim + i] = (int8_t)q;
+    }
+  }
+  return QCO_OK;
+}
+
+/* kernels/quantization/quantization_ref.cpp:228-244: out = scale[row] *
+ * float(int(code) - zero_point[row]). */
+int qco_dequantize_int8_asymmetric(const int8_t* codes, const float* scales,
+                                   const int* zero_points, float* out, long long rows,
+                                   long long dim) {
+  if (rows <= 0 || dim <= 0 || rows > LLONG_MAX / dim) return QCO_INVALID_SHAPE;
+  if (!codes || !scales || !zero_points || !out) return QCO_INVALID_ARGUMENT;
+  for (long long r = 0; r < rows; ++r)
+    for (long long i = 0; i < dim; ++i)
+      out[r * dim + i] = scales[r] * (float)wrap_sub((int)codes[r * dim + i], zero_points[r]);
+  return QCO_OK;
+}

@@ -70,6 +70,21 @@ void qco_int8_gemm_entries(const int8_t* w, const int8_t* x, const float* ws,
                            const float* as, const long long* rows, const long long* cols,
                            long long count, long long k, int64_t* acc64, float* y);
 
+/* Residual add + RMSNorm + dynamic int8 quantization (per row, or per group
+ * of group_size columns); status 3 after all rows if a group's normalized
+ * values are not finite (that group's scale and codes are left unwritten). */
+int qco_rms_norm_add_quant_int8(const float* x, const float* residual, const float* weight,
+                                int8_t* codes, float* residual_out, float* scales,
+                                long long rows, long long hidden, float eps,
+                                long long group_size);
+
+/* Per-row asymmetric int8: codes in [-128, 127], value ~ scale * (code - zero). */
+int qco_quantize_int8_asymmetric(const float* x, int8_t* codes, float* scales,
+                                 int* zero_points, long long rows, long long dim);
+int qco_dequantize_int8_asymmetric(const int8_t* codes, const float* scales,
+                                   const int* zero_points, float* out, long long rows,
+                                   long long dim);
+
 #ifdef __cplusplus
 }
 #endif

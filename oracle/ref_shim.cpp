@@ -10,6 +10,9 @@
 //   int8_gemm   -> the public dispatcher    (src/dispatch/int8_gemm.cpp:67-94)
 //   quantize_int8 -> the public function    (kernels/quantization/quantization_ref.cpp:143-168)
 //   qgemv_w8a8  -> quant::q{4,8}_0_gemv_w8a8_ref (src/dispatch/qgemv_w8a8.cpp:27-34,66-73)
+//   rms_norm_add_quant_int8, quantize_int8_asymmetric, dequantize_int8_asymmetric
+//               -> the public functions  (kernels/norms/norm_quant_ref.cpp:1060-1068;
+//                                          kernels/quantization/quantization_ref.cpp:190-244)
 #include <cstddef>
 #include <cstdint>
 
@@ -83,6 +86,26 @@ void qcref_q8_0_gemv_w8a8(const void* packed, const float* x, float* y, long lon
 }
 
 const char* qcref_int8_gemm_variant() { return qc::int8_gemm_variant(); }
+
+int qcref_rms_norm_add_quant_int8(const float* x, const float* residual, const float* weight,
+                                  std::int8_t* codes, float* residual_out, float* scales,
+                                  long long rows, long long hidden, float eps,
+                                  long long group_size) {
+  return static_cast<int>(qc::rms_norm_add_quant_int8(x, residual, weight, codes, residual_out,
+                                                      scales, rows, hidden, eps, group_size));
+}
+
+int qcref_quantize_int8_asymmetric(const float* x, std::int8_t* codes, float* scales,
+                                   int* zero_points, long long rows, long long dim) {
+  return static_cast<int>(qc::quantize_int8_asymmetric(x, codes, scales, zero_points, rows, dim));
+}
+
+int qcref_dequantize_int8_asymmetric(const std::int8_t* codes, const float* scales,
+                                     const int* zero_points, float* out, long long rows,
+                                     long long dim) {
+  return static_cast<int>(qc::dequantize_int8_asymmetric(codes, scales, zero_points, out, rows,
+                                                        dim));
+}
 
 void qcref_set_num_threads(int n) { qc::set_num_threads(n); }
 int qcref_num_threads() { return qc::num_threads(); }

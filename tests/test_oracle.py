@@ -27,6 +27,20 @@ mistake would break:
                         over its own test grid (test_int8_gemm.cpp:106-116),
                         numpy int64 matmul, and the known answers
                         {0, -1.5} / AZP {-5, -2} (test_projection_ops.cpp:81-97).
+  * rms_norm_add_quant_int8 -- bit-identical to the reference's function
+                        (oracle/_ref) over random shapes, groups, eps, scales
+                        spanning 60 decades, invalid groups (overflowing or
+                        non-finite weights, NaN inputs) and every validation
+                        case; the reference test's own known answer
+                        (test_remaining_ops.cpp:197-215), its codes worked by
+                        hand; residual_out = x + residual exactly; per group
+                        max |code| = 127 and codes within half a step of the
+                        float64 normalized values.
+  * quantize_int8_asymmetric / dequantize -- bit-identical to the reference's
+                        functions on random rows and on the out-of-range
+                        conversions (1-ulp spreads); the reference test's
+                        known answers (test_quantization.cpp:113-136), both
+                        rows worked by hand; round trip within half a step.
 """
 import math
 
@@ -369,3 +383,138 @@ def test_int8_gemm_entries(oracle):
     acc, ye = oracle.int8_gemm_entries(w, x, ws, as_, rows, cols)
     assert np.array_equal(acc, (x.astype(np.int64) @ w.astype(np.int64).T)[rows, cols])
     assert np.array_equal(ye.view(np.uint32), y[rows, cols].view(np.uint32))
+
+
+# ------------------------------------------------ rms_norm_add_quant_int8 ---
+
+def _bits_equal(a, b):
+    """(status, arrays...) tuples equal, the arrays bit for bit."""
+    return a[0] == b[0] and all(
+        np.array_equal(np.ascontiguousarray(p).view(np.uint8), np.ascontiguousarray(q).view(np.uint8))
+        for p, q in zip(a[1:], b[1:]))
+
+
+def test_rms_norm_add_quant_known_answer(oracle):
+    # test_remaining_ops.cpp:197-215: x = {1,2,3,4}, residual = 1, weight = 1
+    x = np.array([[1, 2, 3, 4]], np.float32)
+    st, c, ro, sc = oracle.rms_norm_add_quant_int8(x, np.ones((1, 4), np.float32),
+                                                   np.ones(4, np.float32))
+    assert st == 0 and ro[0, 3] == 5.0
+    # by hand: values {2,3,4,5}, codes rint(v / 5 * 127) = {51, 76, 102, 127}
+    assert list(c[0]) == [51, 76, 102, 127]
+    inv = np.float32(1.0 / np.sqrt(54.0 / 4.0 + np.float64(np.float32(1e-5))))
+    assert sc[0, 0] == np.float32(np.float32(5.0) * inv) / np.float32(127.0)
+    # dequantized within the reference test's 0.02 of rms_norm_add
+    ref = np.array([2, 3, 4, 5], np.float64) / np.sqrt(54.0 / 4 + 1e-5)
+    assert np.all(np.abs(c[0] * np.float64(sc[0, 0]) - ref) <= 0.02)
+
+
+def _norm_case(rng, rows, hidden, decades=30):
+    sc = 10.0 ** rng.uniform(-decades, decades)
+    x = (rng.standard_normal((rows, hidden)) * sc).astype(np.float32)
+    r = (rng.standard_normal((rows, hidden)) * sc).astype(np.float32)
+    w = rng.standard_normal(hidden).astype(np.float32)
+    return x, r, w
+
+
+def test_rms_norm_add_quant_matches_reference(oracle, ref):
+    rng = np.random.default_rng(11)
+    for trial in range(120):
+        hidden = int(rng.choice([4, 32, 96, 128, 1000, 4096]))
+        group = int(rng.choice([0, hidden, 4, 32])) if hidden % 32 == 0 else 0
+        eps = float(rng.choice([1e-5, 0.0, 1e-6]))
+        x, r, w = _norm_case(rng, int(rng.integers(1, 5)), hidden)
+        assert _bits_equal(oracle.rms_norm_add_quant_int8(x, r, w, eps, group),
+                           ref.rms_norm_add_quant_int8(x, r, w, eps, group))
+
+
+def test_rms_norm_add_quant_invalid_groups_match_reference(oracle, ref):
+    rng = np.random.default_rng(12)
+    x, r, w = _norm_case(rng, 3, 64, 1)
+    w[5] = np.float32(3e38)
+    w[40] = np.inf
+    for group in (0, 32, 16):
+        a = oracle.rms_norm_add_quant_int8(x, r, w, 1e-5, group)
+        assert a[0] == 3 and _bits_equal(a, ref.rms_norm_add_quant_int8(x, r, w, 1e-5, group))
+    x[1, 3] = np.nan
+    a = oracle.rms_norm_add_quant_int8(x, r, np.ones(64, np.float32), 1e-5, 16)
+    assert a[0] == 3 and np.all(a[3][1] == oracle.SCALE_SENTINEL)
+    assert _bits_equal(a, ref.rms_norm_add_quant_int8(x, r, np.ones(64, np.float32), 1e-5, 16))
+    for eps, group in ((1e-5, 5), (float("nan"), 0), (-1.0, 0), (1e-5, -32), (float("inf"), 0)):
+        assert oracle.rms_norm_add_quant_int8(x, r, w, eps, group)[0] == 1
+        assert ref.rms_norm_add_quant_int8(x, r, w, eps, group)[0] == 1
+
+
+def test_rms_norm_add_quant_properties(oracle):
+    rng = np.random.default_rng(13)
+    for hidden, group in ((4096, 0), (4096, 32), (96, 0), (256, 128)):
+        x, r, w = _norm_case(rng, 3, hidden, 20)
+        st, c, ro, sc = oracle.rms_norm_add_quant_int8(x, r, w, 1e-5, group)
+        assert st == 0
+        assert np.array_equal(ro.view(np.uint32), (x + r).view(np.uint32))
+        v = ro.astype(np.float64)
+        n64 = v / np.sqrt(np.mean(v * v, axis=1, keepdims=True) + np.float64(np.float32(1e-5)))
+        n64 = n64 * w.astype(np.float64)
+        g = hidden if group == 0 else group
+        cg = c.reshape(3, hidden // g, g).astype(np.float64)
+        scg = sc.reshape(3, hidden // g, 1).astype(np.float64)
+        assert np.all(np.abs(cg).max(axis=2) == 127)
+        err = np.abs(cg * scg - n64.reshape(3, hidden // g, g))
+        assert np.all(err <= scg * (0.5 + 1e-4))
+
+
+# ------------------------------------------------ quantize_int8_asymmetric ---
+
+def test_quantize_int8_asymmetric_known_answers(oracle):
+    # test_quantization.cpp:113-124 and, by hand: row 0 scale 4/255, zero
+    # rint(-128 + 127.5) = 0, codes rint({-127.5, -31.875, 0, 127.5}) clamped;
+    # row 1 scale 3/255, zero -128 - 85 = -213, codes {85, 170, 255, 340} - 213
+    x = np.array([[-2.0, -0.5, 0.0, 2.0], [1.0, 2.0, 3.0, 4.0]], np.float32)
+    st, c, s, z = oracle.quantize_int8_asymmetric(x)
+    assert st == 0
+    assert list(c[0]) == [-128, -32, 0, 127] and list(c[1]) == [-128, -43, 42, 127]
+    assert list(z) == [0, -213]
+    assert s[0] == np.float32(4.0 / 255.0) and s[1] == np.float32(3.0 / 255.0)
+    st, d = oracle.dequantize_int8_asymmetric(c, s, z)
+    assert st == 0 and abs(d[0, 0] + 2.0) <= 0.02 and abs(d[0, 3] - 2.0) <= 0.02
+    # test_quantization.cpp:125-136: {-FLT_MAX, FLT_MAX} keeps distinct endpoints
+    fmax = np.finfo(np.float32).max
+    st, c, s, z = oracle.quantize_int8_asymmetric(np.array([[-fmax, fmax]], np.float32))
+    assert st == 0 and np.isfinite(s[0]) and s[0] > 0 and list(c[0]) == [-128, 127]
+    # constant row: scale max(|v| / 127, 1e-7), zero -128 - v / scale
+    st, c, s, z = oracle.quantize_int8_asymmetric(np.full((1, 3), 2.54, np.float32))
+    assert s[0] == np.float32(np.float64(np.float32(2.54)) / 127.0) and z[0] == -255
+    bad = np.ones((2, 4), np.float32)
+    bad[1, 1] = np.nan
+    assert oracle.quantize_int8_asymmetric(bad)[0] == 3
+
+
+def test_quantize_int8_asymmetric_matches_reference(oracle, ref):
+    rng = np.random.default_rng(14)
+    cases = [np.array([[0.99999994, 1.0]], np.float32),       # out-of-range zero point
+             np.array([[1e-30, 1e-30], [0.0, -0.0]], np.float32),
+             np.array([[-3.4028235e38, 3.4028235e38]], np.float32)]
+    for trial in range(150):
+        rows, dim = int(rng.integers(1, 5)), int(rng.integers(1, 300))
+        x = (rng.standard_normal((rows, dim)) * 10.0 ** rng.uniform(-40, 38)).astype(np.float32)
+        if trial % 5 == 0:
+            x[:, :] = x[:, :1]
+        if trial % 7 == 0:
+            x += np.float32(rng.uniform(-1e3, 1e3))
+        cases.append(x)
+    for x in cases:
+        a = oracle.quantize_int8_asymmetric(x)
+        b = ref.quantize_int8_asymmetric(x)
+        assert _bits_equal(a, b)
+        assert _bits_equal(oracle.dequantize_int8_asymmetric(*a[1:]),
+                           ref.dequantize_int8_asymmetric(*b[1:]))
+
+
+def test_quantize_int8_asymmetric_round_trip(oracle):
+    rng = np.random.default_rng(15)
+    x = (rng.standard_normal((8, 512)) * 3.0 + 1.0).astype(np.float32)
+    st, c, s, z = oracle.quantize_int8_asymmetric(x)
+    st2, d = oracle.dequantize_int8_asymmetric(c, s, z)
+    assert st == st2 == 0
+    assert np.all(np.abs(d - x) <= s[:, None] * 0.5001)
+    assert np.all(c.min(axis=1) == -128) and np.all(c.max(axis=1) >= 126)
