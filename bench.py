@@ -237,6 +237,53 @@ def quant_case(qc, m, k, steps, warmup):
             "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
 
 
+def norm_quant_case(qc, m, k, steps, warmup):
+    """rms_norm_add_quant_int8 (the W8A8 producer): reads x, residual and the
+    weight, writes residual_out, codes and per-row scales."""
+    import torch
+    dev = torch.device("cuda:0")
+    fp = 4 * m * k * 3 + m * k + 4 * m + 4 * k
+    copies = rotation(fp)
+    xs = [torch.randn((m, k), device=dev) for _ in range(copies)]
+    rs = [torch.randn((m, k), device=dev) for _ in range(copies)]
+    w = torch.randn(k, device=dev)
+    out = torch.empty((m, k), dtype=torch.float32, device=dev)
+    codes = torch.empty((m, k), dtype=torch.int8, device=dev)
+    scales = torch.empty((m, 1), dtype=torch.float32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def launch(i):
+        st = qc.rms_norm_add_quant_int8_raw(xs[i % copies], rs[i % copies], w, codes, out, scales,
+                                            m, k, 1e-5, 0, status)
+        if st:
+            raise RuntimeError(f"rms_norm_add_quant status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu,
+            "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
+
+
+def asym_case(qc, m, k, steps, warmup):
+    import torch
+    dev = torch.device("cuda:0")
+    fp = 4 * m * k + m * k + 8 * m
+    copies = rotation(fp)
+    xs = [torch.randn((m, k), device=dev) for _ in range(copies)]
+    codes = torch.empty((m, k), dtype=torch.int8, device=dev)
+    scales = torch.empty(m, dtype=torch.float32, device=dev)
+    zps = torch.empty(m, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def launch(i):
+        st = qc.quantize_int8_asymmetric_raw(xs[i % copies], codes, scales, zps, m, k, status)
+        if st:
+            raise RuntimeError(f"quantize_int8_asymmetric status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu,
+            "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
+
+
 def w8a8_case(qc, m, n, k, steps, warmup):
     import torch
     dev = torch.device("cuda:0")
@@ -412,6 +459,8 @@ def main():
         s = {}
         if args.only == "w8a8":
             s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
+            s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
+            s["quantize_int8_asymmetric_m2048_k4096"] = asym_case(qc, 2048, 4096, K, W)
             s["w8a8_m2048_k4096_n4096"] = w8a8_case(qc, 2048, 4096, 4096, K, W)
             s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, K, W)
         else:
@@ -441,6 +490,8 @@ def main():
         for m in (4, 8, 16, 32):
             s[f"q8_0_qgemm_m{m}_k4096_n14336"] = qgemm_case(qc, 14336, 4096, m, K, W, seed=4 + m)
         s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
+        s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
+        s["quantize_int8_asymmetric_m2048_k4096"] = asym_case(qc, 2048, 4096, K, W)
         s["w8a8_m2048_k4096_n4096"] = w8a8_case(qc, 2048, 4096, 4096, max(20, K // 4), W)
         s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, max(20, K // 4), W)
         for key, r in layer_sweep(qc, max(20, K // 4), W).items():

@@ -135,6 +135,37 @@ const char* qc_hip_qgemv_w8a8_variant(int format);
 int qc_hip_quantize_int8(const float* x, int8_t* codes, float* scales, long long rows,
                          long long dim, long long group_size, int* dev_status, void* stream);
 
+/* residual_out = x + residual; codes / scales = per-group int8 quantization of
+ * RMSNorm(residual_out) * weight (group_size 0: one group per row; scales is
+ * [rows][hidden / group_size]).  Bit-identical to the reference.  Replaces
+ * rms_norm_add_quant_int8 (include/quixicore_cpu/quantization.h:112-116;
+ * kernels/norms/norm_quant_ref.cpp:1060-1068).  A group whose normalized
+ * values are not finite keeps its scale and codes unwritten: with dev_status
+ * NULL the call blocks and returns 3, with a device int it stays asynchronous
+ * and sets it to 3.  residual_out may be the same array as x or residual. */
+int qc_hip_rms_norm_add_quant_int8(const float* x, const float* residual, const float* weight,
+                                   int8_t* codes, float* residual_out, float* scales,
+                                   long long rows, long long hidden, float eps,
+                                   long long group_size, int* dev_status, void* stream);
+
+/* Per-row asymmetric int8: scale = (max - min) / 255 (or max(|min| / 127,
+ * 1e-7) for a constant row), zero = rint(-128 - min / scale), code =
+ * clamp(rint(x / scale) + zero, -128, 127), all in double as the reference.
+ * Bit-identical.  Replaces quantize_int8_asymmetric
+ * (include/quixicore_cpu/quantization.h:49-51;
+ * kernels/quantization/quantization_ref.cpp:190-226).  dev_status as for
+ * qc_hip_quantize_int8 (non-finite rows left unwritten). */
+int qc_hip_quantize_int8_asymmetric(const float* x, int8_t* codes, float* scales,
+                                    int* zero_points, long long rows, long long dim,
+                                    int* dev_status, void* stream);
+
+/* out = scale[row] * float(code - zero_point[row]).  Replaces
+ * dequantize_int8_asymmetric (include/quixicore_cpu/quantization.h:52-54;
+ * kernels/quantization/quantization_ref.cpp:228-244). */
+int qc_hip_dequantize_int8_asymmetric(const int8_t* codes, const float* scales,
+                                      const int* zero_points, float* out, long long rows,
+                                      long long dim, void* stream);
+
 /* y[m][n] = (float(sum_k W[n][k]*X[m][k] - zp[m]*row_sum[n]) * ws[n]) * as[m]
  * (the zp term only when asymmetric != 0).  Exact integer accumulation.
  * Replaces int8_gemm (include/quixicore_cpu/qgemm.h:235;
@@ -187,6 +218,12 @@ int qc_hip_set_int8_gemm_route(int route);
  * the contract tolerance for every split, and reruns with one split are
  * bit-identical.  Tuning and test knob with no reference counterpart. */
 int qc_hip_set_qgemm_plan(int waves, int stages);
+
+/* on != 0: qc_hip_rms_norm_add_quant_int8 replays the element-order sum of
+ * squares for every row instead of only for rows whose float norm the
+ * parallel sum cannot settle (process-wide; results are identical either
+ * way).  Test knob with no reference counterpart. */
+int qc_hip_set_norm_sequential_sum(int on);
 
 #ifdef __cplusplus
 }

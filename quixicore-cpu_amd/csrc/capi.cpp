@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <initializer_list>
@@ -21,6 +22,7 @@ namespace {
 thread_local std::string g_last_error;
 qc::GemvTuning g_tuning;
 int g_int8_route = qc::kInt8Auto;
+bool g_norm_sequential = false;
 
 int device_error(hipError_t e) {
   g_last_error = hipGetErrorString(e);
@@ -412,6 +414,71 @@ int qc_hip_set_qgemm_plan(int waves, int stages) {
     return QC_INVALID_ARGUMENT;
   g_tuning.qgemm_waves = waves;
   g_tuning.qgemm_stages = stages;
+  return QC_OK;
+}
+
+// kernels/norms/norm_quant_ref.cpp:106-114,117-130 (shape: rows x hidden
+// product, finite eps >= 0, group 0 -> hidden dividing hidden; then nulls).
+// Data-dependent failure (a group whose normalized values are not finite)
+// is reported after the work, as the reference does: that group's scale and
+// codes are left unwritten, everything else is written.
+int qc_hip_rms_norm_add_quant_int8(const float* x, const float* residual, const float* weight,
+                                   int8_t* codes, float* residual_out, float* scales,
+                                   long long rows, long long hidden, float eps,
+                                   long long group_size, int* dev_status, void* stream) {
+  if (!valid_product({rows, hidden}) || !std::isfinite(eps) || eps < 0.0f)
+    return QC_INVALID_SHAPE;
+  if (group_size == 0) group_size = hidden;
+  if (group_size <= 0 || hidden % group_size != 0) return QC_INVALID_SHAPE;
+  if (!x || !residual || !weight || !codes || !residual_out || !scales)
+    return QC_INVALID_ARGUMENT;
+  const hipStream_t s = as_stream(stream);
+  const bool seq = g_norm_sequential;
+  if (dev_status != nullptr)
+    return finish(qc::launch_rms_norm_add_quant_int8(x, residual, weight, codes, residual_out,
+                                                     scales, rows, hidden, eps, group_size,
+                                                     seq, dev_status, s));
+  int bad = 0;
+  const int st = with_flag(s, &bad, [&](int* flag) {
+    return qc::launch_rms_norm_add_quant_int8(x, residual, weight, codes, residual_out, scales,
+                                              rows, hidden, eps, group_size, seq, flag, s);
+  });
+  if (st != QC_OK) return st;
+  return bad ? QC_INVALID_ARGUMENT : QC_OK;
+}
+
+// kernels/quantization/quantization_ref.cpp:190-197: shape, nulls, finite x.
+int qc_hip_quantize_int8_asymmetric(const float* x, int8_t* codes, float* scales,
+                                    int* zero_points, long long rows, long long dim,
+                                    int* dev_status, void* stream) {
+  if (!valid_product({rows, dim})) return QC_INVALID_SHAPE;
+  if (!x || !codes || !scales || !zero_points) return QC_INVALID_ARGUMENT;
+  const hipStream_t s = as_stream(stream);
+  if (dev_status != nullptr)
+    return finish(qc::launch_quantize_int8_asymmetric(x, codes, scales, zero_points, rows, dim,
+                                                      dev_status, s));
+  bool finite = false;
+  const int st = all_finite(x, rows * dim, s, &finite);
+  if (st != QC_OK) return st;
+  if (!finite) return QC_INVALID_ARGUMENT;
+  hipError_t e = qc::launch_quantize_int8_asymmetric(x, codes, scales, zero_points, rows, dim,
+                                                     nullptr, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return finish(e);
+}
+
+// kernels/quantization/quantization_ref.cpp:228-244.
+int qc_hip_dequantize_int8_asymmetric(const int8_t* codes, const float* scales,
+                                      const int* zero_points, float* out, long long rows,
+                                      long long dim, void* stream) {
+  if (!valid_product({rows, dim})) return QC_INVALID_SHAPE;
+  if (!codes || !scales || !zero_points || !out) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_dequantize_int8_asymmetric(codes, scales, zero_points, out, rows,
+                                                      dim, as_stream(stream)));
+}
+
+int qc_hip_set_norm_sequential_sum(int on) {
+  g_norm_sequential = on != 0;
   return QC_OK;
 }
 

@@ -90,6 +90,16 @@ void* Staging::out(void* host_or_device, std::size_t bytes) {
   return d;
 }
 
+void* Staging::inout(void* host_or_device, std::size_t bytes) {
+  if (host_or_device == nullptr || device_accessible(host_or_device)) return host_or_device;
+  void* d = device(bytes);
+  if (d == nullptr) return nullptr;
+  const hipError_t e = hipMemcpyAsync(d, host_or_device, bytes, hipMemcpyHostToDevice, stream_);
+  if (e != hipSuccess) status_ = from_hip(e);
+  back_.push_back({host_or_device, d, bytes});
+  return d;
+}
+
 Status Staging::finish(int capi_status) {
   if (capi_status != QC_OK) {
     (void)hipStreamSynchronize(stream_);
@@ -100,6 +110,12 @@ Status Staging::finish(int capi_status) {
     if (e != hipSuccess) return from_hip(e);
   }
   return from_hip(hipStreamSynchronize(stream_));
+}
+
+Status Staging::finish_written(int capi_status) {
+  if (capi_status != QC_INVALID_ARGUMENT) return finish(capi_status);
+  const Status copied = finish(QC_OK);
+  return copied == Status::kOk ? Status::kInvalidArgument : copied;
 }
 
 }  // namespace detail
@@ -286,6 +302,66 @@ Status quantize_int8(const float* x, std::int8_t* codes, float* scales, long lon
   if (g.status() != Status::kOk) return g.status();
   return g.finish(
       qc_hip_quantize_int8(xd, cd, sd, rows, dim, group_size, nullptr, g.stream()));
+}
+
+Status rms_norm_add_quant_int8(const float* x, const float* residual, const float* weight,
+                               std::int8_t* codes, float* residual_out, float* scales,
+                               long long rows, long long hidden, float eps,
+                               long long group_size) {
+  // Shape and null validation first, without touching memory.
+  const int pre = qc_hip_rms_norm_add_quant_int8(nullptr, nullptr, nullptr, nullptr, nullptr,
+                                                 nullptr, rows, hidden, eps, group_size, nullptr,
+                                                 nullptr);
+  if (pre == QC_INVALID_SHAPE) return Status::kInvalidShape;
+  if (!x || !residual || !weight || !codes || !residual_out || !scales)
+    return Status::kInvalidArgument;
+  const long long groups = hidden / (group_size == 0 ? hidden : group_size);
+  Staging g(nullptr);
+  const size_t row_bytes = sizeof(float) * rows * hidden;
+  // residual_out may be x or residual itself: stage such a buffer once
+  float* rod = static_cast<float*>(g.inout(residual_out, row_bytes));
+  const float* xd = x == residual_out ? rod : static_cast<const float*>(g.in(x, row_bytes));
+  const float* rd =
+      residual == residual_out ? rod : static_cast<const float*>(g.in(residual, row_bytes));
+  const float* wd = static_cast<const float*>(g.in(weight, sizeof(float) * hidden));
+  // an invalid group keeps the caller's codes and scale, as in the reference
+  auto* cd = static_cast<std::int8_t*>(g.inout(codes, static_cast<size_t>(rows * hidden)));
+  float* sd = static_cast<float*>(g.inout(scales, sizeof(float) * rows * groups));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish_written(qc_hip_rms_norm_add_quant_int8(xd, rd, wd, cd, rod, sd, rows, hidden,
+                                                         eps, group_size, nullptr, g.stream()));
+}
+
+Status quantize_int8_asymmetric(const float* x, std::int8_t* codes, float* scales,
+                                int* zero_points, long long rows, long long dim) {
+  const int pre = qc_hip_quantize_int8_asymmetric(nullptr, nullptr, nullptr, nullptr, rows, dim,
+                                                  nullptr, nullptr);
+  if (pre == QC_INVALID_SHAPE) return Status::kInvalidShape;
+  if (!x || !codes || !scales || !zero_points) return Status::kInvalidArgument;
+  Staging g(nullptr);
+  const float* xd = static_cast<const float*>(g.in(x, sizeof(float) * rows * dim));
+  auto* cd = static_cast<std::int8_t*>(g.out(codes, static_cast<size_t>(rows * dim)));
+  float* sd = static_cast<float*>(g.out(scales, sizeof(float) * rows));
+  int* zd = static_cast<int*>(g.out(zero_points, sizeof(int) * rows));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(
+      qc_hip_quantize_int8_asymmetric(xd, cd, sd, zd, rows, dim, nullptr, g.stream()));
+}
+
+Status dequantize_int8_asymmetric(const std::int8_t* codes, const float* scales,
+                                  const int* zero_points, float* out, long long rows,
+                                  long long dim) {
+  const int pre = qc_hip_dequantize_int8_asymmetric(nullptr, nullptr, nullptr, nullptr, rows,
+                                                    dim, nullptr);
+  if (pre == QC_INVALID_SHAPE) return Status::kInvalidShape;
+  if (!codes || !scales || !zero_points || !out) return Status::kInvalidArgument;
+  Staging g(nullptr);
+  const auto* cd = static_cast<const std::int8_t*>(g.in(codes, static_cast<size_t>(rows * dim)));
+  const float* sd = static_cast<const float*>(g.in(scales, sizeof(float) * rows));
+  const int* zd = static_cast<const int*>(g.in(zero_points, sizeof(int) * rows));
+  float* od = static_cast<float*>(g.out(out, sizeof(float) * rows * dim));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(qc_hip_dequantize_int8_asymmetric(cd, sd, zd, od, rows, dim, g.stream()));
 }
 
 Status int8_gemm(const std::int8_t* weights, const std::int8_t* x, const float* weight_scale,

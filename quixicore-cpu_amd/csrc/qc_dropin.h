@@ -24,6 +24,10 @@ Status from_hip(hipError_t e);
 // the buffer itself when the GPU can address it, else a device copy (taken
 // from `workspace` when one is given, else hipMalloc'd and freed on scope
 // exit).  finish() copies staged outputs back and waits for the stream.
+// inout() is out() for a buffer the call may leave partly unwritten: the
+// device copy starts as the caller's data.  finish_written() also copies
+// back after a data-dependent failure reported once the work has run
+// (kInvalidArgument), for ops whose reference writes what it can.
 class Staging {
  public:
   explicit Staging(Workspace* workspace)
@@ -34,7 +38,9 @@ class Staging {
 
   const void* in(const void* host_or_device, std::size_t bytes);
   void* out(void* host_or_device, std::size_t bytes);
+  void* inout(void* host_or_device, std::size_t bytes);
   Status finish(int capi_status);
+  Status finish_written(int capi_status);
   Status status() const { return status_; }
   hipStream_t stream() const { return stream_; }
 

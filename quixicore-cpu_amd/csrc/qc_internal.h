@@ -46,6 +46,26 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
 hipError_t launch_quantize_int8(const float* x, int8_t* codes, float* scales, long long rows,
                                 long long dim, long long group, int* status, hipStream_t s);
 
+// Residual add + RMSNorm + per-group int8 quantization (group divides
+// hidden).  Groups whose normalized values are not finite are left
+// unwritten and set *status = 3 (status must not be null).
+// force_sequential replays the element-order sum of squares for every row
+// (it is otherwise replayed only for rows on a float rounding boundary).
+hipError_t launch_rms_norm_add_quant_int8(const float* x, const float* residual,
+                                          const float* weight, int8_t* codes,
+                                          float* residual_out, float* scales, long long rows,
+                                          long long hidden, float eps, long long group,
+                                          bool force_sequential, int* status, hipStream_t s);
+
+// Per-row asymmetric int8.  status == nullptr: caller has verified that x is
+// finite; otherwise non-finite rows are left unwritten and set *status = 3.
+hipError_t launch_quantize_int8_asymmetric(const float* x, int8_t* codes, float* scales,
+                                           int* zero_points, long long rows, long long dim,
+                                           int* status, hipStream_t s);
+hipError_t launch_dequantize_int8_asymmetric(const int8_t* codes, const float* scales,
+                                             const int* zero_points, float* out, long long rows,
+                                             long long dim, hipStream_t s);
+
 // *flag = 1 if any of x[0..count) is NaN or +-inf (flag must start at 0).
 hipError_t launch_nonfinite_scan(const float* x, long long count, int* flag, hipStream_t s);
 

@@ -54,6 +54,11 @@ _SIGS = {
     "qc_hip_set_gemv_rows_per_wave": ([_I], _I),
     "qc_hip_set_int8_gemm_route": ([_I], _I),
     "qc_hip_set_qgemm_plan": ([_I, _I], _I),
+    "qc_hip_rms_norm_add_quant_int8": ([_P, _P, _P, _P, _P, _P, _LL, _LL, ctypes.c_float, _LL,
+                                        _P, _P], _I),
+    "qc_hip_quantize_int8_asymmetric": ([_P, _P, _P, _P, _LL, _LL, _P, _P], _I),
+    "qc_hip_dequantize_int8_asymmetric": ([_P, _P, _P, _P, _LL, _LL, _P], _I),
+    "qc_hip_set_norm_sequential_sum": ([_I], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -133,6 +138,25 @@ def unpack_raw(fmt, packed, w, n, k, stream=None):
 def quantize_int8_raw(x, codes, scales, rows, dim, group_size=0, dev_status=None, stream=None):
     return lib.qc_hip_quantize_int8(_ptr(x), _ptr(codes), _ptr(scales), rows, dim, group_size,
                                     _ptr(dev_status), _stream(stream))
+
+
+def rms_norm_add_quant_int8_raw(x, residual, weight, codes, residual_out, scales, rows, hidden,
+                                eps=1e-5, group_size=0, dev_status=None, stream=None):
+    return lib.qc_hip_rms_norm_add_quant_int8(_ptr(x), _ptr(residual), _ptr(weight), _ptr(codes),
+                                              _ptr(residual_out), _ptr(scales), rows, hidden, eps,
+                                              group_size, _ptr(dev_status), _stream(stream))
+
+
+def quantize_int8_asymmetric_raw(x, codes, scales, zero_points, rows, dim, dev_status=None,
+                                 stream=None):
+    return lib.qc_hip_quantize_int8_asymmetric(_ptr(x), _ptr(codes), _ptr(scales),
+                                               _ptr(zero_points), rows, dim, _ptr(dev_status),
+                                               _stream(stream))
+
+
+def dequantize_int8_asymmetric_raw(codes, scales, zero_points, out, rows, dim, stream=None):
+    return lib.qc_hip_dequantize_int8_asymmetric(_ptr(codes), _ptr(scales), _ptr(zero_points),
+                                                 _ptr(out), rows, dim, _stream(stream))
 
 
 def int8_gemm_raw(w, x, ws, as_, row_sum, zp, y, m, n, k, asymmetric=False, dev_status=None,
@@ -228,6 +252,37 @@ def set_qgemm_plan(waves=0, stages=0):
     """Small-batch GEMM work split: waves per workgroup (4/8) and K stages
     per workgroup (1/2/4/8/16); 0 = from the shape."""
     _check(lib.qc_hip_set_qgemm_plan(waves, stages), "set_qgemm_plan")
+
+
+def set_norm_sequential_sum(on):
+    """Replay the element-order sum of squares for every row of
+    rms_norm_add_quant_int8 (results are identical either way)."""
+    _check(lib.qc_hip_set_norm_sequential_sum(int(bool(on))), "set_norm_sequential_sum")
+
+
+def rms_norm_add_quant_int8(x, residual, weight, eps=1e-5, group_size=0, dev_status=None):
+    """Returns (codes, residual_out, scales)."""
+    import torch
+    rows, hidden = x.shape
+    g = hidden if group_size == 0 else group_size
+    codes = torch.empty((rows, hidden), dtype=torch.int8, device=x.device)
+    resid = torch.empty((rows, hidden), dtype=torch.float32, device=x.device)
+    scales = torch.empty((rows, hidden // g), dtype=torch.float32, device=x.device)
+    _check(rms_norm_add_quant_int8_raw(x, residual, weight, codes, resid, scales, rows, hidden,
+                                       eps, group_size, dev_status), "rms_norm_add_quant_int8")
+    return codes, resid, scales
+
+
+def quantize_int8_asymmetric(x, dev_status=None):
+    """Returns (codes, scales, zero_points)."""
+    import torch
+    rows, dim = x.shape
+    codes = torch.empty((rows, dim), dtype=torch.int8, device=x.device)
+    scales = torch.empty(rows, dtype=torch.float32, device=x.device)
+    zps = torch.empty(rows, dtype=torch.int32, device=x.device)
+    _check(quantize_int8_asymmetric_raw(x, codes, scales, zps, rows, dim, dev_status),
+           "quantize_int8_asymmetric")
+    return codes, scales, zps
 
 
 def set_int8_gemm_route(route):

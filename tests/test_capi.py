@@ -40,6 +40,9 @@ def test_cpp_dropin_symbols_exported():
                 "quixicore_cpu::int8_gemm(", "quixicore_cpu::qgemm_w8a8(",
                 "quixicore_cpu::qgemv_w8a8(", "quixicore_cpu::qgemv_w8a8_packed_size(",
                 "quixicore_cpu::qgemm_prepacked(", "quixicore_cpu::CpuPackedWeights::prepare(",
+                "quixicore_cpu::rms_norm_add_quant_int8(",
+                "quixicore_cpu::quantize_int8_asymmetric(",
+                "quixicore_cpu::dequantize_int8_asymmetric(",
                 "quixicore_cpu::Workspace::allocate("):
         assert sym in out, sym
 
@@ -94,6 +97,20 @@ def test_packed_size_and_validation_without_device():
     assert q.qgemv_w8a8_variant(3) == "unsupported"
     assert q.qgemv_variant(0) == "hip_gfx950_q8_0" and q.qgemv_variant(5) == "unsupported"
     assert q.lib.qc_hip_set_gemv_rows_per_wave(3) == 3
+    # rms_norm_add_quant_int8 (kernels/norms/norm_quant_ref.cpp:106-130): rows x
+    # hidden, finite eps >= 0, group dividing hidden, then nulls
+    for rows, hidden, eps, group in ((0, 8, 1e-5, 0), (2, 8, float("nan"), 0), (2, 8, -1.0, 0),
+                                     (2, 8, float("inf"), 0), (2, 8, 1e-5, 3),
+                                     (2, 8, 1e-5, -8)):
+        assert L.qc_hip_rms_norm_add_quant_int8(None, None, None, None, None, None, rows, hidden,
+                                                eps, group, None, None) == 1
+    assert L.qc_hip_rms_norm_add_quant_int8(None, None, None, None, None, None, 2, 8, 0.0, 4,
+                                            None, None) == 3
+    # quantize / dequantize_int8_asymmetric (quantization_ref.cpp:190-197,228-235)
+    assert L.qc_hip_quantize_int8_asymmetric(None, None, None, None, 0, 8, None, None) == 1
+    assert L.qc_hip_quantize_int8_asymmetric(None, None, None, None, 2, 8, None, None) == 3
+    assert L.qc_hip_dequantize_int8_asymmetric(None, None, None, None, 2, -1, None) == 1
+    assert L.qc_hip_dequantize_int8_asymmetric(None, None, None, None, 2, 8, None) == 3
 
 
 def test_product_does_not_reference_oracle():
