@@ -219,6 +219,13 @@ int qc_hip_set_int8_gemm_route(int route);
  * bit-identical.  Tuning and test knob with no reference counterpart. */
 int qc_hip_set_qgemm_plan(int waves, int stages);
 
+/* Route of qc_hip_qgemm for M >= 2 (K % 64 == 0): 0 (the default) runs the
+ * 2-D tiled GEMM for M >= 64 and passes of at most 32 rows below; -1 always
+ * uses the passes; 1 / 2 always use the 2-D GEMM with one / two K ranges.
+ * Results stay within the contract tolerance on every route.  Tuning and
+ * test knob with no reference counterpart. */
+int qc_hip_set_qgemm_panel(int mode);
+
 /* on != 0: qc_hip_rms_norm_add_quant_int8 replays the element-order sum of
  * squares for every row instead of only for rows whose float norm the
  * parallel sum cannot settle (process-wide; results are identical either

@@ -477,6 +477,12 @@ int qc_hip_dequantize_int8_asymmetric(const int8_t* codes, const float* scales,
                                                       dim, as_stream(stream)));
 }
 
+int qc_hip_set_qgemm_panel(int mode) {
+  if (mode < -1 || mode > 2) return QC_INVALID_ARGUMENT;
+  g_tuning.qgemm_panel = mode;
+  return QC_OK;
+}
+
 int qc_hip_set_norm_sequential_sum(int on) {
   g_norm_sequential = on != 0;
   return QC_OK;

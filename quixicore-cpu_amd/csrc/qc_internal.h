@@ -11,6 +11,7 @@ struct GemvTuning {
   int rows_per_wave = 0;  // GEMV rows per wavefront (1, 2, 4, 7, 8, 14; 0 = from the shape)
   int qgemm_waves = 0;    // small-batch GEMM waves per workgroup (4, 8; 0 = from the shape)
   int qgemm_stages = 0;   // small-batch GEMM K stages per workgroup (1..16; 0 = from the shape)
+  int qgemm_panel = 0;    // 2-D GEMM route: 0 = for m >= 64, -1 = never, 1 / 2 = always (K ranges)
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
@@ -34,11 +35,14 @@ hipError_t launch_qgemv_multi(int fmt, int nseg, const void* const* W, float* co
 hipError_t launch_qgemv_w8a8(int fmt, const void* W, const float* x, float* y, long long n,
                              long long k, int rows_per_wave, int* status, hipStream_t s);
 
-// Small-batch GEMM on MFMA (m >= 2, K % 64 == 0, W 4-byte aligned): int8
-// digit planes for up to 8 rows per pass, bf16 hi/lo above.  waves / stages:
-// plan override (0 = from the shape).
+// GEMM on MFMA (m >= 2, K % 64 == 0, W 4-byte aligned): int8 digit planes
+// for up to 8 rows per pass, bf16 hi/lo above; for m >= 64 one 2-D tiled
+// kernel (the panel route) instead of passes of 32 rows.  waves / stages:
+// small-batch plan override (0 = from the shape); panel: 0 = from m, -1 =
+// never, 1 / 2 = always (one / two K ranges).
 hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
-                             int k, hipStream_t s, int waves = 0, int stages = 0);
+                             int k, hipStream_t s, int waves = 0, int stages = 0,
+                             int panel = 0);
 
 // Per-group symmetric int8 quantization.  status == nullptr: caller has
 // already verified that x is finite.  Otherwise non-finite groups are left

@@ -190,7 +190,42 @@ __device__ __forceinline__ void dma16_addr(const void* addr, const void* lds) {
       : "v"(addr), "s"(m0)
       : "memory", "m0");
 }
+// One dword per lane from a wave-uniform base plus a per-lane byte offset to
+// LDS byte lds + 4 * lane.
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, const void* lds) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %0, %1"
+      :
+      : "v"(voff), "s"(base), "s"(m0)
+      : "memory", "m0");
+}
 #pragma clang diagnostic pop
+
+// Per-row power-of-two scale of the activations for the bf16 layouts:
+// e(m) = the frexp exponent of max |x[m][:]| (0 for a zero or non-finite
+// row).  The fragments hold x * 2^-e(m), so every row's largest element is in
+// [0.5, 1): no element that matters is subnormal in bf16 (which would leave
+// it a few bits) and no product overflows; outputs are scaled back by 2^e(m),
+// exactly.  One 256-thread workgroup per row.
+__global__ __launch_bounds__(256) void row_exponents(const float* __restrict__ x, int K,
+                                                     int* __restrict__ rexp) {
+  __shared__ float smax[4];
+  const float* xr = x + static_cast<long long>(blockIdx.x) * K;
+  float mx = 0.f;
+  for (int i = threadIdx.x; i < K; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+  mx = wave_max_nonneg(mx);
+  if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    int e = 0;
+    if (mx > 0.f && mx <= 3.402823466e38f) (void)frexpf(mx, &e);
+    rexp[blockIdx.x] = e;
+  }
+}
 
 // Activation fragments: one 64-thread workgroup per (block b, m-tile t).
 // Lane l covers row 16t + (l & 15), codes 8(l >> 4) .. +7 of the block.
@@ -203,7 +238,8 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
                                                  float* __restrict__ bias, float* zero_y,
                                                  long long zero_count,
                                                  const uint8_t* __restrict__ tail_src, int tail,
-                                                 uint8_t* __restrict__ tail_pad, int pad_bytes) {
+                                                 uint8_t* __restrict__ tail_pad, int pad_bytes,
+                                                 const int* __restrict__ rexp) {
   if (blockIdx.x == 0 && tail > 0)
     for (int i = threadIdx.x; i < pad_bytes; i += 64) tail_pad[i] = i < tail ? tail_src[i] : 0;
   using XB = XBlock<XL, BIAS>;
@@ -283,8 +319,9 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
     float v[8];
     const bool live = m < M && b < nb;
     const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * b : 0) + 8 * j;
+    const int er = live ? rexp[m] : 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = live ? src[i] : 0.0f;
+    for (int i = 0; i < 8; ++i) v[i] = live ? ldexpf(src[i], -er) : 0.0f;
     bf16x8 hi, lo;
     float s = 0.0f;
 #pragma unroll
@@ -360,7 +397,7 @@ template <int FMT, int XL, int NW, int NST>
 __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
     float* __restrict__ y, float* __restrict__ partial, const uint8_t* __restrict__ tail_pad,
-    int M, int N, int K, int nslabs, int ks_count, int nstages) {
+    const int* __restrict__ rexp, int M, int N, int K, int nslabs, int ks_count, int nstages) {
   using L = StageLayout<FMT, XL, NW>;
   using XB = typename L::XB;
   using WS = WStage<FMT>;
@@ -565,6 +602,7 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
   if (n >= N) return;
   auto put = [&](int m, float v) {
     if (m >= M) return;
+    if constexpr (!XB::digits) v = ldexpf(v, rexp[m]);   // undo the row scale
     const long long o = static_cast<long long>(m) * N + n;
     if (ks_count == 1) y[o] = v;
     else if (ks_count == 2) atomicAdd(y + o, v);
@@ -598,11 +636,14 @@ int device_cus() {
 struct StreamWorkspace {
   int device;
   hipStream_t stream;
+  int tag;
   void* ptr;
   size_t bytes;
 };
 
-hipError_t workspace_for(hipStream_t s, size_t bytes, void** out) {
+// tag 0: a pass's fragments and partial sums; tag 1: the call's row exponents
+// (live across all passes of one call).
+hipError_t workspace_for(hipStream_t s, size_t bytes, void** out, int tag = 0) {
   static std::mutex mu;
   static std::vector<StreamWorkspace> table;
   static std::vector<void*> retired;
@@ -611,7 +652,7 @@ hipError_t workspace_for(hipStream_t s, size_t bytes, void** out) {
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lock(mu);
   for (auto& w : table) {
-    if (w.device != dev || w.stream != s) continue;
+    if (w.device != dev || w.stream != s || w.tag != tag) continue;
     if (w.bytes >= bytes) {
       *out = w.ptr;
       return hipSuccess;
@@ -638,30 +679,30 @@ hipError_t workspace_for(hipStream_t s, size_t bytes, void** out) {
   void* p = nullptr;
   e = hipMalloc(&p, bytes);
   if (e != hipSuccess) return e;
-  table.push_back({dev, s, p, bytes});
+  table.push_back({dev, s, tag, p, bytes});
   *out = p;
   return hipSuccess;
 }
 
 template <int FMT, int XL, int NW, int NST>
 hipError_t launch_nst(const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
-                      float* partial, const uint8_t* tail_pad, int m, int n, int k, int nslabs,
-                      int ks, int nstages, hipStream_t s) {
+                      float* partial, const uint8_t* tail_pad, const int* rexp, int m, int n, int k,
+                      int nslabs, int ks, int nstages, hipStream_t s) {
   qgemm_mfma<FMT, XL, NW, NST><<<nslabs * ks, 64 * NW, 0, s>>>(W, xf, bias, y, partial, tail_pad,
-                                                              m, n, k, nslabs, ks, nstages);
+                                                              rexp, m, n, k, nslabs, ks, nstages);
   return hipGetLastError();
 }
 
 template <int FMT, int XL, int NW>
 hipError_t launch_nw(int nst, const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
-                     float* partial, const uint8_t* tail_pad, int m, int n, int k, int nslabs,
-                     int ks, int nstages, hipStream_t s) {
+                     float* partial, const uint8_t* tail_pad, const int* rexp, int m, int n, int k,
+                     int nslabs, int ks, int nstages, hipStream_t s) {
   switch (nst) {
-    case 16: return launch_nst<FMT, XL, NW, 16>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    case 8: return launch_nst<FMT, XL, NW, 8>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    case 4: return launch_nst<FMT, XL, NW, 4>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    case 2: return launch_nst<FMT, XL, NW, 2>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
-    default: return launch_nst<FMT, XL, NW, 1>(W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    case 16: return launch_nst<FMT, XL, NW, 16>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
+    case 8: return launch_nst<FMT, XL, NW, 8>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
+    case 4: return launch_nst<FMT, XL, NW, 4>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
+    case 2: return launch_nst<FMT, XL, NW, 2>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
+    default: return launch_nst<FMT, XL, NW, 1>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
   }
 }
 
@@ -699,7 +740,7 @@ Plan plan_for(int n, int nstages, int cus) {
 
 template <int FMT, int XL>
 hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, hipStream_t s,
-               int waves, int stages) {
+               int waves, int stages, const int* rexp) {
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
@@ -724,44 +765,366 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   float* bias = reinterpret_cast<float*>(xf + xf_bytes);
   float* partial = reinterpret_cast<float*>(xf + xf_bytes + bias_bytes);
   uint8_t* tail_pad = xf + xf_bytes + bias_bytes + part_bytes;
+
   const long long outs = static_cast<long long>(m) * n;
   const long long row_bytes = static_cast<long long>(nb) * PairLayout<FMT>::bytes / 2;
   const int tail = (k / 64) % kStagePairs * PairLayout<FMT>::bytes;
   const uint8_t* tail_src = W + (n - 1) * row_bytes + static_cast<long long>(nstages - 1) * WStage<FMT>::row_bytes;
   qgemm_prep<XL, FMT == kQ4_0><<<nbp * XB::prep_groups, 64, 0, s>>>(x, m, k, xf, bias, y, ks == 2 ? outs : 0,
                                                      tail_src, tail, tail_pad,
-                                                     static_cast<int>(pad_bytes));
+                                                     static_cast<int>(pad_bytes), rexp);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (plan.nw == 8)
-    e = launch_nw<FMT, XL, 8>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    e = launch_nw<FMT, XL, 8>(plan.nst, W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
   else
-    e = launch_nw<FMT, XL, 4>(plan.nst, W, xf, bias, y, partial, tail_pad, m, n, k, nslabs, ks, nstages, s);
+    e = launch_nw<FMT, XL, 4>(plan.nst, W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
   if (e != hipSuccess || ks <= 2) return e;
   const long long blocks = (outs + 255) / 256;
   qgemm_reduce<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(partial, y, outs, ks);
   return hipGetLastError();
 }
 
+// ------------------------------------------------ panel route, M >= 64 ---
+//
+// The reference switches qgemm_prepacked to a row-panel GEMM at M >= 64
+// (kernels/quantization/qgemm_panel.cpp:234-286).  Here every M >= 64 call
+// (qgemm and qgemm_prepacked) runs one 2-D tiled GEMM instead of passes of 32
+// rows, each of which re-streams the whole weight matrix.  Numerics are those
+// of the bf16 path above (hi/lo activations, exact codes, per-block f32
+// scaling), so the contract bound is unchanged.
+//
+// Workgroup: 8 wavefronts as 2 (m) x 4 (n), each computing 64 x 64 outputs
+// as 4 x 4 tiles of v_mfma_f32_16x16x32_bf16; workgroup tile 128 x 256.  K
+// runs in stages of one block pair (64 elements) through a 3-deep LDS ring
+// filled by global_load_lds: the activation fragments of the workgroup's 8
+// m-tiles (hi, lo, and the q4_0 bias) as 16-byte chunks, and the pair's bytes
+// of its 256 weight rows as dwords.  Every wavefront issues the same loads
+// per stage (spare weight lanes re-read a valid dword into padding), so the
+// waits are exact counts, as in the small-batch kernel.
+constexpr int kPTM = 4, kPTN = 4;                 // 16x16 tiles per wave (m, n)
+constexpr int kPWM = 2, kPWN = 4;                 // waves per workgroup (m, n)
+constexpr int kPWaves = kPWM * kPWN;
+constexpr int kPBM = 16 * kPTM * kPWM;            // 128 rows of x per workgroup
+constexpr int kPBN = 16 * kPTN * kPWN;            // 256 rows of W per workgroup
+constexpr int kPMT = kPBM / 16;                   // 8 m-tiles per workgroup
+constexpr int kPRing = 3;
+
+template <int FMT>
+struct PanelStage {
+  static constexpr bool bias = FMT == kQ4_0;
+  static constexpr int pd = PairLayout<FMT>::bytes / 4;             // 17 / 9 dwords per row
+  static constexpr int x_bytes = kPMT * 2 * kFragBytes;             // 32 KB
+  static constexpr int x_loads = x_bytes / 16 / (64 * kPWaves);     // 4 chunks per lane
+  static constexpr int b_bytes = bias ? kPMT * 2 * 64 : 0;          // 1 KB
+  static constexpr int w_dwords = kPBN * pd;
+  static constexpr int w_loads = (w_dwords + 64 * kPWaves - 1) / (64 * kPWaves);  // 9 / 5
+  static constexpr int w_bytes = kPWaves * w_loads * 256;           // with padding
+  static constexpr int bytes = x_bytes + b_bytes + w_bytes;
+  static constexpr int g = x_loads + (bias ? 1 : 0) + w_loads;      // loads per wave per stage
+  static_assert(x_bytes % (16 * 64 * kPWaves) == 0, "whole x loads");
+  static_assert(kPRing * bytes <= 160 * 1024, "LDS");
+  static_assert(g * (kPRing - 1) < 64, "vmcnt range");
+};
+
+// Activation fragments [m-tile][block][hi | lo][64 lanes][16 B] and (q4_0)
+// bias [m-tile][block][16 rows]; rows >= M are zero.  Grid: mtiles * nb
+// workgroups of 64 threads.  Also clears y when two K halves add into it.
+template <bool BIAS>
+__global__ __launch_bounds__(64) void panel_prep(const float* __restrict__ x, int M, int K,
+                                                 uint8_t* __restrict__ xf,
+                                                 float* __restrict__ bias, float* zero_y,
+                                                 long long zero_count,
+                                                 const int* __restrict__ rexp) {
+  const int nb = K / 32;
+  const int t = blockIdx.x / nb, b = blockIdx.x % nb;
+  const int l = threadIdx.x;
+  const int m = 16 * t + (l & 15), j = l >> 4;
+  const bool live = m < M;
+  const float* src = x + static_cast<long long>(live ? m : 0) * K + 32 * b + 8 * j;
+  const int er = live ? rexp[m] : 0;
+  bf16x8 hi, lo;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float v = live ? ldexpf(src[i], -er) : 0.0f;
+    hi[i] = static_cast<__bf16>(v);
+    const float h = static_cast<float>(hi[i]);
+    lo[i] = static_cast<__bf16>(v - h);
+    s += h + static_cast<float>(lo[i]);
+  }
+  uint8_t* dst = xf + (static_cast<long long>(t) * nb + b) * kFragBytes + 16 * l;
+  *reinterpret_cast<bf16x8*>(dst) = hi;
+  *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
+  if constexpr (BIAS) {
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    if (j == 0) bias[(static_cast<long long>(t) * nb + b) * 16 + (l & 15)] = -8.0f * s;
+  }
+  for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
+       i += static_cast<long long>(gridDim.x) * 64)
+    zero_y[i] = 0.0f;
+}
+
+template <int FMT>
+__global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
+    const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
+    float* __restrict__ y, const int* __restrict__ rexp, int M, int N, int K,
+    int pairs_per_split, int ks_count) {
+  using PS = PanelStage<FMT>;
+  constexpr int PB = PairLayout<FMT>::bytes;
+  constexpr int G = PS::g;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring0[PS::bytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring1[PS::bytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring2[PS::bytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % kPWM, wn = wave / kPWM;
+  const int j = lane >> 4;
+  const int n0 = blockIdx.x * kPBN;
+  const int mt0 = blockIdx.y * kPMT;
+  const int nb = K / 32, npairs = K / 64;
+  const int p0 = blockIdx.z * pairs_per_split;
+  const int p1 = min(p0 + pairs_per_split, npairs);
+  const long long row_bytes = static_cast<long long>(nb) * (PB / 2);
+
+  // Sources: a wave-uniform base per workgroup and stage (scalar registers)
+  // plus a per-lane 32-bit offset that never changes, so issuing a stage
+  // costs no vector arithmetic.  x chunk c = (wave * x_loads + i) * 64 + lane:
+  // m-tile c >> 8, byte 16 (c & 255) of its pair (blocks 2p, 2p + 1 adjacent).
+  const uint8_t* xbase = xf + static_cast<long long>(mt0) * nb * kFragBytes;
+  uint32_t xoff[PS::x_loads];
+#pragma unroll
+  for (int i = 0; i < PS::x_loads; ++i) {
+    const int c = (wave * PS::x_loads + i) * 64 + lane;
+    xoff[i] = static_cast<uint32_t>((c >> 8) * nb * kFragBytes + 16 * (c & 255));
+  }
+  // bias: wave w, lanes 0..7, 128 B of m-tile w's two blocks
+  const uint8_t* bbase = reinterpret_cast<const uint8_t*>(bias) +
+                         static_cast<long long>(mt0) * nb * 64;
+  const uint32_t boff = static_cast<uint32_t>(wave * nb * 64 + 16 * (lane & 7));
+  // weight dword d = (wave * w_loads + i) * 64 + lane: row d / pd, dword
+  // d % pd; d past the stage re-reads the stage's last dword
+  const uint8_t* wbase = W + static_cast<long long>(n0) * row_bytes;
+  uint32_t woff[PS::w_loads];
+#pragma unroll
+  for (int i = 0; i < PS::w_loads; ++i) {
+    int d = (wave * PS::w_loads + i) * 64 + lane;
+    d = d < PS::w_dwords ? d : PS::w_dwords - 1;
+    const int r = min(n0 + d / PS::pd, N - 1) - n0;
+    woff[i] = static_cast<uint32_t>(r * row_bytes + 4 * (d % PS::pd));
+  }
+  auto slot_base = [&](int slot) -> uint8_t* { return slot == 0 ? ring0 : slot == 1 ? ring1 : ring2; };
+  auto issue = [&](int p, int slot) {
+    uint8_t* base = slot_base(slot);
+    const uint8_t* xs = xbase + static_cast<long long>(2 * p) * kFragBytes;
+#pragma unroll
+    for (int i = 0; i < PS::x_loads; ++i) dma16(xs, xoff[i], base + 16 * (wave * PS::x_loads + i) * 64);
+    if constexpr (PS::bias)
+      if (lane < 8) dma16(bbase + 128 * p, boff, base + PS::x_bytes + 128 * wave);
+    const uint8_t* ws = wbase + static_cast<long long>(p) * PB;
+#pragma unroll
+    for (int i = 0; i < PS::w_loads; ++i)
+      dma4(ws, woff[i], base + PS::x_bytes + PS::b_bytes + 256 * (wave * PS::w_loads + i));
+  };
+
+  f32x4 acc[kPTM][kPTN];
+#pragma unroll
+  for (int a = 0; a < kPTM; ++a)
+#pragma unroll
+    for (int b = 0; b < kPTN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int slot) {
+    const uint8_t* base = slot_base(slot);
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(base + PS::x_bytes + PS::b_bytes);
+    const float* sb = reinterpret_cast<const float*>(base + PS::x_bytes);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 wv[kPTN];
+      float d[kPTN];
+#pragma unroll
+      for (int tn = 0; tn < kPTN; ++tn) {
+        const uint32_t* pr = sw + (wn * 64 + tn * 16 + (lane & 15)) * PS::pd;
+        uint32_t c0, c1, dbits;
+        if (h == 0) {
+          const uint32_t b0x = pr[PairLayout<FMT>::blk0_dword(j)];
+          const uint32_t b0y = pr[PairLayout<FMT>::blk0_dword(j) + 1];
+          const uint32_t b0z = pr[PairLayout<FMT>::blk0_dword(j) + 2];
+          c0 = __builtin_amdgcn_alignbyte(b0y, b0x, 2);
+          c1 = __builtin_amdgcn_alignbyte(b0z, b0y, 2);
+          dbits = pr[0] & 0xFFFFu;
+        } else {
+          c0 = pr[PairLayout<FMT>::blk1_dword(j)];
+          c1 = pr[PairLayout<FMT>::blk1_dword(j) + 1];
+          dbits = pr[PairLayout<FMT>::scale1_dword] >> 16;
+        }
+        wv[tn] = codes_bf16<FMT>(c0, c1, j);
+        d[tn] = half_bits_to_float(dbits);
+      }
+#pragma unroll
+      for (int tm = 0; tm < kPTM; ++tm) {
+        const int mt = wm * kPTM + tm;
+        const uint8_t* f = base + (mt * 2 + h) * kFragBytes + 16 * lane;
+        const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
+        const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+        f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (PS::bias) c0 = *reinterpret_cast<const f32x4*>(sb + (mt * 2 + h) * 16 + 4 * j);
+#pragma unroll
+        for (int tn = 0; tn < kPTN; ++tn) {
+          f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv[tn], c0, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv[tn], c, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[tm][tn][e] = fmaf(c[e], d[tn], acc[tm][tn][e]);
+        }
+      }
+    }
+  };
+
+  // Ring: stages p0 .. p0 + kPRing - 2 in flight before the loop; step i
+  // waits for stage p0 + i, meets the workgroup (the slot the next issue
+  // overwrites is no longer read), issues stage p0 + i + kPRing - 1 and
+  // computes.  Unrolled by the ring depth so every slot index is a constant.
+  const int count = p1 - p0;
+#pragma unroll
+  for (int i = 0; i < kPRing - 1; ++i)
+    if (i < count) issue(p0 + i, i);
+  auto step = [&](int i, int slot) {
+    // stages issued after this one and still possibly in flight
+    const int ahead = min(kPRing - 2, count - 1 - i);
+    wait_stages<G, kPRing - 2>(ahead);
+    wait_lgkmcnt0();
+    ring_barrier();
+    if (i + kPRing - 1 < count) issue(p0 + i + kPRing - 1, (slot + kPRing - 1) % kPRing);
+    compute(slot);
+#pragma unroll
+    for (int a = 0; a < kPTM; ++a)
+#pragma unroll
+      for (int b = 0; b < kPTN; ++b) asm volatile("" : "+v"(acc[a][b]));
+  };
+  for (int i = 0; i < count; i += kPRing) {
+    step(i, 0);
+    if (i + 1 < count) step(i + 1, 1);
+    if (i + 2 < count) step(i + 2, 2);
+  }
+  wait_vmcnt<0>();   // no global->LDS load may outlive the workgroup's LDS
+
+  // acc[tm][tn][e] is output (m = 16 (mt0 + 4 wm + tm) + 4 j + e,
+  // n = n0 + 64 wn + 16 tn + (lane & 15)).
+#pragma unroll
+  for (int tn = 0; tn < kPTN; ++tn) {
+    const int n = n0 + wn * 64 + tn * 16 + (lane & 15);
+    if (n >= N) continue;
+#pragma unroll
+    for (int tm = 0; tm < kPTM; ++tm) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 16 * (mt0 + wm * kPTM + tm) + 4 * j + e;
+        if (m >= M) continue;
+        const long long o = static_cast<long long>(m) * N + n;
+        const float v = ldexpf(acc[tm][tn][e], rexp[m]);   // undo the row scale
+        if (ks_count == 1) y[o] = v;
+        else atomicAdd(y + o, v);
+      }
+    }
+  }
+}
+
+// K ranges of the 2-D GEMM: two (atomic adds onto a cleared y, two addends
+// onto zero: order-independent) when both halves' workgroups still run in one
+// round at one workgroup per CU, else one.
+int panel_split(int m, int n, int k, int cus) {
+  const long long tiles = static_cast<long long>((m + kPBM - 1) / kPBM) * ((n + kPBN - 1) / kPBN);
+  return 2 * tiles <= cus && k / 64 >= 2 ? 2 : 1;
+}
+
+// Route for m >= 64 from two time models fitted on MI355X (q8_0 and q4_0
+// alike): a 2-D GEMM workgroup spends ~2.45 us per block pair of its K range
+// (MFMA and VALU issue bound, independent of how full the chip is), in
+// ceil(workgroups / CUs) rounds; a pass of 32 rows costs max(N K / 2.3e12 s,
+// 17 us).  The passes win for small M at small N or long K.
+bool panel_pays(int m, int n, int k, int cus) {
+  const int ks = panel_split(m, n, k, cus);
+  const long long tiles = static_cast<long long>((m + kPBM - 1) / kPBM) * ((n + kPBN - 1) / kPBN);
+  const long long rounds = (tiles * ks + cus - 1) / cus;
+  const double panel = rounds * ((k / 64 + ks - 1) / ks) * 2.45e-6 + 4e-6;
+  const double passes = ((m + 31) / 32) * std::max(static_cast<double>(n) * k / 2.3e12, 17e-6);
+  return panel < passes;
+}
+
+template <int FMT>
+hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, int k,
+                     hipStream_t s, int split, const int* rexp) {
+  const int nb = k / 32, npairs = k / 64;
+  const int mblocks = (m + kPBM - 1) / kPBM, nblocks = (n + kPBN - 1) / kPBN;
+  const int mtiles = mblocks * kPMT;
+  // per-lane 32-bit source offsets within a workgroup's rows
+  if (static_cast<long long>(kPBN) * nb * (PairLayout<FMT>::bytes / 2) >= (1LL << 32) ||
+      static_cast<long long>(kPMT) * nb * kFragBytes >= (1LL << 32))
+    return hipErrorInvalidValue;
+  int ks = panel_split(m, n, k, device_cus());
+  if (split == 1 || split == 2) ks = split;
+  if (npairs < 2) ks = 1;
+  const int per = (npairs + ks - 1) / ks;
+  const size_t xf_bytes = static_cast<size_t>(mtiles) * nb * kFragBytes;
+  const size_t bias_bytes = FMT == kQ4_0 ? static_cast<size_t>(mtiles) * nb * 64 : 0;
+  void* ws = nullptr;
+  hipError_t e = workspace_for(s, xf_bytes + bias_bytes + 256, &ws);
+  if (e != hipSuccess) return e;
+  uint8_t* xf = static_cast<uint8_t*>(ws);
+  float* bias = reinterpret_cast<float*>(xf + xf_bytes);
+  const long long outs = static_cast<long long>(m) * n;
+  panel_prep<FMT == kQ4_0><<<static_cast<unsigned>(mtiles * nb), 64, 0, s>>>(
+      x, m, k, xf, bias, y, ks == 2 ? outs : 0, rexp);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(mblocks),
+                  static_cast<unsigned>(ks));
+  qgemm_panel<FMT><<<grid, 64 * kPWaves, 0, s>>>(W, xf, bias, y, rexp, m, n, k, per, ks);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
-                             int k, hipStream_t s, int waves, int stages) {
+                             int k, hipStream_t s, int waves, int stages, int panel) {
   const auto* w = static_cast<const uint8_t*>(W);
+  // panel: 0 = from the shape (for m >= 64), -1 = never, 1 / 2 = always
+  // (for m >= 2) with one / two K ranges
+  const bool use_panel = panel > 0 || (panel == 0 && m >= 64 && panel_pays(m, n, k, device_cus()));
+  // The bf16 layouts (the panel and passes of more than 8 rows) scale each
+  // row by its power of two: one exponent kernel for the whole call.
+  int* rexp = nullptr;
+  if (use_panel || m > 8) {
+    void* p = nullptr;
+    hipError_t e = workspace_for(s, sizeof(int) * static_cast<size_t>(m) + 256, &p, 1);
+    if (e != hipSuccess) return e;
+    rexp = static_cast<int*>(p);
+    row_exponents<<<static_cast<unsigned>(m), 256, 0, s>>>(x, k, rexp);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (use_panel)
+    return fmt == kQ8_0 ? run_panel<kQ8_0>(w, x, y, m, n, k, s, panel, rexp)
+                        : run_panel<kQ4_0>(w, x, y, m, n, k, s, panel, rexp);
   for (int m0 = 0; m0 < m; m0 += 32) {
     const int mt = m - m0 < 32 ? m - m0 : 32;
     const float* xm = x + static_cast<long long>(m0) * k;
     float* ym = y + static_cast<long long>(m0) * n;
+    const int* rm = rexp != nullptr ? rexp + m0 : nullptr;
     // activation layout: compact rows for M <= 4 / 8, dense 16-row tiles above
     hipError_t e;
     if (fmt == kQ8_0)
-      e = mt <= 4 ? run<kQ8_0, 4>(w, xm, ym, mt, n, k, s, waves, stages)
-        : mt <= 8 ? run<kQ8_0, 8>(w, xm, ym, mt, n, k, s, waves, stages)
-        : mt <= 16 ? run<kQ8_0, 16>(w, xm, ym, mt, n, k, s, waves, stages) : run<kQ8_0, 32>(w, xm, ym, mt, n, k, s, waves, stages);
+      e = mt <= 4 ? run<kQ8_0, 4>(w, xm, ym, mt, n, k, s, waves, stages, rm)
+        : mt <= 8 ? run<kQ8_0, 8>(w, xm, ym, mt, n, k, s, waves, stages, rm)
+        : mt <= 16 ? run<kQ8_0, 16>(w, xm, ym, mt, n, k, s, waves, stages, rm)
+                   : run<kQ8_0, 32>(w, xm, ym, mt, n, k, s, waves, stages, rm);
     else
-      e = mt <= 4 ? run<kQ4_0, 4>(w, xm, ym, mt, n, k, s, waves, stages)
-        : mt <= 8 ? run<kQ4_0, 8>(w, xm, ym, mt, n, k, s, waves, stages)
-        : mt <= 16 ? run<kQ4_0, 16>(w, xm, ym, mt, n, k, s, waves, stages) : run<kQ4_0, 32>(w, xm, ym, mt, n, k, s, waves, stages);
+      e = mt <= 4 ? run<kQ4_0, 4>(w, xm, ym, mt, n, k, s, waves, stages, rm)
+        : mt <= 8 ? run<kQ4_0, 8>(w, xm, ym, mt, n, k, s, waves, stages, rm)
+        : mt <= 16 ? run<kQ4_0, 16>(w, xm, ym, mt, n, k, s, waves, stages, rm)
+                   : run<kQ4_0, 32>(w, xm, ym, mt, n, k, s, waves, stages, rm);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -269,7 +269,8 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, 
   // one stage of row overrun).
   const long long w_bytes = static_cast<long long>(n) * (k / 32) * Fmt<FMT>::block_bytes;
   if (k % 64 == 0 && w_bytes + 4096 < (1LL << 32))
-    return launch_qgemm_mfma(FMT, W, x, y, m, n, k, s, t.qgemm_waves, t.qgemm_stages);
+    return launch_qgemm_mfma(FMT, W, x, y, m, n, k, s, t.qgemm_waves, t.qgemm_stages,
+                             t.qgemm_panel);
   const int grid = (n + kWaves - 1) / kWaves;
   for (int m0 = 0; m0 < m; m0 += 8) {
     const int mt = m - m0 < 8 ? m - m0 : 8;

@@ -59,6 +59,7 @@ _SIGS = {
     "qc_hip_quantize_int8_asymmetric": ([_P, _P, _P, _P, _LL, _LL, _P, _P], _I),
     "qc_hip_dequantize_int8_asymmetric": ([_P, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_set_norm_sequential_sum": ([_I], _I),
+    "qc_hip_set_qgemm_panel": ([_I], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -252,6 +253,12 @@ def set_qgemm_plan(waves=0, stages=0):
     """Small-batch GEMM work split: waves per workgroup (4/8) and K stages
     per workgroup (1/2/4/8/16); 0 = from the shape."""
     _check(lib.qc_hip_set_qgemm_plan(waves, stages), "set_qgemm_plan")
+
+
+def set_qgemm_panel(mode=0):
+    """qgemm route for M >= 2: 0 = 2-D GEMM for M >= 64, -1 = never,
+    1 / 2 = always with one / two K ranges."""
+    _check(lib.qc_hip_set_qgemm_panel(mode), "set_qgemm_panel")
 
 
 def set_norm_sequential_sum(on):
