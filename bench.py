@@ -312,11 +312,12 @@ LAYER = [(4, 4096, 4096), (2, 14336, 4096), (1, 4096, 14336)]
 
 def layer_sweep(qc, steps, warmup):
     """Per-layer sum of kernel times for each regime of config 4: q4_0 weights
-    at M=1 (GEMV) and M=8 (small-batch GEMM); W8A8 at M=512 and M=2048
+    at M=1 (GEMV), M=8 (small-batch GEMM) and M=512 (prefill, the 2-D GEMM);
+    W8A8 at M=512 and M=2048
     (per-token activation quantization + int8 GEMM).  Each matmul is timed on
     its own (same graph discipline, rotated weight copies)."""
     out = {}
-    for m in (1, 8):
+    for m in (1, 8, 512):
         us, wbytes = 0.0, 0
         for cnt, n, k in LAYER:
             if m == 1:
@@ -325,8 +326,10 @@ def layer_sweep(qc, steps, warmup):
                 r = qgemm_case(qc, n, k, m, steps, warmup, seed=200 + n + k, fmt=1)
             us += cnt * r["gpu_ms"] * 1e3
             wbytes += cnt * n * (k // 32) * 18
+        flops = sum(cnt * 2.0 * m * n * k for cnt, n, k in LAYER)
         out[f"q4_0_m{m}"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
-                             "weight_gbs": wbytes / (us * 1e-6) / 1e9}
+                             "weight_gbs": wbytes / (us * 1e-6) / 1e9,
+                             "tflops": flops / (us * 1e-6) / 1e12}
     # M = 1 with the fused decode seams: Q/K/V in one launch (4096 x 3 rows),
     # O alone, gate/up in one launch, down alone.
     us, wbytes = 0.0, 0

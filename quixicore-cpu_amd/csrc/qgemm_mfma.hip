@@ -215,7 +215,29 @@ __global__ __launch_bounds__(256) void row_exponents(const float* __restrict__ x
   __shared__ float smax[4];
   const float* xr = x + static_cast<long long>(blockIdx.x) * K;
   float mx = 0.f;
-  for (int i = threadIdx.x; i < K; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+  // four independent loads in flight per step (one memory latency for
+  // K <= 16384 instead of K / 256 of them)
+  int i = threadIdx.x;
+  if (K % 4 == 0 && reinterpret_cast<uintptr_t>(xr) % 16 == 0) {
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    const int n4 = K / 4;
+    for (; i + 768 < n4; i += 1024) {
+      const float4 a = x4[i], b = x4[i + 256], c = x4[i + 512], d = x4[i + 768];
+      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                           fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
+                           fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
+    }
+    for (; i < n4; i += 256) {
+      const float4 a = x4[i];
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
+  } else {
+    for (; i + 768 < K; i += 1024)
+      mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xr[i]), fabsf(xr[i + 256]))),
+                 fmaxf(fabsf(xr[i + 512]), fabsf(xr[i + 768])));
+    for (; i < K; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+  }
   mx = wave_max_nonneg(mx);
   if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
   __syncthreads();
