@@ -42,10 +42,11 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=["headline", "all", "copy", "w8a8", "qgemm"], default="all",
+    p.add_argument("--only", choices=["headline", "all", "copy", "w8a8", "qgemm", "prefill"],
+                   default="all",
                    help="copy: a plain 64 MiB device copy, the calibration kernel for "
-                        "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm: only those "
-                        "secondary cases (for profiling), no JSON line")
+                        "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm / prefill: only "
+                        "those secondary cases (for profiling), no JSON line")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--rows-per-wave", type=int, default=0)
@@ -458,9 +459,15 @@ def main():
         print(json.dumps({"copy_bytes": 64 << 20, "launches": args.warmup + args.steps}))
         return
     K, W = args.steps, args.warmup
-    if args.only in ("w8a8", "qgemm"):
+    if args.only in ("w8a8", "qgemm", "prefill"):
         s = {}
-        if args.only == "w8a8":
+        if args.only == "prefill":
+            # the 2-D GEMM route (M >= 64) at a 4096 / 14336 layer's FFN shape
+            for fmt, name in ((1, "q4_0"), (0, "q8_0")):
+                for m in (512, 2048):
+                    s[f"{name}_qgemm_m{m}_k4096_n14336"] = qgemm_case(qc, 14336, 4096, m, K, W,
+                                                                     seed=8 + m, fmt=fmt)
+        elif args.only == "w8a8":
             s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
             s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
             s["quantize_int8_asymmetric_m2048_k4096"] = asym_case(qc, 2048, 4096, K, W)
