@@ -773,29 +773,32 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
 // of its 256 weight rows as dwords.  Every wavefront issues the same loads
 // per stage (spare weight lanes re-read a valid dword into padding), so the
 // waits are exact counts, as in the small-batch kernel.
-constexpr int kPTM = 4, kPTN = 4;                 // 16x16 tiles per wave (m, n)
+constexpr int kPTN = 4;                           // 16x16 tiles per wave (n)
 constexpr int kPWM = 2, kPWN = 4;                 // waves per workgroup (m, n)
 constexpr int kPWaves = kPWM * kPWN;
-constexpr int kPBM = 16 * kPTM * kPWM;            // 128 rows of x per workgroup
 constexpr int kPBN = 16 * kPTN * kPWN;            // 256 rows of W per workgroup
-constexpr int kPMT = kPBM / 16;                   // 8 m-tiles per workgroup
-constexpr int kPRing = 3;
 
-template <int FMT>
+// TM: 16x16 tiles per wave along m (4: 128 x 256 workgroup tiles with a
+// 3-deep ring; 8: 256 x 256 with a 2-deep ring).
+template <int FMT, int TM>
 struct PanelStage {
   static constexpr bool bias = FMT == kQ4_0;
+  static constexpr int bm = 16 * TM * kPWM;                         // rows of x per workgroup
+  static constexpr int mt = bm / 16;                                // m-tiles per workgroup
   static constexpr int pd = PairLayout<FMT>::bytes / 4;             // 17 / 9 dwords per row
-  static constexpr int x_bytes = kPMT * 2 * kFragBytes;             // 32 KB
-  static constexpr int x_loads = x_bytes / 16 / (64 * kPWaves);     // 4 chunks per lane
-  static constexpr int b_bytes = bias ? kPMT * 2 * 64 : 0;          // 1 KB
+  static constexpr int x_bytes = mt * 2 * kFragBytes;               // 32 / 64 KB
+  static constexpr int x_loads = x_bytes / 16 / (64 * kPWaves);     // 4 / 8 chunks per lane
+  static constexpr int b_bytes = bias ? mt * 2 * 64 : 0;            // 1 / 2 KB
   static constexpr int w_dwords = kPBN * pd;
   static constexpr int w_loads = (w_dwords + 64 * kPWaves - 1) / (64 * kPWaves);  // 9 / 5
   static constexpr int w_bytes = kPWaves * w_loads * 256;           // with padding
   static constexpr int bytes = x_bytes + b_bytes + w_bytes;
+  static constexpr int ring = 3 * bytes <= 160 * 1024 ? 3 : 2;
   static constexpr int g = x_loads + (bias ? 1 : 0) + w_loads;      // loads per wave per stage
   static_assert(x_bytes % (16 * 64 * kPWaves) == 0, "whole x loads");
-  static_assert(kPRing * bytes <= 160 * 1024, "LDS");
-  static_assert(g * (kPRing - 1) < 64, "vmcnt range");
+  static_assert(ring * bytes <= 160 * 1024, "LDS");
+  static_assert(g * (ring - 1) < 64, "vmcnt range");
+  static_assert(!bias || mt <= 64 && kPWaves * 8 >= mt, "bias loads: lanes 0..7 of one wave per m-tile");
 };
 
 // Activation fragments [m-tile][block][hi | lo][64 lanes][16 B] and (q4_0)
@@ -837,17 +840,19 @@ __global__ __launch_bounds__(64) void panel_prep(const float* __restrict__ x, in
     zero_y[i] = 0.0f;
 }
 
-template <int FMT>
+template <int FMT, int TM>
 __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
     float* __restrict__ y, const int* __restrict__ rexp, int M, int N, int K,
     int pairs_per_split, int ks_count) {
-  using PS = PanelStage<FMT>;
+  using PS = PanelStage<FMT, TM>;
   constexpr int PB = PairLayout<FMT>::bytes;
   constexpr int G = PS::g;
+  constexpr int R = PS::ring;
+  constexpr int BR = PS::mt / kPWaves;           // bias m-tiles per wave (1 / 2)
   __shared__ __attribute__((aligned(1024))) uint8_t ring0[PS::bytes];
   __shared__ __attribute__((aligned(1024))) uint8_t ring1[PS::bytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t ring2[PS::bytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring2[R > 2 ? PS::bytes : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -855,7 +860,7 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
   const int wm = wave % kPWM, wn = wave / kPWM;
   const int j = lane >> 4;
   const int n0 = blockIdx.x * kPBN;
-  const int mt0 = blockIdx.y * kPMT;
+  const int mt0 = blockIdx.y * PS::mt;
   const int nb = K / 32, npairs = K / 64;
   const int p0 = blockIdx.z * pairs_per_split;
   const int p1 = min(p0 + pairs_per_split, npairs);
@@ -872,10 +877,12 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
     const int c = (wave * PS::x_loads + i) * 64 + lane;
     xoff[i] = static_cast<uint32_t>((c >> 8) * nb * kFragBytes + 16 * (c & 255));
   }
-  // bias: wave w, lanes 0..7, 128 B of m-tile w's two blocks
+  // bias: wave w, lanes 0 .. 8 BR - 1, 128 B of each of m-tiles
+  // BR w .. BR w + BR - 1 (the pair's two blocks)
   const uint8_t* bbase = reinterpret_cast<const uint8_t*>(bias) +
                          static_cast<long long>(mt0) * nb * 64;
-  const uint32_t boff = static_cast<uint32_t>(wave * nb * 64 + 16 * (lane & 7));
+  const uint32_t boff = static_cast<uint32_t>((wave * BR + ((lane >> 3) & (BR - 1))) * nb * 64 +
+                                              16 * (lane & 7));
   // weight dword d = (wave * w_loads + i) * 64 + lane: row d / pd, dword
   // d % pd; d past the stage re-reads the stage's last dword
   const uint8_t* wbase = W + static_cast<long long>(n0) * row_bytes;
@@ -888,96 +895,133 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
     woff[i] = static_cast<uint32_t>(r * row_bytes + 4 * (d % PS::pd));
   }
   auto slot_base = [&](int slot) -> uint8_t* { return slot == 0 ? ring0 : slot == 1 ? ring1 : ring2; };
-  auto issue = [&](int p, int slot) {
+  // Load l (0 .. G - 1; a constant after unrolling) of stage p into a slot:
+  // the x chunks, then (q4_0) the bias, then the weight dwords.
+  auto issue_one = [&](int p, int slot, int l) {
     uint8_t* base = slot_base(slot);
-    const uint8_t* xs = xbase + static_cast<long long>(2 * p) * kFragBytes;
+    if (l < PS::x_loads) {
+      dma16(xbase + static_cast<long long>(2 * p) * kFragBytes, xoff[l < PS::x_loads ? l : 0],
+            base + 16 * (wave * PS::x_loads + l) * 64);
+    } else if (PS::bias && l == PS::x_loads) {
+      if (lane < 8 * BR) dma16(bbase + 128 * p, boff, base + PS::x_bytes + 128 * BR * wave);
+    } else {
+      const int wl = l - PS::x_loads - (PS::bias ? 1 : 0);
+      dma4(wbase + static_cast<long long>(p) * PB, woff[wl >= 0 ? wl : 0],
+           base + PS::x_bytes + PS::b_bytes + 256 * (wave * PS::w_loads + wl));
+    }
+  };
+  auto issue = [&](int p, int slot) {
 #pragma unroll
-    for (int i = 0; i < PS::x_loads; ++i) dma16(xs, xoff[i], base + 16 * (wave * PS::x_loads + i) * 64);
-    if constexpr (PS::bias)
-      if (lane < 8) dma16(bbase + 128 * p, boff, base + PS::x_bytes + 128 * wave);
-    const uint8_t* ws = wbase + static_cast<long long>(p) * PB;
-#pragma unroll
-    for (int i = 0; i < PS::w_loads; ++i)
-      dma4(ws, woff[i], base + PS::x_bytes + PS::b_bytes + 256 * (wave * PS::w_loads + i));
+    for (int l = 0; l < G; ++l) issue_one(p, slot, l);
   };
 
-  f32x4 acc[kPTM][kPTN];
+  f32x4 acc[TM][kPTN];
 #pragma unroll
-  for (int a = 0; a < kPTM; ++a)
+  for (int a = 0; a < TM; ++a)
 #pragma unroll
     for (int b = 0; b < kPTN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int slot) {
-    const uint8_t* base = slot_base(slot);
-    const uint32_t* sw = reinterpret_cast<const uint32_t*>(base + PS::x_bytes + PS::b_bytes);
-    const float* sb = reinterpret_cast<const float*>(base + PS::x_bytes);
+  // Decoded weight fragments of one half stage (one block of the pair):
+  // codes as bf16 and the block scales of the wave's 4 n-tiles.
+  struct HalfW {
+    bf16x8 w[kPTN];
+    float d[kPTN];
+  };
+  auto decode = [&](int slot, int h, HalfW& o) {
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(slot_base(slot) + PS::x_bytes + PS::b_bytes);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      bf16x8 wv[kPTN];
-      float d[kPTN];
-#pragma unroll
-      for (int tn = 0; tn < kPTN; ++tn) {
-        const uint32_t* pr = sw + (wn * 64 + tn * 16 + (lane & 15)) * PS::pd;
-        uint32_t c0, c1, dbits;
-        if (h == 0) {
-          const uint32_t b0x = pr[PairLayout<FMT>::blk0_dword(j)];
-          const uint32_t b0y = pr[PairLayout<FMT>::blk0_dword(j) + 1];
-          const uint32_t b0z = pr[PairLayout<FMT>::blk0_dword(j) + 2];
-          c0 = __builtin_amdgcn_alignbyte(b0y, b0x, 2);
-          c1 = __builtin_amdgcn_alignbyte(b0z, b0y, 2);
-          dbits = pr[0] & 0xFFFFu;
-        } else {
-          c0 = pr[PairLayout<FMT>::blk1_dword(j)];
-          c1 = pr[PairLayout<FMT>::blk1_dword(j) + 1];
-          dbits = pr[PairLayout<FMT>::scale1_dword] >> 16;
-        }
-        wv[tn] = codes_bf16<FMT>(c0, c1, j);
-        d[tn] = half_bits_to_float(dbits);
+    for (int tn = 0; tn < kPTN; ++tn) {
+      const uint32_t* pr = sw + (wn * 64 + tn * 16 + (lane & 15)) * PS::pd;
+      uint32_t c0, c1, dbits;
+      if (h == 0) {
+        const uint32_t b0x = pr[PairLayout<FMT>::blk0_dword(j)];
+        const uint32_t b0y = pr[PairLayout<FMT>::blk0_dword(j) + 1];
+        const uint32_t b0z = pr[PairLayout<FMT>::blk0_dword(j) + 2];
+        c0 = __builtin_amdgcn_alignbyte(b0y, b0x, 2);
+        c1 = __builtin_amdgcn_alignbyte(b0z, b0y, 2);
+        dbits = pr[0] & 0xFFFFu;
+      } else {
+        c0 = pr[PairLayout<FMT>::blk1_dword(j)];
+        c1 = pr[PairLayout<FMT>::blk1_dword(j) + 1];
+        dbits = pr[PairLayout<FMT>::scale1_dword] >> 16;
       }
-#pragma unroll
-      for (int tm = 0; tm < kPTM; ++tm) {
-        const int mt = wm * kPTM + tm;
-        const uint8_t* f = base + (mt * 2 + h) * kFragBytes + 16 * lane;
-        const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
-        const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
-        f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (PS::bias) c0 = *reinterpret_cast<const f32x4*>(sb + (mt * 2 + h) * 16 + 4 * j);
-#pragma unroll
-        for (int tn = 0; tn < kPTN; ++tn) {
-          f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv[tn], c0, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv[tn], c, 0, 0, 0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[tm][tn][e] = fmaf(c[e], d[tn], acc[tm][tn][e]);
-        }
-      }
+      o.w[tn] = codes_bf16<FMT>(c0, c1, j);
+      o.d[tn] = half_bits_to_float(dbits);
     }
   };
-
-  // Ring: stages p0 .. p0 + kPRing - 2 in flight before the loop; step i
-  // waits for stage p0 + i, meets the workgroup (the slot the next issue
-  // overwrites is no longer read), issues stage p0 + i + kPRing - 1 and
-  // computes.  Unrolled by the ring depth so every slot index is a constant.
-  const int count = p1 - p0;
+  // The 2 x kPTN MFMAs of m-tile tm against one decoded half, each tile's
+  // block sum scaled into the accumulators.
+  auto mma = [&](int slot, int h, int tm, const HalfW& hw) {
+    const uint8_t* base = slot_base(slot);
+    const int mt = wm * TM + tm;
+    const uint8_t* f = base + (mt * 2 + h) * kFragBytes + 16 * lane;
+    const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
+    const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+    f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (PS::bias)
+      c0 = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base + PS::x_bytes) +
+                                           (mt * 2 + h) * 16 + 4 * j);
 #pragma unroll
-  for (int i = 0; i < kPRing - 1; ++i)
-    if (i < count) issue(p0 + i, i);
-  auto step = [&](int i, int slot) {
-    // stages issued after this one and still possibly in flight
-    const int ahead = min(kPRing - 2, count - 1 - i);
-    wait_stages<G, kPRing - 2>(ahead);
-    wait_lgkmcnt0();
-    ring_barrier();
-    if (i + kPRing - 1 < count) issue(p0 + i + kPRing - 1, (slot + kPRing - 1) % kPRing);
-    compute(slot);
+    for (int tn = 0; tn < kPTN; ++tn) {
+      f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, hw.w[tn], c0, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, hw.w[tn], c, 0, 0, 0);
 #pragma unroll
-    for (int a = 0; a < kPTM; ++a)
+      for (int e = 0; e < 4; ++e) acc[tm][tn][e] = fmaf(c[e], hw.d[tn], acc[tm][tn][e]);
+    }
+  };
+  auto pin_acc = [&]() {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
       for (int b = 0; b < kPTN; ++b) asm volatile("" : "+v"(acc[a][b]));
   };
-  for (int i = 0; i < count; i += kPRing) {
-    step(i, 0);
-    if (i + 1 < count) step(i + 1, 1);
-    if (i + 2 < count) step(i + 2, 2);
+
+  // Ring of R stages.  Stages p0 .. p0 + R - 2 are in flight before the
+  // loop.  Step i starts with the wave's wait for stage p0 + i + 1 and a
+  // workgroup barrier, after which that stage is visible to every wave and
+  // no wave reads stage p0 + i - 1, whose slot receives stage p0 + i + R - 1.
+  // Those loads are spread over block 0's MFMAs so that the eight waves do
+  // not queue them all at once.  Weights are decoded one half stage ahead:
+  // block 1's decode overlaps block 0's MFMAs, and block 0 of stage
+  // p0 + i + 1 is decoded during block 1's.  Past the last stage the loads
+  // repeat stage p1 - 1 into the free slot and the decode reads a slot whose
+  // result is unused, so every step is the same straight-line code.
+  // Unrolled by the ring depth so every slot index is a constant.
+  static_assert(R >= 3, "the next stage must land while the current one is read");
+  const int count = p1 - p0;
+  if (count > 0) {
+#pragma unroll
+    for (int i = 0; i < R - 1; ++i)
+      if (i < count) issue(p0 + i, i);
+    wait_stages<G, R - 2>(min(R - 2, count - 1));
+    wait_lgkmcnt0();
+    ring_barrier();
+    HalfW h0, h1;
+    decode(0, 0, h0);
+    auto step = [&](int i, int slot) {
+      // stages issued after stage i + 1 and possibly still in flight
+      wait_stages<G, R - 3>(min(R - 3, count - 2 - i));
+      wait_lgkmcnt0();
+      ring_barrier();
+      const int pi = min(p0 + i + R - 1, p1 - 1);
+      const int si = (slot + R - 1) % R;
+      decode(slot, 1, h1);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int l = tm * G / TM; l < (tm + 1) * G / TM; ++l) issue_one(pi, si, l);
+        mma(slot, 0, tm, h0);
+      }
+      decode((slot + 1) % R, 0, h0);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) mma(slot, 1, tm, h1);
+      pin_acc();
+    };
+    for (int i = 0; i < count; i += R) {
+#pragma unroll
+      for (int u = 0; u < R; ++u)
+        if (i + u < count) step(i + u, u);
+    }
   }
   wait_vmcnt<0>();   // no global->LDS load may outlive the workgroup's LDS
 
@@ -988,10 +1032,10 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
     const int n = n0 + wn * 64 + tn * 16 + (lane & 15);
     if (n >= N) continue;
 #pragma unroll
-    for (int tm = 0; tm < kPTM; ++tm) {
+    for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int m = 16 * (mt0 + wm * kPTM + tm) + 4 * j + e;
+        const int m = 16 * (mt0 + wm * TM + tm) + 4 * j + e;
         if (m >= M) continue;
         const long long o = static_cast<long long>(m) * N + n;
         const float v = ldexpf(acc[tm][tn][e], rexp[m]);   // undo the row scale
@@ -1005,8 +1049,8 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
 // K ranges of the 2-D GEMM: two (atomic adds onto a cleared y, two addends
 // onto zero: order-independent) when both halves' workgroups still run in one
 // round at one workgroup per CU, else one.
-int panel_split(int m, int n, int k, int cus) {
-  const long long tiles = static_cast<long long>((m + kPBM - 1) / kPBM) * ((n + kPBN - 1) / kPBN);
+int panel_split(int m, int n, int k, int cus, int bm) {
+  const long long tiles = static_cast<long long>((m + bm - 1) / bm) * ((n + kPBN - 1) / kPBN);
   return 2 * tiles <= cus && k / 64 >= 2 ? 2 : 1;
 }
 
@@ -1016,25 +1060,27 @@ int panel_split(int m, int n, int k, int cus) {
 // ceil(workgroups / CUs) rounds; a pass of 32 rows costs max(N K / 2.3e12 s,
 // 17 us).  The passes win for small M at small N or long K.
 bool panel_pays(int m, int n, int k, int cus) {
-  const int ks = panel_split(m, n, k, cus);
-  const long long tiles = static_cast<long long>((m + kPBM - 1) / kPBM) * ((n + kPBN - 1) / kPBN);
+  constexpr int bm = PanelStage<kQ8_0, 4>::bm;
+  const int ks = panel_split(m, n, k, cus, bm);
+  const long long tiles = static_cast<long long>((m + bm - 1) / bm) * ((n + kPBN - 1) / kPBN);
   const long long rounds = (tiles * ks + cus - 1) / cus;
   const double panel = rounds * ((k / 64 + ks - 1) / ks) * 2.45e-6 + 4e-6;
   const double passes = ((m + 31) / 32) * std::max(static_cast<double>(n) * k / 2.3e12, 17e-6);
   return panel < passes;
 }
 
-template <int FMT>
+template <int FMT, int TM>
 hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, int k,
                      hipStream_t s, int split, const int* rexp) {
+  using PS = PanelStage<FMT, TM>;
   const int nb = k / 32, npairs = k / 64;
-  const int mblocks = (m + kPBM - 1) / kPBM, nblocks = (n + kPBN - 1) / kPBN;
-  const int mtiles = mblocks * kPMT;
+  const int mblocks = (m + PS::bm - 1) / PS::bm, nblocks = (n + kPBN - 1) / kPBN;
+  const int mtiles = mblocks * PS::mt;
   // per-lane 32-bit source offsets within a workgroup's rows
   if (static_cast<long long>(kPBN) * nb * (PairLayout<FMT>::bytes / 2) >= (1LL << 32) ||
-      static_cast<long long>(kPMT) * nb * kFragBytes >= (1LL << 32))
+      static_cast<long long>(PS::mt) * nb * kFragBytes >= (1LL << 32))
     return hipErrorInvalidValue;
-  int ks = panel_split(m, n, k, device_cus());
+  int ks = panel_split(m, n, k, device_cus(), PS::bm);
   if (split == 1 || split == 2) ks = split;
   if (npairs < 2) ks = 1;
   const int per = (npairs + ks - 1) / ks;
@@ -1052,7 +1098,7 @@ hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, i
   if (e != hipSuccess) return e;
   const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(mblocks),
                   static_cast<unsigned>(ks));
-  qgemm_panel<FMT><<<grid, 64 * kPWaves, 0, s>>>(W, xf, bias, y, rexp, m, n, k, per, ks);
+  qgemm_panel<FMT, TM><<<grid, 64 * kPWaves, 0, s>>>(W, xf, bias, y, rexp, m, n, k, per, ks);
   return hipGetLastError();
 }
 
@@ -1077,8 +1123,8 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
     if (e != hipSuccess) return e;
   }
   if (use_panel)
-    return fmt == kQ8_0 ? run_panel<kQ8_0>(w, x, y, m, n, k, s, panel, rexp)
-                        : run_panel<kQ4_0>(w, x, y, m, n, k, s, panel, rexp);
+    return fmt == kQ8_0 ? run_panel<kQ8_0, 4>(w, x, y, m, n, k, s, panel, rexp)
+                        : run_panel<kQ4_0, 4>(w, x, y, m, n, k, s, panel, rexp);
   for (int m0 = 0; m0 < m; m0 += 32) {
     const int mt = m - m0 < 32 ? m - m0 : 32;
     const float* xm = x + static_cast<long long>(m0) * k;
