@@ -49,6 +49,7 @@ namespace qc {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -119,11 +120,15 @@ __device__ __forceinline__ bf16x8 codes_bf16(uint32_t lo, uint32_t hi, int j) {
   } else {
     const int sh = (j >> 1) * 4;          // lane groups 2, 3 take the high nibbles
     const uint32_t a = (lo >> sh) & 0x0F0F0F0Fu, b = (hi >> sh) & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {   // v_cvt_f32_ubyte{0..3}
-      v[i] = static_cast<__bf16>(static_cast<float>(static_cast<uint8_t>(a >> (8 * i))));
-      v[4 + i] = static_cast<__bf16>(static_cast<float>(static_cast<uint8_t>(b >> (8 * i))));
-    }
+    // A nibble byte u (0..15) is the OCP e4m3 encoding of u * 2^-9
+    // (subnormal below 8, exponent field 1 from 8), so the scaled fp8
+    // conversion gives bf16(u) exactly, two bytes per instruction (low word:
+    // bytes 0, 1; high word: bytes 2, 3).
+    const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(a, 512.0f, false);
+    const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(a, 512.0f, true);
+    const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(b, 512.0f, false);
+    const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(b, 512.0f, true);
+    v = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
   }
   return v;
 }
