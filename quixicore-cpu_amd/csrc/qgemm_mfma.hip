@@ -158,70 +158,155 @@ __device__ __forceinline__ void ring_barrier() {
 }
 
 
-// Per-row power-of-two scale of the activations for the bf16 layouts:
-// e(m) = the frexp exponent of max |x[m][:]| (0 for a zero or non-finite
-// row).  The fragments hold x * 2^-e(m), so every row's largest element is in
-// [0.5, 1): no element that matters is subnormal in bf16 (which would leave
-// it a few bits) and no product overflows; outputs are scaled back by 2^e(m),
-// exactly.  One 256-thread workgroup per row.
-__global__ __launch_bounds__(256) void row_exponents(const float* __restrict__ x, int K,
-                                                     int* __restrict__ rexp) {
-  __shared__ float smax[4];
-  const float* xr = x + static_cast<long long>(blockIdx.x) * K;
-  float mx = 0.f;
-  // four independent loads in flight per step (one memory latency for
-  // K <= 16384 instead of K / 256 of them)
-  int i = threadIdx.x;
-  if (K % 4 == 0 && reinterpret_cast<uintptr_t>(xr) % 16 == 0) {
-    const float4* x4 = reinterpret_cast<const float4*>(xr);
-    const int n4 = K / 4;
-    for (; i + 768 < n4; i += 1024) {
-      const float4 a = x4[i], b = x4[i + 256], c = x4[i + 512], d = x4[i + 768];
-      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                           fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
-      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
-                           fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
-    }
-    for (; i < n4; i += 256) {
-      const float4 a = x4[i];
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
-    }
-  } else {
-    for (; i + 768 < K; i += 1024)
-      mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xr[i]), fabsf(xr[i + 256]))),
-                 fmaxf(fabsf(xr[i + 512]), fabsf(xr[i + 768])));
-    for (; i < K; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
-  }
-  mx = wave_max_nonneg(mx);
-  if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
-    int e = 0;
-    if (mx > 0.f && mx <= 3.402823466e38f) (void)frexpf(mx, &e);
-    rexp[blockIdx.x] = e;
-  }
-}
-
-// Activation fragments: one 64-thread workgroup per (block b, m-tile t).
-// Lane l covers row 16t + (l & 15), codes 8(l >> 4) .. +7 of the block.
-// Block 0 also copies the weights' last row's short final stage (`tail`
-// bytes from `tail_src`) into the zero-padded `tail_pad` (pad_bytes), which
-// the GEMM reads instead of running past the end of W.
-template <int XL, bool BIAS>
-__global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, int M, int K,
-                                                 uint8_t* __restrict__ xf,
-                                                 float* __restrict__ bias, float* zero_y,
+// Activation fragments of the bf16 layouts, 2 KB per (16-row m-tile, block):
+// lane l holds row 16t + (l & 15), elements 8(l >> 4) .. +7 of the block as
+// bf16 hi (bytes 0..1023) and lo = bf16(v - hi) (bytes 1024..2047), and
+// (q4_0) the bias -8 * sum(hi + lo) per row and block, the MFMA's C input
+// for the nibble offset.  Small-batch passes store fragment (b, t) at
+// b * T + t over nbp blocks (those past K zero), the panel route at
+// t * nb + b.
+//
+// Per-row power-of-two scale: e(m) = the frexp exponent of max |x[m][:]| (0
+// for a zero or non-finite row).  The fragments hold v = x * 2^-e(m), so
+// every row's largest element is in [0.5, 1): no element that matters is
+// subnormal in bf16 (which would leave it a few bits) and no product
+// overflows; outputs are scaled back by 2^e(m), exactly.
+//
+// One 256-thread workgroup per row of the layout (rows past M are zero): the
+// row's maximum, then its fragments, in one launch.  Thread t converts the
+// half blocks h = t + 256 i; the two halves of a block sit in lanes t, t ^ 1,
+// and the bias sum keeps the order ((s0 + s1) + (s2 + s3)) of the four
+// 8-element chunk sums.  Workgroup 0 also copies the weights' short final
+// stage into `tail_pad` (small-batch passes), and all of them clear y when
+// two K ranges add into it.
+template <bool PANEL, bool BIAS>
+__global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, int M, int K,
+                                                 int nbo, int T, uint8_t* __restrict__ xf,
+                                                 float* __restrict__ bias,
+                                                 int* __restrict__ rexp, float* zero_y,
                                                  long long zero_count,
                                                  const uint8_t* __restrict__ tail_src, int tail,
-                                                 uint8_t* __restrict__ tail_pad, int pad_bytes,
-                                                 const int* __restrict__ rexp) {
+                                                 uint8_t* __restrict__ tail_pad, int pad_bytes) {
+  __shared__ float smax[4];
+  // Workgroups are dealt to the 8 XCDs in turn (id mod 8), and each 128-byte
+  // line of a fragment holds 8 consecutive rows: give those rows to one XCD
+  // (ids 8q + c of each group of 64 take rows 8c + q), so each line is
+  // assembled in one L2 instead of being written back in pieces from eight.
+  const int m = gridDim.x % 64 == 0
+                    ? (blockIdx.x & ~63) | ((blockIdx.x & 7) << 3) | ((blockIdx.x >> 3) & 7)
+                    : static_cast<int>(blockIdx.x);
+  const int tid = threadIdx.x;
+  const bool live = m < M;
+  const int nb = K / 32;
+  const float* xr = x + static_cast<long long>(live ? m : 0) * K;
+  if (blockIdx.x == 0 && tail > 0)
+    for (int i = tid; i < pad_bytes; i += 256) tail_pad[i] = i < tail ? tail_src[i] : 0;
+
+  // max |x[m][:]|, four independent loads in flight per step
+  float mx = 0.f;
+  if (live) {
+    int i = tid;
+    if (reinterpret_cast<uintptr_t>(xr) % 16 == 0) {
+      const float4* x4 = reinterpret_cast<const float4*>(xr);
+      const int n4 = K / 4;
+      for (; i + 768 < n4; i += 1024) {
+        const float4 a = x4[i], b = x4[i + 256], c = x4[i + 512], d = x4[i + 768];
+        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                             fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
+                             fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
+      }
+      for (; i < n4; i += 256) {
+        const float4 a = x4[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+      }
+    } else {
+      for (; i + 768 < K; i += 1024)
+        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xr[i]), fabsf(xr[i + 256]))),
+                   fmaxf(fabsf(xr[i + 512]), fabsf(xr[i + 768])));
+      for (; i < K; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+    }
+  }
+  mx = wave_max_nonneg(mx);
+  if ((tid & 63) == 0) smax[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+  int e = 0;
+  if (mx > 0.f && mx <= 3.402823466e38f) (void)frexpf(mx, &e);
+  if (live && tid == 0) rexp[m] = e;
+
+  const int t = m >> 4, r = m & 15;
+  const int nh = 2 * nbo;                          // half blocks of the layout's row
+  for (int h0 = 0; h0 < nh; h0 += 256) {           // uniform trip count: the shuffle below
+    const int h = h0 + tid;
+    const int blk = h >> 1, half = h & 1;
+    const bool in = live && blk < nb;
+    float v[16];
+    if (in) {
+      const float* src = xr + 32 * blk + 16 * half;
+      if (reinterpret_cast<uintptr_t>(xr) % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<float4*>(&v[4 * i]) = reinterpret_cast<const float4*>(src)[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = src[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = ldexpf(v[i], -e);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    }
+    float sc[2];
+    const long long f = PANEL ? static_cast<long long>(t) * nbo + blk
+                              : static_cast<long long>(blk) * T + t;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      bf16x8 hi, lo;
+      float sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        hi[i] = static_cast<__bf16>(v[8 * c + i]);
+        const float hv = static_cast<float>(hi[i]);
+        lo[i] = static_cast<__bf16>(v[8 * c + i] - hv);
+        sum += hv + static_cast<float>(lo[i]);
+      }
+      sc[c] = sum;
+      if (h < nh) {
+        uint8_t* dst = xf + f * kFragBytes + 16 * (r + 16 * (2 * half + c));
+        *reinterpret_cast<bf16x8*>(dst) = hi;
+        *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
+      }
+    }
+    if constexpr (BIAS) {
+      float sp = sc[0] + sc[1];
+      sp += __shfl_xor(sp, 1);
+      if (h < nh && half == 0) bias[f * 16 + r] = -8.0f * sp;
+    }
+  }
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + tid; i < zero_count;
+       i += static_cast<long long>(gridDim.x) * 256)
+    zero_y[i] = 0.0f;
+}
+
+// Digit fragments of the compact layouts (M <= 8): one 64-thread workgroup
+// per block.  Block 0 also copies the weights' last row's short final stage
+// (`tail` bytes from `tail_src`) into the zero-padded `tail_pad`
+// (pad_bytes), which the GEMM reads instead of running past the end of W.
+template <int XL, bool BIAS>
+__global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, int M, int K,
+                                                 uint8_t* __restrict__ xf, float* zero_y,
+                                                 long long zero_count,
+                                                 const uint8_t* __restrict__ tail_src, int tail,
+                                                 uint8_t* __restrict__ tail_pad, int pad_bytes) {
   if (blockIdx.x == 0 && tail > 0)
     for (int i = threadIdx.x; i < pad_bytes; i += 64) tail_pad[i] = i < tail ? tail_src[i] : 0;
   using XB = XBlock<XL, BIAS>;
+  static_assert(XB::digits, "the bf16 layouts are built by prep_rows");
   const int l = threadIdx.x;
   const int nb = K / 32;
-  if constexpr (XB::digits) {
+  {
     // Thread l: row m = l >> 3, elements 4 (l & 7) .. +3 of block b.  The
     // digits are those of the M = 1 path: e = frexp exponent of max|x_b| - 21,
     // q = rint(x * 2^-e) clamped to [-2^21, 2^21), q = 2^14 d0 + 2^7 d1 + d2.
@@ -287,33 +372,6 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
         c[2] = -8 * sum[2];
         c[3] = 0;
       }
-    }
-  } else {
-    constexpr int T = XB::T;
-    const int b = blockIdx.x / T, t = blockIdx.x % T;
-    const int m = 16 * t + (l & 15), j = l >> 4;
-    float v[8];
-    const bool live = m < M && b < nb;
-    const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * b : 0) + 8 * j;
-    const int er = live ? rexp[m] : 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = live ? ldexpf(src[i], -er) : 0.0f;
-    bf16x8 hi, lo;
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      hi[i] = static_cast<__bf16>(v[i]);
-      const float h = static_cast<float>(hi[i]);
-      lo[i] = static_cast<__bf16>(v[i] - h);
-      s += h + static_cast<float>(lo[i]);
-    }
-    uint8_t* dst = xf + (static_cast<long long>(b) * T + t) * kFragBytes + 16 * l;
-    *reinterpret_cast<bf16x8*>(dst) = hi;
-    *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
-    if constexpr (BIAS) {
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
-      if (j == 0) bias[(static_cast<long long>(b) * T + t) * 16 + (l & 15)] = -8.0f * s;
     }
   }
   // y is accumulated with two atomic adds when K is split in two: clear it.
@@ -716,7 +774,7 @@ Plan plan_for(int n, int nstages, int cus) {
 
 template <int FMT, int XL>
 hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, hipStream_t s,
-               int waves, int stages, const int* rexp) {
+               int waves, int stages, int* rexp) {
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
@@ -746,9 +804,13 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const long long row_bytes = static_cast<long long>(nb) * PairLayout<FMT>::bytes / 2;
   const int tail = (k / 64) % kStagePairs * PairLayout<FMT>::bytes;
   const uint8_t* tail_src = W + (n - 1) * row_bytes + static_cast<long long>(nstages - 1) * WStage<FMT>::row_bytes;
-  qgemm_prep<XL, FMT == kQ4_0><<<nbp * XB::prep_groups, 64, 0, s>>>(x, m, k, xf, bias, y, ks == 2 ? outs : 0,
-                                                     tail_src, tail, tail_pad,
-                                                     static_cast<int>(pad_bytes), rexp);
+  if constexpr (XB::digits)
+    qgemm_prep<XL, FMT == kQ4_0><<<nbp, 64, 0, s>>>(x, m, k, xf, y, ks == 2 ? outs : 0, tail_src,
+                                                    tail, tail_pad, static_cast<int>(pad_bytes));
+  else
+    prep_rows<false, FMT == kQ4_0><<<XL, 256, 0, s>>>(x, m, k, nbp, XB::T, xf, bias, rexp, y,
+                                                      ks == 2 ? outs : 0, tail_src, tail, tail_pad,
+                                                      static_cast<int>(pad_bytes));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (plan.nw == 8)
@@ -805,45 +867,6 @@ struct PanelStage {
   static_assert(g * (ring - 1) < 64, "vmcnt range");
   static_assert(!bias || mt <= 64 && kPWaves * 8 >= mt, "bias loads: lanes 0..7 of one wave per m-tile");
 };
-
-// Activation fragments [m-tile][block][hi | lo][64 lanes][16 B] and (q4_0)
-// bias [m-tile][block][16 rows]; rows >= M are zero.  Grid: mtiles * nb
-// workgroups of 64 threads.  Also clears y when two K halves add into it.
-template <bool BIAS>
-__global__ __launch_bounds__(64) void panel_prep(const float* __restrict__ x, int M, int K,
-                                                 uint8_t* __restrict__ xf,
-                                                 float* __restrict__ bias, float* zero_y,
-                                                 long long zero_count,
-                                                 const int* __restrict__ rexp) {
-  const int nb = K / 32;
-  const int t = blockIdx.x / nb, b = blockIdx.x % nb;
-  const int l = threadIdx.x;
-  const int m = 16 * t + (l & 15), j = l >> 4;
-  const bool live = m < M;
-  const float* src = x + static_cast<long long>(live ? m : 0) * K + 32 * b + 8 * j;
-  const int er = live ? rexp[m] : 0;
-  bf16x8 hi, lo;
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float v = live ? ldexpf(src[i], -er) : 0.0f;
-    hi[i] = static_cast<__bf16>(v);
-    const float h = static_cast<float>(hi[i]);
-    lo[i] = static_cast<__bf16>(v - h);
-    s += h + static_cast<float>(lo[i]);
-  }
-  uint8_t* dst = xf + (static_cast<long long>(t) * nb + b) * kFragBytes + 16 * l;
-  *reinterpret_cast<bf16x8*>(dst) = hi;
-  *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
-  if constexpr (BIAS) {
-    s += __shfl_xor(s, 16);
-    s += __shfl_xor(s, 32);
-    if (j == 0) bias[(static_cast<long long>(t) * nb + b) * 16 + (l & 15)] = -8.0f * s;
-  }
-  for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
-       i += static_cast<long long>(gridDim.x) * 64)
-    zero_y[i] = 0.0f;
-}
 
 template <int FMT, int TM>
 __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
@@ -1076,7 +1099,7 @@ bool panel_pays(int m, int n, int k, int cus) {
 
 template <int FMT, int TM>
 hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, int k,
-                     hipStream_t s, int split, const int* rexp) {
+                     hipStream_t s, int split, int* rexp) {
   using PS = PanelStage<FMT, TM>;
   const int nb = k / 32, npairs = k / 64;
   const int mblocks = (m + PS::bm - 1) / PS::bm, nblocks = (n + kPBN - 1) / kPBN;
@@ -1097,8 +1120,8 @@ hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, i
   uint8_t* xf = static_cast<uint8_t*>(ws);
   float* bias = reinterpret_cast<float*>(xf + xf_bytes);
   const long long outs = static_cast<long long>(m) * n;
-  panel_prep<FMT == kQ4_0><<<static_cast<unsigned>(mtiles * nb), 64, 0, s>>>(
-      x, m, k, xf, bias, y, ks == 2 ? outs : 0, rexp);
+  prep_rows<true, FMT == kQ4_0><<<static_cast<unsigned>(16 * mtiles), 256, 0, s>>>(
+      x, m, k, nb, 0, xf, bias, rexp, y, ks == 2 ? outs : 0, nullptr, 0, nullptr, 0);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(mblocks),
@@ -1116,16 +1139,13 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
   // (for m >= 2) with one / two K ranges
   const bool use_panel = panel > 0 || (panel == 0 && m >= 64 && panel_pays(m, n, k, device_cus()));
   // The bf16 layouts (the panel and passes of more than 8 rows) scale each
-  // row by its power of two: one exponent kernel for the whole call.
+  // row by its power of two; their prep kernels store the exponents here.
   int* rexp = nullptr;
   if (use_panel || m > 8) {
     void* p = nullptr;
     hipError_t e = workspace_for(s, sizeof(int) * static_cast<size_t>(m) + 256, &p, 1);
     if (e != hipSuccess) return e;
     rexp = static_cast<int*>(p);
-    row_exponents<<<static_cast<unsigned>(m), 256, 0, s>>>(x, k, rexp);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
   }
   if (use_panel)
     return fmt == kQ8_0 ? run_panel<kQ8_0, 4>(w, x, y, m, n, k, s, panel, rexp)
@@ -1134,7 +1154,7 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
     const int mt = m - m0 < 32 ? m - m0 : 32;
     const float* xm = x + static_cast<long long>(m0) * k;
     float* ym = y + static_cast<long long>(m0) * n;
-    const int* rm = rexp != nullptr ? rexp + m0 : nullptr;
+    int* rm = rexp != nullptr ? rexp + m0 : nullptr;
     // activation layout: compact rows for M <= 4 / 8, dense 16-row tiles above
     hipError_t e;
     if (fmt == kQ8_0)
