@@ -382,8 +382,9 @@ __device__ __forceinline__ void write_tile32(const v16i (&acc)[FN][FM], long lon
 //     MFMAs of quarter q run;
 //   quarter 3: wait for this wave's loads of step k+1, barrier (all waves'
 //     loads are in and every wave has finished reading stage k), issue the
-//     loads of step k+S into stage k, read quarter 0 of step k+1, then the
-//     MFMAs of quarter 3.
+//     loads of step k+S into stage k (with S >= 3 only the first quarter of
+//     them; the rest go out before the MFMAs of quarters 1..3 of step k+1),
+//     read quarter 0 of step k+1, then the MFMAs of quarter 3.
 // Past the last step the loads repeat the last step into stages that are
 // never read again, which keeps every wait count a constant.  The last step
 // runs separately and, when K is not a multiple of 128, skips the quarters
@@ -495,18 +496,40 @@ __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
   wait_vmcnt<G * (S - 1)>();
   ring_barrier();
   read_frags(0, 0, 0);
+  // With three or more stages the loads of a step are spread over the
+  // quarters of the next one (part 0 after the barrier, part q before
+  // quarter q's MFMAs) instead of being queued by all waves at once: they
+  // are needed only S - 2 steps later.  With two stages they are needed at
+  // the end of the next step and go out together.
+  constexpr int SPREAD = S >= 3 ? QPS : 1;
   int stage = 0;
+  int pstep = 0, pstage = 0;                // the step being loaded and its stage
+  auto issue_part = [&](int part) {
+    int8_t* base = ring + pstage * kStage;
+    const int k0 = pstep * kLine;
+#pragma unroll
+    for (int j = part * G / SPREAD; j < (part + 1) * G / SPREAD; ++j) {
+      int off = k0 + coff[j & 1];
+      off = off < K - 16 ? off : K - 16;
+      int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
+                           : base + TN * kLine + (wave * GX + (j - GW)) * 1024;
+      load_lds16(src[j] + off, dst);
+    }
+  };
   for (int k = 0; k + 1 < nk; ++k) {
 #pragma unroll
     for (int q = 1; q < QPS; ++q) {
+      if (q < SPREAD && k > 0) issue_part(q);
       read_frags(stage, q, q & 1);
       mfmas((q - 1) & 1);
     }
-    // Loads issued: steps up to k+S-1; step k+1 must be in.
+    // Loads issued: steps up to k+S-1, all parts; step k+1 must be in.
     wait_vmcnt<G * (S - 2)>();
     wait_lgkmcnt0();
     ring_barrier();
-    issue(k + S < nk ? k + S : nk - 1, stage);
+    pstep = k + S < nk ? k + S : nk - 1;
+    pstage = stage;
+    issue_part(0);
     stage = stage + 1 < S ? stage + 1 : 0;
     read_frags(stage, 0, 0);
     mfmas((QPS - 1) & 1);
