@@ -285,13 +285,26 @@ def asym_case(qc, m, k, steps, warmup):
             "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
 
 
+def w8a8_operands(qc, m, n, k, seed=7):
+    """BASELINE config 3's operands: weights f32 ~N(0, 0.02) quantized per
+    output channel (absmax / 127), activations f32 ~N(0, 1) with 0.1% of the
+    elements scaled by 20, quantized per row -- both with quantize_int8."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    wf = torch.randn((n, k), generator=g, device=dev) * 0.02
+    w, ws = qc.quantize_int8(wf)
+    del wf
+    xf = torch.randn((m, k), generator=g, device=dev)
+    xf = torch.where(torch.rand((m, k), generator=g, device=dev) < 1e-3, xf * 20.0, xf)
+    x, as_ = qc.quantize_int8(xf)
+    return w, x, ws.reshape(-1), as_.reshape(-1)
+
+
 def w8a8_case(qc, m, n, k, steps, warmup):
     import torch
     dev = torch.device("cuda:0")
-    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev)
-    x = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev)
-    ws = torch.rand(n, device=dev) * 0.01
-    as_ = torch.rand(m, device=dev) * 0.1
+    w, x, ws, as_ = w8a8_operands(qc, m, n, k)
     y = torch.empty((m, n), dtype=torch.float32, device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev)
 
