@@ -212,3 +212,29 @@ def test_qgemv_adversarial_activations(qc, oracle, synth, dev, fmt):
         assert np.all(np.isfinite(y)), i
         worst = _check_rows(oracle, fmt, packed, x, y, n, k)
         print(f"case {i}: worst normalised error {worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("m,off", [(12, 1), (32, 0), (25, 3)])
+def test_qgemm_dense_activation_range(qc, oracle, synth, dev, fmt, m, off):
+    """The bf16 layouts of passes with more than 8 rows: activations over 40
+    decades, a zero row, a row of subnormals and one near the float maximum,
+    with x at a 4-byte offset from 16-byte alignment (scalar loads in the
+    row-exponent and fragment kernel)."""
+    import torch
+    print(f"qgemm dense range fmt={fmt} m={m} off={off}", flush=True)
+    n, k = 200, 1024
+    packed, _ = _case(oracle, synth, fmt, n, k, 55 + m)
+    rng = np.random.default_rng(m + off)
+    x = (rng.standard_normal((m, k)) * 10.0 ** rng.uniform(-20, 20, (m, k))).astype(np.float32)
+    x[1] = 0.0
+    x[2] = (rng.standard_normal(k) * 1e-40).astype(np.float32)
+    x[3] = (rng.standard_normal(k) * 1e37).astype(np.float32)
+    X = torch.zeros(m * k + off, dtype=torch.float32, device=dev)
+    X[off:] = torch.from_numpy(x.reshape(-1)).to(dev)
+    Y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    P = torch.from_numpy(packed).to(dev)
+    assert qc.qgemm_raw(fmt, P, X[off:], Y, m, n, k) == 0
+    Y = Y.cpu().numpy()
+    for r in range(m):
+        _check_rows(oracle, fmt, packed, x[r], Y[r], n, k)
