@@ -203,7 +203,8 @@ def test_asym_shapes(qc, oracle, dev, rows, dim, off):
 
 def test_asym_edges(qc, oracle, dev):
     """Out-of-range zero points and codes (1-ulp spreads across a binade),
-    constant rows, the float extremes, tiny values and signed zeros."""
+    constant rows, the float extremes, tiny values, signed zeros and exact
+    half-integer quotients."""
     fmax = np.finfo(np.float32).max
     rows = [np.array([0.99999994, 1.0] * 32, np.float32),
             np.array([1.0, 1.0000001] * 32, np.float32),
@@ -211,7 +212,12 @@ def test_asym_edges(qc, oracle, dev):
             np.array([-fmax, fmax] * 32, np.float32),
             np.array([1e-30, 2e-30] * 32, np.float32),
             np.array([0.0, -0.0] * 32, np.float32),
-            np.linspace(-3.0, 5.0, 64).astype(np.float32)]
+            np.linspace(-3.0, 5.0, 64).astype(np.float32),
+            # exact half-integer quotients (scales 1, 2, 1/2, 1/2): ties to even
+            np.array([0.0, 255.0] + [k + 0.5 for k in range(62)], np.float32),
+            np.array([0.0, 510.0] + [2 * k + 1 for k in range(62)], np.float32),
+            np.array([-127.5, 0.0] + [-(k + 0.5) / 2 for k in range(62)], np.float32),
+            np.array([-64.0, 63.5] + [(k - 31) * 0.75 for k in range(62)], np.float32)]
     _asym_check(qc, oracle, dev, np.stack(rows))
 
 
