@@ -865,7 +865,8 @@ struct PanelStage {
   static_assert(x_bytes % (16 * 64 * kPWaves) == 0, "whole x loads");
   static_assert(ring * bytes <= 160 * 1024, "LDS");
   static_assert(g * (ring - 1) < 64, "vmcnt range");
-  static_assert(mt % kPWaves == 0 && mt / kPWaves <= 8, "bias loads: 8 lanes per m-tile, whole m-tiles per wave");
+  static_assert(mt % kPWaves == 0 && mt / kPWaves <= 8 && ((mt / kPWaves) & (mt / kPWaves - 1)) == 0,
+                "bias loads: 8 lanes per m-tile, a power-of-two count of whole m-tiles per wave");
 };
 
 template <int FMT, int TM>
