@@ -39,6 +39,7 @@
 // back the XCD's whole L2 and costs far more than the extra launch.)
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "qc_device.h"
@@ -50,6 +51,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -107,16 +110,39 @@ struct PairLayout<kQ4_0> {
 typedef uint32_t u32x3_a4 __attribute__((ext_vector_type(3), aligned(4)));
 typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
 
-// Eight codes of this lane for one block as a bf16 MFMA operand.
+// MFMA operand type of the bf16-layout routes: q8_0 runs in f16 (codes and
+// hi/lo activations), q4_0 in bf16.
 template <int FMT>
-__device__ __forceinline__ bf16x8 codes_bf16(uint32_t lo, uint32_t hi, int j) {
-  bf16x8 v;
+struct OpType {
+  using T = bf16x8;
+};
+template <>
+struct OpType<kQ8_0> {
+  using T = f16x8;
+};
+
+__device__ __forceinline__ f32x4 mfma_op(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_op(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Eight codes of this lane for one block as an MFMA operand (lo: codes 0..3,
+// hi: codes 4..7 of the lane's eight bytes).
+template <int FMT>
+__device__ __forceinline__ typename OpType<FMT>::T codes_op(uint32_t lo, uint32_t hi, int j) {
   if constexpr (FMT == kQ8_0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>(lo >> (8 * i))));
-      v[4 + i] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>(hi >> (8 * i))));
-    }
+    // Code byte q flipped to q + 128 (0..255) under the high byte 0x64 of
+    // f16(1024) is f16(1024 + q + 128), exactly; one packed f16 subtraction
+    // of 1152 leaves q.  v_perm_b32 interleaves two code bytes with 0x64.
+    const uint32_t a = lo ^ 0x80808080u, b = hi ^ 0x80808080u;
+    const f16x2 k = f16x2{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+    const f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u)) - k;
+    const f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u)) - k;
+    const f16x2 p2 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u)) - k;
+    const f16x2 p3 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) - k;
+    return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
   } else {
     const int sh = (j >> 1) * 4;          // lane groups 2, 3 take the high nibbles
     const uint32_t a = (lo >> sh) & 0x0F0F0F0Fu, b = (hi >> sh) & 0x0F0F0F0Fu;
@@ -128,9 +154,8 @@ __device__ __forceinline__ bf16x8 codes_bf16(uint32_t lo, uint32_t hi, int j) {
     const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(a, 512.0f, true);
     const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(b, 512.0f, false);
     const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(b, 512.0f, true);
-    v = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    return bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
   }
-  return v;
 }
 
 // Waits until at most G * min(D, ahead) loads are outstanding (`ahead` is a
@@ -233,6 +258,9 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
   mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
   int e = 0;
   if (mx > 0.f && mx <= 3.402823466e38f) (void)frexpf(mx, &e);
+  // q4_0 (bf16): largest element in [0.5, 1); q8_0 (f16): in [2^14, 2^15), so
+  // that only elements below 2^-28 of the row's maximum reach f16 subnormals
+  if constexpr (!BIAS) e -= 15;
   if (live && tid == 0) rexp[m] = e;
 
   const int t = m >> 4, r = m & 15;
@@ -263,20 +291,22 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
                               : static_cast<long long>(blk) * T + t;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      bf16x8 hi, lo;
+      using Op = std::conditional_t<BIAS, bf16x8, f16x8>;
+      using El = std::conditional_t<BIAS, __bf16, _Float16>;
+      Op hi, lo;
       float sum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        hi[i] = static_cast<__bf16>(v[8 * c + i]);
+        hi[i] = static_cast<El>(v[8 * c + i]);
         const float hv = static_cast<float>(hi[i]);
-        lo[i] = static_cast<__bf16>(v[8 * c + i] - hv);
+        lo[i] = static_cast<El>(v[8 * c + i] - hv);
         sum += hv + static_cast<float>(lo[i]);
       }
       sc[c] = sum;
       if (h < nh) {
         uint8_t* dst = xf + f * kFragBytes + 16 * (r + 16 * (2 * half + c));
-        *reinterpret_cast<bf16x8*>(dst) = hi;
-        *reinterpret_cast<bf16x8*>(dst + 1024) = lo;
+        *reinterpret_cast<Op*>(dst) = hi;
+        *reinterpret_cast<Op*>(dst + 1024) = lo;
       }
     }
     if constexpr (BIAS) {
@@ -580,18 +610,19 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
             accd[t] += valid ? blk_dot : 0.0f;
           }
         } else {
-          const bf16x8 wv = codes_bf16<FMT>(c0, c1, j);
+          using Op = typename OpType<FMT>::T;
+          const Op wv = codes_op<FMT>(c0, c1, j);
           const float d = valid ? half_bits_to_float(dbits) : 0.0f;
 #pragma unroll
           for (int t = 0; t < T; ++t) {
             const uint8_t* f = xs + (blk * T + t) * kFragBytes + lane * 16;
-            const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
-            const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+            const Op xh = *reinterpret_cast<const Op*>(f);
+            const Op xl = *reinterpret_cast<const Op*>(f + 1024);
             f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
             if constexpr (L::bias)
               c = *reinterpret_cast<const f32x4*>(xs + L::x_bytes + (blk * T + t) * 64 + 16 * j);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv, c, 0, 0, 0);
+            c = mfma_op(xh, wv, c);
+            c = mfma_op(xl, wv, c);
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(c[e], d, acc[t][e]);
           }
@@ -952,8 +983,9 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
 
   // Decoded weight fragments of one half stage (one block of the pair):
   // codes as bf16 and the block scales of the wave's 4 n-tiles.
+  using Op = typename OpType<FMT>::T;
   struct HalfW {
-    bf16x8 w[kPTN];
+    Op w[kPTN];
     float d[kPTN];
   };
   auto decode = [&](int slot, int h, HalfW& o) {
@@ -974,7 +1006,7 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
         c1 = pr[PairLayout<FMT>::blk1_dword(j) + 1];
         dbits = pr[PairLayout<FMT>::scale1_dword] >> 16;
       }
-      o.w[tn] = codes_bf16<FMT>(c0, c1, j);
+      o.w[tn] = codes_op<FMT>(c0, c1, j);
       o.d[tn] = half_bits_to_float(dbits);
     }
   };
@@ -984,16 +1016,16 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
     const uint8_t* base = slot_base(slot);
     const int mt = wm * TM + tm;
     const uint8_t* f = base + (mt * 2 + h) * kFragBytes + 16 * lane;
-    const bf16x8 xh = *reinterpret_cast<const bf16x8*>(f);
-    const bf16x8 xl = *reinterpret_cast<const bf16x8*>(f + 1024);
+    const Op xh = *reinterpret_cast<const Op*>(f);
+    const Op xl = *reinterpret_cast<const Op*>(f + 1024);
     f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (PS::bias)
       c0 = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base + PS::x_bytes) +
                                            (mt * 2 + h) * 16 + 4 * j);
 #pragma unroll
     for (int tn = 0; tn < kPTN; ++tn) {
-      f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, hw.w[tn], c0, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, hw.w[tn], c, 0, 0, 0);
+      f32x4 c = mfma_op(xh, hw.w[tn], c0);
+      c = mfma_op(xl, hw.w[tn], c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[tm][tn][e] = fmaf(c[e], hw.d[tn], acc[tm][tn][e]);
     }
