@@ -68,45 +68,61 @@ int packed_bytes(int format, long long n, long long k, size_t* size) {
   return QC_OK;
 }
 
-// One device int per device for the synchronous (dev_status == NULL) paths.
-struct Scratch {
+// Device ints for the synchronous (dev_status == NULL) paths: a per-device
+// pool, one int per call in flight, so that synchronous calls from several
+// host threads (on different streams) never share a flag.
+struct FlagPool {
   std::mutex mu;
-  std::vector<int*> flag;
+  std::vector<std::vector<int*>> free;   // [device] -> idle flags
 };
-Scratch& scratch() {
-  static Scratch s;
-  return s;
+FlagPool& flag_pool() {
+  static FlagPool p;
+  return p;
 }
 
-int* device_flag(hipError_t* err) {
-  int dev = 0;
-  *err = hipGetDevice(&dev);
+int* acquire_flag(int* dev, hipError_t* err) {
+  *err = hipGetDevice(dev);
   if (*err != hipSuccess) return nullptr;
-  Scratch& s = scratch();
-  std::lock_guard<std::mutex> lock(s.mu);
-  if (static_cast<int>(s.flag.size()) <= dev) s.flag.resize(dev + 1, nullptr);
-  if (s.flag[dev] == nullptr) {
-    *err = hipMalloc(&s.flag[dev], sizeof(int));
-    if (*err != hipSuccess) {
-      s.flag[dev] = nullptr;
-      return nullptr;
+  FlagPool& p = flag_pool();
+  {
+    std::lock_guard<std::mutex> lock(p.mu);
+    if (static_cast<int>(p.free.size()) <= *dev) p.free.resize(*dev + 1);
+    std::vector<int*>& idle = p.free[*dev];
+    if (!idle.empty()) {
+      int* f = idle.back();
+      idle.pop_back();
+      return f;
     }
   }
-  return s.flag[dev];
+  int* f = nullptr;
+  *err = hipMalloc(&f, sizeof(int));
+  return *err == hipSuccess ? f : nullptr;
+}
+
+void release_flag(int dev, int* f) {
+  FlagPool& p = flag_pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  p.free[dev].push_back(f);
 }
 
 // Runs `launch(flag)` with a zeroed device flag and returns its value.
 template <class F>
 int with_flag(hipStream_t s, int* value, F&& launch) {
   hipError_t e = hipSuccess;
-  int* flag = device_flag(&e);
+  int dev = 0;
+  int* flag = acquire_flag(&dev, &e);
   if (flag == nullptr) return device_error(e);
-  if ((e = hipMemsetAsync(flag, 0, sizeof(int), s)) != hipSuccess) return device_error(e);
-  if ((e = launch(flag)) != hipSuccess) return device_error(e);
-  if ((e = hipMemcpyAsync(value, flag, sizeof(int), hipMemcpyDeviceToHost, s)) != hipSuccess)
-    return device_error(e);
-  if ((e = hipStreamSynchronize(s)) != hipSuccess) return device_error(e);
-  return QC_OK;
+  if ((e = hipMemsetAsync(flag, 0, sizeof(int), s)) == hipSuccess &&
+      (e = launch(flag)) == hipSuccess &&
+      (e = hipMemcpyAsync(value, flag, sizeof(int), hipMemcpyDeviceToHost, s)) == hipSuccess)
+    e = hipStreamSynchronize(s);
+  if (e == hipSuccess) {
+    release_flag(dev, flag);
+    return QC_OK;
+  }
+  // After a failure the flag may still be in use by queued work: keep it out
+  // of the pool.
+  return device_error(e);
 }
 
 // Synchronous all_finite over a device array.

@@ -100,3 +100,34 @@ def test_pack_rejects_nonfinite(qc, dev):
     w[1, 40] = float("inf")
     out = torch.zeros(2 * 2 * 34, dtype=torch.uint8, device=dev)
     assert qc.pack_raw(0, w, out, 2, 64) == 3
+
+
+def test_sync_status_concurrent_streams(qc, dev):
+    """Synchronous calls (dev_status NULL) from two host threads on two streams:
+    each call has its own device flag, so a non-finite input on one stream
+    never leaks its status 3 into the other stream's finite calls (or is lost)."""
+    import threading
+    import torch
+    rows, dim = 64, 256
+    x_bad = torch.ones(rows, dim, device=dev)
+    x_bad[5, 7] = float("nan")
+    x_ok = torch.ones(rows, dim, device=dev)
+    streams = {"bad": torch.cuda.Stream(), "ok": torch.cuda.Stream()}
+    results = {"bad": [], "ok": []}
+
+    def run(name, x):
+        codes = torch.empty(rows, dim, dtype=torch.int8, device=dev)
+        scales = torch.empty(rows, device=dev)
+        s = streams[name].cuda_stream
+        for _ in range(300):
+            results[name].append(qc.quantize_int8_raw(x, codes, scales, rows, dim, 0, None, s))
+
+    print("sync status from two threads", flush=True)
+    threads = [threading.Thread(target=run, args=(nm, x)) for nm, x in (("bad", x_bad), ("ok", x_ok))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    torch.cuda.synchronize()
+    assert len(results["bad"]) == 300 and len(results["ok"]) == 300
+    assert set(results["bad"]) == {3} and set(results["ok"]) == {0}
