@@ -604,8 +604,10 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
             // D lane (n, j): digit sums S_0..S_3 of row m = 4t + j (S_3 = 0)
             c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wq, c, 0, 0, 0);
             const int2 me = *reinterpret_cast<const int2*>(rec + XB::meta_off + 8 * (4 * t + j));
+            // 2^7 S1 + S2 is exact in int32 (|S| < 2^20), and its float
+            // conversion is the same single rounding as fmaf(S1, 128, S2)
             const float f = fmaf(static_cast<float>(c[0]), 16384.f,
-                                 fmaf(static_cast<float>(c[1]), 128.f, static_cast<float>(c[2])));
+                                 static_cast<float>((c[1] << 7) + c[2]));
             const float blk_dot = ldexpf((dw * __int_as_float(me.y)) * f, me.x);
             accd[t] += valid ? blk_dot : 0.0f;
           }
