@@ -820,6 +820,8 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const int nslabs = (n + 16 * plan.nw - 1) / (16 * plan.nw);
   const int ks = plan.ks;
   using XB = XBlock<XL, FMT == kQ4_0>;
+  // the bf16 / f16 layouts store and apply per-row exponents
+  if (!XB::digits && rexp == nullptr) return hipErrorInvalidValue;
   const size_t xf_bytes = static_cast<size_t>(nbp) * XB::bytes;
   const size_t bias_bytes = static_cast<size_t>(nbp) * XB::bias_bytes;
   const size_t part_bytes = ks > 2 ? static_cast<size_t>(ks) * m * n * sizeof(float) : 0;
@@ -1136,6 +1138,7 @@ template <int FMT, int TM>
 hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, int k,
                      hipStream_t s, int split, int* rexp) {
   using PS = PanelStage<FMT, TM>;
+  if (rexp == nullptr) return hipErrorInvalidValue;   // per-row exponents (see prep_rows)
   const int nb = k / 32, npairs = k / 64;
   const int mblocks = (m + PS::bm - 1) / PS::bm, nblocks = (n + kPBN - 1) / kPBN;
   const int mtiles = mblocks * PS::mt;
