@@ -454,7 +454,8 @@ def main():
     EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is design-only (see DESIGN.md).", file=sys.stderr)
+              "sharding N across GPUs (replicated x, one all-gather of y) is designed, not "
+              "built.", file=sys.stderr)
         sys.exit(2)
     import torch
     import quixicore_hip as qc
