@@ -183,19 +183,20 @@ __device__ __forceinline__ void ring_barrier() {
 }
 
 
-// Activation fragments of the bf16 layouts, 2 KB per (16-row m-tile, block):
-// lane l holds row 16t + (l & 15), elements 8(l >> 4) .. +7 of the block as
-// bf16 hi (bytes 0..1023) and lo = bf16(v - hi) (bytes 1024..2047), and
-// (q4_0) the bias -8 * sum(hi + lo) per row and block, the MFMA's C input
-// for the nibble offset.  Small-batch passes store fragment (b, t) at
-// b * T + t over nbp blocks (those past K zero), the panel route at
-// t * nb + b.
+// Activation fragments of the bf16 / f16 layouts (q4_0 / q8_0), 2 KB per
+// (16-row m-tile, block): lane l holds row 16t + (l & 15), elements
+// 8(l >> 4) .. +7 of the block as hi (bytes 0..1023) and lo = the rounding
+// of v - hi (bytes 1024..2047), and (q4_0) the bias -8 * sum(hi + lo) per
+// row and block, the MFMA's C input for the nibble offset.  Small-batch
+// passes store fragment (b, t) at b * T + t over nbp blocks (those past K
+// zero), the panel route at t * nb + b.
 //
-// Per-row power-of-two scale: e(m) = the frexp exponent of max |x[m][:]| (0
-// for a zero or non-finite row).  The fragments hold v = x * 2^-e(m), so
-// every row's largest element is in [0.5, 1): no element that matters is
-// subnormal in bf16 (which would leave it a few bits) and no product
-// overflows; outputs are scaled back by 2^e(m), exactly.
+// Per-row power-of-two scale: the fragments hold v = x * 2^-e(m), with e(m)
+// from the frexp exponent of max |x[m][:]| (0 for a zero or non-finite row)
+// so that the row's largest element is in [0.5, 1) (bf16) or [2^14, 2^15)
+// (f16): no element that matters is subnormal in the operand type (which
+// would leave it a few bits) and no product overflows; rexp[m] = e(m), and
+// outputs are scaled back by 2^e(m), exactly.
 //
 // One 256-thread workgroup per row of the layout (rows past M are zero): the
 // row's maximum, then its fragments, in one launch.  Thread t converts the
