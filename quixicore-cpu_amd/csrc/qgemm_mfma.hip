@@ -1,27 +1,30 @@
 // Small-batch q8_0 / q4_0 GEMM (2 <= M, in tiles of 16 activation rows) on
-// gfx950 bf16 MFMA.
+// gfx950 MFMA: int8 digit planes for up to 8 rows per pass, f16 (q8_0) or
+// bf16 (q4_0) operands above, and a 2-D tiled kernel for M >= 64.
 //
 // Semantics as the reference's qgemm (kernels/quantization/qgemm_ref.cpp:
 // 156-162, one qgemv per activation row: y[m][n] = sum_b d[n][b] *
 // sum_{k in b} q[n][k] * x[m][k]); the f32 outputs are held to the contract
 // bound |y - y_exact| <= 1e-4 * ||x_m|| * ||w_n|| like the M = 1 path.
 //
-// Numerics.  Each activation is split into two bf16 values, hi = bf16(x) and
-// lo = bf16(x - hi), so x - hi - lo is within 2^-17 |x|; the q8_0 codes
-// (|q| <= 127) and the q4_0 nibbles (0..15) are exact in bf16.  One
-// v_mfma_f32_16x16x32_bf16 covers exactly one 32-element block, so the block
-// dot sum_k q*hi + sum_k q*lo comes out of two MFMAs with f32 accumulation
-// and is then scaled by the block's fp16 d with one FMA per output.  For
-// q4_0 the -8 offset enters through the MFMA's C input: the block starts from
-// bias = -8 * sum_k (hi + lo), precomputed per activation row and block.
-// Worst-case error, normalised by ||x_m|| * ||w_n||: 2^-17 from the split,
-// about 32 * 2^-24 * 15/8 * sqrt(32) ~ 2e-5 from the f32 accumulation of the
-// q4 block sums, plus 2^-24 per block for the scaled accumulation -- well
-// inside 1e-4.
+// Numerics of the f16 / bf16 layouts.  Each activation (scaled per row by a
+// power of two) is split into two values, hi and lo = the rounding of
+// x - hi, so x - hi - lo is within 2^-17 |x| (bf16) or 2^-22 |x| (f16); the
+// q8_0 codes (|q| <= 128, in f16) and the q4_0 nibbles (0..15, in bf16) are
+// exact.  One v_mfma_f32_16x16x32_{f16,bf16} covers exactly one 32-element
+// block, so the block dot sum_k q*hi + sum_k q*lo comes out of two MFMAs with
+// f32 accumulation and is then scaled by the block's fp16 d with one FMA per
+// output.  For q4_0 the -8 offset enters through the MFMA's C input: the
+// block starts from bias = -8 * sum_k (hi + lo), precomputed per activation
+// row and block.  Worst-case error, normalised by ||x_m|| * ||w_n||: the
+// split, about 32 * 2^-24 * 15/8 * sqrt(32) ~ 2e-5 from the f32 accumulation
+// of the q4 block sums, plus 2^-24 per block for the scaled accumulation --
+// well inside 1e-4.
 //
-// Data flow.  A prep kernel writes the activation fragments in the MFMA
-// operand layout ([block][m-tile][hi | lo][64 lanes][16 B]) plus the q4 bias,
-// and zeroes y when two K halves will add into it.  The GEMM workgroup (4 or
+// Data flow.  A prep kernel (qgemm_prep for the digit layouts, prep_rows
+// for f16 / bf16) writes the activation fragments in the MFMA operand layout
+// ([block][m-tile][hi | lo][64 lanes][16 B]) plus the q4 bias, and zeroes y
+// when two K halves will add into it.  The GEMM workgroup (4 or
 // 8 wavefronts, 16 weight rows each) runs a ring of LDS stages, each
 // holding 4 block pairs (256 K) of its weight rows -- whole row segments,
 // copied with global_load_lds_dwordx4, so every weight byte crosses the
@@ -865,11 +868,11 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
 // (kernels/quantization/qgemm_panel.cpp:234-286).  Here every M >= 64 call
 // (qgemm and qgemm_prepacked) runs one 2-D tiled GEMM instead of passes of 32
 // rows, each of which re-streams the whole weight matrix.  Numerics are those
-// of the bf16 path above (hi/lo activations, exact codes, per-block f32
-// scaling), so the contract bound is unchanged.
+// of the f16 / bf16 passes above (hi/lo activations, exact codes, per-block
+// f32 scaling), so the contract bound is unchanged.
 //
 // Workgroup: 8 wavefronts as 2 (m) x 4 (n), each computing 64 x 64 outputs
-// as 4 x 4 tiles of v_mfma_f32_16x16x32_bf16; workgroup tile 128 x 256.  K
+// as 4 x 4 tiles of v_mfma_f32_16x16x32_{f16,bf16}; workgroup tile 128 x 256.  K
 // runs in stages of one block pair (64 elements) through a 3-deep LDS ring
 // filled by global_load_lds: the activation fragments of the workgroup's 8
 // m-tiles (hi, lo, and the q4_0 bias) as 16-byte chunks, and the pair's bytes
