@@ -192,6 +192,7 @@ int qc_hip_qgemv(int format, const void* packed, const float* x, float* y, long 
 int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long long m,
                  long long n, long long k, void* stream) {
   if (!valid_product({m, k}) || !valid_product({m, n})) return QC_INVALID_SHAPE;
+  if (m > INT_MAX) return QC_INVALID_SHAPE;   // this library's dimension limit (as for n, k)
   if (packed == nullptr || x == nullptr || y == nullptr) return QC_INVALID_ARGUMENT;
   size_t size = 0;
   const int st = qc_hip_qgemv_packed_size(format, n, k, &size);

@@ -8,6 +8,7 @@
 // Validation happens in the C ABI first, so an invalid call touches nothing.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -276,7 +277,8 @@ const char* qgemv_w8a8_variant(QuantFormat format) {
 Status qgemm(QuantFormat format, const void* packed_weights, const float* x, float* y,
              long long m, long long n, long long k) {
   const size_t bytes = packed_or_zero(format, n, k);
-  if (bytes == 0 || m <= 0 || packed_weights == nullptr || x == nullptr || y == nullptr)
+  if (bytes == 0 || m <= 0 || m > INT_MAX || packed_weights == nullptr || x == nullptr ||
+      y == nullptr)
     return static_cast<Status>(
         qc_hip_qgemm(fmt_id(format), packed_weights, x, y, m, n, k, nullptr));
   Staging g(nullptr);

@@ -292,7 +292,8 @@ Status qgemm_prepacked(const CpuPackedWeights& weights, const float* x, float* y
   const CpuPackedWeightsInfo info = weights.info();
   if (m <= 0 || info.rows <= 0 || info.columns <= 0 ||
       m > std::numeric_limits<long long>::max() / info.rows ||
-      m * info.rows > std::numeric_limits<long long>::max() / info.columns)
+      m * info.rows > std::numeric_limits<long long>::max() / info.columns ||
+      m > std::numeric_limits<int>::max())   // this library's dimension limit (as for n, k)
     return Status::kInvalidShape;
   if (x == nullptr || y == nullptr || weights.device_data() == nullptr)
     return Status::kInvalidArgument;

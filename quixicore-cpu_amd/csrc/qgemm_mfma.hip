@@ -41,6 +41,7 @@
 // device-scope fence, as a "last workgroup reduces" scheme needs, writes
 // back the XCD's whole L2 and costs far more than the extra launch.)
 #include <algorithm>
+#include <memory>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -699,61 +700,94 @@ int device_cus() {
   return cus;
 }
 
-// Workspace (activation fragments and partial sums) kept per
-// (device, stream) and reused by every call on that stream: stream order
-// keeps successive calls from overlapping, and calls on different streams
-// never share a buffer.  A buffer only grows; the one it replaces is freed
-// after the stream drains (or, under graph capture, kept until exit).
+// Scratch (activation fragments, q4 bias, partial sums, row exponents) of
+// one qgemm call.  Region 0 holds one pass's fragments and partial sums,
+// region 1 the call's row exponents (live across all passes).
+//
+// Allocating entry points take it from a per-(device, stream) cache: a call
+// holds that entry's `call` lock from its first use of the buffers to its
+// last launch, so two host threads on one stream enqueue whole calls, and
+// stream order then keeps one call's kernels from reading the other's
+// fragments.  A buffer only grows.  The one it replaces is freed after the
+// stream drains, unless it was handed out while the stream was being
+// captured into a graph (the graph has its address baked in): such a
+// buffer is retired and kept until the process ends.  Calls on different
+// streams never share a buffer.
 struct StreamWorkspace {
   int device;
   hipStream_t stream;
-  int tag;
-  void* ptr;
-  size_t bytes;
+  std::mutex call;
+  void* ptr[2] = {nullptr, nullptr};
+  size_t bytes[2] = {0, 0};
+  bool captured[2] = {false, false};
 };
 
-// tag 0: a pass's fragments and partial sums; tag 1: the call's row exponents
-// (live across all passes of one call).
-hipError_t workspace_for(hipStream_t s, size_t bytes, void** out, int tag = 0) {
-  static std::mutex mu;
-  static std::vector<StreamWorkspace> table;
-  static std::vector<void*> retired;
+std::mutex g_ws_mu;                                        // guards the two lists below
+std::vector<std::unique_ptr<StreamWorkspace>> g_ws_table;  // entries live until exit
+std::vector<void*> g_ws_retired;
+
+hipError_t stream_workspace(hipStream_t s, StreamWorkspace** out) {
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  const hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(mu);
-  for (auto& w : table) {
-    if (w.device != dev || w.stream != s || w.tag != tag) continue;
-    if (w.bytes >= bytes) {
-      *out = w.ptr;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (auto& w : g_ws_table)
+    if (w->device == dev && w->stream == s) {
+      *out = w.get();
+      return hipSuccess;
+    }
+  g_ws_table.push_back(std::make_unique<StreamWorkspace>());
+  g_ws_table.back()->device = dev;
+  g_ws_table.back()->stream = s;
+  *out = g_ws_table.back().get();
+  return hipSuccess;
+}
+
+// Where a call's scratch comes from: a per-stream cache entry (whose `call`
+// lock the caller holds), or a fixed region given by the caller -- region 1
+// at [0, fixed_split), region 0 at [fixed_split, fixed_bytes).  A fixed
+// region never grows: a request beyond it fails with hipErrorOutOfMemory
+// before anything is launched (the first pass of a call needs the most).
+struct Scratch {
+  StreamWorkspace* w = nullptr;
+  uint8_t* fixed = nullptr;
+  size_t fixed_split = 0, fixed_bytes = 0;
+
+  hipError_t get(hipStream_t s, size_t bytes, void** out, int tag = 0) {
+    if (w == nullptr) {
+      const size_t lo = tag == 1 ? 0 : fixed_split;
+      const size_t hi = tag == 1 ? fixed_split : fixed_bytes;
+      if (bytes > hi - lo) return hipErrorOutOfMemory;
+      *out = fixed + lo;
       return hipSuccess;
     }
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(s, &cap);
+    hipError_t e = hipStreamIsCapturing(s, &cap);
     if (e != hipSuccess) return e;
-    if (cap == hipStreamCaptureStatusNone) {
-      e = hipStreamSynchronize(s);
-      if (e != hipSuccess) return e;
-      e = hipFree(w.ptr);
-      if (e != hipSuccess) return e;
-    } else {
-      retired.push_back(w.ptr);   // may still be used by the captured work
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    if (w->bytes[tag] >= bytes) {
+      w->captured[tag] = w->captured[tag] || capturing;
+      *out = w->ptr[tag];
+      return hipSuccess;
     }
-    w.ptr = nullptr;
-    w.bytes = 0;
-    e = hipMalloc(&w.ptr, bytes);
-    if (e != hipSuccess) return e;
-    w.bytes = bytes;
-    *out = w.ptr;
+    if (w->ptr[tag] != nullptr) {
+      if (capturing || w->captured[tag]) {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        g_ws_retired.push_back(w->ptr[tag]);
+      } else {
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+        if ((e = hipFree(w->ptr[tag])) != hipSuccess) return e;
+      }
+      w->ptr[tag] = nullptr;
+      w->bytes[tag] = 0;
+    }
+    if ((e = hipMalloc(&w->ptr[tag], bytes)) != hipSuccess) return e;
+    w->bytes[tag] = bytes;
+    w->captured[tag] = capturing;
+    *out = w->ptr[tag];
     return hipSuccess;
   }
-  void* p = nullptr;
-  e = hipMalloc(&p, bytes);
-  if (e != hipSuccess) return e;
-  table.push_back({dev, s, tag, p, bytes});
-  *out = p;
-  return hipSuccess;
-}
+};
 
 template <int FMT, int XL, int NW, int NST>
 hipError_t launch_nst(const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
@@ -811,7 +845,7 @@ Plan plan_for(int n, int nstages, int cus) {
 
 template <int FMT, int XL>
 hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, hipStream_t s,
-               int waves, int stages, int* rexp) {
+               int waves, int stages, int* rexp, Scratch& scratch) {
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
@@ -832,7 +866,7 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const size_t pad_bytes = WStage<FMT>::row_bytes;
   const size_t total = xf_bytes + bias_bytes + part_bytes + pad_bytes + 256;
   void* ws = nullptr;
-  hipError_t e = workspace_for(s, total, &ws);
+  hipError_t e = scratch.get(s, total, &ws);
   if (e != hipSuccess) return e;
   uint8_t* xf = static_cast<uint8_t*>(ws);
   float* bias = reinterpret_cast<float*>(xf + xf_bytes);
@@ -1140,7 +1174,7 @@ bool panel_pays(int m, int n, int k, int cus) {
 
 template <int FMT, int TM>
 hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, int k,
-                     hipStream_t s, int split, int* rexp) {
+                     hipStream_t s, int split, int* rexp, Scratch& scratch) {
   using PS = PanelStage<FMT, TM>;
   if (rexp == nullptr) return hipErrorInvalidValue;   // per-row exponents (see prep_rows)
   const int nb = k / 32, npairs = k / 64;
@@ -1157,7 +1191,7 @@ hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, i
   const size_t xf_bytes = static_cast<size_t>(mtiles) * nb * kFragBytes;
   const size_t bias_bytes = FMT == kQ4_0 ? static_cast<size_t>(mtiles) * nb * 64 : 0;
   void* ws = nullptr;
-  hipError_t e = workspace_for(s, xf_bytes + bias_bytes + 256, &ws);
+  hipError_t e = scratch.get(s, xf_bytes + bias_bytes + 256, &ws);
   if (e != hipSuccess) return e;
   uint8_t* xf = static_cast<uint8_t*>(ws);
   float* bias = reinterpret_cast<float*>(xf + xf_bytes);
@@ -1174,8 +1208,10 @@ hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, i
 
 }  // namespace
 
-hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
-                             int k, hipStream_t s, int waves, int stages, int panel) {
+namespace {
+
+hipError_t qgemm_mfma_with(int fmt, const void* W, const float* x, float* y, int m, int n, int k,
+                           hipStream_t s, int waves, int stages, int panel, Scratch& scratch) {
   const auto* w = static_cast<const uint8_t*>(W);
   // panel: 0 = from the shape (for m >= 64), -1 = never, 1 / 2 = always
   // (for m >= 2) with one / two K ranges
@@ -1185,13 +1221,13 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
   int* rexp = nullptr;
   if (use_panel || m > 8) {
     void* p = nullptr;
-    hipError_t e = workspace_for(s, sizeof(int) * static_cast<size_t>(m) + 256, &p, 1);
+    hipError_t e = scratch.get(s, sizeof(int) * static_cast<size_t>(m) + 256, &p, 1);
     if (e != hipSuccess) return e;
     rexp = static_cast<int*>(p);
   }
   if (use_panel)
-    return fmt == kQ8_0 ? run_panel<kQ8_0, 4>(w, x, y, m, n, k, s, panel, rexp)
-                        : run_panel<kQ4_0, 4>(w, x, y, m, n, k, s, panel, rexp);
+    return fmt == kQ8_0 ? run_panel<kQ8_0, 4>(w, x, y, m, n, k, s, panel, rexp, scratch)
+                        : run_panel<kQ4_0, 4>(w, x, y, m, n, k, s, panel, rexp, scratch);
   for (int m0 = 0; m0 < m; m0 += 32) {
     const int mt = m - m0 < 32 ? m - m0 : 32;
     const float* xm = x + static_cast<long long>(m0) * k;
@@ -1200,18 +1236,31 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
     // activation layout: compact rows for M <= 4 / 8, dense 16-row tiles above
     hipError_t e;
     if (fmt == kQ8_0)
-      e = mt <= 4 ? run<kQ8_0, 4>(w, xm, ym, mt, n, k, s, waves, stages, rm)
-        : mt <= 8 ? run<kQ8_0, 8>(w, xm, ym, mt, n, k, s, waves, stages, rm)
-        : mt <= 16 ? run<kQ8_0, 16>(w, xm, ym, mt, n, k, s, waves, stages, rm)
-                   : run<kQ8_0, 32>(w, xm, ym, mt, n, k, s, waves, stages, rm);
+      e = mt <= 4 ? run<kQ8_0, 4>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch)
+        : mt <= 8 ? run<kQ8_0, 8>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch)
+        : mt <= 16 ? run<kQ8_0, 16>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch)
+                   : run<kQ8_0, 32>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch);
     else
-      e = mt <= 4 ? run<kQ4_0, 4>(w, xm, ym, mt, n, k, s, waves, stages, rm)
-        : mt <= 8 ? run<kQ4_0, 8>(w, xm, ym, mt, n, k, s, waves, stages, rm)
-        : mt <= 16 ? run<kQ4_0, 16>(w, xm, ym, mt, n, k, s, waves, stages, rm)
-                   : run<kQ4_0, 32>(w, xm, ym, mt, n, k, s, waves, stages, rm);
+      e = mt <= 4 ? run<kQ4_0, 4>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch)
+        : mt <= 8 ? run<kQ4_0, 8>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch)
+        : mt <= 16 ? run<kQ4_0, 16>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch)
+                   : run<kQ4_0, 32>(w, xm, ym, mt, n, k, s, waves, stages, rm, scratch);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
+                             int k, hipStream_t s, int waves, int stages, int panel) {
+  StreamWorkspace* ws = nullptr;
+  const hipError_t e = stream_workspace(s, &ws);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> hold(ws->call);   // until the call's last launch
+  Scratch scratch;
+  scratch.w = ws;
+  return qgemm_mfma_with(fmt, W, x, y, m, n, k, s, waves, stages, panel, scratch);
 }
 
 }  // namespace qc

@@ -674,7 +674,7 @@ hipError_t launch_one(const GemvSegs& sg, const float* x, int k, int* status, hi
   static_assert(RB * NPM * Fmt<FMT>::pair_dwords <= 144, "register budget");
   constexpr int WIN = window<FMT, NPM * RB>();
   const int kc = NPM * 4096 < k ? NPM * 4096 : k;
-  const int grid = (n + NW * RB - 1) / (NW * RB);
+  const unsigned grid = static_cast<unsigned>((static_cast<long long>(n) + NW * RB - 1) / (NW * RB));
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if constexpr (KIND == 0) {
     if (vec)

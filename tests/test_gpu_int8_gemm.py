@@ -46,18 +46,24 @@ def route(request, qc):
                                    (300, 200, 128), (520, 130, 192), (1100, 390, 320),
                                    (64, 96, 32), (513, 257, 96), (260, 140, 4128),
                                    (33, 4100, 160), (1030, 6150, 96), (200, 16400, 64),
-                                   (1030, 9990, 96)])
+                                   (1030, 9990, 96),
+                                   # steady-state loops of the deep-K tiles: 128 x 128 with a
+                                   # 4-deep ring (M 129..256, wide N) and 256 x 256 with a
+                                   # 2-deep ring, 8 whole 128-B K steps plus a ragged 32-B one
+                                   (256, 14336, 4096), (1030, 9990, 1056)])
 def test_accumulators_exact(qc, dev, route, m, n, k):
+    import torch
     print(f"int8 acc route={route} m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(m * n + k)
     w = rng.integers(-128, 128, (n, k), dtype=np.int8)
     x = rng.integers(-128, 128, (m, k), dtype=np.int8)
     w[0, :] = -128
     x[0, :] = -128  # the largest products
-    acc = qc.int8_gemm_i32(_t(w, dev), _t(x, dev)).cpu().numpy()
-    # float64 BLAS is exact here: every partial sum is an integer below 2^53
-    want = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64)
-    assert np.array_equal(acc.astype(np.int64), want)
+    wd, xd = _t(w, dev), _t(x, dev)
+    acc = qc.int8_gemm_i32(wd, xd)
+    # a float64 product is exact here: every partial sum is an integer below 2^53
+    want = xd.double() @ wd.double().T.contiguous()
+    assert torch.equal(acc.double(), want)
 
 
 @pytest.mark.parametrize("asym", [False, True])
@@ -77,6 +83,30 @@ def test_epilogue_bit_exact(qc, oracle, dev, route, m, n, k, asym):
     y = qc.int8_gemm(_t(w, dev), _t(x, dev), _t(ws, dev), _t(as_, dev),
                      _t(rs, dev) if asym else None, _t(zp, dev) if asym else None, asym)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("asym", [False, True])
+def test_epilogue_deep_tile_rows(qc, oracle, dev, route, asym):
+    """The 256 x 256 two-stage tile (M=1030, N=9990, K=1056: 8 whole K steps and a
+    ragged one), bit-exact against the oracle on rows that straddle every
+    m-tile boundary, over all N columns."""
+    print(f"int8 epilogue deep tile route={route} asym={asym}", flush=True)
+    m, n, k = 1030, 9990, 1056
+    rng = np.random.default_rng(1056 + asym)
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    x = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    ws = rng.uniform(1e-4, 1e-2, n).astype(np.float32)
+    as_ = rng.uniform(1e-3, 1e-1, m).astype(np.float32)
+    rs = w.astype(np.int32).sum(axis=1).astype(np.int32) if asym else None
+    zp = rng.integers(-128, 128, m).astype(np.int32) if asym else None
+    y = qc.int8_gemm(_t(w, dev), _t(x, dev), _t(ws, dev), _t(as_, dev),
+                     _t(rs, dev) if asym else None, _t(zp, dev) if asym else None,
+                     asym).cpu().numpy()
+    rows = np.array([0, 1, 31, 32, 127, 128, 255, 256, 511, 512, 767, 768, 1023, 1024, 1029])
+    st, want = oracle.int8_gemm(w, x[rows], ws, as_[rows], rs,
+                                zp[rows] if asym else None, asym)
+    assert st == 0
+    assert np.array_equal(y[rows].view(np.uint32), want.view(np.uint32))
 
 
 def test_config3_sampled_bit_exact(qc, oracle, synth, dev):
@@ -100,6 +130,32 @@ def test_config3_sampled_bit_exact(qc, oracle, synth, dev):
     assert np.array_equal(Y[rows, cols].view(np.uint32), want.view(np.uint32))
     A = qc.int8_gemm_i32(_t(wq, dev), _t(xq, dev))
     ref = (torch.from_numpy(xq).to(dev).double() @ torch.from_numpy(wq).to(dev).double().T)
+    assert torch.equal(A.double(), ref)
+
+
+def test_config3_n14336_bit_exact(qc, oracle, synth, dev):
+    """BASELINE config 3 at N=14336 (M=2048, K=4096; also config 4's W8A8
+    gate/up shape), which takes the 256 x 256 two-stage ring tile: the whole
+    int32 matrix against a float64 product, and 4096 sampled f32 outputs
+    bit-exact against the oracle."""
+    import torch
+    print("int8 config3 M=2048 N=14336 K=4096", flush=True)
+    m, n, k = 2048, 14336, 4096
+    wf = synth.weights(3, n, k, tensor_id=4)
+    st, wq, ws = oracle.quantize_int8(wf)
+    ws = ws[:, 0].copy()
+    x = synth.activations_outliers_fast(3, m, k)
+    st, xq, as_ = oracle.quantize_int8(x)
+    as_ = as_[:, 0].copy()
+    wd, xd = _t(wq, dev), _t(xq, dev)
+    Y = qc.int8_gemm(wd, xd, _t(ws, dev), _t(as_, dev)).cpu().numpy()
+    rng = np.random.default_rng(14336)
+    rows = rng.integers(0, m, 4096)
+    cols = rng.integers(0, n, 4096)
+    acc, want = oracle.int8_gemm_entries(wq, xq, ws, as_, rows, cols)
+    assert np.array_equal(Y[rows, cols].view(np.uint32), want.view(np.uint32))
+    A = qc.int8_gemm_i32(wd, xd)
+    ref = xd.double() @ wd.double().T.contiguous()
     assert torch.equal(A.double(), ref)
 
 
