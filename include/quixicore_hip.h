@@ -80,6 +80,27 @@ int qc_hip_qgemv(int format, const void* packed, const float* x, float* y, long 
 int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long long m,
                  long long n, long long k, void* stream);
 
+/* qc_hip_qgemm for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops): no counterpart in the reference.
+ * Same validation, kernels and numerics; the small-batch kernels' scratch
+ * (activation fragments, partial sums, row exponents) lives in a fixed
+ * device array of QC_QGEMM_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends, instead of memory the library allocates.  Every call on a
+ * GPU shares that GPU's array, so calls that overlap on one GPU (any
+ * streams, any threads) race: serialize them.  M >= 2 runs passes of at
+ * most 32 rows (never the 2-D M >= 64 route, whose scratch grows with m) with
+ * the fewest K splits.  Limits: m <= QC_QGEMM_NOALLOC_MAX_M and
+ * k <= QC_QGEMM_NOALLOC_MAX_K, else 1 (QC_INVALID_SHAPE) with a message in
+ * qc_hip_last_error().  Within k <= 8192 every such call fits; above it, a
+ * call whose K-split partial sums (ceil(k/4096) * min(m, 32) * n * 4 bytes)
+ * do not fit beside the fragments is also rejected with 1, before anything
+ * is launched. */
+#define QC_QGEMM_NOALLOC_SCRATCH_BYTES (16ull << 20)
+#define QC_QGEMM_NOALLOC_MAX_M 1048576LL
+#define QC_QGEMM_NOALLOC_MAX_K 16384LL
+int qc_hip_qgemm_noalloc(int format, const void* packed, const float* x, float* y, long long m,
+                         long long n, long long k, void* stream);
+
 /* Fused decode projections over one x, one launch where the shapes allow:
  * up = W_up . x and gate = W_gate . x ([n][k] each).  Same numerics as
  * qc_hip_qgemv per matrix.  Replaces qgemv_up_gate

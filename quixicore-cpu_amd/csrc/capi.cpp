@@ -200,6 +200,33 @@ int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long 
   return finish(qc::launch_qgemm(format, packed, x, y, m, n, k, as_stream(stream), g_tuning));
 }
 
+// qc_hip_qgemm without allocating: the same validation and kernels, with the
+// scratch in a fixed per-GPU device array (see launch_qgemm_mfma_noalloc).
+int qc_hip_qgemm_noalloc(int format, const void* packed, const float* x, float* y, long long m,
+                         long long n, long long k, void* stream) {
+  if (!valid_product({m, k}) || !valid_product({m, n})) return QC_INVALID_SHAPE;
+  if (m > INT_MAX) return QC_INVALID_SHAPE;
+  if (m > QC_QGEMM_NOALLOC_MAX_M || k > QC_QGEMM_NOALLOC_MAX_K) {
+    g_last_error = "qgemm_noalloc: m <= " + std::to_string(QC_QGEMM_NOALLOC_MAX_M) +
+                   " and k <= " + std::to_string(QC_QGEMM_NOALLOC_MAX_K) +
+                   " (fixed scratch of " + std::to_string(qc::kQgemmNoAllocScratchBytes) +
+                   " bytes)";
+    return QC_INVALID_SHAPE;
+  }
+  if (packed == nullptr || x == nullptr || y == nullptr) return QC_INVALID_ARGUMENT;
+  size_t size = 0;
+  const int st = qc_hip_qgemv_packed_size(format, n, k, &size);
+  if (st != QC_OK) return st;
+  const hipError_t e = qc::launch_qgemm(format, packed, x, y, m, n, k, as_stream(stream),
+                                        g_tuning, /*noalloc=*/true);
+  if (e == hipErrorOutOfMemory) {
+    g_last_error = "qgemm_noalloc: this shape needs more than the fixed scratch of " +
+                   std::to_string(qc::kQgemmNoAllocScratchBytes) + " bytes";
+    return QC_INVALID_SHAPE;
+  }
+  return finish(e);
+}
+
 // kernels/quantization/quantization_ref.cpp:17-21 (quant_shape), 143-147.
 int qc_hip_quantize_int8(const float* x, int8_t* codes, float* scales, long long rows,
                          long long dim, long long group_size, int* dev_status, void* stream) {

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "quixicore_hip.h"
+
 namespace qc {
 
 struct GemvTuning {
@@ -15,8 +17,10 @@ struct GemvTuning {
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
+// noalloc: never allocate (the MFMA route takes launch_qgemm_mfma_noalloc).
 hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long long m,
-                        long long n, long long k, hipStream_t s, const GemvTuning& t);
+                        long long n, long long k, hipStream_t s, const GemvTuning& t,
+                        bool noalloc = false);
 
 // M = 1 GEMV with exact int8 digit dots (K % 64 == 0, W 4-byte aligned).
 hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, int n, int k,
@@ -43,6 +47,15 @@ hipError_t launch_qgemv_w8a8(int fmt, const void* W, const float* x, float* y, l
 hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
                              int k, hipStream_t s, int waves = 0, int stages = 0,
                              int panel = 0);
+
+// launch_qgemm_mfma without allocating: the scratch is a fixed device
+// array of kQgemmNoAllocScratchBytes per GPU, shared by every such call on
+// that GPU (calls must not overlap).  Passes of at most 32 rows, the fewest
+// K splits.  hipErrorOutOfMemory, before anything is launched, when the
+// call's scratch exceeds the array.
+constexpr size_t kQgemmNoAllocScratchBytes = QC_QGEMM_NOALLOC_SCRATCH_BYTES;
+hipError_t launch_qgemm_mfma_noalloc(int fmt, const void* W, const float* x, float* y, int m,
+                                     int n, int k, hipStream_t s);
 
 // Per-group symmetric int8 quantization.  status == nullptr: caller has
 // already verified that x is finite.  Otherwise non-finite groups are left

@@ -752,6 +752,7 @@ struct Scratch {
   StreamWorkspace* w = nullptr;
   uint8_t* fixed = nullptr;
   size_t fixed_split = 0, fixed_bytes = 0;
+  int max_ks = 0;   // > 0: K split limit for the small-batch plan (see plan_for)
 
   hipError_t get(hipStream_t s, size_t bytes, void** out, int tag = 0) {
     if (w == nullptr) {
@@ -820,14 +821,18 @@ hipError_t launch_nw(int nst, const uint8_t* W, const uint8_t* xf, const float* 
 struct Plan {
   int nw, nst, ks;
 };
+// max_ks > 0 limits the K split to max(max_ks, the fewest ranges possible),
+// which bounds the partial-sum scratch.
 template <int FMT>
-Plan plan_for(int n, int nstages, int cus) {
-  Plan best{8, 1, nstages};
+Plan plan_for(int n, int nstages, int cus, int max_ks = 0) {
+  Plan best{8, 16, (nstages + 15) / 16};
   double best_t = 1e30;
+  const int ks_cap = max_ks > 0 ? std::max(max_ks, (nstages + 15) / 16) : nstages;
   for (int nw : {8, 4}) {
     const int nslabs = (n + 16 * nw - 1) / (16 * nw);
     for (int nst : {16, 8, 4, 2, 1}) {
       const int ks = (nstages + nst - 1) / nst;
+      if (ks > ks_cap) continue;
       const long long wgs = static_cast<long long>(nslabs) * ks;
       const long long active = wgs < cus ? wgs : cus;
       const long long rounds = (wgs + cus - 1) / cus;
@@ -849,7 +854,7 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
-  Plan plan = plan_for<FMT>(n, nstages, device_cus());
+  Plan plan = plan_for<FMT>(n, nstages, device_cus(), scratch.max_ks);
   if (waves) plan.nw = waves;                      // test / tuning overrides
   if (stages) {
     plan.nst = stages;
@@ -1261,6 +1266,53 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
   Scratch scratch;
   scratch.w = ws;
   return qgemm_mfma_with(fmt, W, x, y, m, n, k, s, waves, stages, panel, scratch);
+}
+
+
+// ------------------------------------------- scratch that is never allocated ---
+//
+// For callers that cannot allocate (graph capture, serving loops): the
+// qgemm scratch lives in this file-scope device array, one copy per GPU,
+// held until the process ends.  Host code uses the address that
+// hipGetSymbolAddress returns for the current device (the array's name is
+// only a host-side handle).  Every no-allocation call on a GPU shares that
+// GPU's array, so such calls must not overlap on one GPU.  Nothing in it
+// has to start at zero: each call's prep kernels write every byte its GEMM
+// kernels read.
+static __device__ __align__(256) uint8_t noalloc_scratch[kQgemmNoAllocScratchBytes];
+
+static hipError_t noalloc_scratch_base(void** out) {
+  static std::mutex mu;
+  static std::vector<void*> base;   // [device], resolved once per device
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if (static_cast<int>(base.size()) <= dev) base.resize(dev + 1, nullptr);
+  if (base[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
+    if (e != hipSuccess) return e;
+    base[dev] = p;
+  }
+  *out = base[dev];
+  return hipSuccess;
+}
+
+hipError_t launch_qgemm_mfma_noalloc(int fmt, const void* W, const float* x, float* y, int m,
+                                     int n, int k, hipStream_t s) {
+  void* base = nullptr;
+  const hipError_t e = noalloc_scratch_base(&base);
+  if (e != hipSuccess) return e;
+  Scratch scratch;
+  scratch.fixed = static_cast<uint8_t*>(base);
+  // region 1: the row exponents; region 0: one pass's fragments and partials
+  scratch.fixed_split = (sizeof(int) * static_cast<size_t>(m) + 256 + 255) / 256 * 256;
+  scratch.fixed_bytes = kQgemmNoAllocScratchBytes;
+  scratch.max_ks = 2;
+  if (scratch.fixed_split >= scratch.fixed_bytes) return hipErrorOutOfMemory;
+  // passes of at most 32 rows: the panel route's fragments grow with m
+  return qgemm_mfma_with(fmt, W, x, y, m, n, k, s, 0, 0, -1, scratch);
 }
 
 }  // namespace qc

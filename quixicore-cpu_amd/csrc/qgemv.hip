@@ -257,7 +257,7 @@ size_t lds_bytes(int fmt, int mt, int kc) {
 
 template <int FMT>
 hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, int k,
-                      hipStream_t s, const GemvTuning& t) {
+                      hipStream_t s, const GemvTuning& t, bool noalloc) {
   const bool fast = ((k >> 5) % 2 == 0) && (reinterpret_cast<uintptr_t>(W) % 4 == 0);
   if (!fast) {
     qgemm_generic_kernel<FMT><<<(n + kWaves - 1) / kWaves, kThreads, 0, s>>>(W, x, y, m, n, k);
@@ -269,8 +269,9 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, 
   // one stage of row overrun).
   const long long w_bytes = static_cast<long long>(n) * (k / 32) * Fmt<FMT>::block_bytes;
   if (k % 64 == 0 && w_bytes + 4096 < (1LL << 32))
-    return launch_qgemm_mfma(FMT, W, x, y, m, n, k, s, t.qgemm_waves, t.qgemm_stages,
-                             t.qgemm_panel);
+    return noalloc ? launch_qgemm_mfma_noalloc(FMT, W, x, y, m, n, k, s)
+                   : launch_qgemm_mfma(FMT, W, x, y, m, n, k, s, t.qgemm_waves, t.qgemm_stages,
+                                       t.qgemm_panel);
   const int grid = (n + kWaves - 1) / kWaves;
   for (int m0 = 0; m0 < m; m0 += 8) {
     const int mt = m - m0 < 8 ? m - m0 : 8;
@@ -294,10 +295,11 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, 
 }  // namespace
 
 hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long long m,
-                        long long n, long long k, hipStream_t s, const GemvTuning& t) {
+                        long long n, long long k, hipStream_t s, const GemvTuning& t,
+                        bool noalloc) {
   const auto* w = static_cast<const uint8_t*>(W);
-  return fmt == kQ8_0 ? launch_fmt<kQ8_0>(w, x, y, (int)m, (int)n, (int)k, s, t)
-                      : launch_fmt<kQ4_0>(w, x, y, (int)m, (int)n, (int)k, s, t);
+  return fmt == kQ8_0 ? launch_fmt<kQ8_0>(w, x, y, (int)m, (int)n, (int)k, s, t, noalloc)
+                      : launch_fmt<kQ4_0>(w, x, y, (int)m, (int)n, (int)k, s, t, noalloc);
 }
 
 }  // namespace qc

@@ -38,6 +38,7 @@ _SIGS = {
     "qc_hip_qgemv_unpack": ([_I, _P, _LL, _LL, _P, _P], _I),
     "qc_hip_qgemv": ([_I, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_qgemm": ([_I, _P, _P, _P, _LL, _LL, _LL, _P], _I),
+    "qc_hip_qgemm_noalloc": ([_I, _P, _P, _P, _LL, _LL, _LL, _P], _I),
     "qc_hip_qgemv_w8a8": ([_I, _P, _P, _P, _LL, _LL, _P, _P], _I),
     "qc_hip_qgemv_up_gate": ([_I, _P, _P, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_qgemv_up_gate_activation": ([_I, _P, _P, _P, _P, _LL, _LL, _I, _P], _I),
@@ -125,6 +126,11 @@ def qgemv_qkv_raw(fmt, pq, pk, pv, x, q, k_out, v_out, query_dim, kv_dim, input_
 
 def qgemm_raw(fmt, packed, x, y, m, n, k, stream=None):
     return lib.qc_hip_qgemm(fmt, _ptr(packed), _ptr(x), _ptr(y), m, n, k, _stream(stream))
+
+
+def qgemm_noalloc_raw(fmt, packed, x, y, m, n, k, stream=None):
+    return lib.qc_hip_qgemm_noalloc(fmt, _ptr(packed), _ptr(x), _ptr(y), m, n, k,
+                                    _stream(stream))
 
 
 def pack_raw(fmt, w, packed, n, k, dev_status=None, stream=None):
