@@ -9,15 +9,21 @@ graph and replayed once, between two device synchronisations.  Each step
 reads a different copy of the weights (ceil(256 MB / footprint) + 1 copies)
 so that every step streams from HBM, not from the 256 MB Infinity Cache.
 
-Secondary lines (same discipline) cover the other BASELINE configs: q8_0 GEMV
-(config 0), q4_0 K=14336 -> N=4096, the q8_0 small-batch GEMM (config 2), the
-activation quantizer and the W8A8 GEMM at M=2048 (config 3), and the per-layer
-sums of the 32-layer decoder sweep (config 4).
+`legs` holds every part of BASELINE.json's metric, each with its roofline and
+CPU baseline: q4_0 and q8_0 GEMV at K4096xN14336 (GB/s, HBM), the W8A8 int8
+GEMM at M=2048, K=4096, N=4096 and 14336 (TOPS, int8 MFMA), and config 3's
+per-token activation quantizer.  Secondary lines (same discipline) cover the
+other BASELINE configs: q8_0 GEMV (config 0), q4_0 K=14336 -> N=4096, the
+q8_0 small-batch GEMM (config 2), the other W8A8 producers, and the
+per-layer sums of the 32-layer decoder sweep (config 4).
 
-cpu_baseline: the reference's own x86 route for the headline op (AVX2
-q4_rows, compiled from the reference sources into oracle/_ref by
-oracle/Makefile), timed on this host's cores; the same call provides the
-correctness gate of the GPU result before its number is reported.
+cpu_baseline: the reference's own x86 routes (compiled from the reference
+sources into oracle/_ref by oracle/Makefile) on this host's cores -- q4_0
+gguf_gemv_avx2 (q4_rows), q8_0_gemv_ref, the dispatched int8_gemm (AVX-512
+VNNI where present) on 64 of the 2048 rows, and quantize_int8 -- at the
+physical cores of NUMA node 0 available to this process and at 1 thread.
+The same legs gate each GPU result (contract tolerance for the GEMVs, bit
+for bit for the int8 GEMM) before its number is reported.
 """
 from __future__ import annotations
 
@@ -42,11 +48,12 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=["headline", "all", "copy", "w8a8", "qgemm", "prefill"],
+    p.add_argument("--only", choices=["headline", "all", "copy", "w8a8", "qgemm", "prefill",
+                                      "legs"],
                    default="all",
                    help="copy: a plain 64 MiB device copy, the calibration kernel for "
-                        "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm / prefill: only "
-                        "those secondary cases (for profiling), no JSON line")
+                        "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm / prefill / legs: "
+                        "only those cases (for profiling), no JSON line")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--rows-per-wave", type=int, default=0)
@@ -301,7 +308,7 @@ def w8a8_operands(qc, m, n, k, seed=7):
     return w, x, ws.reshape(-1), as_.reshape(-1)
 
 
-def w8a8_case(qc, m, n, k, steps, warmup):
+def w8a8_case(qc, m, n, k, steps, warmup, keep=False):
     import torch
     dev = torch.device("cuda:0")
     w, x, ws, as_ = w8a8_operands(qc, m, n, k)
@@ -315,8 +322,9 @@ def w8a8_case(qc, m, n, k, steps, warmup):
 
     wall, gpu = time_steps(launch, steps, warmup)
     ops = 2.0 * m * n * k
-    return {"m": m, "n": n, "k": k, "ops": ops, "wall_ms": wall, "gpu_ms": gpu,
-            "tops": ops / (wall * 1e-3) / 1e12, "kernel_tops": ops / (gpu * 1e-3) / 1e12}
+    r = {"m": m, "n": n, "k": k, "ops": ops, "wall_ms": wall, "gpu_ms": gpu,
+         "tops": ops / (wall * 1e-3) / 1e12, "kernel_tops": ops / (gpu * 1e-3) / 1e12}
+    return (r, (w, x, ws, as_, y)) if keep else r
 
 
 # the matmuls of one layer of a synthetic 32-layer,
@@ -382,64 +390,174 @@ def profiled_traffic(name):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(packed_dev, x_dev, y_dev, n, k, seconds):
-    """Reference x86 q4_0 route (oracle/_ref) on this host: timing + gate."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+def host_cpu():
+    """The host's CPU as the CPU baselines use it: model, the ISA features the
+    reference's dispatch looks at, and the thread count -- the physical cores
+    of NUMA node 0 that this process may run on, capped by its cgroup CPU
+    quota (the GPU box's share of the host)."""
+    info = {"model": None, "isa": [], "numa_node0_physical_cores": None,
+            "allowed_cpus": len(os.sched_getaffinity(0)), "cgroup_cpu_quota": None}
+    try:
+        flags = set()
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and info["model"] is None:
+                info["model"] = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+        info["isa"] = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl",
+                                   "avx512dq", "avx512_vnni", "avx_vnni", "amx_int8")
+                       if f in flags]
+    except OSError:
+        pass
+    allowed = os.sched_getaffinity(0)
+    try:
+        node0 = set()
+        for part in open("/sys/devices/system/node/node0/cpulist").read().strip().split(","):
+            a, _, b = part.partition("-")
+            node0.update(range(int(a), int(b or a) + 1))
+        cores = set()
+        for c in sorted(node0 & allowed):
+            topo = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            cores.add((open(topo + "physical_package_id").read().strip(),
+                       open(topo + "core_id").read().strip()))
+        info["numa_node0_physical_cores"] = len(cores)
+    except (OSError, ValueError):
+        pass
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if quota != "max":
+            info["cgroup_cpu_quota"] = int(quota) / int(period)
+    except (OSError, ValueError):
+        pass
+    threads = info["numa_node0_physical_cores"] or info["allowed_cpus"]
+    if info["cgroup_cpu_quota"]:
+        threads = min(threads, max(1, int(info["cgroup_cpu_quota"])))
+    info["threads"] = max(1, threads)
+    return info
+
+
+def time_cpu(call, budget):
+    """The reference harness's discipline (benchmarks/harness/timing.cpp:19-85):
+    warmup >= 3 calls and >= 50 ms, then >= 20 samples of batches >= 2 ms until
+    the budget is spent; returns (median seconds per call, samples)."""
     import numpy as np
+    t_end = time.perf_counter() + 0.05
+    calls = 0
+    while calls < 3 or time.perf_counter() < t_end:
+        call()
+        calls += 1
+    samples = []
+    deadline = time.perf_counter() + budget
+    while len(samples) < 20 or time.perf_counter() < deadline:
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            call()
+            reps += 1
+            if time.perf_counter() - t0 >= 2e-3:
+                break
+        samples.append((time.perf_counter() - t0) / reps)
+    return float(np.median(samples)), len(samples)
+
+
+def reference():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     if not oracle.Reference.available():
-        return None, None
-    ref = oracle.Reference()
+        return None, oracle
+    return oracle.Reference(), oracle
+
+
+def cpu_legs(ref, oracle, cpu, seconds, work, unit, describe):
+    """One CPU baseline: `work(threads)` returns (call, units per call); timed
+    at the chosen thread count and at 1 thread, the reference's thread pool
+    set explicitly (its default is 1, include/quixicore_cpu/threading.h:6-11)."""
+    threads = cpu["threads"]
+    ref.set_threads(threads)
+    call, units = work()
+    t_all, s_all = time_cpu(call, seconds * 0.7)
+    ref.set_threads(1)
+    t_one, s_one = time_cpu(call, seconds * 0.3)
+    scale = 1e9 if unit == "GB/s" else 1e12
+    return {"value": units / t_all / scale, "unit": unit, "cores": threads, "kind": "reference",
+            "sample": (f"{describe}; median of {s_all} samples (>=2 ms batches, "
+                       f"~{seconds * 0.7:.0f} s) at {threads} threads"),
+            "value_1thread": units / t_one / scale, "ms_per_call": t_all * 1e3,
+            "ms_per_call_1thread": t_one * 1e3,
+            "cpu": {"model": cpu["model"], "isa": cpu["isa"],
+                    "numa_node0_physical_cores": cpu["numa_node0_physical_cores"],
+                    "cgroup_cpu_quota": cpu["cgroup_cpu_quota"]}}
+
+
+def gemv_baseline(ref, oracle, cpu, fmt, packed_dev, x_dev, y_dev, n, k, seconds):
+    """The reference's x86 GEMV route on this host (q4_0: gguf_gemv_avx2's
+    q4_rows; q8_0: q8_0_gemv_ref, its only x86 route) on the same packed
+    bytes, plus the correctness gate of one fresh GPU step: f64 contract
+    oracle and the reference's own f32 output, both at 1e-4 normalised."""
+    import numpy as np
     import quixicore_hip as qc
     packed = packed_dev.cpu().numpy()
     x = x_dev.cpu().numpy()
-    st = qc.qgemv_raw(qc.Q4_0, packed_dev, x_dev, y_dev, n, k)   # one fresh step on copy 0
+    st = qc.qgemv_raw(fmt, packed_dev, x_dev, y_dev, n, k)
     if st:
         raise RuntimeError(f"qgemv status {st}")
     y_gpu = y_dev.cpu().numpy()
-    # correctness gate: GPU vs f64 contract oracle (1e-4 normalised) and vs
-    # the reference's own f32 output
-    y64, wn = oracle.gemv_f64(oracle.Q4_0, packed, x, n, k)
+    y64, wn = oracle.gemv_f64(fmt, packed, x, n, k)
     ok, worst = oracle.within_contract(y_gpu, y64, wn, x, 1e-4)
-    y_ref = ref.gemv(oracle.Q4_0, packed, x, n, k)
+    y_ref = ref.gemv(fmt, packed, x, n, k)
     ok_ref, worst_ref = oracle.within_contract(y_gpu, y_ref.astype(np.float64), wn, x, 1e-4)
     gate = {"pass": bool(ok and ok_ref), "max_norm_err_vs_f64": worst,
             "max_norm_err_vs_reference": worst_ref}
-
-    def timed(threads, budget):
-        ref.set_threads(threads)
-        y = np.empty(n, dtype=np.float32)
-        t_end = time.perf_counter() + 0.05
-        calls = 0
-        while calls < 3 or time.perf_counter() < t_end:     # warmup >= 3 calls and >= 50 ms
-            ref.lib.qcref_q4_0_gemv_avx2(oracle._ptr(packed), oracle._ptr(x), oracle._ptr(y), n, k)
-            calls += 1
-        samples = []
-        deadline = time.perf_counter() + budget
-        while len(samples) < 20 or time.perf_counter() < deadline:
-            t0 = time.perf_counter()
-            reps = 0
-            while True:                                      # batch >= 2 ms
-                ref.lib.qcref_q4_0_gemv_avx2(oracle._ptr(packed), oracle._ptr(x), oracle._ptr(y),
-                                             n, k)
-                reps += 1
-                if time.perf_counter() - t0 >= 2e-3:
-                    break
-            samples.append((time.perf_counter() - t0) / reps)
-        return float(np.median(samples)), len(samples)
-
-    threads = min(16, os.cpu_count() or 1)
-    alg = n * (k // 32) * 18 + 4 * k + 4 * n
-    t_all, s_all = timed(threads, seconds * 0.7)
-    t_one, s_one = timed(1, seconds * 0.3)
-    ref.set_threads(1)
-    base = {"value": alg / t_all / 1e9, "unit": "GB/s", "cores": threads, "kind": "reference",
-            "sample": (f"reference gguf_gemv_avx2 (q4_rows) q4_0 GEMV K={k} N={n} on the same "
-                       f"packed bytes, median of {s_all} samples (>=2 ms batches, "
-                       f"~{seconds * 0.7:.0f} s) at {threads} threads"),
-            "value_1thread": alg / t_one / 1e9, "ms_per_call": t_all * 1e3,
-            "ms_per_call_1thread": t_one * 1e3}
+    y = np.empty(n, dtype=np.float32)
+    fn = ref.lib.qcref_q8_0_gemv if fmt == 0 else ref.lib.qcref_q4_0_gemv_avx2
+    args = (oracle._ptr(packed), oracle._ptr(x), oracle._ptr(y), n, k)
+    alg = n * (k // 32) * (34 if fmt == 0 else 18) + 4 * k + 4 * n
+    name = "q8_0_gemv_ref" if fmt == 0 else "gguf_gemv_avx2 (q4_rows)"
+    base = cpu_legs(ref, oracle, cpu, seconds, lambda: (lambda: fn(*args), alg), "GB/s",
+                    f"reference {name} {'q8_0' if fmt == 0 else 'q4_0'} GEMV K={k} N={n} on the "
+                    "same packed bytes")
     return base, gate
+
+
+def w8a8_baseline(ref, oracle, cpu, w_dev, x_dev, ws_dev, as_dev, y_dev, sample_rows, seconds):
+    """The reference's dispatched int8_gemm (src/dispatch/int8_gemm.cpp:20-63:
+    AVX-512 VNNI where avx512f/bw/vl/dq + vnni are present) on the first
+    `sample_rows` activation rows of the same operands, plus the bit-exact
+    gate of the GPU output on those rows."""
+    import numpy as np
+    w = w_dev.cpu().numpy()
+    x = np.ascontiguousarray(x_dev[:sample_rows].cpu().numpy())
+    ws = ws_dev.cpu().numpy()
+    as_ = np.ascontiguousarray(as_dev[:sample_rows].cpu().numpy())
+    n, k = w.shape
+    st, y_ref = ref.int8_gemm(w, x, ws, as_)
+    gpu = y_dev[:sample_rows].cpu().numpy()
+    gate = {"pass": bool(st == 0 and np.array_equal(gpu.view(np.uint32), y_ref.view(np.uint32))),
+            "rows_checked": sample_rows, "bit_exact": True}
+    y = np.empty((sample_rows, n), dtype=np.float32)
+    args = (oracle._ptr(w), oracle._ptr(x), oracle._ptr(ws), oracle._ptr(as_), None, None,
+            oracle._ptr(y), sample_rows, n, k, 0)
+    ops = 2.0 * sample_rows * n * k
+    base = cpu_legs(ref, oracle, cpu, seconds,
+                    lambda: (lambda: ref.lib.qcref_int8_gemm(*args), ops), "TOPS",
+                    f"reference int8_gemm ({ref.variant()} route) M={sample_rows} of the 2048 "
+                    f"rows, N={n} K={k}, same int8 operands")
+    return base, gate
+
+
+def quant_baseline(ref, oracle, cpu, m, k, seconds):
+    """The reference's quantize_int8 (kernels/quantization/quantization_ref.cpp:
+    143-168, scalar per row) over config 3's whole M x K activation matrix."""
+    import numpy as np
+    from quixicore_hip import synth
+    x = synth.activations_outliers_fast(3, m, k)
+    codes = np.empty((m, k), dtype=np.int8)
+    scales = np.empty(m, dtype=np.float32)
+    args = (oracle._ptr(x), oracle._ptr(codes), oracle._ptr(scales), m, k, 0)
+    fp = 4 * m * k + m * k + 4 * m
+    return cpu_legs(ref, oracle, cpu, seconds,
+                    lambda: (lambda: ref.lib.qcref_quantize_int8(*args), fp), "GB/s",
+                    f"reference quantize_int8 M={m} K={k} (config 3 activations)")
 
 
 def print_cases(cases):
@@ -473,9 +591,16 @@ def main():
         print(json.dumps({"copy_bytes": 64 << 20, "launches": args.warmup + args.steps}))
         return
     K, W = args.steps, args.warmup
-    if args.only in ("w8a8", "qgemm", "prefill"):
+    if args.only in ("w8a8", "qgemm", "prefill", "legs"):
         s = {}
-        if args.only == "prefill":
+        if args.only == "legs":
+            # the metric's legs in the order the JSON line lists them
+            s["q4_0_gemv_k4096_n14336"], *_ = gemv_case(qc, 1, 14336, 4096, K, W, seed=1)
+            s["q8_0_gemv_k4096_n14336"], *_ = gemv_case(qc, 0, 14336, 4096, K, W, seed=5)
+            s["w8a8_m2048_k4096_n4096"] = w8a8_case(qc, 2048, 4096, 4096, K, W)
+            s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, K, W)
+            s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
+        elif args.only == "prefill":
             # the 2-D GEMM route (M >= 64) at a 4096 / 14336 layer's FFN shape
             for fmt, name in ((1, "q4_0"), (0, "q8_0")):
                 for m in (512, 2048):
@@ -500,6 +625,14 @@ def main():
     print(f"# headline q4_0 GEMV K={k} N={n}: {head['gbs']:.1f} GB/s wall, "
           f"{head['kernel_gbs']:.1f} GB/s kernel ({head['gpu_ms'] * 1e3:.2f} us)",
           file=sys.stderr, flush=True)
+    # the other legs of BASELINE.json's metric
+    q8, packed8, x8, y8 = gemv_case(qc, 0, n, k, K, W, seed=5)
+    w8, w8ops = {}, {}
+    for n_ in (4096, 14336):
+        w8[n_], w8ops[n_] = w8a8_case(qc, 2048, n_, 4096, max(20, K // 4), W, keep=True)
+    quant = quant_case(qc, 2048, 4096, K, W)
+    print_cases({"q8_0_gemv_k4096_n14336": q8, "w8a8_m2048_k4096_n4096": w8[4096],
+                 "w8a8_m2048_k4096_n14336": w8[14336], "quantize_int8_m2048_k4096": quant})
     secondary = {}
     if args.only == "all":
         s = {}
@@ -511,21 +644,60 @@ def main():
         s["q8_0_gemv_w8a8_k4096_n4096"] = gemv_w8a8_case(qc, 0, 4096, 4096, K, W, seed=12)
         s["q4_0_up_gate_k4096_n2x14336"] = fused_case(qc, "up_gate", 1, (14336, 14336), 4096, K, W,
                                                       seed=13)
-        for m in (4, 8, 16, 32):
-            s[f"q8_0_qgemm_m{m}_k4096_n14336"] = qgemm_case(qc, 14336, 4096, m, K, W, seed=4 + m)
-        s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
+        for n_ in (4096, 14336):
+            for m in (4, 8, 16, 32):
+                s[f"q8_0_qgemm_m{m}_k4096_n{n_}"] = qgemm_case(qc, n_, 4096, m, K, W, seed=4 + m)
         s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
         s["quantize_int8_asymmetric_m2048_k4096"] = asym_case(qc, 2048, 4096, K, W)
-        s["w8a8_m2048_k4096_n4096"] = w8a8_case(qc, 2048, 4096, 4096, max(20, K // 4), W)
-        s["w8a8_m2048_k4096_n14336"] = w8a8_case(qc, 2048, 14336, 4096, max(20, K // 4), W)
         for key, r in layer_sweep(qc, max(20, K // 4), W).items():
             s[f"decoder_layer_{key}"] = r
         print_cases(s)
         secondary = s
-    base, gate = (None, None)
-    if not args.no_cpu:
-        base, gate = cpu_baseline(packed, x, y, n, k, args.cpu_seconds)
-    achieved = head["kernel_gbs"]
+
+    cpu = host_cpu()
+    ref, oracle = (None, None) if args.no_cpu else reference()
+    bases = {}
+    if ref is not None:
+        sec = args.cpu_seconds
+        bases["q4_0"] = gemv_baseline(ref, oracle, cpu, 1, packed, x, y, n, k, sec)
+        bases["q8_0"] = gemv_baseline(ref, oracle, cpu, 0, packed8, x8, y8, n, k, sec * 0.5)
+        for n_ in (4096, 14336):
+            bases[n_] = w8a8_baseline(ref, oracle, cpu, w8ops[n_][0], w8ops[n_][1], w8ops[n_][2],
+                                      w8ops[n_][3], w8ops[n_][4], 64, sec * 0.5)
+        bases["quant"] = (quant_baseline(ref, oracle, cpu, 2048, 4096, sec * 0.3), None)
+        ref.set_threads(1)
+    del w8ops
+
+    def gemv_leg(r, key, name):
+        base, gate = bases.get(key, (None, None))
+        return {"value": round(r["gbs"], 2), "unit": "GB/s",
+                "pct_hbm_peak": round(100.0 * r["gbs"] / HBM_PEAK_GBS, 2),
+                "kernel_us": round(r["gpu_ms"] * 1e3, 3), "bytes_per_step": r["bytes"],
+                "roofline": {"bound": "hbm", "achieved": round(r["kernel_gbs"], 2),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                             "traffic": profiled_traffic(name)},
+                "cpu_baseline": base, "check": gate}
+
+    def w8a8_leg(r, key, name):
+        base, gate = bases.get(key, (None, None))
+        return {"value": round(r["tops"], 2), "unit": "TOPS",
+                "kernel_us": round(r["gpu_ms"] * 1e3, 3), "ops_per_step": r["ops"],
+                "roofline": {"bound": "mfma", "achieved": round(r["kernel_tops"], 2),
+                             "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                             "frac": round(r["kernel_tops"] / INT8_PEAK_TOPS, 4),
+                             "traffic": profiled_traffic(name)},
+                "cpu_baseline": base, "check": gate}
+
+    legs = {
+        "q4_0_gemv_k4096_n14336": gemv_leg(head, "q4_0", "q4_0_gemv_k4096_n14336"),
+        "q8_0_gemv_k4096_n14336": gemv_leg(q8, "q8_0", "q8_0_gemv_k4096_n14336"),
+        "w8a8_gemm_m2048_k4096_n4096": w8a8_leg(w8[4096], 4096, "w8a8_int8_gemm_m2048_k4096_n4096"),
+        "w8a8_gemm_m2048_k4096_n14336": w8a8_leg(w8[14336], 14336,
+                                                 "w8a8_int8_gemm_m2048_k4096_n14336"),
+        "quantize_int8_m2048_k4096": gemv_leg(quant, "quant", "quantize_int8_m2048_k4096"),
+    }
+    head_leg = legs["q4_0_gemv_k4096_n14336"]
     line = {
         "metric": "q4_0 GEMV GB/s (% HBM peak) at K4096xN14336",
         "value": round(head["gbs"], 2),
@@ -537,7 +709,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights (u8 nibbles + fp16 scales), f32 activations/accumulation",
+        "dtype": "int32 (exact int8 dot4 block sums) + f32",
+        "dtype_note": ("q4_0 weights (4-bit codes, fp16 block scales); each 32-element block of "
+                       "the f32 activations is encoded as 22-bit fixed point (three int8 digit "
+                       "planes), block dots are exact int32 v_dot4_i32_i8 sums, scaled and "
+                       "accumulated in f32"),
         "data": ("synthetic: torch-seeded N(0,0.02) f32 weights packed to q4_0 on the GPU, "
                  f"{head['copies']} rotated copies (HBM-resident, > Infinity Cache); x ~ N(0,1)"),
         "config": {"workload": "qgemv q4_0 M=1 K=4096 N=14336 (BASELINE config 1, up/gate)",
@@ -545,12 +721,11 @@ def main():
                    "weight_bytes_per_step": head["weight_bytes"],
                    "parallelism": "single GPU"},
         "pct_hbm_peak": round(100.0 * head["gbs"] / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic("q4_0_gemv_k4096_n14336"),
-                     "kernel_us": round(head["gpu_ms"] * 1e3, 3)},
-        "cpu_baseline": base,
-        "check": gate,
+        "roofline": dict(head_leg["roofline"], kernel_us=round(head["gpu_ms"] * 1e3, 3)),
+        "cpu_baseline": head_leg["cpu_baseline"],
+        "check": head_leg["check"],
+        "legs": legs,
+        "host_cpu": cpu,
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
