@@ -273,6 +273,12 @@ class Reference:
         L.qcref_quantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
         L.qcref_dequantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
         L.qcref_set_num_threads.restype = None
+        L.qcref_prepare_gguf.argtypes = [ctypes.c_int, _P, _LL, _LL, ctypes.c_int, _P, _LL, _P]
+        L.qcref_prepare_smoothquant.argtypes = [_P, _P, _LL, _LL, _P, _LL, _P, ctypes.c_int, _P,
+                                                _LL, _P]
+        L.qcref_prepare_canonical_int8.argtypes = [
+            ctypes.c_int, _LL, _LL, _LL, ctypes.c_int, _P, _P, _LL, _P, _P, _LL, _P, _P,
+            ctypes.c_int, _P, _LL, _P]
 
     @staticmethod
     def available(path=REF_PATH):
@@ -357,6 +363,44 @@ class Reference:
             _ptr(codes), _ptr(np.ascontiguousarray(scales, np.float32)),
             _ptr(np.ascontiguousarray(zps, np.int32)), _ptr(out), rows, dim)
         return st, out
+
+    def prepare_gguf(self, fmt, packed, rows, cols, layout):
+        """The reference's CpuPackedWeights::prepare: (status, panel bytes, info[24])."""
+        info = np.zeros(24, dtype=np.int64)
+        cap = max(1, len(packed)) * 32 + (1 << 16)
+        panel = np.zeros(cap, dtype=np.uint8)
+        st = self.lib.qcref_prepare_gguf(fmt, _ptr(np.ascontiguousarray(packed)), rows, cols,
+                                         layout, _ptr(panel), cap, _ptr(info))
+        return st, panel[:int(info[13])] if st == 0 else None, info
+
+    def prepare_canonical_int8(self, affine, data, rows, cols, group_size, scale_mode, scales,
+                               zps=None, act_scales=None, act_zps=None, row_sums=None,
+                               layout=0):
+        info = np.zeros(24, dtype=np.int64)
+        cap = rows * cols * 32 + (1 << 16)
+        panel = np.zeros(cap, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        a = np.ascontiguousarray(act_scales if act_scales is not None else [], np.float32)
+        st = self.lib.qcref_prepare_canonical_int8(
+            int(affine), rows, cols, group_size, scale_mode,
+            _ptr(np.ascontiguousarray(data, np.int8)), _ptr(scales), len(scales),
+            _ptr(None if zps is None else np.ascontiguousarray(zps, np.float32)),
+            _ptr(a), len(a), _ptr(None if act_zps is None else np.ascontiguousarray(act_zps, np.int32)),
+            _ptr(None if row_sums is None else np.ascontiguousarray(row_sums, np.int32)),
+            layout, _ptr(panel), cap, _ptr(info))
+        return st, panel[:int(info[13])] if st == 0 else None, info
+
+    def prepare_smoothquant(self, w, ws, act_scales, act_zps, layout):
+        rows, cols = w.shape
+        info = np.zeros(24, dtype=np.int64)
+        cap = rows * cols * 32 + (1 << 16)
+        panel = np.zeros(cap, dtype=np.uint8)
+        st = self.lib.qcref_prepare_smoothquant(
+            _ptr(np.ascontiguousarray(w, np.int8)), _ptr(np.ascontiguousarray(ws, np.float32)),
+            rows, cols, _ptr(np.ascontiguousarray(act_scales, np.float32)), len(act_scales),
+            _ptr(None if act_zps is None else np.ascontiguousarray(act_zps, np.int32)), layout,
+            _ptr(panel), cap, _ptr(info))
+        return st, panel[:int(info[13])] if st == 0 else None, info
 
     def variant(self):
         return self.lib.qcref_int8_gemm_variant().decode()

@@ -13,13 +13,19 @@
 //   rms_norm_add_quant_int8, quantize_int8_asymmetric, dequantize_int8_asymmetric
 //               -> the public functions  (kernels/norms/norm_quant_ref.cpp:1060-1068;
 //                                          kernels/quantization/quantization_ref.cpp:190-244)
+//   CpuPackedWeights::prepare (both overloads), info(), panel_data()
+//               -> src/memory/packed_weights.cpp:197-412
 #include <cstddef>
 #include <cstdint>
 
 #include "kernels/quantization/gguf_ref.h"
 #include "kernels/quantization/qgemv.h"
 #include "kernels/quantization/qgemv_w8a8.h"
+#include <cstring>
+
+#include "quixicore_cpu/packed_weights.h"
 #include "quixicore_cpu/qgemm.h"
+#include "quixicore_cpu/quant_import.h"
 #include "quixicore_cpu/quantization.h"
 #include "quixicore_cpu/threading.h"
 
@@ -105,6 +111,107 @@ int qcref_dequantize_int8_asymmetric(const std::int8_t* codes, const float* scal
                                      long long dim) {
   return static_cast<int>(qc::dequantize_int8_asymmetric(codes, scales, zero_points, out, rows,
                                                         dim));
+}
+
+// info fields of a prepared weight as 24 integers (the order the tests read).
+static void dump_info(const qc::CpuPackedWeightsInfo& i, long long* out) {
+  const long long v[] = {static_cast<long long>(i.layout), i.rows, i.columns, i.row_tile,
+                         i.block_size, i.blocks_per_row, static_cast<long long>(i.block_bytes),
+                         static_cast<long long>(i.contract_bytes),
+                         static_cast<long long>(i.panel_bytes), i.prepared_version,
+                         static_cast<long long>(i.required_isa), i.column_tile,
+                         static_cast<long long>(i.panel_alignment),
+                         static_cast<long long>(i.prepared_bytes),
+                         static_cast<long long>(i.logical_bytes), i.has_canonical_layout,
+                         static_cast<long long>(i.canonical_layout),
+                         static_cast<long long>(i.scale_table_offset),
+                         static_cast<long long>(i.zero_point_table_offset),
+                         static_cast<long long>(i.activation_scale_offset),
+                         static_cast<long long>(i.activation_zero_point_offset),
+                         static_cast<long long>(i.row_sum_table_offset),
+                         static_cast<long long>(i.format),
+                         static_cast<long long>(i.memory_amplification * 1e6)};
+  std::memcpy(out, v, sizeof(v));
+}
+
+// Status of prepare; on kOk the panel (prepared_bytes, at most cap) and info.
+int qcref_prepare_gguf(int format, const void* bytes, long long rows, long long columns,
+                       int layout, void* panel, long long cap, long long* info) {
+  qc::CpuPackedWeights w;
+  const qc::Status s = w.prepare(static_cast<qc::QuantFormat>(format), bytes, rows, columns,
+                                 static_cast<qc::CpuPanelLayout>(layout));
+  if (s != qc::Status::kOk) return static_cast<int>(s);
+  const qc::CpuPackedWeightsInfo i = w.info();
+  dump_info(i, info);
+  const long long n = static_cast<long long>(i.prepared_bytes);
+  std::memcpy(panel, w.panel_data(), static_cast<size_t>(n < cap ? n : cap));
+  return 0;
+}
+
+// A kInt8Symmetric / kInt8Affine tensor with row, channel or group scales,
+// optional zero points, activation scales / zero points and row sums.
+int qcref_prepare_canonical_int8(int affine, long long rows, long long columns,
+                                 long long group_size, int scale_mode, const int8_t* data,
+                                 const float* scales, long long nscales, const float* zps,
+                                 const float* act_scales, long long nact, const int* act_zps,
+                                 const int32_t* row_sums, int layout, void* panel,
+                                 long long cap, long long* info) {
+  qc::CanonicalQuantTensor t;
+  t.metadata.layout = affine ? qc::CanonicalQuantLayout::kInt8Affine
+                             : qc::CanonicalQuantLayout::kInt8Symmetric;
+  t.metadata.logical_rows = rows;
+  t.metadata.logical_columns = columns;
+  t.metadata.group_size = group_size;
+  t.metadata.scale_mode = static_cast<qc::QuantScaleMode>(scale_mode);
+  t.metadata.scale_encoding = qc::QuantScaleEncoding::kFP32;
+  t.metadata.scale_count = static_cast<size_t>(nscales);
+  const auto* d = reinterpret_cast<const uint8_t*>(data);
+  t.data.assign(d, d + rows * columns);
+  t.scales.assign(scales, scales + nscales);
+  if (affine) {
+    t.metadata.zero_point_mode = qc::QuantZeroPointMode::kInteger;
+    t.metadata.zero_point_count = static_cast<size_t>(nscales);
+    t.zero_points.assign(zps, zps + nscales);
+  }
+  if (nact > 0) t.activation_scales.assign(act_scales, act_scales + nact);
+  if (nact > 0 && act_zps != nullptr) t.activation_zero_points.assign(act_zps, act_zps + nact);
+  if (row_sums != nullptr) t.row_sums.assign(row_sums, row_sums + rows);
+  qc::CpuPackedWeights w;
+  const qc::Status s = w.prepare(t, static_cast<qc::CpuPanelLayout>(layout));
+  if (s != qc::Status::kOk) return static_cast<int>(s);
+  const qc::CpuPackedWeightsInfo i = w.info();
+  dump_info(i, info);
+  const long long n = static_cast<long long>(i.prepared_bytes);
+  std::memcpy(panel, w.panel_data(), static_cast<size_t>(n < cap ? n : cap));
+  return 0;
+}
+
+// import_smoothquant_w8a8 (row sums computed by the importer), then prepare.
+int qcref_prepare_smoothquant(const int8_t* w, const float* ws, long long rows, long long columns,
+                              const float* act_scales, long long nact, const int* act_zps,
+                              int layout, void* panel, long long cap, long long* info) {
+  qc::SmoothQuantW8A8Source src;
+  src.weights = w;
+  src.weight_count = static_cast<size_t>(rows * columns);
+  src.weight_scales = ws;
+  src.weight_scale_count = static_cast<size_t>(rows);
+  src.activation_scales = act_scales;
+  src.activation_scale_count = static_cast<size_t>(nact);
+  src.activation_zero_points = act_zps;
+  src.activation_zero_point_count = act_zps != nullptr ? static_cast<size_t>(nact) : 0;
+  src.rows = rows;
+  src.columns = columns;
+  qc::CanonicalQuantTensor t;
+  qc::Status s = qc::import_smoothquant_w8a8(src, &t);
+  if (s != qc::Status::kOk) return 100 + static_cast<int>(s);
+  qc::CpuPackedWeights pw;
+  s = pw.prepare(t, static_cast<qc::CpuPanelLayout>(layout));
+  if (s != qc::Status::kOk) return static_cast<int>(s);
+  const qc::CpuPackedWeightsInfo i = pw.info();
+  dump_info(i, info);
+  const long long n = static_cast<long long>(i.prepared_bytes);
+  std::memcpy(panel, pw.panel_data(), static_cast<size_t>(n < cap ? n : cap));
+  return 0;
 }
 
 void qcref_set_num_threads(int n) { qc::set_num_threads(n); }
