@@ -312,16 +312,6 @@ int qc_hip_set_gemv_rows_per_wave(int rows) {
 // temporary up vector.
 namespace {
 
-__global__ void fused_activation_kernel(float* out, const float* up, long long n, int act) {
-  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float v = out[i];
-  constexpr float kSqrt2OverPi = 0.7978845608028654f;
-  const float a = act == 1 ? 0.5f * v * (1.0f + tanhf(kSqrt2OverPi * (v + 0.044715f * v * v * v)))
-                           : v / (1.0f + expf(-v));
-  out[i] = a * up[i];
-}
-
 int fused_gemv(int format, int nseg, const void* const* w, float* const* y,
                const long long* rows, int act, const float* x, long long k, hipStream_t s) {
   bool fast = (k >> 5) % 2 == 0 && k < (1LL << 31) && reinterpret_cast<uintptr_t>(x) % 16 == 0;
@@ -349,9 +339,7 @@ int fused_gemv(int format, int nseg, const void* const* w, float* const* y,
   e = qc::launch_qgemm(format, w[0], x, up, 1, rows[0], k, s, g_tuning);
   if (e == hipSuccess) e = qc::launch_qgemm(format, w[1], x, y[0], 1, rows[0], k, s, g_tuning);
   if (e == hipSuccess) {
-    fused_activation_kernel<<<static_cast<unsigned>((rows[0] + 255) / 256), 256, 0, s>>>(
-        y[0], up, rows[0], act);
-    e = hipGetLastError();
+    e = qc::launch_fused_activation(y[0], up, rows[0], act, s);
   }
   const hipError_t f = hipFreeAsync(up, s);
   return finish(e != hipSuccess ? e : f);

@@ -33,6 +33,10 @@ hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, in
 hipError_t launch_qgemv_multi(int fmt, int nseg, const void* const* W, float* const* y,
                               const int* rows, int act, const float* x, int k, hipStream_t s);
 
+// out[i] = activation(out[i]) * up[i] over n elements (act 0: SiLU, 1: GELU-tanh).
+hipError_t launch_fused_activation(float* out, const float* up, long long n, int act,
+                                   hipStream_t s);
+
 // qgemv_w8a8: x quantized per 32-element block to int8, exact integer block
 // dots, y bit-identical to the reference.  status (optional): set to 3 when x
 // holds a non-finite value (the affected outputs are NaN).

@@ -885,4 +885,19 @@ hipError_t launch_qgemv_w8a8(int fmt, const void* Wv, const float* x, float* y, 
   return hipGetLastError();
 }
 
+// out[i] = activation(out[i]) * up[i]: the per-matrix route of the fused
+// up/gate activation, with the single-launch epilogue's arithmetic.
+__global__ void fused_activation_kernel(float* out, const float* up, long long n, int act) {
+  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = fused_activation(out[i], act) * up[i];
+}
+
+hipError_t launch_fused_activation(float* out, const float* up, long long n, int act,
+                                   hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  fused_activation_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(out, up, n, act);
+  return hipGetLastError();
+}
+
 }  // namespace qc
