@@ -68,7 +68,7 @@ Status qgemv(QuantFormat format, const void* packed, const float* x, float* y, l
 // include/quixicore_cpu/qgemv.h:166
 const char* qgemv_variant(QuantFormat format);
 
-// Fused decode projections over one x (include/quixicore_cpu/qgemv.h:143-153
+// Fused decode projections over one x (include/quixicore_cpu/qgemv.h:143-163
 // of the reference), one GPU launch: up/gate [n][k] each; the activation form
 // stores out = activation(gate) * up (GELU-tanh or SiLU) without storing either
 // projection; Q [query_dim][input_dim], K and V [kv_dim][input_dim].  q8_0 and
@@ -81,5 +81,15 @@ Status qgemv_up_gate_activation(QuantFormat format, const void* packed_up,
 Status qgemv_qkv(QuantFormat format, const void* packed_q, const void* packed_k,
                  const void* packed_v, const float* x, float* q, float* k_out, float* v_out,
                  long long query_dim, long long kv_dim, long long input_dim);
+// include/quixicore_cpu/qgemv.h:157-163: one decode token's Q/K/V with
+// split-half RoPE on Q and K at `position` (cosine / sine are
+// [max_position][head_dim / 2]) and K/V stored into slot `slot` of the
+// [slots][kv_heads][head_dim] caches (slot -1: Q only).
+Status qgemv_qkv_rope_kv(QuantFormat format, const void* packed_q, const void* packed_k,
+                         const void* packed_v, const float* x, const float* cosine,
+                         const float* sine, float* q, float* key_cache, float* value_cache,
+                         long long query_heads, long long kv_heads, long long head_dim,
+                         long long input_dim, long long slots, long long max_position,
+                         int position, int slot);
 
 }  // namespace quixicore_cpu

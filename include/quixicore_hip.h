@@ -127,6 +127,25 @@ int qc_hip_qgemv_qkv(int format, const void* packed_q, const void* packed_k,
                      float* v_out, long long query_dim, long long kv_dim, long long input_dim,
                      void* stream);
 
+/* One decode token's Q/K/V projections with split-half (GPT-NeoX) RoPE and
+ * direct KV-cache insertion, one launch where the shapes allow.  Q is
+ * [query_heads * head_dim][input_dim], K and V [kv_heads * head_dim]
+ * [input_dim].  For each head and d < head_dim / 2, with a = row d and
+ * b = row d + head_dim / 2 of that head's projection, c = cosine[position *
+ * head_dim / 2 + d] and s = sine[...]: out[d] = a * c - b * s and
+ * out[d + head_dim / 2] = b * c + a * s.  q receives rotated Q; the rotated K
+ * and plain V go to key_cache / value_cache rows [slot * kv_heads *
+ * head_dim, (slot + 1) * kv_heads * head_dim) (caches are [slots][kv_heads]
+ * [head_dim]); slot == -1 skips K and V.  Projections have qc_hip_qgemv's
+ * numerics.  Replaces qgemv_qkv_rope_kv (include/quixicore_cpu/qgemv.h:
+ * 157-163; kernels/quantization/qgemv_fused_ref.cpp:342-443). */
+int qc_hip_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packed_k,
+                             const void* packed_v, const float* x, const float* cosine,
+                             const float* sine, float* q, float* key_cache, float* value_cache,
+                             long long query_heads, long long kv_heads, long long head_dim,
+                             long long input_dim, long long slots, long long max_position,
+                             int position, int slot, void* stream);
+
 /* Activation-quantizing GEMV: x is quantized per 32-element block to int8
  * (scale = max|x_b| / 127, round half to even, clamp +-127), each block dot is
  * an exact integer sum, and y[r] = sum_b (float(dot) * d_w) * d_x in block

@@ -32,6 +32,10 @@ def build():
     subprocess.check_call(["make", "-s", "-C", HERE, "all"])
 
 
+_ROPE_ARGS = [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _LL, _LL, _LL,
+              ctypes.c_int, ctypes.c_int]
+
+
 def _load():
     if not os.path.exists(LIB_PATH):
         build()
@@ -58,6 +62,7 @@ def _load():
     lib.qco_quantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
     lib.qco_dequantize_int8_asymmetric.argtypes = [_P, _P, _P, _P, _LL, _LL]
     lib.qco_int8_gemm_entries.restype = None
+    lib.qco_qgemv_qkv_rope_kv.argtypes = _ROPE_ARGS
     return lib
 
 
@@ -197,6 +202,31 @@ def dequantize_int8_asymmetric(codes, scales, zps):
     return st, out
 
 
+def _rope_kv_call(fn, fmt, pq, pk, pv, x, cosine, sine, query_heads, kv_heads, head_dim,
+                  input_dim, slots, max_position, position, slot, key_cache=None,
+                  value_cache=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    cosine = np.ascontiguousarray(cosine, dtype=np.float32)
+    sine = np.ascontiguousarray(sine, dtype=np.float32)
+    q = np.zeros(max(query_heads * head_dim, 1), dtype=np.float32)
+    kv = max(slots * kv_heads * head_dim, 1)
+    kc = np.zeros(kv, np.float32) if key_cache is None else np.array(key_cache, np.float32)
+    vc = np.zeros(kv, np.float32) if value_cache is None else np.array(value_cache, np.float32)
+    st = fn(fmt, _ptr(pq), _ptr(pk), _ptr(pv), _ptr(x), _ptr(cosine), _ptr(sine), _ptr(q),
+            _ptr(kc), _ptr(vc), query_heads, kv_heads, head_dim, input_dim, slots, max_position,
+            position, slot)
+    return st, q, kc, vc
+
+
+def qkv_rope_kv(fmt, pq, pk, pv, x, cosine, sine, query_heads, kv_heads, head_dim, input_dim,
+                slots, max_position, position, slot, key_cache=None, value_cache=None):
+    """qgemv_qkv_rope_kv in the reference's x86 row orders.  Returns
+    (status, q, key_cache, value_cache); the caches start as given (zeros)."""
+    return _rope_kv_call(lib.qco_qgemv_qkv_rope_kv, fmt, pq, pk, pv, x, cosine, sine,
+                         query_heads, kv_heads, head_dim, input_dim, slots, max_position,
+                         position, slot, key_cache, value_cache)
+
+
 def gemv_w8a8(fmt, packed, x, n, k):
     """qgemv_w8a8: per-32-block int8 activations, integer block dots,
     y = sum_b (float(dot) * d_w) * d_x in block order.  Returns (status, y)."""
@@ -276,6 +306,7 @@ class Reference:
         L.qcref_prepare_gguf.argtypes = [ctypes.c_int, _P, _LL, _LL, ctypes.c_int, _P, _LL, _P]
         L.qcref_prepare_smoothquant.argtypes = [_P, _P, _LL, _LL, _P, _LL, _P, ctypes.c_int, _P,
                                                 _LL, _P]
+        L.qcref_qgemv_qkv_rope_kv.argtypes = _ROPE_ARGS
         L.qcref_prepare_canonical_int8.argtypes = [
             ctypes.c_int, _LL, _LL, _LL, ctypes.c_int, _P, _P, _LL, _P, _P, _LL, _P, _P,
             ctypes.c_int, _P, _LL, _P]
@@ -283,6 +314,13 @@ class Reference:
     @staticmethod
     def available(path=REF_PATH):
         return os.path.exists(path)
+
+    def qkv_rope_kv(self, fmt, pq, pk, pv, x, cosine, sine, query_heads, kv_heads, head_dim,
+                    input_dim, slots, max_position, position, slot, key_cache=None,
+                    value_cache=None):
+        return _rope_kv_call(self.lib.qcref_qgemv_qkv_rope_kv, fmt, pq, pk, pv, x, cosine, sine,
+                             query_heads, kv_heads, head_dim, input_dim, slots, max_position,
+                             position, slot, key_cache, value_cache)
 
     def pack(self, fmt, w):
         w = np.ascontiguousarray(w, dtype=np.float32)

@@ -280,6 +280,80 @@ void qco_q4_0_gemv_avx2order(const void* packed, const float* x, float* y, long 
   }
 }
 
+/* Fused decode seam qgemv_qkv_rope_kv: kernels/quantization/qgemv_fused_ref.cpp:
+ * 342-443, with packed_row_dot (:151-160) on the x86 build: q8_0_row_dot (:131-149,
+ * the order of qco_q8_0_gemv) and q4_0_row_dot (:57-83, the interleaved order of
+ * qco_q4_0_gemv_ref).  Validation as :348-391.  Per head and d < half, with
+ * first = row d and second = row d + half: out[d] = first * c - second * s,
+ * out[d + half] = second * c + first * s, c / s from row `position` of the
+ * [max_position][half] tables; V rows are stored as projected. */
+static int product_ok(const long long* dims, int count) {
+  long long product = 1;
+  for (int i = 0; i < count; ++i) {
+    if (dims[i] <= 0 || product > LLONG_MAX / dims[i]) return 0;
+    product *= dims[i];
+  }
+  return 1;
+}
+
+static float row_dot(int format, const uint8_t* row, const float* x, long long k) {
+  float y = 0.0f;
+  if (format == QCO_Q8_0)
+    qco_q8_0_gemv(row, x, &y, 1, k);
+  else
+    qco_q4_0_gemv_ref(row, x, &y, 1, k);
+  return y;
+}
+
+int qco_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packed_k,
+                          const void* packed_v, const float* x, const float* cosine,
+                          const float* sine, float* q, float* key_cache, float* value_cache,
+                          long long query_heads, long long kv_heads, long long head_dim,
+                          long long input_dim, long long slots, long long max_position,
+                          int position, int slot) {
+  const long long qdims[3] = {query_heads, head_dim, input_dim};
+  const long long kdims[3] = {slots, kv_heads, head_dim};
+  if (!product_ok(qdims, 3) || !product_ok(kdims, 3) || head_dim % 2 != 0 || position < 0 ||
+      position >= max_position || slot < -1 || slot >= slots)
+    return QCO_INVALID_SHAPE;
+  if (!packed_q || !packed_k || !packed_v || !x || !cosine || !sine || !q || !key_cache ||
+      !value_cache)
+    return QCO_INVALID_ARGUMENT;
+  const long long query_dim = query_heads * head_dim, kv_dim = kv_heads * head_dim;
+  size_t bytes = 0;
+  int st = qco_packed_size(format, query_dim, input_dim, &bytes);
+  if (st != QCO_OK) return st;
+  if (qco_packed_size(format, kv_dim, input_dim, &bytes) != QCO_OK) return QCO_INVALID_SHAPE;
+  const long long row_bytes = (input_dim / 32) * block_bytes_of(format);
+  const long long half = head_dim / 2;
+  const float* c = cosine + (long long)position * half;
+  const float* sn = sine + (long long)position * half;
+  const uint8_t* wq = (const uint8_t*)packed_q;
+  const uint8_t* wk = (const uint8_t*)packed_k;
+  const uint8_t* wv = (const uint8_t*)packed_v;
+  for (long long h = 0; h < query_heads; ++h)
+    for (long long d = 0; d < half; ++d) {
+      const long long r0 = h * head_dim + d, r1 = r0 + half;
+      const float first = row_dot(format, wq + r0 * row_bytes, x, input_dim);
+      const float second = row_dot(format, wq + r1 * row_bytes, x, input_dim);
+      q[r0] = first * c[d] - second * sn[d];
+      q[r1] = second * c[d] + first * sn[d];
+    }
+  if (slot < 0) return QCO_OK;
+  float* kc = key_cache + (long long)slot * kv_dim;
+  float* vc = value_cache + (long long)slot * kv_dim;
+  for (long long h = 0; h < kv_heads; ++h)
+    for (long long d = 0; d < half; ++d) {
+      const long long r0 = h * head_dim + d, r1 = r0 + half;
+      const float first = row_dot(format, wk + r0 * row_bytes, x, input_dim);
+      const float second = row_dot(format, wk + r1 * row_bytes, x, input_dim);
+      kc[r0] = first * c[d] - second * sn[d];
+      kc[r1] = second * c[d] + first * sn[d];
+    }
+  for (long long r = 0; r < kv_dim; ++r) vc[r] = row_dot(format, wv + r * row_bytes, x, input_dim);
+  return QCO_OK;
+}
+
 /* f64 contract oracle ("THE qgemv contract oracle"):
  * tests/correctness/test_qgemv.cpp:278-303 -- double accumulation over the
  * exactly dequantized weights.  Also returns ||w_hat_row||_2 for the

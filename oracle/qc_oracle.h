@@ -50,6 +50,15 @@ void qco_q4_0_gemv_ref(const void* packed, const float* x, float* y, long long n
 void qco_q4_0_gemv_avx2order(const void* packed, const float* x, float* y, long long n,
                              long long k, int fused_scale_add);
 
+/* One decode token's Q/K/V projections (the reference's x86 row orders) with
+ * split-half RoPE on Q and K and K/V stored into cache slot `slot`. */
+int qco_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packed_k,
+                          const void* packed_v, const float* x, const float* cosine,
+                          const float* sine, float* q, float* key_cache, float* value_cache,
+                          long long query_heads, long long kv_heads, long long head_dim,
+                          long long input_dim, long long slots, long long max_position,
+                          int position, int slot);
+
 /* f64 contract oracle: y64 = dequant(W) . x in double, plus ||w_hat_row||_2. */
 int qco_qgemv_f64(int format, const void* packed, const float* x, double* y64,
                   double* wnorm, long long n, long long k);

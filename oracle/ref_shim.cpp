@@ -13,6 +13,7 @@
 //   rms_norm_add_quant_int8, quantize_int8_asymmetric, dequantize_int8_asymmetric
 //               -> the public functions  (kernels/norms/norm_quant_ref.cpp:1060-1068;
 //                                          kernels/quantization/quantization_ref.cpp:190-244)
+//   qgemv_qkv_rope_kv -> the public function (kernels/quantization/qgemv_fused_ref.cpp:342-443)
 //   CpuPackedWeights::prepare (both overloads), info(), panel_data()
 //               -> src/memory/packed_weights.cpp:197-412
 #include <cstddef>
@@ -212,6 +213,18 @@ int qcref_prepare_smoothquant(const int8_t* w, const float* ws, long long rows, 
   const long long n = static_cast<long long>(i.prepared_bytes);
   std::memcpy(panel, pw.panel_data(), static_cast<size_t>(n < cap ? n : cap));
   return 0;
+}
+
+int qcref_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packed_k,
+                            const void* packed_v, const float* x, const float* cosine,
+                            const float* sine, float* q, float* key_cache, float* value_cache,
+                            long long query_heads, long long kv_heads, long long head_dim,
+                            long long input_dim, long long slots, long long max_position,
+                            int position, int slot) {
+  return static_cast<int>(qc::qgemv_qkv_rope_kv(
+      static_cast<qc::QuantFormat>(format), packed_q, packed_k, packed_v, x, cosine, sine, q,
+      key_cache, value_cache, query_heads, kv_heads, head_dim, input_dim, slots, max_position,
+      position, slot));
 }
 
 void qcref_set_num_threads(int n) { qc::set_num_threads(n); }

@@ -401,6 +401,66 @@ int qc_hip_qgemv_qkv(int format, const void* packed_q, const void* packed_k,
   return fused_gemv(format, 3, w, y, rows, -1, x, input_dim, as_stream(stream));
 }
 
+// kernels/quantization/qgemv_fused_ref.cpp:342-443 (qgemv_qkv_rope_kv):
+// products, even head_dim, position and slot ranges; nulls; the Q layout
+// (format, K) and the KV layout (shape); then the item-count overflow check.
+int qc_hip_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packed_k,
+                             const void* packed_v, const float* x, const float* cosine,
+                             const float* sine, float* q, float* key_cache, float* value_cache,
+                             long long query_heads, long long kv_heads, long long head_dim,
+                             long long input_dim, long long slots, long long max_position,
+                             int position, int slot, void* stream) {
+  if (!valid_product({query_heads, head_dim, input_dim}) ||
+      !valid_product({slots, kv_heads, head_dim}) || head_dim % 2 != 0 || position < 0 ||
+      position >= max_position || slot < -1 || slot >= slots)
+    return QC_INVALID_SHAPE;
+  if (!packed_q || !packed_k || !packed_v || !x || !cosine || !sine || !q || !key_cache ||
+      !value_cache)
+    return QC_INVALID_ARGUMENT;
+  const long long query_dim = query_heads * head_dim;
+  const long long kv_dim = kv_heads * head_dim;
+  size_t bytes = 0;
+  const int st = qc_hip_qgemv_packed_size(format, query_dim, input_dim, &bytes);
+  if (st != QC_OK) return st;
+  if (qc_hip_qgemv_packed_size(format, kv_dim, input_dim, &bytes) != QC_OK)
+    return QC_INVALID_SHAPE;
+  const long long half = head_dim / 2;
+  const long long query_pairs = query_heads * half;
+  const long long key_pairs = slot >= 0 ? kv_heads * half : 0;
+  const long long value_rows = slot >= 0 ? kv_dim : 0;
+  if (query_pairs > LLONG_MAX - key_pairs || query_pairs + key_pairs > LLONG_MAX - value_rows)
+    return QC_INVALID_SHAPE;
+  const float* rc = cosine + static_cast<long long>(position) * half;
+  const float* rs = sine + static_cast<long long>(position) * half;
+  float* kc = key_cache + (slot >= 0 ? slot * kv_dim : 0);
+  float* vc = value_cache + (slot >= 0 ? slot * kv_dim : 0);
+  const long long kv_rows = slot >= 0 ? kv_dim : 0;
+  const hipStream_t s = as_stream(stream);
+  const bool fast = (input_dim >> 5) % 2 == 0 && input_dim < (1LL << 31) &&
+                    reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(packed_q) % 4 == 0 &&
+                    reinterpret_cast<uintptr_t>(packed_k) % 4 == 0 &&
+                    reinterpret_cast<uintptr_t>(packed_v) % 4 == 0 &&
+                    query_dim + 2 * kv_rows < (1LL << 30);
+  if (fast)
+    return finish(qc::launch_qgemv_qkv_rope(format, packed_q, packed_k, packed_v, q, kc, vc,
+                                            static_cast<int>(query_dim),
+                                            static_cast<int>(kv_rows), static_cast<int>(half),
+                                            rc, rs, x, static_cast<int>(input_dim), s));
+  if (half > INT_MAX) return QC_INVALID_SHAPE;   // this library's dimension limit
+  hipError_t e = qc::launch_qgemm(format, packed_q, x, q, 1, query_dim, input_dim, s, g_tuning);
+  if (e == hipSuccess)
+    e = qc::launch_rope_pairs(q, query_heads, static_cast<int>(half), rc, rs, s);
+  if (e == hipSuccess && slot >= 0) {
+    e = qc::launch_qgemm(format, packed_k, x, kc, 1, kv_dim, input_dim, s, g_tuning);
+    if (e == hipSuccess)
+      e = qc::launch_rope_pairs(kc, kv_heads, static_cast<int>(half), rc, rs, s);
+    if (e == hipSuccess)
+      e = qc::launch_qgemm(format, packed_v, x, vc, 1, kv_dim, input_dim, s, g_tuning);
+  }
+  return finish(e);
+}
+
 // src/dispatch/qgemv_w8a8.cpp:108-125 (qgemv_w8a8_packed_size).
 int qc_hip_qgemv_w8a8_packed_size(int format, long long n, long long k, long long* bytes) {
   size_t size = 0;

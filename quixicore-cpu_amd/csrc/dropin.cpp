@@ -247,6 +247,52 @@ Status qgemv_qkv(QuantFormat format, const void* packed_q, const void* packed_k,
                                    input_dim, g.stream()));
 }
 
+// Only the position's cos / sin rows and the slot's cache rows are staged;
+// the C ABI then sees one position and one slot.
+Status qgemv_qkv_rope_kv(QuantFormat format, const void* packed_q, const void* packed_k,
+                         const void* packed_v, const float* x, const float* cosine,
+                         const float* sine, float* q, float* key_cache, float* value_cache,
+                         long long query_heads, long long kv_heads, long long head_dim,
+                         long long input_dim, long long slots, long long max_position,
+                         int position, int slot) {
+  const int pre = qc_hip_qgemv_qkv_rope_kv(fmt_id(format), nullptr, nullptr, nullptr, nullptr,
+                                           nullptr, nullptr, nullptr, nullptr, nullptr,
+                                           query_heads, kv_heads, head_dim, input_dim, slots,
+                                           max_position, position, slot, nullptr);
+  if (pre == QC_INVALID_SHAPE) return Status::kInvalidShape;
+  if (!packed_q || !packed_k || !packed_v || !x || !cosine || !sine || !q || !key_cache ||
+      !value_cache)
+    return Status::kInvalidArgument;
+  const long long query_dim = query_heads * head_dim;
+  const long long kv_dim = kv_heads * head_dim;
+  const long long half = head_dim / 2;
+  const size_t qb = packed_or_zero(format, query_dim, input_dim);
+  const size_t kb = packed_or_zero(format, kv_dim, input_dim);
+  if (qb == 0 || kb == 0)
+    return static_cast<Status>(qc_hip_qgemv_qkv_rope_kv(
+        fmt_id(format), packed_q, packed_k, packed_v, x, cosine, sine, q, key_cache,
+        value_cache, query_heads, kv_heads, head_dim, input_dim, slots, max_position, position,
+        slot, nullptr));
+  Staging g(nullptr);
+  const void* pq = g.in(packed_q, qb);
+  const void* pk = slot >= 0 ? g.in(packed_k, kb) : packed_k;
+  const void* pv = slot >= 0 ? g.in(packed_v, kb) : packed_v;
+  const float* xd = static_cast<const float*>(g.in(x, sizeof(float) * input_dim));
+  const float* cd = static_cast<const float*>(g.in(cosine + position * half, sizeof(float) * half));
+  const float* sd = static_cast<const float*>(g.in(sine + position * half, sizeof(float) * half));
+  float* qd = static_cast<float*>(g.out(q, sizeof(float) * query_dim));
+  float* kd = key_cache;
+  float* vd = value_cache;
+  if (slot >= 0) {
+    kd = static_cast<float*>(g.out(key_cache + slot * kv_dim, sizeof(float) * kv_dim));
+    vd = static_cast<float*>(g.out(value_cache + slot * kv_dim, sizeof(float) * kv_dim));
+  }
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(qc_hip_qgemv_qkv_rope_kv(fmt_id(format), pq, pk, pv, xd, cd, sd, qd, kd, vd,
+                                           query_heads, kv_heads, head_dim, input_dim, 1, 1, 0,
+                                           slot >= 0 ? 0 : -1, g.stream()));
+}
+
 Status qgemv_w8a8(QuantFormat format, const void* packed_weights, const float* x, float* y,
                   long long n, long long k) {
   const size_t bytes = packed_or_zero(format, n, k);

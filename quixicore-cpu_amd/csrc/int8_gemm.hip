@@ -716,7 +716,7 @@ hipError_t launch_int8_gemm(const int8_t* W, const int8_t* X, const float* ws, c
       // bytes moved per MFMA through a CU's global->LDS path bound this
       // kernel, and a 256 x 256 tile moves 2/3 of what 128 x 256 does.
       auto tiles = [&](long long tn, long long tm) { return ((n + tn - 1) / tn) * ((m + tm - 1) / tm); };
-      const long long cus = 256;
+      const long long cus = device_cu_count();
       if (wide && tiles(256, 256) >= cus * 3 / 4)
         return launch_ring<256, 256, 2, 4, 2>(W, X, ws, as, row_sum, zp, y, acc_out, m, n, k,
                                               asymmetric, status, s);

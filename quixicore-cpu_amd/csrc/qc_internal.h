@@ -9,6 +9,9 @@
 
 namespace qc {
 
+// Compute units of the current device (the grid planners size by it).
+int device_cu_count();
+
 struct GemvTuning {
   int rows_per_wave = 0;  // GEMV rows per wavefront (1, 2, 4, 7, 8, 14; 0 = from the shape)
   int qgemm_waves = 0;    // small-batch GEMM waves per workgroup (4, 8; 0 = from the shape)
@@ -32,6 +35,19 @@ hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, in
 // (act 0: SiLU, 1: GELU-tanh).  Same numerics as launch_qgemm with m = 1.
 hipError_t launch_qgemv_multi(int fmt, int nseg, const void* const* W, float* const* y,
                               const int* rows, int act, const float* x, int k, hipStream_t s);
+
+// Single-token Q/K/V projections with split-half RoPE on Q and K, one launch
+// (same layout conditions as launch_qgemv_multi): q_rows = query_heads *
+// 2 * half rows of Wq into q; kv_rows (0: Q only) rows of Wk / Wv into kc /
+// vc.  rc / rs: the position's cos / sin rows (half values).
+hipError_t launch_qgemv_qkv_rope(int fmt, const void* Wq, const void* Wk, const void* Wv,
+                                 float* q, float* kc, float* vc, int q_rows, int kv_rows,
+                                 int half, const float* rc, const float* rs, const float* x,
+                                 int k, hipStream_t s);
+
+// Rotates the (d, d + half) pairs of `heads` heads of 2 * half values in place.
+hipError_t launch_rope_pairs(float* out, long long heads, int half, const float* rc,
+                             const float* rs, hipStream_t s);
 
 // out[i] = activation(out[i]) * up[i] over n elements (act 0: SiLU, 1: GELU-tanh).
 hipError_t launch_fused_activation(float* out, const float* up, long long n, int act,

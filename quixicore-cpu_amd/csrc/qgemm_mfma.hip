@@ -691,14 +691,6 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
   }
 }
 
-int device_cus() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus <= 0)
-    cus = 256;
-  return cus;
-}
 
 // Scratch (activation fragments, q4 bias, partial sums, row exponents) of
 // one qgemm call.  Region 0 holds one pass's fragments and partial sums,
@@ -854,7 +846,7 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
-  Plan plan = plan_for<FMT>(n, nstages, device_cus(), scratch.max_ks);
+  Plan plan = plan_for<FMT>(n, nstages, device_cu_count(), scratch.max_ks);
   if (waves) plan.nw = waves;                      // test / tuning overrides
   if (stages) {
     plan.nst = stages;
@@ -1189,7 +1181,7 @@ hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, i
   if (static_cast<long long>(kPBN) * nb * (PairLayout<FMT>::bytes / 2) >= (1LL << 32) ||
       static_cast<long long>(PS::mt) * nb * kFragBytes >= (1LL << 32))
     return hipErrorInvalidValue;
-  int ks = panel_split(m, n, k, device_cus(), PS::bm);
+  int ks = panel_split(m, n, k, device_cu_count(), PS::bm);
   if (split == 1 || split == 2) ks = split;
   if (npairs < 2) ks = 1;
   const int per = (npairs + ks - 1) / ks;
@@ -1220,7 +1212,7 @@ hipError_t qgemm_mfma_with(int fmt, const void* W, const float* x, float* y, int
   const auto* w = static_cast<const uint8_t*>(W);
   // panel: 0 = from the shape (for m >= 64), -1 = never, 1 / 2 = always
   // (for m >= 2) with one / two K ranges
-  const bool use_panel = panel > 0 || (panel == 0 && m >= 64 && panel_pays(m, n, k, device_cus()));
+  const bool use_panel = panel > 0 || (panel == 0 && m >= 64 && panel_pays(m, n, k, device_cu_count()));
   // The bf16 layouts (the panel and passes of more than 8 rows) scale each
   // row by its power of two; their prep kernels store the exponents here.
   int* rexp = nullptr;

@@ -302,4 +302,15 @@ hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long l
                       : launch_fmt<kQ4_0>(w, x, y, (int)m, (int)n, (int)k, s, t, noalloc);
 }
 
+// Compute units of the current device (256 on a full MI355X; fewer under a
+// compute partition).  The tile and split planners size their grids by it.
+int device_cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  return cus;
+}
+
 }  // namespace qc

@@ -268,13 +268,31 @@ __device__ __forceinline__ void load_pair(uint32_t* d, const uint8_t* p) {
 // interleaved, stored as out[i] = activation(gate[i]) * up[i] (act 0: SiLU,
 // 1: GELU-tanh; kernels/quantization/qgemv_fused_ref.cpp:184-192).  The same
 // x is shared by every row.
+//
+// RoPE (half > 0, kernels/quantization/qgemv_fused_ref.cpp:342-443): in the
+// first nrope segments, logical rows 2j and 2j + 1 are rows d and d + half of
+// head h (j = h * half + d) of that matrix, and the pair is stored rotated:
+// out[d] = a * cos[d] - b * sin[d], out[d + half] = b * cos[d] + a * sin[d]
+// for the head's rows a = row d, b = row d + half (rc / rs: the position's
+// cos / sin rows, half values each).
 struct GemvSegs {
   const uint8_t* w[3];
   float* y[3];
   int start[4];    // start[nseg] = total logical rows
   int nseg;
   int act;         // -1: plain segments
+  int half;        // > 0: RoPE pairs in segments [0, nrope); head_dim = 2 * half
+  int nrope;
+  const float* rc;
+  const float* rs;
 };
+
+// Weight row of logical row `local` of a RoPE segment.
+__device__ __forceinline__ int rope_row(int local, int half) {
+  const int j = local >> 1;
+  const int head = j / half;
+  return head * 2 * half + (j - head * half) + (local & 1) * half;
+}
 
 __device__ __forceinline__ float fused_activation(float v, int act) {
   constexpr float kSqrt2OverPi = 0.7978845608028654f;
@@ -324,6 +342,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
     const uint8_t* const w1 = segs.w[1];
     const uint8_t* const w2 = segs.w[2];
     const int s1 = segs.start[1], s2 = segs.start[2], nseg = segs.nseg, act = segs.act;
+    const int half = segs.half, nrope = segs.nrope;
     total = nseg == 1 ? s1 : nseg == 2 ? s2 : segs.start[3];
     const bool three = nseg > 2;
 #pragma unroll
@@ -331,7 +350,8 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
       const int g = min(row0 + r, total - 1);
       const bool in2 = three && g >= s2, in1 = g >= s1;
       const uint8_t* const base = act >= 0 ? ((g & 1) ? w1 : w0) : in2 ? w2 : in1 ? w1 : w0;
-      const int local = act >= 0 ? g >> 1 : g - (in2 ? s2 : in1 ? s1 : 0);
+      int local = act >= 0 ? g >> 1 : g - (in2 ? s2 : in1 ? s1 : 0);
+      if (half > 0 && (in2 ? 2 : in1 ? 1 : 0) < nrope) local = rope_row(local, half);
       wrow[r] = base + static_cast<long long>(local) * row_bytes;
     }
   }
@@ -393,6 +413,33 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
 #pragma unroll
       for (int r = 0; r + 1 < RB; r += 2)
         if (row0 + r < total) y0[(row0 + r) >> 1] = fused_activation(t[r + 1], act) * t[r];
+      return;
+    }
+    const int half = segs.half;
+    if (half > 0) {
+      // RB, row0 and every segment start are even: rows (2j, 2j+1) are one
+      // (d, d + half) pair of a RoPE segment, or two rows of a plain one
+      const int nrope = segs.nrope;
+#pragma unroll
+      for (int r = 0; r + 1 < RB; r += 2) {
+        const int g = row0 + r;
+        if (g >= total) continue;
+        const bool in2 = three && g >= s2, in1 = g >= s1;
+        float* const out = in2 ? y2 : in1 ? y1 : y0;
+        const int local = g - (in2 ? s2 : in1 ? s1 : 0);
+        if ((in2 ? 2 : in1 ? 1 : 0) < nrope) {
+          const int j = local >> 1;
+          const int head = j / half;
+          const int d = j - head * half;
+          const float c = segs.rc[d], sn = segs.rs[d];
+          const float a = t[r], b = t[r + 1];
+          out[head * 2 * half + d] = a * c - b * sn;
+          out[head * 2 * half + d + half] = b * c + a * sn;
+        } else {
+          out[local] = t[r];
+          out[local + 1] = t[r + 1];
+        }
+      }
       return;
     }
 #pragma unroll
@@ -694,16 +741,6 @@ hipError_t launch_one(const GemvSegs& sg, const float* x, int k, int* status, hi
   return hipGetLastError();
 }
 
-int cu_count() {
-  static int count = [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    return n;
-  }();
-  return count;
-}
 
 struct Shape {
   int nw, rb;
@@ -718,7 +755,7 @@ struct Shape {
 // one's digit build with the other's loads), then to the earlier candidate.
 // `forced_rb` (non-zero) restricts the choice to that many rows per wave.
 Shape pick_shape(int n, const int* cand, int ncand, int forced_rb) {
-  const int cus = cu_count();
+  const int cus = device_cu_count();
   Shape best{8, forced_rb ? forced_rb : cand[0]};
   for (int pass = 0; pass < 2; ++pass) {
     long long best_score = -1;
@@ -778,15 +815,15 @@ hipError_t launch_rb(int rb, const GemvSegs& sg, const float* x, int k, int* sta
   }
 }
 
-// Candidates of rows per wave: with an activation epilogue only even counts
-// (each wave holds whole (up, gate) row pairs).
+// Candidates of rows per wave: with an activation or RoPE epilogue only even
+// counts (each wave holds whole (up, gate) or (d, d + half) row pairs).
 template <int KIND, int FMT, int NPM>
 hipError_t launch_npm(const int* cand_all, int ncand_all, const GemvSegs& sg, const float* x,
                       int k, int rb, int* status, hipStream_t s) {
   int cand[8];
   int ncand = 0;
   for (int i = 0; i < ncand_all; ++i)
-    if (sg.act < 0 || cand_all[i] % 2 == 0) cand[ncand++] = cand_all[i];
+    if ((sg.act < 0 && sg.half == 0) || cand_all[i] % 2 == 0) cand[ncand++] = cand_all[i];
   bool listed = false;
   for (int i = 0; i < ncand; ++i) listed = listed || cand[i] == rb;
   const Shape sh = pick_shape(sg.start[sg.nseg], cand, ncand, listed ? rb : 0);
@@ -857,6 +894,62 @@ hipError_t launch_qgemv_multi(int fmt, int nseg, const void* const* W, float* co
   }
   return fmt == kQ8_0 ? launch_fmt<2, kQ8_0>(sg, x, k, 0, nullptr, s)
                       : launch_fmt<2, kQ4_0>(sg, x, k, 0, nullptr, s);
+}
+
+// Q (and, kv_rows > 0, K and V) projections of one token with RoPE on Q and
+// K, in one launch (K % 64 == 0, every W 4-byte aligned, x 16-byte aligned,
+// checked by the caller).  q: q_rows outputs; kc / vc: the slot's kv_rows
+// outputs in the key / value cache.
+hipError_t launch_qgemv_qkv_rope(int fmt, const void* Wq, const void* Wk, const void* Wv,
+                                 float* q, float* kc, float* vc, int q_rows, int kv_rows,
+                                 int half, const float* rc, const float* rs, const float* x,
+                                 int k, hipStream_t s) {
+  GemvSegs sg{};
+  sg.act = -1;
+  sg.half = half;
+  sg.rc = rc;
+  sg.rs = rs;
+  sg.w[0] = static_cast<const uint8_t*>(Wq);
+  sg.y[0] = q;
+  sg.start[0] = 0;
+  sg.start[1] = q_rows;
+  sg.nseg = 1;
+  sg.nrope = 1;
+  if (kv_rows > 0) {
+    sg.w[1] = static_cast<const uint8_t*>(Wk);
+    sg.w[2] = static_cast<const uint8_t*>(Wv);
+    sg.y[1] = kc;
+    sg.y[2] = vc;
+    sg.start[2] = q_rows + kv_rows;
+    sg.start[3] = q_rows + 2 * kv_rows;
+    sg.nseg = 3;
+    sg.nrope = 2;
+  }
+  return fmt == kQ8_0 ? launch_fmt<2, kQ8_0>(sg, x, k, 0, nullptr, s)
+                      : launch_fmt<2, kQ4_0>(sg, x, k, 0, nullptr, s);
+}
+
+// out[h * 2 * half + d] and out[h * 2 * half + d + half] rotated in place for
+// every head h < heads and d < half (the per-matrix route of the RoPE seam).
+__global__ void rope_pairs_kernel(float* out, long long pairs, int half,
+                                  const float* __restrict__ rc, const float* __restrict__ rs) {
+  const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= pairs) return;
+  const long long head = i / half;
+  const int d = static_cast<int>(i - head * half);
+  float* const p = out + head * 2 * half + d;
+  const float a = p[0], b = p[half], c = rc[d], sn = rs[d];
+  p[0] = a * c - b * sn;
+  p[half] = b * c + a * sn;
+}
+
+hipError_t launch_rope_pairs(float* out, long long heads, int half, const float* rc,
+                             const float* rs, hipStream_t s) {
+  const long long pairs = heads * half;
+  if (pairs <= 0) return hipSuccess;
+  rope_pairs_kernel<<<static_cast<unsigned>((pairs + 255) / 256), 256, 0, s>>>(out, pairs, half,
+                                                                               rc, rs);
+  return hipGetLastError();
 }
 
 // qgemv_w8a8: the fast kernel when K/32 is even, W is 4-byte aligned and the

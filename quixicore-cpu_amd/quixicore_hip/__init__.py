@@ -43,6 +43,8 @@ _SIGS = {
     "qc_hip_qgemv_up_gate": ([_I, _P, _P, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_qgemv_up_gate_activation": ([_I, _P, _P, _P, _P, _LL, _LL, _I, _P], _I),
     "qc_hip_qgemv_qkv": ([_I, _P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _P], _I),
+    "qc_hip_qgemv_qkv_rope_kv": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _LL,
+                                  _LL, _LL, _I, _I, _P], _I),
     "qc_hip_qgemv_w8a8_packed_size": ([_I, _LL, _LL, _P], _I),
     "qc_hip_qgemv_w8a8_variant": ([_I], ctypes.c_char_p),
     "qc_hip_quantize_int8": ([_P, _P, _P, _LL, _LL, _LL, _P, _P], _I),
@@ -122,6 +124,15 @@ def qgemv_up_gate_activation_raw(fmt, p_up, p_gate, x, out, n, k, gelu_tanh=True
 def qgemv_qkv_raw(fmt, pq, pk, pv, x, q, k_out, v_out, query_dim, kv_dim, input_dim, stream=None):
     return lib.qc_hip_qgemv_qkv(fmt, _ptr(pq), _ptr(pk), _ptr(pv), _ptr(x), _ptr(q), _ptr(k_out),
                                 _ptr(v_out), query_dim, kv_dim, input_dim, _stream(stream))
+
+
+def qgemv_qkv_rope_kv_raw(fmt, pq, pk, pv, x, cosine, sine, q, key_cache, value_cache,
+                         query_heads, kv_heads, head_dim, input_dim, slots, max_position,
+                         position, slot, stream=None):
+    return lib.qc_hip_qgemv_qkv_rope_kv(fmt, _ptr(pq), _ptr(pk), _ptr(pv), _ptr(x), _ptr(cosine),
+                                        _ptr(sine), _ptr(q), _ptr(key_cache), _ptr(value_cache),
+                                        query_heads, kv_heads, head_dim, input_dim, slots,
+                                        max_position, position, slot, _stream(stream))
 
 
 def qgemm_raw(fmt, packed, x, y, m, n, k, stream=None):

@@ -112,6 +112,29 @@ int main(int argc, char** argv) {
     out.put(p + "qkv_q", q, "f32");
     out.put(p + "qkv_k", kk, "f32");
     out.put(p + "qkv_v", vv, "f32");
+    // RoPE seam: 6 query heads and 3 kv heads of 16, cache slot 1 of 3 at position 2
+    {
+      const long long hd = 16, slots = 3, max_pos = 4;
+      std::vector<float> cs = values(61 + f, max_pos * hd / 2, 1.0f);
+      std::vector<float> sn = values(71 + f, max_pos * hd / 2, 1.0f);
+      std::vector<float> rq(n), kc = values(81, slots * n / 2, 9.0f), vc = values(82, slots * n / 2, 9.0f);
+      out.put(p + "rope_cos", cs, "f32");
+      out.put(p + "rope_sin", sn, "f32");
+      out.put(p + "rope_kc0", kc, "f32");
+      out.put(p + "rope_vc0", vc, "f32");
+      out.status(p + "qkv_rope", qc::qgemv_qkv_rope_kv(fmt, pw.data(), pw2.data(),
+                                                        pw2.data() + bytes / 2, x.data(), cs.data(),
+                                                        sn.data(), rq.data(), kc.data(), vc.data(),
+                                                        n / hd, n / 2 / hd, hd, k, slots, max_pos,
+                                                        2, 1));
+      out.put(p + "rope_q", rq, "f32");
+      out.put(p + "rope_kc", kc, "f32");
+      out.put(p + "rope_vc", vc, "f32");
+      out.status(p + "qkv_rope_badpos", qc::qgemv_qkv_rope_kv(
+                                            fmt, pw.data(), pw2.data(), pw2.data(), x.data(),
+                                            cs.data(), sn.data(), rq.data(), kc.data(), vc.data(),
+                                            n / hd, n / 2 / hd, hd, k, slots, max_pos, 4, 1));
+    }
     out.status(p + "w8a8", qc::qgemv_w8a8(fmt, pw.data(), x.data(), y.data(), n, k));
     out.put(p + "w8a8_y", y, "f32");
 

@@ -89,6 +89,21 @@ def test_dropin_quantized_matmuls(run, oracle, fmt, p):
     _contract(oracle, fmt, packed, x[0], a[p + "qkv_q"], n, k)
     _contract(oracle, fmt, packed2[: row * (n // 2)], x[0], a[p + "qkv_k"], n // 2, k)
     _contract(oracle, fmt, packed2[row * (n // 2):], x[0], a[p + "qkv_v"], n // 2, k)
+    # RoPE seam: the rotation of the plain projections, in f32; other slots kept
+    assert st[p + "qkv_rope"] == 0 and st[p + "qkv_rope_badpos"] == 1
+    hd, half, kvd = 16, 8, n // 2
+    c, s_ = a[p + "rope_cos"][2 * half:3 * half], a[p + "rope_sin"][2 * half:3 * half]
+
+    def rot(y, heads):
+        v = y.reshape(heads, 2, half)
+        return np.stack([v[:, 0] * c - v[:, 1] * s_, v[:, 1] * c + v[:, 0] * s_], 1).reshape(-1)
+
+    assert _bits_equal(a[p + "rope_q"], rot(a[p + "qkv_q"], n // hd))
+    kc, vc, kc0, vc0 = a[p + "rope_kc"], a[p + "rope_vc"], a[p + "rope_kc0"], a[p + "rope_vc0"]
+    assert _bits_equal(kc[kvd:2 * kvd], rot(a[p + "qkv_k"], kvd // hd))
+    assert _bits_equal(vc[kvd:2 * kvd], a[p + "qkv_v"])
+    for sl in (slice(0, kvd), slice(2 * kvd, 3 * kvd)):
+        assert _bits_equal(kc[sl], kc0[sl]) and _bits_equal(vc[sl], vc0[sl])
     st_w8, y_w8 = oracle.gemv_w8a8(fmt, packed, x[0], n, k)
     assert st_w8 == 0 and _bits_equal(a[p + "w8a8_y"], y_w8)
 

@@ -1,10 +1,14 @@
 """GPU parity: fused decode projections (qgemv_up_gate, qgemv_up_gate_activation,
-qgemv_qkv; kernels/quantization/qgemv_fused_ref.cpp:184-327) through the C ABI.
+qgemv_qkv, qgemv_qkv_rope_kv; kernels/quantization/qgemv_fused_ref.cpp:184-443)
+through the C ABI.
 
 Each projection of the fused launch uses the GEMV's per-row arithmetic, so it
 is bit-identical to qc_hip_qgemv of that matrix (itself held to the 1e-4
 contract against the f64 oracle in test_gpu_gemv.py), and also checked against
-the f64 oracle here.  The activation form is checked against
+the f64 oracle here.  The RoPE seam's outputs are bit-identical to the
+reference's rotation (out[d] = a*c - b*s, out[d+half] = b*c + a*s, each
+operation rounded in f32) applied to those projections, with every other
+cache slot left as it was.  The activation form is checked against
 activation(gate) * up evaluated in f64 from the plain fused projections.
 """
 import numpy as np
@@ -118,3 +122,71 @@ def test_qkv(qc, oracle, synth, dev, fmt, qd, kvd, k, x_off):
         y = y.cpu().numpy()
         assert np.array_equal(_bits(y), _bits(qc.qgemv(fmt, P, X, n, k).cpu().numpy()))
         _check_contract(oracle, fmt, p, x, y, n, k)
+
+
+def _rope_f32(y, heads, hd, c, sn):
+    """The reference's rotation in f32 (qgemv_fused_ref.cpp:398-433)."""
+    v = y.reshape(heads, 2, hd // 2)
+    a, b = v[:, 0], v[:, 1]
+    return np.stack([a * c - b * sn, b * c + a * sn], axis=1).reshape(-1).astype(np.float32)
+
+
+# (fmt, query heads, kv heads, head_dim, K, slots, position, slot, x offset, w offset)
+@pytest.mark.parametrize("fmt,qh,kvh,hd,k,slots,pos,slot,x_off,w_off", [
+    (1, 32, 8, 128, 4096, 4, 17, 2, 0, 0),    # config 4's attention shape (one launch)
+    (0, 32, 8, 128, 4096, 2, 5, 0, 0, 0),
+    (1, 8, 2, 64, 4096, 3, 3, -1, 0, 0),      # slot -1: Q only
+    (0, 4, 4, 6, 512, 2, 0, 1, 0, 0),         # half = 3
+    (1, 2, 1, 6, 96, 3, 1, 2, 0, 0),          # odd K/32: per-matrix route
+    (0, 8, 2, 64, 512, 2, 2, 1, 1, 0),        # misaligned x: per-matrix route
+    (1, 4, 2, 32, 256, 2, 2, 0, 0, 2),        # misaligned W: per-matrix route
+])
+def test_qkv_rope_kv(qc, oracle, synth, dev, fmt, qh, kvh, hd, k, slots, pos, slot, x_off, w_off):
+    import torch
+    print(f"qkv_rope_kv fmt={fmt} heads={qh}/{kvh} hd={hd} k={k} slot={slot} x_off={x_off} "
+          f"w_off={w_off}", flush=True)
+    qd, kvd, half = qh * hd, kvh * hd, hd // 2
+    pq = _packed(oracle, synth, fmt, qd, k, 80)
+    pk = _packed(oracle, synth, fmt, kvd, k, 81)
+    pv = _packed(oracle, synth, fmt, kvd, k, 82)
+    x = synth.normal_fast(83 + k, k)
+    max_pos = pos + 3
+    ang = synth.normal_fast(84, max_pos * half).reshape(max_pos, half) * np.float32(3.0)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    PQ, PK, PV = _dev(pq, dev, w_off), _dev(pk, dev, w_off), _dev(pv, dev, w_off)
+    X, C, S = _dev(x, dev, x_off), _dev(cos.reshape(-1), dev), _dev(sin.reshape(-1), dev)
+    fill = np.arange(slots * kvd, dtype=np.float32) + np.float32(0.5)
+    KC, VC = _dev(fill, dev), _dev(-fill, dev)
+    q = torch.full((qd,), 7.0, dtype=torch.float32, device=dev)
+    assert qc.qgemv_qkv_rope_kv_raw(fmt, PQ, PK, PV, X, C, S, q, KC, VC, qh, kvh, hd, k, slots,
+                                    max_pos, pos, slot) == 0
+    plain = [qc.qgemv(fmt, P, X, n, k).cpu().numpy() for P, n in ((PQ, qd), (PK, kvd), (PV, kvd))]
+    for p, y, n in zip((pq, pk, pv), plain, (qd, kvd, kvd)):
+        _check_contract(oracle, fmt, p, x, y, n, k)
+    c, sn = cos[pos], sin[pos]
+    assert np.array_equal(_bits(q.cpu().numpy()), _bits(_rope_f32(plain[0], qh, hd, c, sn)))
+    kc, vc = KC.cpu().numpy(), VC.cpu().numpy()
+    keep = np.ones(slots * kvd, bool)
+    if slot >= 0:
+        sl = slice(slot * kvd, (slot + 1) * kvd)
+        keep[sl] = False
+        assert np.array_equal(_bits(kc[sl]), _bits(_rope_f32(plain[1], kvh, hd, c, sn)))
+        assert np.array_equal(_bits(vc[sl]), _bits(plain[2]))
+    assert np.array_equal(kc[keep], fill[keep]) and np.array_equal(vc[keep], -fill[keep])
+
+
+def test_qkv_rope_kv_validation(qc, oracle, synth, dev):
+    import torch
+    pq = _dev(_packed(oracle, synth, 0, 8, 64, 90), dev)
+    x, cs = _dev(synth.normal_fast(91, 64), dev), _dev(np.ones(8, np.float32), dev)
+    q = torch.zeros(8, dtype=torch.float32, device=dev)
+    kc = torch.zeros(16, dtype=torch.float32, device=dev)
+    call = lambda fmt=0, hd=4, pos=1, slot=0, ptr=pq, k=64, maxp=4: qc.qgemv_qkv_rope_kv_raw(
+        fmt, ptr, pq, pq, x, cs, cs, q, kc, kc, 2, 1, hd, k, 2, maxp, pos, slot)
+    assert call(hd=3) == 1 and call(pos=4) == 1 and call(pos=-1) == 1 and call(slot=2) == 1
+    assert call(slot=-2) == 1 and call(k=48) == 1
+    assert call(ptr=None) == 3
+    assert call(fmt=5) == 2
+    torch.cuda.synchronize()
+    assert np.all(q.cpu().numpy() == 0) and np.all(kc.cpu().numpy() == 0)
+    assert call() == 0

@@ -36,6 +36,15 @@ mistake would break:
                         hand; residual_out = x + residual exactly; per group
                         max |code| = 127 and codes within half a step of the
                         float64 normalized values.
+  * qgemv_qkv_rope_kv -- bit-identical to the reference's function (oracle/_ref)
+                        on random q8_0/q4_0 shapes, positions and slots
+                        (slot -1 included) with the caches' other slots left
+                        as they were, and on every validation case; the
+                        reference test's known answer (test_remaining_ops.cpp:
+                        217-257: a 90-degree rotation gives (-q1, q0) exactly);
+                        at a zero angle the outputs are the plain row orders'
+                        GEMV outputs bit for bit; each rotated pair keeps its
+                        f64 norm.
   * quantize_int8_asymmetric / dequantize -- bit-identical to the reference's
                         functions on random rows and on the out-of-range
                         conversions (1-ulp spreads); the reference test's
@@ -518,3 +527,96 @@ def test_quantize_int8_asymmetric_round_trip(oracle):
     assert st == st2 == 0
     assert np.all(np.abs(d - x) <= s[:, None] * 0.5001)
     assert np.all(c.min(axis=1) == -128) and np.all(c.max(axis=1) >= 126)
+
+
+# ------------------------------------------------------- qgemv_qkv_rope_kv ---
+
+def _rope_inputs(oracle, fmt, qh, kvh, hd, k, max_pos, seed):
+    rng = np.random.default_rng(seed)
+    packs = []
+    for rows in (qh * hd, kvh * hd, kvh * hd):
+        st, p = oracle.pack(fmt, (0.02 * rng.standard_normal((rows, k))).astype(np.float32))
+        assert st == 0
+        packs.append(p)
+    x = rng.standard_normal(k).astype(np.float32)
+    ang = rng.uniform(-np.pi, np.pi, (max_pos, hd // 2))
+    return packs, x, np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def test_qkv_rope_kv_matches_reference(oracle, ref):
+    for case, (fmt, qh, kvh, hd, k, slots, pos, slot) in enumerate(
+            [(0, 4, 2, 8, 64, 3, 5, 1), (1, 4, 2, 8, 64, 3, 0, 2), (1, 8, 2, 64, 512, 2, 7, -1),
+             (0, 2, 1, 6, 96, 4, 3, 0), (1, 3, 3, 2, 32, 1, 1, 0)]):
+        packs, x, c, sn = _rope_inputs(oracle, fmt, qh, kvh, hd, k, 8, 300 + case)
+        kc0 = np.arange(slots * kvh * hd, dtype=np.float32)     # other slots must survive
+        args = (fmt, *packs, x, c, sn, qh, kvh, hd, k, slots, 8, pos, slot)
+        got = oracle.qkv_rope_kv(*args, key_cache=kc0, value_cache=-kc0)
+        want = ref.qkv_rope_kv(*args, key_cache=kc0, value_cache=-kc0)
+        assert got[0] == want[0] == 0
+        for g, w in zip(got[1:], want[1:]):
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), case
+        kvd = kvh * hd
+        keep = np.ones(slots * kvd, bool)
+        if slot >= 0:
+            keep[slot * kvd:(slot + 1) * kvd] = False
+        assert np.array_equal(got[2][keep], kc0[keep]) and np.array_equal(got[3][keep], -kc0[keep])
+
+
+def test_qkv_rope_kv_validation_matches_reference(oracle, ref):
+    packs, x, c, sn = _rope_inputs(oracle, 0, 2, 1, 4, 64, 4, 9)
+    good = dict(query_heads=2, kv_heads=1, head_dim=4, input_dim=64, slots=2, max_position=4,
+                position=1, slot=0)
+    cases = [dict(head_dim=3), dict(position=4), dict(position=-1), dict(slot=2), dict(slot=-2),
+             dict(query_heads=0), dict(slots=0), dict(input_dim=48), dict(input_dim=40),
+             dict(kv_heads=-1), dict(max_position=1)]
+    # q8_0 / q4_0, and an id past the reference's QuantFormat list (the
+    # reference implements its other formats; this build reports them unsupported)
+    for fmt in (0, 1, 37):
+        for over in cases + [dict()]:
+            a = dict(good, **over)
+            args = (fmt, *packs, x, c, sn, a["query_heads"], a["kv_heads"], a["head_dim"],
+                    a["input_dim"], a["slots"], a["max_position"], a["position"], a["slot"])
+            if fmt in (0, 1) and not over:
+                continue
+            got, want = oracle.qkv_rope_kv(*args)[0], ref.qkv_rope_kv(*args)[0]
+            assert got == want, (fmt, over, got, want)
+            assert got != 0
+
+
+def test_qkv_rope_kv_reference_test_case(oracle):
+    # tests/correctness/test_remaining_ops.cpp:217-257
+    n, k = 2, 32
+    proj = np.array([(i % 5 - 2) * 0.1 for i in range(n * k)], np.float32).reshape(n, k)
+    act = np.array([(i % 7 - 3) * 0.2 for i in range(k)], np.float32)
+    st, p = oracle.pack(0, proj)
+    assert st == 0
+    qv = oracle.gemv(0, p, act, n, k)
+    cos, sin = np.array([1, 0], np.float32), np.array([0, 1], np.float32)
+    st, q, kc, vc = oracle.qkv_rope_kv(0, p, p, p, act, cos, sin, 1, 1, 2, k, 2, 2, 1, 1)
+    assert st == 0
+    assert q[0] == -qv[1] and q[1] == qv[0]
+    assert kc[2] == -qv[1] and kc[3] == qv[0] and vc[2] == qv[0] and vc[3] == qv[1]
+    assert np.all(kc[:2] == 0) and np.all(vc[:2] == 0)
+    st = oracle.qkv_rope_kv(0, p, p, p, act, cos, sin, 1, 1, 2, k, 2, 2, 2, 1)[0]
+    assert st == 1
+
+
+def test_qkv_rope_kv_properties(oracle):
+    for fmt in (0, 1):
+        qh, kvh, hd, k = 3, 2, 8, 128
+        packs, x, c, sn = _rope_inputs(oracle, fmt, qh, kvh, hd, k, 3, 40 + fmt)
+        c[1], sn[1] = 1.0, 0.0                                  # zero angle at position 1
+        st, q, kc, vc = oracle.qkv_rope_kv(fmt, *packs, x, c, sn, qh, kvh, hd, k, 1, 3, 1, 0)
+        assert st == 0
+        plain = [oracle.gemv(fmt, packs[i], x, rows, k, order="portable" if fmt else "reference")
+                 for i, rows in enumerate((qh * hd, kvh * hd, kvh * hd))]
+        assert np.array_equal(q.view(np.uint32), plain[0].view(np.uint32))
+        assert np.array_equal(kc.view(np.uint32), plain[1].view(np.uint32))
+        assert np.array_equal(vc.view(np.uint32), plain[2].view(np.uint32))
+        # a rotation keeps each (d, d + half) pair's length
+        st, q, kc, _ = oracle.qkv_rope_kv(fmt, *packs, x, c, sn, qh, kvh, hd, k, 1, 3, 2, 0)
+        for out, heads in ((q, qh), (kc, kvh)):
+            o = out.reshape(heads, 2, hd // 2).astype(np.float64)
+            p = plain[0 if out is q else 1].reshape(heads, 2, hd // 2).astype(np.float64)
+            assert np.allclose(np.hypot(o[:, 0], o[:, 1]), np.hypot(p[:, 0], p[:, 1]),
+                               rtol=1e-6, atol=1e-9)
