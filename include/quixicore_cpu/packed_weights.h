@@ -104,6 +104,7 @@ class CpuPackedWeights {
   // (nullptr when the tensor has none, or for GGUF formats).
   const float* device_scales() const noexcept;
   const std::int32_t* device_row_sums() const noexcept;
+  const float* device_zero_points() const noexcept;   // canonical zero points (f32)
 
  private:
   struct Impl;

@@ -4,6 +4,8 @@
 
 #include <cstdint>
 
+#include "quixicore_cpu/float_storage.h"
+#include "quixicore_cpu/ops.h"
 #include "quixicore_cpu/packed_weights.h"
 #include "quixicore_cpu/qgemv.h"
 #include "quixicore_cpu/workspace.h"
@@ -16,9 +18,66 @@ Status qgemm(QuantFormat format, const void* packed_weights, const float* x, flo
 // qgemm.h:26 -- prepared equivalent of qgemm, reading the device mirror.
 Status qgemm_prepacked(const CpuPackedWeights& weights, const float* x, float* y, long long m,
                        Workspace* workspace = nullptr);
-// qgemm.h:42
+// qgemm.h:42 -- the M = 1 storage projection with f32 x and y (as in the
+// reference, weights prepared from GGUF bytes return kUnsupportedFormat here;
+// qgemm_prepacked takes them).
 Status qgemv_prepacked(const CpuPackedWeights& weights, const float* x, float* y,
                        Workspace* workspace = nullptr);
+
+// Prepared storage projections (qgemm.h:32-101).  Weights prepared from a
+// CanonicalQuantTensor; GGUF-prepared weights return kUnsupportedFormat, as in
+// the reference (kernels/quantization/qgemm_canonical.cpp:4275-4291).  This
+// GPU route computes the int8 canonical layouts (kInt8Symmetric,
+// kInt8Affine; row, channel or group scales); other canonical layouts return
+// kUnsupportedFormat after the reference's validation.
+Status qgemm_prepacked_storage(const CpuPackedWeights& weights, FloatStorageInput x,
+                               FloatStorageOutput y, long long m,
+                               Workspace* workspace = nullptr);
+Status qgemm_prepacked_epilogue_storage(const CpuPackedWeights& weights, FloatStorageInput x,
+                                        const float* bias, FloatStorageOutput y, long long m,
+                                        LinearActivation activation,
+                                        Workspace* workspace = nullptr);
+Status qgemv_prepacked_storage(const CpuPackedWeights& weights, FloatStorageInput x,
+                               FloatStorageOutput y, Workspace* workspace = nullptr);
+Status qgemm_prepacked_gate_up_storage(const CpuPackedWeights& gate_weights,
+                                       const CpuPackedWeights& up_weights, FloatStorageInput x,
+                                       FloatStorageOutput gate_output,
+                                       FloatStorageOutput up_output, long long m,
+                                       Workspace* workspace = nullptr);
+Status qgemv_prepacked_gate_up_storage(const CpuPackedWeights& gate_weights,
+                                       const CpuPackedWeights& up_weights, FloatStorageInput x,
+                                       FloatStorageOutput gate_output,
+                                       FloatStorageOutput up_output,
+                                       Workspace* workspace = nullptr);
+Status qgemm_prepacked_qkv_storage(const CpuPackedWeights& q_weights,
+                                   const CpuPackedWeights& k_weights,
+                                   const CpuPackedWeights& v_weights, FloatStorageInput x,
+                                   FloatStorageOutput q_output, FloatStorageOutput k_output,
+                                   FloatStorageOutput v_output, long long m,
+                                   Workspace* workspace = nullptr);
+Status qgemv_prepacked_qkv_storage(const CpuPackedWeights& q_weights,
+                                   const CpuPackedWeights& k_weights,
+                                   const CpuPackedWeights& v_weights, FloatStorageInput x,
+                                   FloatStorageOutput q_output, FloatStorageOutput k_output,
+                                   FloatStorageOutput v_output, Workspace* workspace = nullptr);
+// Q / K get split-half RoPE at `position` (cosine / sine [max_position]
+// [head_dim / 2]); K and V go to slot `slot` of [slots][kv_heads][head_dim]
+// caches (slot -1: Q only).
+Status qgemv_prepacked_qkv_rope_kv_storage(
+    const CpuPackedWeights& q_weights, const CpuPackedWeights& k_weights,
+    const CpuPackedWeights& v_weights, FloatStorageInput x, const float* cosine,
+    const float* sine, FloatStorageOutput q_output, FloatStorageOutput key_cache,
+    FloatStorageOutput value_cache, long long query_heads, long long kv_heads,
+    long long head_dim, long long slots, long long max_position, int position, int slot,
+    Workspace* workspace = nullptr);
+// output = SiLU(gate) * up; neither projection is stored.
+Status qgemm_prepacked_swiglu_storage(const CpuPackedWeights& gate_weights,
+                                      const CpuPackedWeights& up_weights, FloatStorageInput x,
+                                      FloatStorageOutput output, long long m,
+                                      Workspace* workspace = nullptr);
+Status qgemv_prepacked_swiglu_storage(const CpuPackedWeights& gate_weights,
+                                      const CpuPackedWeights& up_weights, FloatStorageInput x,
+                                      FloatStorageOutput output, Workspace* workspace = nullptr);
 
 // qgemm.h:235 -- prequantized integer GEMM, X token-major [M,K], W [N,K].
 Status int8_gemm(const std::int8_t* weights, const std::int8_t* x, const float* weight_scale,

@@ -146,6 +146,53 @@ int qc_hip_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packe
                              long long input_dim, long long slots, long long max_position,
                              int position, int slot, void* stream);
 
+/* ---- Canonical int8 projections (the prepared storage seams) ----------
+ * Weights in the reference's canonical kInt8Symmetric / kInt8Affine layout
+ * (include/quixicore_cpu/quant_contract.h): int8 codes [rows][cols]
+ * row-major, f32 scales [rows][groups] (groups = 1: one per row), and for
+ * kInt8Affine f32 zero points of the same shape.  Element (n, c) is
+ * scale * (code - zero) of group c / (cols / groups)
+ * (kernels/quantization/qgemm_canonical.cpp:125-176). */
+typedef struct qc_cint8_weights {
+  const int8_t* codes;
+  const float* scales;
+  const float* zero_points;   /* NULL: symmetric */
+  long long rows;
+  long long cols;
+  long long groups;
+} qc_cint8_weights;
+
+/* Float storage of activations and outputs (FloatStorageType order of
+ * include/quixicore_cpu/float_storage.h:18): raw IEEE binary32 / binary16 /
+ * bfloat16; 16-bit values are decoded exactly, accumulation is f32 and each
+ * output is rounded once (bf16: nearest even, NaN kept). */
+#define QC_STORAGE_F32 0
+#define QC_STORAGE_F16 1
+#define QC_STORAGE_BF16 2
+
+/* y = x . dequant(W)^T for m activation rows x [m][cols] (x_type) over up to
+ * three matrices sharing x, with the reference's prepared-projection
+ * epilogues fused:
+ *   mode 0: nw = 1..3 projections, y[i] = [m][w[i].rows] of y_type[i]; with
+ *           nw = 1, bias (f32 [rows] or NULL) is added and `activation`
+ *           applied (LinearActivation order: 0 none, 1 GELU-erf, 2 GELU-tanh,
+ *           3 SiLU, 4 ReLU^2; qgemm_canonical.cpp:361-379,2570-2581).
+ *   mode 1: nw = 2 (gate, up, same shape): y[0] = SiLU(gate) * up
+ *           (qgemm_canonical.cpp:2550-2560); neither projection is stored.
+ *   mode 2: m = 1, nw = 1 (Q) or 3 (Q, K, V), rows multiples of head_dim
+ *           (even): the (d, d + head_dim/2) pairs of every Q (and K) head are
+ *           stored rotated, out[d] = a*c - b*s, out[d + half] = b*c + a*s with
+ *           c = rope_cos[d], s = rope_sin[d] (the position's row); y[0] = Q,
+ *           y[1] / y[2] = the cache slot's K / V rows (qgemm_canonical.cpp:
+ *           5032-5225).
+ * The matrices must share cols and groups, and all or none have zero
+ * points.  Status: 1 shapes, 2 unknown storage type, 3 NULL pointers or a
+ * bad mode / activation. */
+int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void* x, int x_type,
+                         long long m, void* const* y, const int* y_type, const float* bias,
+                         int activation, const float* rope_cos, const float* rope_sin,
+                         long long head_dim, void* stream);
+
 /* Activation-quantizing GEMV: x is quantized per 32-element block to int8
  * (scale = max|x_b| / 127, round half to even, clamp +-127), each block dot is
  * an exact integer sum, and y[r] = sum_b (float(dot) * d_w) * d_x in block

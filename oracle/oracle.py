@@ -227,6 +227,44 @@ def qkv_rope_kv(fmt, pq, pk, pv, x, cosine, sine, query_heads, kv_heads, head_di
                          position, slot, key_cache, value_cache)
 
 
+# ------------------------------------------------------------ canonical int8 ---
+
+def cint8_dequant(codes, scales, zeros, rows, cols, groups):
+    """The reference's f32 decode of a kInt8Symmetric / kInt8Affine tensor
+    (kernels/quantization/qgemm_canonical.cpp:168-174): value = scale * (code -
+    zero), each step rounded in f32; scale / zero of group col // (cols /
+    groups) of the row."""
+    q = np.asarray(codes, dtype=np.int8).reshape(rows, cols).astype(np.float32)
+    g = cols // groups
+    s = np.repeat(np.asarray(scales, np.float32).reshape(rows, groups), g, axis=1)
+    if zeros is None:
+        return (s * q).astype(np.float32)
+    z = np.repeat(np.asarray(zeros, np.float32).reshape(rows, groups), g, axis=1)
+    return (s * (q - z).astype(np.float32)).astype(np.float32)
+
+
+def cint8_project_f64(x, what):
+    """f64 projection x [m][cols] . what^T over the decoded weights, and each
+    output row's ||w_hat_row||_2 (for the normalised contract)."""
+    w = what.astype(np.float64)
+    return np.asarray(x, np.float64) @ w.T, np.linalg.norm(w, axis=1)
+
+
+def linear_activation_f64(v, act):
+    """projection_activation (qgemm_canonical.cpp:361-379) in f64."""
+    import math
+    v = np.asarray(v, np.float64)
+    if act == 1:
+        return 0.5 * v * (1.0 + np.vectorize(math.erf)(v / math.sqrt(2.0)))
+    if act == 2:
+        return 0.5 * v * (1.0 + np.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))
+    if act == 3:
+        return v / (1.0 + np.exp(-v))
+    if act == 4:
+        return np.where(v > 0, v * v, 0.0)
+    return v
+
+
 def gemv_w8a8(fmt, packed, x, n, k):
     """qgemv_w8a8: per-32-block int8 activations, integer block dots,
     y = sum_b (float(dot) * d_w) * d_x in block order.  Returns (status, y)."""
@@ -321,6 +359,12 @@ class Reference:
         return _rope_kv_call(self.lib.qcref_qgemv_qkv_rope_kv, fmt, pq, pk, pv, x, cosine, sine,
                              query_heads, kv_heads, head_dim, input_dim, slots, max_position,
                              position, slot, key_cache, value_cache)
+
+    def storage_scenarios(self, directory):
+        """Runs tests/cpp/storage_scenarios.h through the reference's own
+        prepared storage projections, writing under `directory`."""
+        self.lib.qcref_storage_scenarios.argtypes = [ctypes.c_char_p]
+        return self.lib.qcref_storage_scenarios(str(directory).encode())
 
     def pack(self, fmt, w):
         w = np.ascontiguousarray(w, dtype=np.float32)

@@ -14,6 +14,8 @@
 //               -> the public functions  (kernels/norms/norm_quant_ref.cpp:1060-1068;
 //                                          kernels/quantization/quantization_ref.cpp:190-244)
 //   qgemv_qkv_rope_kv -> the public function (kernels/quantization/qgemv_fused_ref.cpp:342-443)
+//   qgemm_prepacked_*_storage -> the public functions (kernels/quantization/qgemm_canonical.cpp),
+//               run over tests/cpp/storage_scenarios.h
 //   CpuPackedWeights::prepare (both overloads), info(), panel_data()
 //               -> src/memory/packed_weights.cpp:197-412
 #include <cstddef>
@@ -29,6 +31,7 @@
 #include "quixicore_cpu/quant_import.h"
 #include "quixicore_cpu/quantization.h"
 #include "quixicore_cpu/threading.h"
+#include "../tests/cpp/storage_scenarios.h"
 
 namespace qc = quixicore_cpu;
 
@@ -225,6 +228,15 @@ int qcref_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packed
       static_cast<qc::QuantFormat>(format), packed_q, packed_k, packed_v, x, cosine, sine, q,
       key_cache, value_cache, query_heads, kv_heads, head_dim, input_dim, slots, max_position,
       position, slot));
+}
+
+// The prepared storage projection scenarios (tests/cpp/storage_scenarios.h)
+// through the reference's own CpuPackedWeights and qgemm_prepacked_*_storage.
+int qcref_storage_scenarios(const char* dir) {
+  storage_scenarios::Sink sink(dir);
+  if (sink.manifest == nullptr) return 1;
+  storage_scenarios::run(sink);
+  return 0;
 }
 
 void qcref_set_num_threads(int n) { qc::set_num_threads(n); }

@@ -1,0 +1,427 @@
+// Projections over canonical int8 weights (kInt8Symmetric / kInt8Affine of
+// the reference's canonical contract): y[m][n] = sum_k x[m][k] * w(n, k) with
+// w(n, k) = scale(n, g) * (code[n][k] - zero(n, g)), g = k / group_size
+// (kernels/quantization/qgemm_canonical.cpp:125-176, decode_prepared_chunk).
+// Activations and outputs are f32, f16 or bf16 (decoded exactly, accumulated
+// in f32, rounded once at the store, kernels/common/float_storage_access.h).
+//
+// One launch covers up to three matrices over the same x (the prepared
+// storage seams of include/quixicore_cpu/qgemm.h:32-101) with the epilogue
+// fused: bias + activation, SiLU(gate) * up over interleaved gate/up rows,
+// or split-half RoPE over the (d, d + half) row pairs of each head.
+//
+// Layout: codes row-major [rows][k] (the canonical bytes, unchanged); scales
+// (and zero points) f32 [rows][groups].  The fast kernel streams each row in
+// 16-byte chunks, one per lane and step (a wave covers 1024 columns of a row
+// per load instruction), with the next step's chunks in flight while the
+// current ones are multiplied against the f32 activations staged in LDS.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qc_device.h"
+#include "qc_internal.h"
+
+namespace qc {
+namespace {
+
+constexpr int kThreads = 256;   // 4 waves
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ float load_x(const void* x, long long i, int type) {
+  if (type == QC_STORAGE_F32) return static_cast<const float*>(x)[i];
+  const uint16_t b = static_cast<const uint16_t*>(x)[i];
+  if (type == QC_STORAGE_F16) return static_cast<float>(__builtin_bit_cast(_Float16, b));
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// float_to_bf16 of kernels/utils/float_storage_ref.cpp:184-193 (round to
+// nearest even; NaNs stay NaN) and IEEE binary16 round to nearest even.
+__device__ __forceinline__ void store_y(void* y, long long i, int type, float v) {
+  if (type == QC_STORAGE_F32) {
+    static_cast<float*>(y)[i] = v;
+  } else if (type == QC_STORAGE_F16) {
+    asm volatile("" : "+v"(v));   // keep the conversion a plain v_cvt_f16_f32
+    static_cast<uint16_t*>(y)[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  } else {
+    const uint32_t bits = __float_as_uint(v);
+    uint16_t out;
+    if ((bits & 0x7f800000u) == 0x7f800000u && (bits & 0x007fffffu) != 0)
+      out = static_cast<uint16_t>((bits >> 16) | 0x0040u);
+    else
+      out = static_cast<uint16_t>((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+    static_cast<uint16_t*>(y)[i] = out;
+  }
+}
+
+// projection_activation of kernels/quantization/qgemm_canonical.cpp:361-379
+// (LinearActivation: 0 none, 1 GELU-erf, 2 GELU-tanh, 3 SiLU, 4 ReLU^2).
+__device__ __forceinline__ float linear_activation(float v, int act) {
+  constexpr float kInvSqrt2 = 0.7071067811865475f;
+  constexpr float kSqrt2OverPi = 0.7978845608028654f;
+  switch (act) {
+    case 1: return 0.5f * v * (1.0f + erff(v * kInvSqrt2));
+    case 2: return 0.5f * v * (1.0f + tanhf(kSqrt2OverPi * (v + 0.044715f * v * v * v)));
+    case 3: return v / (1.0f + expf(-v));
+    case 4: return v > 0.0f ? v * v : 0.0f;
+    default: return v;
+  }
+}
+
+// The launch's row space: segments of logical rows over up to three
+// matrices.  mode 0: plain rows (segment s, row r -> y[s][m * ld + r]), with
+// bias and activation on segment 0 when given.  mode 1: one segment whose
+// logical rows 2i / 2i + 1 are gate / up row i (w[0] / w[1]); out[m * ld + i]
+// = SiLU(gate) * up.  mode 2 (m = 1): segments below nrope hold RoPE pairs:
+// logical rows 2j / 2j + 1 are rows d / d + half of head j / half.
+struct CSegs {
+  const int8_t* w[3];
+  const float* scale[3];
+  const float* zero[3];
+  void* y[3];
+  long long ld[3];     // elements between activation rows of y[s]
+  int ytype[3];
+  int start[4];        // start[nseg] = logical rows
+  int nseg;
+  int mode;
+  int groups;          // scale groups per row (1: one scale per row)
+  int gshift;          // log2(group size) when groups > 1 (power of two >= 16), else 0
+  int gsize;
+  const float* bias;
+  int act;
+  int half, nrope;
+  const float* rc;
+  const float* rs;
+};
+
+struct RowRef {
+  int seg;    // segment of the row (mode 1: 0 = gate, 1 = up)
+  int row;    // row of that segment's matrix
+};
+
+__device__ __forceinline__ RowRef logical_row(const CSegs& s, int g) {
+  RowRef r;
+  if (s.mode == 1) {
+    r.seg = g & 1;
+    r.row = g >> 1;
+    return r;
+  }
+  r.seg = (s.nseg > 2 && g >= s.start[2]) ? 2 : (s.nseg > 1 && g >= s.start[1]) ? 1 : 0;
+  r.row = g - s.start[r.seg];
+  if (s.mode == 2 && r.seg < s.nrope) {
+    const int j = r.row >> 1;
+    const int head = j / s.half;
+    r.row = head * 2 * s.half + (j - head * s.half) + (r.row & 1) * s.half;
+  }
+  return r;
+}
+
+// Stores the finished values of logical rows g (and g + 1 for the paired
+// modes) for activation row m.  v0 / v1: their projections.
+__device__ __forceinline__ void epilogue(const CSegs& s, int g, int m, float v0, float v1) {
+  if (s.mode == 1) {
+    const float silu = v0 / (1.0f + expf(-v0));
+    store_y(s.y[0], m * s.ld[0] + (g >> 1), s.ytype[0], silu * v1);
+    return;
+  }
+  const RowRef r = logical_row(s, g);
+  if (s.mode == 2) {
+    if (r.seg < s.nrope) {
+      const int d = r.row % (2 * s.half);
+      const float c = s.rc[d], sn = s.rs[d];
+      store_y(s.y[r.seg], r.row, s.ytype[r.seg], v0 * c - v1 * sn);
+      store_y(s.y[r.seg], r.row + s.half, s.ytype[r.seg], v1 * c + v0 * sn);
+    } else {
+      store_y(s.y[r.seg], r.row, s.ytype[r.seg], v0);
+      store_y(s.y[r.seg], r.row + 1, s.ytype[r.seg], v1);
+    }
+    return;
+  }
+  float v = v0;
+  if (r.seg == 0 && (s.bias != nullptr || s.act != 0)) {
+    if (s.bias != nullptr) v += s.bias[r.row];
+    v = linear_activation(v, s.act);
+  }
+  store_y(s.y[r.seg], m * s.ld[r.seg] + r.row, s.ytype[r.seg], v);
+}
+
+__device__ __forceinline__ void unpack16(const uint4& c, float* q) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      q[4 * i + b] = static_cast<float>(static_cast<int32_t>(w[i] << (24 - 8 * b)) >> 24);
+  }
+}
+
+// MB activation rows per pass, RW rows per wave.  GRP: one scale per group of
+// 2^gshift columns (else per row, applied once at the end); AFF: zero points.
+// The activations of a K chunk (kc columns, a multiple of 1024) are staged in
+// LDS as f32.  Requires k % 16 == 0 and 16-byte aligned codes.
+template <int MB, int RW, bool GRP, bool AFF>
+__global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const void* __restrict__ x,
+                                                         int xtype, long long ldx, int m0, int mrows,
+                                                         int k, int kc) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];   // [MB][kc]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int total = segs.start[segs.nseg];
+  const int g0 = (blockIdx.x * kWaves + wave) * RW;
+  const int8_t* wrow[RW];
+  const float* srow[RW];
+  const float* zrow[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const RowRef rr = logical_row(segs, min(g0 + r, total - 1));
+    wrow[r] = segs.w[rr.seg] + static_cast<long long>(rr.row) * k;
+    srow[r] = segs.scale[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
+    zrow[r] = AFF ? segs.zero[rr.seg] + static_cast<long long>(rr.row) * segs.groups : nullptr;
+  }
+  float acc[RW][MB];
+  float sx[MB];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) acc[r][mm] = 0.f;
+#pragma unroll
+  for (int mm = 0; mm < MB; ++mm) sx[mm] = 0.f;
+
+  for (int c0 = 0; c0 < k; c0 += kc) {
+    const int clen = min(kc, k - c0);
+    if (c0) __syncthreads();
+    for (int mm = 0; mm < MB; ++mm) {
+      const int mrow = m0 + mm;
+      for (int i = threadIdx.x; i < clen; i += kThreads)
+        xs[mm * kc + i] = mrow < mrows ? load_x(x, mrow * ldx + c0 + i, xtype) : 0.f;
+    }
+    __syncthreads();
+    const int items = (clen + 1023) >> 10;
+    uint4 cur[RW], nxt[RW];
+    auto fetch = [&](uint4* dst, int j) {
+      const int e = min(c0 + 16 * (lane + 64 * j), k - 16);
+#pragma unroll
+      for (int r = 0; r < RW; ++r) dst[r] = *reinterpret_cast<const uint4*>(wrow[r] + e);
+    };
+    fetch(cur, 0);
+    for (int j = 0; j < items; ++j) {
+      if (j + 1 < items) fetch(nxt, j + 1);
+      const int e = c0 + 16 * (lane + 64 * j);
+      if (e < c0 + clen) {
+        float xv[MB][16];
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm) {
+          const float4* p = reinterpret_cast<const float4*>(xs + mm * kc + (e - c0));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float4 t = p[i];
+            xv[mm][4 * i] = t.x; xv[mm][4 * i + 1] = t.y; xv[mm][4 * i + 2] = t.z; xv[mm][4 * i + 3] = t.w;
+          }
+        }
+        float s16[MB];
+        if constexpr (AFF) {
+#pragma unroll
+          for (int mm = 0; mm < MB; ++mm) {
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t += xv[mm][i];
+            s16[mm] = t;
+            if constexpr (!GRP) sx[mm] += t;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          float q[16];
+          unpack16(cur[r], q);
+          float sc = 1.f, zp = 0.f;
+          if constexpr (GRP) {
+            sc = srow[r][e >> segs.gshift];
+            if constexpr (AFF) zp = zrow[r][e >> segs.gshift];
+          }
+#pragma unroll
+          for (int mm = 0; mm < MB; ++mm) {
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t = fmaf(q[i], xv[mm][i], t);
+            if constexpr (GRP) {
+              if constexpr (AFF) t = fmaf(-zp, s16[mm], t);
+              acc[r][mm] = fmaf(sc, t, acc[r][mm]);
+            } else {
+              acc[r][mm] += t;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RW; ++r) cur[r] = nxt[r];
+    }
+  }
+  // wave sums, returned to every lane; then lane (r * MB + mm) finishes one
+  // value, or (paired modes) one row pair
+  float tot[RW][MB];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) {
+      float v = wave_sum(acc[r][mm]);
+      if constexpr (!GRP) {
+        const float sc = srow[r][0];
+        if constexpr (AFF) v = fmaf(-zrow[r][0], wave_sum(sx[mm]), v);
+        v = sc * v;
+      }
+      tot[r][mm] = v;
+    }
+  if (segs.mode == 0) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int mm = 0; mm < MB; ++mm)
+        if (lane == r * MB + mm && g0 + r < total && m0 + mm < mrows)
+          epilogue(segs, g0 + r, m0 + mm, tot[r][mm], 0.f);
+  } else {
+#pragma unroll
+    for (int r = 0; r + 1 < RW; r += 2)
+#pragma unroll
+      for (int mm = 0; mm < MB; ++mm)
+        if (lane == r * MB + mm && g0 + r < total && m0 + mm < mrows)
+          epilogue(segs, g0 + r, m0 + mm, tot[r][mm], tot[r + 1][mm]);
+  }
+}
+
+// Any layout: one wave per (logical row, activation row), element by
+// element with the reference's decode value = scale * (code - zero), into
+// f32 scratch [m][total] (the epilogue kernel then finishes it).
+__global__ __launch_bounds__(kThreads) void cint8_generic(const CSegs segs, const void* __restrict__ x,
+                                                          int xtype, long long ldx, int mrows, int k,
+                                                          float* __restrict__ out) {
+  const int total = segs.start[segs.nseg];
+  const long long item = static_cast<long long>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (item >= static_cast<long long>(total) * mrows) return;
+  const int g = static_cast<int>(item % total);
+  const int mrow = static_cast<int>(item / total);
+  const RowRef rr = logical_row(segs, g);
+  const int8_t* w = segs.w[rr.seg] + static_cast<long long>(rr.row) * k;
+  const float* sc = segs.scale[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
+  const float* zp = segs.zero[rr.seg] == nullptr
+                        ? nullptr
+                        : segs.zero[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
+  float acc = 0.f;
+  for (int e = threadIdx.x & 63; e < k; e += 64) {
+    const int grp = segs.groups > 1 ? e / segs.gsize : 0;
+    const float z = zp == nullptr ? 0.f : zp[grp];
+    const float v = sc[grp] * (static_cast<float>(w[e]) - z);
+    acc = fmaf(load_x(x, mrow * ldx + e, xtype), v, acc);
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) out[item] = acc;
+}
+
+__global__ __launch_bounds__(kThreads) void cint8_finish(const CSegs segs, const float* __restrict__ p,
+                                                         int mrows) {
+  const int total = segs.start[segs.nseg];
+  const int step = segs.mode == 0 ? 1 : 2;
+  const long long units = static_cast<long long>(total / step) * mrows;
+  const long long u = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (u >= units) return;
+  const int g = static_cast<int>(u % (total / step)) * step;
+  const int mrow = static_cast<int>(u / (total / step));
+  const float* row = p + static_cast<long long>(mrow) * total;
+  epilogue(segs, g, mrow, row[g], step == 2 ? row[g + 1] : 0.f);
+}
+
+template <int MB, int RW, bool GRP, bool AFF>
+hipError_t launch_fast(const CSegs& sg, const void* x, int xtype, long long ldx, int m, int k,
+                       hipStream_t s) {
+  const int total = sg.start[sg.nseg];
+  const int kc = min(((k + 1023) / 1024) * 1024, 16384 / MB);
+  const unsigned grid = static_cast<unsigned>((total + kWaves * RW - 1) / (kWaves * RW));
+  const size_t lds = sizeof(float) * MB * kc;
+  for (int m0 = 0; m0 < m; m0 += MB) {
+    cint8_kernel<MB, RW, GRP, AFF><<<grid, kThreads, lds, s>>>(sg, x, xtype, ldx, m0, m, k, kc);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+template <int MB, int RW>
+hipError_t launch_mb(const CSegs& sg, bool grp, bool aff, const void* x, int xtype, long long ldx,
+                     int m, int k, hipStream_t s) {
+  if (grp)
+    return aff ? launch_fast<MB, RW, true, true>(sg, x, xtype, ldx, m, k, s)
+               : launch_fast<MB, RW, true, false>(sg, x, xtype, ldx, m, k, s);
+  return aff ? launch_fast<MB, RW, false, true>(sg, x, xtype, ldx, m, k, s)
+             : launch_fast<MB, RW, false, false>(sg, x, xtype, ldx, m, k, s);
+}
+
+}  // namespace
+
+// Host entry (all checks done by the caller): see CInt8Launch in qc_internal.h.
+hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
+  CSegs sg{};
+  int total = 0;
+  sg.nseg = L.mode == 1 ? 1 : L.nw;
+  sg.start[0] = 0;
+  for (int i = 0; i < L.nw; ++i) {
+    sg.w[i] = L.w[i].codes;
+    sg.scale[i] = L.w[i].scales;
+    sg.zero[i] = L.w[i].zero_points;
+    sg.y[i] = L.y[i];
+    sg.ytype[i] = L.ytype[i];
+    sg.ld[i] = L.mode == 1 ? L.w[0].rows : L.w[i].rows;
+  }
+  if (L.mode == 1) {
+    total = static_cast<int>(2 * L.w[0].rows);
+    sg.start[1] = total;
+  } else {
+    for (int i = 0; i < L.nw; ++i) sg.start[i + 1] = sg.start[i] + static_cast<int>(L.w[i].rows);
+    total = sg.start[L.nw];
+  }
+  sg.mode = L.mode;
+  sg.groups = static_cast<int>(L.w[0].groups);
+  sg.gsize = static_cast<int>(L.w[0].cols / L.w[0].groups);
+  sg.gshift = 0;
+  if (sg.groups > 1)
+    while ((1 << sg.gshift) < sg.gsize) ++sg.gshift;
+  sg.bias = L.bias;
+  sg.act = L.act;
+  sg.half = L.half;
+  sg.nrope = L.nrope;
+  sg.rc = L.rope_cos;
+  sg.rs = L.rope_sin;
+  const int k = static_cast<int>(L.w[0].cols);
+  const int m = static_cast<int>(L.m);
+  const bool aff = L.w[0].zero_points != nullptr;
+  const bool grp = sg.groups > 1;
+  bool fast = k % 16 == 0 && (!grp || (sg.gsize >= 16 && (1 << sg.gshift) == sg.gsize));
+  for (int i = 0; i < L.nw; ++i)
+    fast = fast && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
+  if (fast) {
+    const int cus = device_cu_count();
+    const bool four = (total + kWaves * 4 - 1) / (kWaves * 4) >= 2 * cus;
+    if (m == 1)
+      return four ? launch_mb<1, 4>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s)
+                  : launch_mb<1, 2>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s);
+    if (m == 2)
+      return four ? launch_mb<2, 4>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s)
+                  : launch_mb<2, 2>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s);
+    return four ? launch_mb<4, 4>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s)
+                : launch_mb<4, 2>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s);
+  }
+  float* p = nullptr;
+  const size_t bytes = sizeof(float) * static_cast<size_t>(total) * m;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&p), bytes ? bytes : 4, s);
+  if (e != hipSuccess) return e;
+  const long long items = static_cast<long long>(total) * m;
+  cint8_generic<<<static_cast<unsigned>((items + kWaves - 1) / kWaves), kThreads, 0, s>>>(
+      sg, L.x, L.xtype, L.ldx, m, k, p);
+  e = hipGetLastError();
+  if (e == hipSuccess) {
+    const long long units = items / (L.mode == 0 ? 1 : 2);
+    cint8_finish<<<static_cast<unsigned>((units + kThreads - 1) / kThreads), kThreads, 0, s>>>(sg, p, m);
+    e = hipGetLastError();
+  }
+  const hipError_t f = hipFreeAsync(p, s);
+  return e != hipSuccess ? e : f;
+}
+
+}  // namespace qc

@@ -461,6 +461,68 @@ int qc_hip_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packe
   return finish(e);
 }
 
+// Canonical int8 projections: shapes (rows, cols, groups; shared cols and
+// groups; the mode's pairing), storage types, then pointers.
+int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void* x, int x_type,
+                         long long m, void* const* y, const int* y_type, const float* bias,
+                         int activation, const float* rope_cos, const float* rope_sin,
+                         long long head_dim, void* stream) {
+  if (mode < 0 || mode > 2 || activation < 0 || activation > 4 || w == nullptr || y == nullptr ||
+      y_type == nullptr)
+    return QC_INVALID_ARGUMENT;
+  if (nw < 1 || nw > 3 || (mode == 1 && nw != 2) || (mode == 2 && nw == 2) || m < 1 ||
+      m > INT_MAX)
+    return QC_INVALID_SHAPE;
+  long long total = 0;
+  for (int i = 0; i < nw; ++i) {
+    const qc_cint8_weights& a = w[i];
+    if (!valid_product({a.rows, a.cols}) || a.groups < 1 || a.cols % a.groups != 0 ||
+        a.cols != w[0].cols || a.groups != w[0].groups || a.cols > INT_MAX)
+      return QC_INVALID_SHAPE;
+    if (mode == 2 && (head_dim <= 0 || head_dim % 2 != 0 || a.rows % head_dim != 0))
+      return QC_INVALID_SHAPE;
+    total += a.rows;
+  }
+  if (mode == 1 && w[1].rows != w[0].rows) return QC_INVALID_SHAPE;
+  if (mode == 1) total = 2 * w[0].rows;
+  if (mode == 2 && m != 1) return QC_INVALID_SHAPE;
+  if (total >= (1LL << 30) || !valid_product({m, total})) return QC_INVALID_SHAPE;
+  const int nout = mode == 1 ? 1 : nw;
+  auto known = [](int t) { return t == QC_STORAGE_F32 || t == QC_STORAGE_F16 || t == QC_STORAGE_BF16; };
+  if (!known(x_type)) return QC_UNSUPPORTED_FORMAT;
+  for (int i = 0; i < nout; ++i)
+    if (!known(y_type[i])) return QC_UNSUPPORTED_FORMAT;
+  if (x == nullptr || (mode == 2 && (rope_cos == nullptr || rope_sin == nullptr)))
+    return QC_INVALID_ARGUMENT;
+  for (int i = 0; i < nw; ++i)
+    if (w[i].codes == nullptr || w[i].scales == nullptr ||
+        (w[i].zero_points == nullptr) != (w[0].zero_points == nullptr))
+      return QC_INVALID_ARGUMENT;
+  for (int i = 0; i < nout; ++i)
+    if (y[i] == nullptr) return QC_INVALID_ARGUMENT;
+  qc::CInt8Launch L;
+  L.mode = mode;
+  L.nw = nw;
+  for (int i = 0; i < nw; ++i) L.w[i] = w[i];
+  L.x = x;
+  L.xtype = x_type;
+  L.ldx = w[0].cols;
+  L.m = m;
+  for (int i = 0; i < nout; ++i) {
+    L.y[i] = y[i];
+    L.ytype[i] = y_type[i];
+  }
+  L.bias = mode == 0 && nw == 1 ? bias : nullptr;
+  L.act = mode == 0 && nw == 1 ? activation : 0;
+  if (mode == 2) {
+    L.half = static_cast<int>(head_dim / 2);
+    L.nrope = nw == 1 ? 1 : 2;
+    L.rope_cos = rope_cos;
+    L.rope_sin = rope_sin;
+  }
+  return finish(qc::launch_cint8(L, as_stream(stream)));
+}
+
 // src/dispatch/qgemv_w8a8.cpp:108-125 (qgemv_w8a8_packed_size).
 int qc_hip_qgemv_w8a8_packed_size(int format, long long n, long long k, long long* bytes) {
   size_t size = 0;

@@ -48,30 +48,21 @@ struct Workspace::Impl {
 
 namespace detail {
 
-// Restores a workspace to the allocation mark taken at construction (the
-// scope-exit rewind of the reference's WorkspaceFrame,
-// src/memory/workspace_internal.h:15-44).
-class WorkspaceFrame {
- public:
-  explicit WorkspaceFrame(Workspace* w) : w_(w) {
-    if (w_ != nullptr && w_->impl_ != nullptr) {
-      segment_ = w_->impl_->segment;
-      offset_ = w_->impl_->offset;
-      used_ = w_->impl_->used;
-    }
+WorkspaceFrame::WorkspaceFrame(Workspace* w) : w_(w) {
+  if (w_ != nullptr && w_->impl_ != nullptr) {
+    segment_ = w_->impl_->segment;
+    offset_ = w_->impl_->offset;
+    used_ = w_->impl_->used;
   }
-  ~WorkspaceFrame() {
-    if (w_ != nullptr && w_->impl_ != nullptr) {
-      w_->impl_->segment = segment_;
-      w_->impl_->offset = offset_;
-      w_->impl_->used = used_;
-    }
-  }
+}
 
- private:
-  Workspace* w_;
-  std::size_t segment_ = 0, offset_ = 0, used_ = 0;
-};
+WorkspaceFrame::~WorkspaceFrame() {
+  if (w_ != nullptr && w_->impl_ != nullptr) {
+    w_->impl_->segment = segment_;
+    w_->impl_->offset = offset_;
+    w_->impl_->used = used_;
+  }
+}
 
 }  // namespace detail
 
@@ -268,6 +259,7 @@ struct CpuPackedWeights::Impl {
   void* device = nullptr;                    // [data | scales | row sums], 256-byte aligned parts
   const float* device_scales = nullptr;
   const std::int32_t* device_row_sums = nullptr;
+  const float* device_zero_points = nullptr;
   ~Impl() {
     if (device != nullptr) (void)hipFree(device);
   }
@@ -423,11 +415,13 @@ Status CpuPackedWeights::prepare(const CanonicalQuantTensor& t, CpuPanelLayout l
   put_table(t.act_order, dst, &cursor, &info.act_order_offset);
   put_table(t.row_sums, dst, &cursor, &info.row_sum_table_offset);
 
-  // device mirror: data, f32 scales and int32 row sums, each 256-byte aligned
+  // device mirror: data, f32 scales, int32 row sums and f32 zero points,
+  // each 256-byte aligned
   auto up = [](std::size_t b) { return (b + 255) / 256 * 256; };
   const std::size_t d_scales = up(t.data.size());
   const std::size_t d_sums = d_scales + up(t.scales.size() * sizeof(float));
-  const std::size_t d_bytes = d_sums + t.row_sums.size() * sizeof(std::int32_t);
+  const std::size_t d_zeros = d_sums + up(t.row_sums.size() * sizeof(std::int32_t));
+  const std::size_t d_bytes = d_zeros + t.zero_points.size() * sizeof(float);
   hipError_t e = hipMalloc(&impl->device, d_bytes ? d_bytes : 256);
   if (e != hipSuccess) {
     impl->device = nullptr;
@@ -440,8 +434,13 @@ Status CpuPackedWeights::prepare(const CanonicalQuantTensor& t, CpuPanelLayout l
                       hipMemcpyHostToDevice)) != hipSuccess) ||
       (!t.row_sums.empty() &&
        (e = hipMemcpy(base + d_sums, t.row_sums.data(), t.row_sums.size() * sizeof(std::int32_t),
+                      hipMemcpyHostToDevice)) != hipSuccess) ||
+      (!t.zero_points.empty() &&
+       (e = hipMemcpy(base + d_zeros, t.zero_points.data(), t.zero_points.size() * sizeof(float),
                       hipMemcpyHostToDevice)) != hipSuccess))
     return Status::kDeviceError;
+  impl->device_zero_points =
+      t.zero_points.empty() ? nullptr : reinterpret_cast<float*>(base + d_zeros);
   impl->device_scales = t.scales.empty() ? nullptr : reinterpret_cast<float*>(base + d_scales);
   impl->device_row_sums =
       t.row_sums.empty() ? nullptr : reinterpret_cast<std::int32_t*>(base + d_sums);
@@ -492,6 +491,9 @@ const float* CpuPackedWeights::device_scales() const noexcept {
 const std::int32_t* CpuPackedWeights::device_row_sums() const noexcept {
   return impl_ == nullptr ? nullptr : impl_->device_row_sums;
 }
+const float* CpuPackedWeights::device_zero_points() const noexcept {
+  return impl_ == nullptr ? nullptr : impl_->device_zero_points;
+}
 
 const char* cpu_prepared_isa_name(CpuPreparedIsa isa) {
   switch (isa) {
@@ -523,16 +525,21 @@ const char* cpu_panel_layout_name(CpuPanelLayout layout) {
 // --------------------------------------------------- prepared entry points ---
 
 // kernels/quantization/qgemm_panel.cpp:214-240: readiness, shape product,
-// nulls; every M is then one launch over the device mirror (the reference
-// routes M == 1 to qgemv and M < 64 to qgemm -- the same arithmetic contract).
+// canonical weights to the storage route, nulls; every M is then one launch
+// over the device mirror (the reference routes M == 1 to qgemv and M < 64 to
+// qgemm -- the same arithmetic contract).
 Status qgemm_prepacked(const CpuPackedWeights& weights, const float* x, float* y, long long m,
                        Workspace* workspace) {
   if (!weights.ready()) return Status::kInvalidArgument;
   const CpuPackedWeightsInfo info = weights.info();
   if (m <= 0 || info.rows <= 0 || info.columns <= 0 ||
       m > std::numeric_limits<long long>::max() / info.rows ||
-      m * info.rows > std::numeric_limits<long long>::max() / info.columns ||
-      m > std::numeric_limits<int>::max())   // this library's dimension limit (as for n, k)
+      m * info.rows > std::numeric_limits<long long>::max() / info.columns)
+    return Status::kInvalidShape;
+  if (info.has_canonical_layout)
+    return qgemm_prepacked_storage(weights, {x, FloatStorageType::kF32, m * info.columns},
+                                   {y, FloatStorageType::kF32, m * info.rows}, m, workspace);
+  if (m > std::numeric_limits<int>::max())   // this library's dimension limit (as for n, k)
     return Status::kInvalidShape;
   if (x == nullptr || y == nullptr || weights.device_data() == nullptr)
     return Status::kInvalidArgument;
@@ -545,9 +552,13 @@ Status qgemm_prepacked(const CpuPackedWeights& weights, const float* x, float* y
                                info.rows, info.columns, g.stream()));
 }
 
+// kernels/quantization/qgemm_canonical.cpp:4647-4653: the storage route with
+// f32 x and y (GGUF-prepared weights: kUnsupportedFormat).
 Status qgemv_prepacked(const CpuPackedWeights& weights, const float* x, float* y,
                        Workspace* workspace) {
-  return qgemm_prepacked(weights, x, y, 1, workspace);
+  const CpuPackedWeightsInfo info = weights.info();
+  return qgemm_prepacked_storage(weights, {x, FloatStorageType::kF32, info.columns},
+                                 {y, FloatStorageType::kF32, info.rows}, 1, workspace);
 }
 
 }  // namespace quixicore_cpu

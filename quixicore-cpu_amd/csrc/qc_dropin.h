@@ -20,6 +20,21 @@ bool device_accessible(const void* p);
 
 Status from_hip(hipError_t e);
 
+// Restores a workspace to the allocation mark taken at construction (the
+// scope-exit rewind of the reference's WorkspaceFrame,
+// src/memory/workspace_internal.h:15-44).
+class WorkspaceFrame {
+ public:
+  explicit WorkspaceFrame(Workspace* w);
+  ~WorkspaceFrame();
+  WorkspaceFrame(const WorkspaceFrame&) = delete;
+  WorkspaceFrame& operator=(const WorkspaceFrame&) = delete;
+
+ private:
+  Workspace* w_;
+  std::size_t segment_ = 0, offset_ = 0, used_ = 0;
+};
+
 // Per-call staging.  in()/out() return a device view of a caller buffer:
 // the buffer itself when the GPU can address it, else a device copy (taken
 // from `workspace` when one is given, else hipMalloc'd and freed on scope

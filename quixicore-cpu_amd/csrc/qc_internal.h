@@ -77,6 +77,28 @@ constexpr size_t kQgemmNoAllocScratchBytes = QC_QGEMM_NOALLOC_SCRATCH_BYTES;
 hipError_t launch_qgemm_mfma_noalloc(int fmt, const void* W, const float* x, float* y, int m,
                                      int n, int k, hipStream_t s);
 
+// Projections over canonical int8 weights (see qc_hip_cint8_project), all
+// checks done by the caller.  half / nrope: mode 2's RoPE half head size and
+// the number of leading matrices rotated (1: Q, 2: Q and K).
+struct CInt8Launch {
+  int mode = 0;
+  int nw = 1;
+  qc_cint8_weights w[3] = {};
+  const void* x = nullptr;
+  int xtype = QC_STORAGE_F32;
+  long long ldx = 0;            // elements between activation rows
+  long long m = 1;
+  void* y[3] = {nullptr, nullptr, nullptr};
+  int ytype[3] = {0, 0, 0};
+  const float* bias = nullptr;
+  int act = 0;
+  int half = 0;
+  int nrope = 0;
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+};
+hipError_t launch_cint8(const CInt8Launch& launch, hipStream_t s);
+
 // Per-group symmetric int8 quantization.  status == nullptr: caller has
 // already verified that x is finite.  Otherwise non-finite groups are left
 // unwritten and *status is set to 3 (kInvalidArgument).

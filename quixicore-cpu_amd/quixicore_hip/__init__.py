@@ -43,6 +43,7 @@ _SIGS = {
     "qc_hip_qgemv_up_gate": ([_I, _P, _P, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_qgemv_up_gate_activation": ([_I, _P, _P, _P, _P, _LL, _LL, _I, _P], _I),
     "qc_hip_qgemv_qkv": ([_I, _P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _P], _I),
+    "qc_hip_cint8_project": ([_I, _P, _I, _P, _I, _LL, _P, _P, _P, _I, _P, _P, _LL, _P], _I),
     "qc_hip_qgemv_qkv_rope_kv": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _LL, _LL, _LL, _LL,
                                   _LL, _LL, _I, _I, _P], _I),
     "qc_hip_qgemv_w8a8_packed_size": ([_I, _LL, _LL, _P], _I),
@@ -133,6 +134,36 @@ def qgemv_qkv_rope_kv_raw(fmt, pq, pk, pv, x, cosine, sine, q, key_cache, value_
                                         _ptr(sine), _ptr(q), _ptr(key_cache), _ptr(value_cache),
                                         query_heads, kv_heads, head_dim, input_dim, slots,
                                         max_position, position, slot, _stream(stream))
+
+
+class CInt8Weights(ctypes.Structure):
+    """qc_cint8_weights (include/quixicore_hip.h)."""
+    _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("zero_points", ctypes.c_void_p), ("rows", ctypes.c_longlong),
+                ("cols", ctypes.c_longlong), ("groups", ctypes.c_longlong)]
+
+
+STORAGE = {"f32": 0, "f16": 1, "bf16": 2}
+
+
+def cint8_weights(codes, scales, zero_points, rows, cols, groups):
+    """A qc_cint8_weights over device tensors; the caller keeps the tensors
+    alive while the struct is in use (it holds raw pointers)."""
+    return CInt8Weights(None if codes is None else codes.data_ptr(),
+                        None if scales is None else scales.data_ptr(),
+                        None if zero_points is None else zero_points.data_ptr(), rows, cols, groups)
+
+
+def cint8_project_raw(mode, weights, x, x_type, m, ys, y_types, bias=None, activation=0,
+                      rope_cos=None, rope_sin=None, head_dim=0, stream=None):
+    """qc_hip_cint8_project: weights is a list of CInt8Weights, ys a list of
+    output tensors (or None), types as STORAGE ids."""
+    arr = (CInt8Weights * max(len(weights), 1))(*weights)
+    yp = (ctypes.c_void_p * max(len(ys), 1))(*[None if y is None else y.data_ptr() for y in ys])
+    yt = (ctypes.c_int * max(len(y_types), 1))(*y_types)
+    return lib.qc_hip_cint8_project(mode, arr, len(weights), _ptr(x), x_type, m, yp, yt,
+                                    _ptr(bias), activation, _ptr(rope_cos), _ptr(rope_sin),
+                                    head_dim, _stream(stream))
 
 
 def qgemm_raw(fmt, packed, x, y, m, n, k, stream=None):

@@ -1,0 +1,181 @@
+"""GPU parity: the prepared storage projections over canonical int8 weights
+(include/quixicore_cpu/qgemm.h:32-101; kernels/quantization/qgemm_canonical.cpp).
+
+* The scenario list of tests/cpp/storage_scenarios.h runs through this library's
+  C++ drop-in with host buffers (tests/cpp/storage_check.cpp) and through the
+  reference's own functions (oracle/_ref): every status must be equal, and
+  every output of this library must meet the normalised contract against the
+  f64 restatement (tests/storage_eval.py), as the reference's own outputs do
+  (tests/test_oracle.py).
+* The C ABI (qc_hip_cint8_project) at a decoder's shapes: the f32 outputs
+  meet the contract; 16-bit outputs are the f32 outputs rounded once (f16:
+  IEEE nearest even, bf16: nearest even), bit for bit; 16-bit activations give
+  the f32 outputs of their decoded values, bit for bit; the byte-loading route
+  (K % 16 != 0, misaligned codes) meets the same contract.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import storage_eval
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BINARY = os.path.join(ROOT, "quixicore-cpu_amd", "lib", "storage_check")
+TOL = 1e-4
+
+
+def test_storage_scenarios_match_reference(qc, oracle, ref, tmp_path):
+    if not os.path.exists(BINARY):
+        pytest.fail(f"{BINARY} is not built (make -C quixicore-cpu_amd)")
+    ours, theirs = tmp_path / "ours", tmp_path / "ref"
+    ours.mkdir()
+    theirs.mkdir()
+    print("running storage_check", flush=True)
+    r = subprocess.run([BINARY, str(ours)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    assert ref.storage_scenarios(theirs) == 0
+    status, bad = storage_eval.check(oracle, ours)
+    assert not bad, bad[:10]
+    ref_status, _ = storage_eval.load(theirs)
+    assert status == ref_status
+
+
+def _bf16_bits(f32):
+    b = np.ascontiguousarray(f32, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _tensor(synth, seed, rows, cols, groups, affine):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(-128, 128, (rows, cols), dtype=np.int8)
+    scales = (rng.random(rows * groups, dtype=np.float32) * 1e-3 + 1e-5).astype(np.float32)
+    zeros = rng.integers(-8, 9, rows * groups).astype(np.float32) if affine else None
+    return codes, scales, zeros
+
+
+def _dev(qc, dev, arr, offset=0):
+    import torch
+    if arr is None:
+        return None
+    raw = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+    t = torch.zeros(raw.size + offset, dtype=torch.uint8, device=dev)
+    t[offset:] = torch.from_numpy(raw).to(dev)
+    return t[offset:]
+
+
+@pytest.mark.parametrize("rows,cols,groups,affine,m,offset", [
+    (14336, 4096, 1, False, 1, 0),     # SmoothQuant-style channel scales, decode
+    (4096, 4096, 32, True, 1, 0),      # affine, groups of 128
+    (4096, 14336, 1, False, 2, 0),
+    (1024, 4096, 64, False, 7, 0),     # passes of 4 activation rows
+    (300, 4008, 1, True, 3, 0),        # K % 16 != 0: byte-loading route
+    (256, 1024, 4, False, 2, 4),       # misaligned codes: byte-loading route
+    (130, 96, 3, True, 5, 0),          # groups of 32 over K = 96
+])
+def test_cint8_project_contract(qc, oracle, synth, dev, rows, cols, groups, affine, m, offset):
+    import torch
+    print(f"cint8 rows={rows} cols={cols} groups={groups} affine={affine} m={m} off={offset}",
+          flush=True)
+    codes, scales, zeros = _tensor(synth, rows + cols, rows, cols, groups, affine)
+    x = synth.normal_fast(7 + m, m * cols).reshape(m, cols)
+    C = _dev(qc, dev, codes, offset)
+    S, Z = _dev(qc, dev, scales), _dev(qc, dev, zeros)
+    w = qc.cint8_weights(C, S, Z, rows, cols, groups)
+    X = torch.from_numpy(x).to(dev)
+    y = torch.empty(m * rows, dtype=torch.float32, device=dev)
+    assert qc.cint8_project_raw(0, [w], X, 0, m, [y], [0]) == 0
+    yf = y.cpu().numpy().reshape(m, rows)
+    what = oracle.cint8_dequant(codes, scales, zeros, rows, cols, groups)
+    y64, wn = oracle.cint8_project_f64(x, what)
+    xn = np.linalg.norm(x.astype(np.float64), axis=1)[:, None]
+    assert np.all(np.abs(yf - y64) <= TOL * xn * wn[None, :])
+    # 16-bit outputs: the f32 values rounded once
+    for name, t, want in (("f16", 1, yf.astype(np.float16).view(np.uint16)),
+                          ("bf16", 2, _bf16_bits(yf))):
+        h = torch.empty(m * rows, dtype=torch.int16, device=dev)
+        assert qc.cint8_project_raw(0, [w], X, 0, m, [h], [t]) == 0
+        got = h.cpu().numpy().view(np.uint16).reshape(m, rows)
+        assert np.array_equal(got, want.reshape(m, rows)), name
+    # 16-bit activations: the f32 outputs of their decoded values
+    xb = _bf16_bits(x)
+    xd = (xb.astype(np.uint32) << 16).view(np.float32).reshape(m, cols)
+    yd = torch.empty(m * rows, dtype=torch.float32, device=dev)
+    assert qc.cint8_project_raw(0, [w], torch.from_numpy(xd).to(dev), 0, m, [yd], [0]) == 0
+    yb = torch.empty(m * rows, dtype=torch.float32, device=dev)
+    XB = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+    assert qc.cint8_project_raw(0, [w], XB, 2, m, [yb], [0]) == 0
+    assert np.array_equal(yb.cpu().numpy().view(np.uint32), yd.cpu().numpy().view(np.uint32))
+
+
+def test_cint8_fused_decode_shapes(qc, oracle, synth, dev):
+    """SwiGLU and RoPE Q/K/V at a decoder's shapes: bit-identical to the f32
+    epilogue applied to the plain projections of the same launch family."""
+    import torch
+    cols = 4096
+    g_codes, g_s, _ = _tensor(synth, 1, 14336, cols, 1, False)
+    u_codes, u_s, _ = _tensor(synth, 2, 14336, cols, 1, False)
+    x = synth.normal_fast(3, cols)
+    X = torch.from_numpy(x).to(dev)
+    keep = [_dev(qc, dev, a) for a in (g_codes, g_s, u_codes, u_s)]   # device buffers stay alive
+    G = qc.cint8_weights(keep[0], keep[1], None, 14336, cols, 1)
+    U = qc.cint8_weights(keep[2], keep[3], None, 14336, cols, 1)
+    gate = torch.empty(14336, dtype=torch.float32, device=dev)
+    up = torch.empty(14336, dtype=torch.float32, device=dev)
+    out = torch.empty(14336, dtype=torch.float32, device=dev)
+    assert qc.cint8_project_raw(0, [G, U], X, 0, 1, [gate, up], [0, 0]) == 0
+    assert qc.cint8_project_raw(1, [G, U], X, 0, 1, [out], [0]) == 0
+    g, u = gate.cpu().numpy(), up.cpu().numpy()
+    gp = torch.empty(14336, dtype=torch.float32, device=dev)
+    assert qc.cint8_project_raw(0, [G], X, 0, 1, [gp], [0]) == 0
+    assert np.array_equal(gp.cpu().numpy().view(np.uint32), g.view(np.uint32))
+    want = (g / (np.float32(1.0) + np.exp(-g))).astype(np.float32) * u
+    o = out.cpu().numpy()
+    assert np.all(np.abs(o - want) <= 4e-7 * np.abs(want) + 1e-30)
+    # RoPE: 32 query heads, 8 kv heads of 128
+    q_c, q_s, _ = _tensor(synth, 4, 4096, cols, 1, False)
+    k_c, k_s, _ = _tensor(synth, 5, 1024, cols, 1, False)
+    v_c, v_s, _ = _tensor(synth, 6, 1024, cols, 1, False)
+    keep += [_dev(qc, dev, a) for a in (q_c, q_s, k_c, k_s, v_c, v_s)]
+    Ws = [qc.cint8_weights(keep[4 + 2 * i], keep[5 + 2 * i], None, c.shape[0], cols, 1)
+          for i, c in enumerate((q_c, k_c, v_c))]
+    ang = synth.normal_fast(8, 64)
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    plain = [torch.empty(r, dtype=torch.float32, device=dev) for r in (4096, 1024, 1024)]
+    assert qc.cint8_project_raw(0, Ws, X, 0, 1, plain, [0, 0, 0]) == 0
+    rot = [torch.empty(r, dtype=torch.float32, device=dev) for r in (4096, 1024, 1024)]
+    assert qc.cint8_project_raw(2, Ws, X, 0, 1, rot, [0, 0, 0], rope_cos=torch.from_numpy(cs).to(dev),
+                                rope_sin=torch.from_numpy(sn).to(dev), head_dim=128) == 0
+    for i, heads in ((0, 32), (1, 8)):
+        p = plain[i].cpu().numpy().reshape(heads, 2, 64)
+        a, b = p[:, 0], p[:, 1]
+        want = np.stack([a * cs - b * sn, b * cs + a * sn], 1).reshape(-1)
+        assert np.array_equal(rot[i].cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(rot[2].cpu().numpy().view(np.uint32), plain[2].cpu().numpy().view(np.uint32))
+
+
+def test_cint8_validation(qc, synth, dev):
+    import torch
+    codes, scales, _ = _tensor(synth, 9, 64, 128, 1, False)
+    C, S = _dev(qc, dev, codes), _dev(qc, dev, scales)
+    w = qc.cint8_weights(C, S, None, 64, 128, 1)
+    x = torch.zeros(128, dtype=torch.float32, device=dev)
+    y = torch.full((64,), 3.0, dtype=torch.float32, device=dev)
+    call = qc.cint8_project_raw
+    assert call(5, [w], x, 0, 1, [y], [0]) == 3                     # mode
+    assert call(0, [w], x, 0, 1, [y], [0], activation=7) == 3       # activation
+    assert call(0, [w], x, 0, 0, [y], [0]) == 1                     # m
+    assert call(1, [w], x, 0, 1, [y], [0]) == 1                     # SwiGLU needs two
+    assert call(2, [w], x, 0, 2, [y], [0], rope_cos=x, rope_sin=x, head_dim=16) == 1
+    assert call(2, [w], x, 0, 1, [y], [0], rope_cos=x, rope_sin=x, head_dim=15) == 1
+    assert call(0, [qc.cint8_weights(C, S, None, 64, 128, 3)], x, 0, 1, [y], [0]) == 1
+    assert call(0, [w], x, 3, 1, [y], [0]) == 2                     # storage type
+    assert call(0, [w], x, 0, 1, [y], [9]) == 2
+    assert call(0, [w], None, 0, 1, [y], [0]) == 3                  # nulls
+    assert call(0, [w], x, 0, 1, [None], [0]) == 3
+    assert call(0, [qc.cint8_weights(C, None, None, 64, 128, 1)], x, 0, 1, [y], [0]) == 3
+    torch.cuda.synchronize()
+    assert np.all(y.cpu().numpy() == 3.0)

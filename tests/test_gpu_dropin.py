@@ -62,15 +62,17 @@ def test_dropin_quantized_matmuls(run, oracle, fmt, p):
     a, st = run
     n, k, m = 96, 256, 5
     for name in ("packed_size", "pack", "pack2", "qgemv", "qgemm", "up_gate", "up_gate_gelu",
-                 "up_gate_silu", "qkv", "w8a8", "prepare", "prepacked_gemv", "prepacked_m5",
-                 "prepacked_m70"):
+                 "up_gate_silu", "qkv", "w8a8", "prepare", "prepacked_m5", "prepacked_m70"):
         assert st[p + name] == 0, name
+    # qgemv_prepacked is the storage route, which (as in the reference,
+    # kernels/quantization/qgemm_canonical.cpp:4275-4291,4647-4653) takes only
+    # canonical-layout weights
+    assert st[p + "prepacked_gemv"] == 2
     w, w2, x = a[p + "w"].reshape(n, k), a[p + "w2"].reshape(n, k), a[p + "x"].reshape(m, k)
     packed, packed2 = a[p + "packed"], a[p + "packed2"]
     assert _bits_equal(packed, oracle.pack(fmt, w)[1])
     assert _bits_equal(packed2, oracle.pack(fmt, w2)[1])
     _contract(oracle, fmt, packed, x[0], a[p + "qgemv_y"], n, k)
-    _contract(oracle, fmt, packed, x[0], a[p + "prepacked_gemv_y"], n, k)
     for name in ("qgemm_y", "prepacked_m5_y"):
         ym = a[p + name].reshape(m, n)
         for r in range(m):

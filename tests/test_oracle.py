@@ -45,6 +45,14 @@ mistake would break:
                         at a zero angle the outputs are the plain row orders'
                         GEMV outputs bit for bit; each rotated pair keeps its
                         f64 norm.
+  * canonical int8 projections (cint8_dequant / cint8_project_f64) -- the
+                        reference's own prepared storage projections
+                        (qgemm_prepacked_*_storage, oracle/_ref) over every
+                        scenario of tests/cpp/storage_scenarios.h (symmetric
+                        and affine, channel and group scales, f32/f16/bf16,
+                        bias + every activation, gate/up, SwiGLU, Q/K/V,
+                        RoPE with cache slots) stay within the normalised
+                        contract of the f64 restatement; a hand-worked case.
   * quantize_int8_asymmetric / dequantize -- bit-identical to the reference's
                         functions on random rows and on the out-of-range
                         conversions (1-ulp spreads); the reference test's
@@ -620,3 +628,25 @@ def test_qkv_rope_kv_properties(oracle):
             p = plain[0 if out is q else 1].reshape(heads, 2, hd // 2).astype(np.float64)
             assert np.allclose(np.hypot(o[:, 0], o[:, 1]), np.hypot(p[:, 0], p[:, 1]),
                                rtol=1e-6, atol=1e-9)
+
+
+# ------------------------------------------------- canonical int8 projections ---
+
+def test_cint8_oracle_matches_reference_scenarios(oracle, ref, tmp_path):
+    import storage_eval
+    assert ref.storage_scenarios(tmp_path) == 0
+    status, bad = storage_eval.check(oracle, tmp_path)
+    assert not bad, bad[:10]
+    assert len(status) > 100
+
+
+def test_cint8_dequant_known_answer(oracle):
+    # two rows, four columns, groups of two; affine zero points
+    codes = np.array([[1, -2, 3, 127], [-128, 0, 5, -5]], np.int8)
+    scales = np.array([0.5, 2.0, 0.25, 1.0], np.float32)
+    zeros = np.array([1.0, -1.0, 0.0, 2.0], np.float32)
+    w = oracle.cint8_dequant(codes, scales, zeros, 2, 4, 2)
+    assert w.tolist() == [[0.0, -1.5, 8.0, 256.0], [-32.0, 0.0, 3.0, -7.0]]
+    y, wn = oracle.cint8_project_f64(np.array([[1, 2, 3, 4]], np.float32), w)
+    assert y.tolist() == [[0 - 3 + 24 + 1024, -32 + 0 + 9 - 28]]
+    assert np.allclose(wn, np.linalg.norm(w.astype(np.float64), axis=1))
