@@ -313,6 +313,13 @@ int qc_hip_set_qgemm_plan(int waves, int stages);
  * test knob with no reference counterpart. */
 int qc_hip_set_qgemm_panel(int mode);
 
+/* qgemm route for 2 <= m <= 8: 0 (default) = by shape (the exact-digit rows
+ * kernel -- one pass over W for all rows, every row bit-identical to
+ * qc_hip_qgemv of that row -- for m = 2 and K <= 4096, and for m <= 4 with
+ * also N <= 8192; the MFMA small-batch kernels otherwise), -1 = never,
+ * 1 = always.  Tuning and test knob with no reference counterpart. */
+int qc_hip_set_qgemm_rows(int mode);
+
 /* on != 0: qc_hip_rms_norm_add_quant_int8 replays the element-order sum of
  * squares for every row instead of only for rows whose float norm the
  * parallel sum cannot settle (process-wide; results are identical either

@@ -17,6 +17,7 @@ struct GemvTuning {
   int qgemm_waves = 0;    // small-batch GEMM waves per workgroup (4, 8; 0 = from the shape)
   int qgemm_stages = 0;   // small-batch GEMM K stages per workgroup (1..16; 0 = from the shape)
   int qgemm_panel = 0;    // 2-D GEMM route: 0 = for m >= 64, -1 = never, 1 / 2 = always (K ranges)
+  int qgemm_rows = 0;     // exact-digit rows route for 2 <= m <= 8: 0 = by shape, -1 = never, 1 = always
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
@@ -28,6 +29,12 @@ hipError_t launch_qgemm(int fmt, const void* W, const float* x, float* y, long l
 // M = 1 GEMV with exact int8 digit dots (K % 64 == 0, W 4-byte aligned).
 hipError_t launch_qgemv_dot(int fmt, const void* W, const float* x, float* y, int n, int k,
                             int rows_per_wave, hipStream_t s);
+
+// y[m][n] for m rows of x (K % 64 == 0, W 4-byte aligned, x rows of k
+// floats): passes of up to 8 activation rows over W, each output
+// bit-identical to launch_qgemv_dot of its row.  rows_per_wave: 0, 1, 2 or 4.
+hipError_t launch_qgemm_rows(int fmt, const void* W, const float* x, float* y, int n, int k,
+                             int m, int rows_per_wave, hipStream_t s);
 
 // Fused GEMVs over one x in a single launch (K % 64 == 0, every W 4-byte
 // aligned, x 16-byte aligned): nseg matrices W[i] of rows[i] rows into y[i] (act = -1), or up

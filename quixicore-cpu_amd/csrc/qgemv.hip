@@ -265,6 +265,18 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, 
   }
   const int vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (k % 4 == 0);
   if (m == 1) return launch_qgemv_dot(FMT, W, x, y, n, k, t.rows_per_wave, s);
+  // The exact-digit rows kernel (one pass over W, no scratch, no prep launch;
+  // every row bit-identical to the GEMV of that row) where it measured faster
+  // than the MFMA kernels on MI355X: m = 2 with K in one 4096-column chunk,
+  // and m = 3, 4 when N is also small enough that the MFMA grid leaves CUs
+  // idle (q8_0 / q4_0, K = 4096: m = 2 N = 4096 8.2 / 7.4 us vs 11.8 / 11.3;
+  // m = 4 N = 4096 11.3 / 10.1 vs 11.3 / 11.5; m = 4 N = 14336 23.4 vs 18.8).
+  const bool rows_pays = k <= 4096 && (m == 2 || (m <= 4 && n <= 8192));
+  if (m <= 8 && k % 64 == 0 && t.qgemm_rows >= 0 && (t.qgemm_rows > 0 || rows_pays)) {
+    int rb = t.rows_per_wave == 1 || t.rows_per_wave == 2 || t.rows_per_wave == 4 ? t.rows_per_wave : 0;
+    if (rb == 0) rb = m == 2 ? 1 : 2;
+    return launch_qgemm_rows(FMT, W, x, y, n, k, m, rb, s);
+  }
   // The MFMA path addresses W with 32-bit offsets from its base (plus up to
   // one stage of row overrun).
   const long long w_bytes = static_cast<long long>(n) * (k / 32) * Fmt<FMT>::block_bytes;

@@ -31,6 +31,8 @@
 // digits of x in LDS (the barrier after the digit build waits on LDS traffic
 // only), and then keeps a small window of (pair, row) items in flight ahead
 // of the one it computes.
+#include <algorithm>
+
 #include "qc_device.h"
 #include "qc_internal.h"
 
@@ -86,8 +88,70 @@ __device__ __forceinline__ void load_x(float (&v)[HPT][16], const float* __restr
   }
 }
 
-// Digits of the loaded half-blocks into LDS; the two halves of a block sit
-// in lanes t and t^1.
+// Digits of half-block h (16 values v) of one row of x into that row's LDS
+// chunk; the two halves of a block sit in lanes t and t^1 (both call this
+// together: the block maximum is exchanged between them).
+template <bool WITH_SUMS>
+__device__ __forceinline__ void build_half(uint8_t* lds, const float* v, int h, int kc) {
+  float m = 0.f;
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    m = fmaxf(m, fabsf(v[i]));
+    finite = finite && isfinite(v[i]);
+  }
+  m = fmaxf(m, xor1_f32(m));
+  finite = finite && (xor1_i32(finite ? 1 : 0) != 0);
+  int ex = 0;
+  (void)frexpf(m, &ex);                            // m < 2^ex
+  const int e = finite ? ex - 21 : 0;
+  int d0[16], d1[16], d2[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    int q = finite ? __float2int_rn(ldexpf(v[i], -e)) : 0;   // |x * 2^-e| <= 2^21
+    q = q > 2097151 ? 2097151 : q;
+    d0[i] = q >> 14;                               // [-128, 127]
+    d1[i] = (q >> 7) & 127;                        // [0, 127]
+    d2[i] = q & 127;                               // [0, 127]
+  }
+  const int pair = h >> 2;
+  uint8_t* rec = lds + pair * kRec + (h & 3) * 16;
+  uint4 p0, p1, p2;
+  p0.x = pack4(d0[0], d0[1], d0[2], d0[3]);    p0.y = pack4(d0[4], d0[5], d0[6], d0[7]);
+  p0.z = pack4(d0[8], d0[9], d0[10], d0[11]);  p0.w = pack4(d0[12], d0[13], d0[14], d0[15]);
+  p1.x = pack4(d1[0], d1[1], d1[2], d1[3]);    p1.y = pack4(d1[4], d1[5], d1[6], d1[7]);
+  p1.z = pack4(d1[8], d1[9], d1[10], d1[11]);  p1.w = pack4(d1[12], d1[13], d1[14], d1[15]);
+  p2.x = pack4(d2[0], d2[1], d2[2], d2[3]);    p2.y = pack4(d2[4], d2[5], d2[6], d2[7]);
+  p2.z = pack4(d2[8], d2[9], d2[10], d2[11]);  p2.w = pack4(d2[12], d2[13], d2[14], d2[15]);
+  *reinterpret_cast<uint4*>(rec) = p0;
+  *reinterpret_cast<uint4*>(rec + 64) = p1;
+  *reinterpret_cast<uint4*>(rec + 128) = p2;
+  const int blk = h >> 1;
+  if constexpr (WITH_SUMS) {
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s0 += d0[i];
+      s1 += d1[i];
+      s2 += d2[i];
+    }
+    s0 += xor1_i32(s0);
+    s1 += xor1_i32(s1);
+    s2 += xor1_i32(s2);
+    if ((h & 1) == 0) {
+      int* sums = reinterpret_cast<int*>(lds + dsum_off(kc));
+      sums[blk] = s0;
+      sums[(kc >> 5) + blk] = s1;
+      sums[2 * (kc >> 5) + blk] = s2;
+    }
+  }
+  if ((h & 1) == 0) {
+    reinterpret_cast<int*>(lds + exp_off(kc))[blk] = e;
+    reinterpret_cast<float*>(lds + gate_off(kc))[blk] = finite ? 1.0f : __builtin_nanf("");
+  }
+}
+
+// Digits of the loaded half-blocks into LDS.
 template <bool WITH_SUMS, int HPT, int NT>
 __device__ __forceinline__ void build_digits(uint8_t* lds, const float (&xv)[HPT][16], int clen,
                                              int kc) {
@@ -96,63 +160,7 @@ __device__ __forceinline__ void build_digits(uint8_t* lds, const float (&xv)[HPT
   for (int j = 0; j < HPT; ++j) {
     const int h = threadIdx.x + NT * j;
     if (h >= nh) break;
-    const float* v = xv[j];
-    float m = 0.f;
-    bool finite = true;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      m = fmaxf(m, fabsf(v[i]));
-      finite = finite && isfinite(v[i]);
-    }
-    m = fmaxf(m, xor1_f32(m));
-    finite = finite && (xor1_i32(finite ? 1 : 0) != 0);
-    int ex = 0;
-    (void)frexpf(m, &ex);                            // m < 2^ex
-    const int e = finite ? ex - 21 : 0;
-    int d0[16], d1[16], d2[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      int q = finite ? __float2int_rn(ldexpf(v[i], -e)) : 0;   // |x * 2^-e| <= 2^21
-      q = q > 2097151 ? 2097151 : q;
-      d0[i] = q >> 14;                               // [-128, 127]
-      d1[i] = (q >> 7) & 127;                        // [0, 127]
-      d2[i] = q & 127;                               // [0, 127]
-    }
-    const int pair = h >> 2;
-    uint8_t* rec = lds + pair * kRec + (h & 3) * 16;
-    uint4 p0, p1, p2;
-    p0.x = pack4(d0[0], d0[1], d0[2], d0[3]);    p0.y = pack4(d0[4], d0[5], d0[6], d0[7]);
-    p0.z = pack4(d0[8], d0[9], d0[10], d0[11]);  p0.w = pack4(d0[12], d0[13], d0[14], d0[15]);
-    p1.x = pack4(d1[0], d1[1], d1[2], d1[3]);    p1.y = pack4(d1[4], d1[5], d1[6], d1[7]);
-    p1.z = pack4(d1[8], d1[9], d1[10], d1[11]);  p1.w = pack4(d1[12], d1[13], d1[14], d1[15]);
-    p2.x = pack4(d2[0], d2[1], d2[2], d2[3]);    p2.y = pack4(d2[4], d2[5], d2[6], d2[7]);
-    p2.z = pack4(d2[8], d2[9], d2[10], d2[11]);  p2.w = pack4(d2[12], d2[13], d2[14], d2[15]);
-    *reinterpret_cast<uint4*>(rec) = p0;
-    *reinterpret_cast<uint4*>(rec + 64) = p1;
-    *reinterpret_cast<uint4*>(rec + 128) = p2;
-    const int blk = h >> 1;
-    if constexpr (WITH_SUMS) {
-      int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s0 += d0[i];
-        s1 += d1[i];
-        s2 += d2[i];
-      }
-      s0 += xor1_i32(s0);
-      s1 += xor1_i32(s1);
-      s2 += xor1_i32(s2);
-      if ((h & 1) == 0) {
-        int* sums = reinterpret_cast<int*>(lds + dsum_off(kc));
-        sums[blk] = s0;
-        sums[(kc >> 5) + blk] = s1;
-        sums[2 * (kc >> 5) + blk] = s2;
-      }
-    }
-    if ((h & 1) == 0) {
-      reinterpret_cast<int*>(lds + exp_off(kc))[blk] = e;
-      reinterpret_cast<float*>(lds + gate_off(kc))[blk] = finite ? 1.0f : __builtin_nanf("");
-    }
+    build_half<WITH_SUMS>(lds, xv[j], h, kc);
   }
 }
 
@@ -451,6 +459,163 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
       out[g - (in2 ? s2 : in1 ? s1 : 0)] = t[r];
     }
   }
+}
+
+// ------------------------------------------------------- small-batch rows
+// qgemm for a few activation rows (kernels/quantization/qgemm_ref.cpp:
+// 141-164: each row of y is the qgemv of that row of x).  The GEMV's method
+// and lane mapping per row -- lane l owns pairs p = l (mod 64) in increasing
+// order, the same digits, pair dots and wave reduction -- so every output is
+// bit-identical to qc_hip_qgemv of its activation row.  MB activation rows
+// share one pass over W: a workgroup builds the digits of all MB rows of a
+// chunk of kc = 4096 columns in LDS (MB records of lds_size(kc)), and each of
+// its waves runs every pair of its RB weight rows against the MB digit sets.
+//
+// When the whole K fits one chunk the grid is persistent: workgroup b builds
+// the digits once and then takes row groups b, b + gridDim.x, ... (NW * RB
+// rows each), with the next group's weights in flight while the current one
+// is computed.  Otherwise each workgroup takes one row group and rebuilds the
+// digits per chunk.  Rows of x past m are masked (their outputs not stored).
+template <int FMT, int NW, int RB, int MB, bool VEC>
+__global__ __launch_bounds__(64 * NW) void qgemm_rows_kernel(const uint8_t* __restrict__ W,
+                                                             const float* __restrict__ x,
+                                                             float* __restrict__ y, int n, int k,
+                                                             int m, int kc) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int BB = Fmt<FMT>::block_bytes;
+  constexpr int PD = Fmt<FMT>::pair_dwords;
+  constexpr int NT = 64 * NW;
+  constexpr int HB = 256;                          // half-blocks per row and chunk (kc <= 4096)
+  constexpr int IPT = (MB * HB + NT - 1) / NT;     // (row, half-block) items per thread
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const long long row_bytes = static_cast<long long>(k >> 5) * BB;
+  const size_t lsz = lds_size(kc);
+  const int groups = (n + NW * RB - 1) / (NW * RB);
+  const bool single = k <= kc;
+
+  // digits of chunk [c0, c0 + clen) of every activation row into LDS
+  auto build = [&](int c0, int clen) {
+    const int nh = clen >> 4;
+    float xv[IPT][16];
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int item = threadIdx.x + NT * j;
+      const int r = min(item / HB, m - 1);
+      const int h = min(item % HB, nh - 1);
+      const float* src = x + static_cast<long long>(r) * k + c0 + 16 * h;
+      if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<float4*>(&xv[j][4 * i]) = reinterpret_cast<const float4*>(src)[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xv[j][i] = src[i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int item = threadIdx.x + NT * j;
+      const int r = item / HB, h = item % HB;
+      if (r < MB && r < m && h < nh) build_half<FMT == kQ4_0>(lds + r * lsz, xv[j], h, kc);
+    }
+  };
+
+  auto rows_of = [&](int g, const uint8_t** wrow) {
+    const int row0 = (g * NW + wave) * RB;
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      wrow[r] = W + static_cast<long long>(min(row0 + r, n - 1)) * row_bytes;
+    return row0;
+  };
+
+  auto store = [&](int row0, float (&acc)[RB][MB]) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int mm = 0; mm < MB; ++mm) {
+        const float t = wave_sum_lane63(acc[r][mm]);
+        if (lane == 63 && row0 + r < n && mm < m) y[static_cast<long long>(mm) * n + row0 + r] = t;
+      }
+  };
+
+  if (single) {
+    // one chunk: digits once, then a stream of row groups; two register sets
+    // of weights alternate (statically, so neither leaves registers): one is
+    // computed while the next group's loads fill the other
+    const int pend = k >> 6;
+    const int p = lane;                            // this lane's only pair
+    const int G = gridDim.x;
+    uint32_t wa[RB][PD], wb[RB][PD];
+    auto issue = [&](uint32_t (&w)[RB][PD], int g) {
+      const uint8_t* wr[RB];
+      rows_of(min(g, groups - 1), wr);
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        load_pair<FMT>(w[r], wr[r] + static_cast<long long>(min(p, pend - 1)) * (2 * BB));
+    };
+    auto compute = [&](const uint32_t (&w)[RB][PD], int g) {
+      const uint8_t* wr[RB];
+      const int row0 = rows_of(g, wr);
+      float acc[RB][MB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm) acc[r][mm] = 0.f;
+      if (p < pend) {
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm) {
+          PairDigits dg;
+          read_digits<FMT>(dg, lds + mm * lsz, p, kc);
+#pragma unroll
+          for (int r = 0; r < RB; ++r) acc[r][mm] = pair_dot<FMT>(w[r], dg, acc[r][mm]);
+        }
+      }
+      store(row0, acc);
+    };
+    int g = blockIdx.x;
+    issue(wa, g);
+    build(0, k);
+    lds_barrier();
+    for (; g < groups; g += 2 * G) {
+      if (g + G < groups) issue(wb, g + G);
+      compute(wa, g);
+      if (g + G >= groups) break;
+      if (g + 2 * G < groups) issue(wa, g + 2 * G);
+      compute(wb, g + G);
+    }
+    return;
+  }
+
+  // several chunks: one row group per workgroup, digits rebuilt per chunk
+  const uint8_t* wrow[RB];
+  const int row0 = rows_of(blockIdx.x, wrow);
+  float acc[RB][MB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) acc[r][mm] = 0.f;
+  for (int c0 = 0; c0 < k; c0 += kc) {
+    const int clen = min(kc, k - c0);
+    const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
+    const int p = first_pair(pbeg, lane);
+    uint32_t w[RB][PD];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) load_pair<FMT>(w[r], wrow[r] + static_cast<long long>(min(p, pend - 1)) * (2 * BB));
+    if (c0) lds_barrier();
+    build(c0, clen);
+    lds_barrier();
+    if (p < pend) {
+#pragma unroll
+      for (int mm = 0; mm < MB; ++mm) {
+        PairDigits dg;
+        read_digits<FMT>(dg, lds + mm * lsz, p - pbeg, kc);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[r][mm] = pair_dot<FMT>(w[r], dg, acc[r][mm]);
+      }
+    }
+  }
+  store(row0, acc);
 }
 
 // ------------------------------------------------------------ qgemv_w8a8
@@ -894,6 +1059,78 @@ hipError_t launch_qgemv_multi(int fmt, int nseg, const void* const* W, float* co
   }
   return fmt == kQ8_0 ? launch_fmt<2, kQ8_0>(sg, x, k, 0, nullptr, s)
                       : launch_fmt<2, kQ4_0>(sg, x, k, 0, nullptr, s);
+}
+
+// Small-batch rows: passes of MB activation rows over W (m <= 8 per pass is
+// the intended use).  K % 64 == 0 and W 4-byte aligned (checked by the
+// caller).  One chunk of kc = 4096 columns per step (MB * lds_size(4096) of
+// LDS); the rows per wave and workgroup width by the GEMV's shape rule.
+template <int FMT, int NW, int RB, int MB>
+hipError_t launch_rows(const uint8_t* W, const float* x, float* y, int n, int k, int m, hipStream_t s) {
+  const int kc = k < 4096 ? k : 4096;
+  const long long groups = (static_cast<long long>(n) + NW * RB - 1) / (NW * RB);
+  const size_t lds = MB * lds_size(kc);
+  // persistent grid (one chunk): as many workgroups as fit on the chip at once
+  // (rounded so that every workgroup takes the same number of row groups)
+  long long grid = groups;
+  if (k <= kc) {
+    const int per_cu = static_cast<int>(std::min<size_t>(160 * 1024 / lds, 16 / NW));
+    const long long most = static_cast<long long>(device_cu_count()) * std::max(per_cu, 1);
+    const long long rounds = (groups + most - 1) / most;
+    grid = (groups + rounds - 1) / rounds;
+  }
+  const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && k % 4 == 0;
+  if (vec)
+    qgemm_rows_kernel<FMT, NW, RB, MB, true><<<static_cast<unsigned>(grid), 64 * NW, lds, s>>>(W, x, y, n, k, m, kc);
+  else
+    qgemm_rows_kernel<FMT, NW, RB, MB, false><<<static_cast<unsigned>(grid), 64 * NW, lds, s>>>(W, x, y, n, k, m, kc);
+  return hipGetLastError();
+}
+
+// Rows per wave: rb (1, 2 or 4) when given, else 2; 8-wave workgroups, or
+// 4-wave ones when K spans several chunks and 8-wave ones would leave CUs
+// idle (the GEMV's shape rule).
+template <int FMT, int MB>
+hipError_t launch_rows_mb(const uint8_t* W, const float* x, float* y, int n, int k, int m,
+                          int rb, hipStream_t s) {
+  if (rb != 1 && rb != 4) rb = 2;
+  if constexpr (MB == 8) rb = rb == 4 ? 2 : rb;    // 4 rows x 8 digit sets exceed the registers
+  if constexpr (MB < 8) {
+    if (k > 4096) {
+      static const int cand[] = {2, 1};
+      const Shape sh = pick_shape(n, cand, 2, rb == 4 ? 2 : rb);
+      if (sh.nw == 4)
+        return sh.rb == 2 ? launch_rows<FMT, 4, 2, MB>(W, x, y, n, k, m, s)
+                          : launch_rows<FMT, 4, 1, MB>(W, x, y, n, k, m, s);
+      rb = sh.rb;
+    }
+  }
+  return rb == 4 ? launch_rows<FMT, 8, 4, MB>(W, x, y, n, k, m, s)
+       : rb == 2 ? launch_rows<FMT, 8, 2, MB>(W, x, y, n, k, m, s)
+                 : launch_rows<FMT, 8, 1, MB>(W, x, y, n, k, m, s);
+}
+
+// y[m][n] for m rows of x in passes of at most 8 rows, each output
+// bit-identical to launch_qgemv_dot of its row.
+hipError_t launch_qgemm_rows(int fmt, const void* Wv, const float* x, float* y, int n, int k,
+                             int m, int rows_per_wave, hipStream_t s) {
+  const auto* W = static_cast<const uint8_t*>(Wv);
+  for (int m0 = 0; m0 < m; m0 += 8) {
+    const int mp = min(8, m - m0);
+    const float* xp = x + static_cast<long long>(m0) * k;
+    float* yp = y + static_cast<long long>(m0) * n;
+    hipError_t e;
+    if (fmt == kQ8_0)
+      e = mp <= 2 ? launch_rows_mb<kQ8_0, 2>(W, xp, yp, n, k, mp, rows_per_wave, s)
+        : mp <= 4 ? launch_rows_mb<kQ8_0, 4>(W, xp, yp, n, k, mp, rows_per_wave, s)
+                  : launch_rows_mb<kQ8_0, 8>(W, xp, yp, n, k, mp, rows_per_wave, s);
+    else
+      e = mp <= 2 ? launch_rows_mb<kQ4_0, 2>(W, xp, yp, n, k, mp, rows_per_wave, s)
+        : mp <= 4 ? launch_rows_mb<kQ4_0, 4>(W, xp, yp, n, k, mp, rows_per_wave, s)
+                  : launch_rows_mb<kQ4_0, 8>(W, xp, yp, n, k, mp, rows_per_wave, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // Q (and, kv_rows > 0, K and V) projections of one token with RoPE on Q and

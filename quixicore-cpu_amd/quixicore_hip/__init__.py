@@ -64,6 +64,7 @@ _SIGS = {
     "qc_hip_dequantize_int8_asymmetric": ([_P, _P, _P, _P, _LL, _LL, _P], _I),
     "qc_hip_set_norm_sequential_sum": ([_I], _I),
     "qc_hip_set_qgemm_panel": ([_I], _I),
+    "qc_hip_set_qgemm_rows": ([_I], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -307,6 +308,13 @@ def set_qgemm_panel(mode=0):
     """qgemm route for M >= 2: 0 = 2-D GEMM for M >= 64, -1 = never,
     1 / 2 = always with one / two K ranges."""
     _check(lib.qc_hip_set_qgemm_panel(mode), "set_qgemm_panel")
+
+
+def set_qgemm_rows(mode=0):
+    """qgemm route for 2 <= M <= 8: 0 = by shape (exact-digit rows kernel for
+    M = 2, and M <= 4 with N <= 8192, at K <= 4096), -1 = never (MFMA
+    small-batch kernels), 1 = always."""
+    _check(lib.qc_hip_set_qgemm_rows(mode), "set_qgemm_rows")
 
 
 def set_norm_sequential_sum(on):

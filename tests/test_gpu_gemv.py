@@ -146,6 +146,7 @@ def test_qgemm_every_plan(qc, oracle, synth, dev, fmt, m):
     packed, _ = _case(oracle, synth, fmt, n, k, 91 + m)
     x = synth.normal_fast(950 + m, m * k).reshape(m, k)
     P, X = torch.from_numpy(packed).to(dev), torch.from_numpy(x).to(dev)
+    qc.set_qgemm_rows(-1)               # the MFMA kernels also for m <= 8
     try:
         for waves in (4, 8):
             for stages in (1, 2, 4, 8, 16):
@@ -156,6 +157,62 @@ def test_qgemm_every_plan(qc, oracle, synth, dev, fmt, m):
                     _check_rows(oracle, fmt, packed, x[r], Y[r], n, k)
     finally:
         qc.set_qgemm_plan(0, 0)
+        qc.set_qgemm_rows(0)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("m,n,k,x_off", [(2, 257, 4096, 0), (3, 4096, 4096, 0),
+                                         (4, 14336, 4096, 0), (5, 300, 14336, 0),
+                                         (8, 4096, 4096, 0), (7, 1000, 64, 0), (6, 70, 8256, 0),
+                                         (8, 130, 4096, 1), (2, 14336, 4096, 3)])
+def test_qgemm_rows_bitwise_gemv(qc, oracle, synth, dev, fmt, m, n, k, x_off):
+    """The exact-digit rows kernel (forced for every 2 <= M <= 8 here): every
+    row of y is bit-identical to qgemv of that activation row (the
+    reference's qgemm is one qgemv per row, kernels/quantization/
+    qgemm_ref.cpp:156-162), for chunked K (> 4096), ragged N, and x off
+    16-byte alignment; the MFMA route for the same shape stays within the
+    contract; the automatic route is one of the two."""
+    import torch
+    print(f"qgemm rows fmt={fmt} m={m} n={n} k={k} x_off={x_off}", flush=True)
+    packed, _ = _case(oracle, synth, fmt, n, k, 500 + m)
+    x = synth.normal_fast(600 + m + k, m * k).reshape(m, k)
+    P = torch.from_numpy(packed).to(dev)
+    buf = torch.zeros(m * k + x_off, dtype=torch.float32, device=dev)
+    buf[x_off:] = torch.from_numpy(x.reshape(-1)).to(dev)
+    X = buf[x_off:].view(m, k)
+    Y = torch.empty(m * n, dtype=torch.float32, device=dev)
+    for rb in (1, 2, 4):
+        qc.set_qgemm_rows(1)
+        qc.set_gemv_rows_per_wave(rb)
+        try:
+            Yr = torch.empty(m * n, dtype=torch.float32, device=dev)
+            assert qc.qgemm_raw(fmt, P, X, Yr, m, n, k) == 0
+        finally:
+            qc.set_qgemm_rows(0)
+            qc.set_gemv_rows_per_wave(0)
+        if rb > 1:
+            assert np.array_equal(Yr.cpu().numpy().view(np.uint32), Y.cpu().numpy().view(np.uint32))
+        Y = Yr
+    Y = Y.cpu().numpy().reshape(m, n)
+    for r in range(m):
+        yr = torch.empty(n, dtype=torch.float32, device=dev)
+        assert qc.qgemv_raw(fmt, P, X[r], yr, n, k) == 0
+        assert np.array_equal(Y[r].view(np.uint32), yr.cpu().numpy().view(np.uint32)), r
+    for r in (0, m - 1):
+        _check_rows(oracle, fmt, packed, x[r], Y[r], n, k)
+    qc.set_qgemm_rows(-1)
+    try:
+        Y2 = torch.empty(m * n, dtype=torch.float32, device=dev)
+        assert qc.qgemm_raw(fmt, P, X, Y2, m, n, k) == 0
+        Y2 = Y2.cpu().numpy().reshape(m, n)
+    finally:
+        qc.set_qgemm_rows(0)
+    for r in (0, m - 1):
+        _check_rows(oracle, fmt, packed, x[r], Y2[r], n, k)
+    Ya = torch.empty(m * n, dtype=torch.float32, device=dev)
+    assert qc.qgemm_raw(fmt, P, X, Ya, m, n, k) == 0
+    Ya = Ya.cpu().numpy().reshape(m, n).view(np.uint32)
+    assert np.array_equal(Ya, Y.view(np.uint32)) or np.array_equal(Ya, Y2.view(np.uint32))
 
 
 @pytest.mark.parametrize("m,n", [(4, 4096), (32, 14336)])
