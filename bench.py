@@ -48,7 +48,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--only", choices=["headline", "all", "copy", "w8a8", "qgemm", "prefill",
+    p.add_argument("--only", choices=["headline", "all", "copy", "stream", "w8a8", "qgemm", "prefill",
                                       "legs"],
                    default="all",
                    help="copy: a plain 64 MiB device copy, the calibration kernel for "
@@ -108,6 +108,44 @@ def time_steps(launch, steps, warmup):
     gpu_ms = start.elapsed_time(end) / steps
     del graph
     return wall_ms, gpu_ms
+
+
+STREAM_SIZES = (("17.9MB_q8_0_k4096_n4096", 17858560), ("33.1MB_q4_0_k4096_n14336", 33103872),
+                ("62.5MB_q8_0_k4096_n14336", 62464000), ("256MB", 256 << 20))
+
+
+def stream_ceiling(qc, steps, warmup, sizes=STREAM_SIZES, wpcs=(1, 2, 4, 8, 16)):
+    """The streaming-read ceiling at the GEMV footprints: qc_hip_stream_read
+    (16-byte loads, sixteen in flight per thread) over rotated buffers of
+    each size, one launch per step, timed like the GEMV; best over 1-16
+    workgroups per CU."""
+    import torch
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(cus * 16 * 256, dtype=torch.int32, device=dev)
+    cases = {}
+    for name, nbytes in sizes:
+        nb = (nbytes + 15) // 16 * 16
+        copies = rotation(nb)
+        bufs = [torch.empty(nb, dtype=torch.uint8, device=dev).random_(0, 255) for _ in range(copies)]
+        best = None
+        for wpc in wpcs:
+            grid = cus * wpc
+
+            def launch(i, grid=grid):
+                st = qc.lib.qc_hip_stream_read(qc._ptr(bufs[i % copies]), nb, qc._ptr(out), grid,
+                                               qc._stream(None))
+                if st:
+                    raise RuntimeError(f"stream_read status {st}")
+
+            wall, gpu = time_steps(launch, steps, warmup)
+            r = {"bytes": nb, "copies": copies, "grid": grid, "wall_ms": wall, "gpu_ms": gpu,
+                 "gbs": nb / (wall * 1e-3) / 1e9, "kernel_gbs": nb / (gpu * 1e-3) / 1e9}
+            if best is None or r["gpu_ms"] < best["gpu_ms"]:
+                best = r
+        cases[f"stream_read_{name}"] = best
+        del bufs
+    return cases
 
 
 def gemv_case(qc, fmt, n, k, steps, warmup, seed):
@@ -583,12 +621,16 @@ def main():
     if args.rows_per_wave:
         qc.set_gemv_rows_per_wave(args.rows_per_wave)
     if args.only == "copy":
+        # the plain 64 MiB copy that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE
         src = torch.randint(0, 255, (64 << 20,), dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
         for _ in range(args.warmup + args.steps):
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": 64 << 20, "launches": args.warmup + args.steps}))
+        return
+    if args.only == "stream":
+        print_cases(stream_ceiling(qc, args.steps, args.warmup))
         return
     K, W = args.steps, args.warmup
     if args.only in ("w8a8", "qgemm", "prefill", "legs"):
@@ -631,6 +673,9 @@ def main():
     for n_ in (4096, 14336):
         w8[n_], w8ops[n_] = w8a8_case(qc, 2048, n_, 4096, max(20, K // 4), W, keep=True)
     quant = quant_case(qc, 2048, 4096, K, W)
+    # the streaming-read ceiling of the same footprints, measured in this process
+    ceil = stream_ceiling(qc, K, W, sizes=STREAM_SIZES[1:3], wpcs=(2, 4))
+    print_cases(ceil)
     print_cases({"q8_0_gemv_k4096_n14336": q8, "w8a8_m2048_k4096_n4096": w8[4096],
                  "w8a8_m2048_k4096_n14336": w8[14336], "quantize_int8_m2048_k4096": quant})
     secondary = {}
@@ -668,9 +713,13 @@ def main():
         ref.set_threads(1)
     del w8ops
 
-    def gemv_leg(r, key, name):
+    def gemv_leg(r, key, name, ceiling=None):
         base, gate = bases.get(key, (None, None))
-        return {"value": round(r["gbs"], 2), "unit": "GB/s",
+        extra = {}
+        if ceiling is not None:
+            extra = {"stream_read_us": round(ceiling["gpu_ms"] * 1e3, 3),
+                     "pct_of_stream_read": round(100.0 * ceiling["gpu_ms"] / r["gpu_ms"], 1)}
+        return {"value": round(r["gbs"], 2), "unit": "GB/s", **extra,
                 "pct_hbm_peak": round(100.0 * r["gbs"] / HBM_PEAK_GBS, 2),
                 "kernel_us": round(r["gpu_ms"] * 1e3, 3), "bytes_per_step": r["bytes"],
                 "roofline": {"bound": "hbm", "achieved": round(r["kernel_gbs"], 2),
@@ -690,8 +739,10 @@ def main():
                 "cpu_baseline": base, "check": gate}
 
     legs = {
-        "q4_0_gemv_k4096_n14336": gemv_leg(head, "q4_0", "q4_0_gemv_k4096_n14336"),
-        "q8_0_gemv_k4096_n14336": gemv_leg(q8, "q8_0", "q8_0_gemv_k4096_n14336"),
+        "q4_0_gemv_k4096_n14336": gemv_leg(head, "q4_0", "q4_0_gemv_k4096_n14336",
+                                           ceil["stream_read_33.1MB_q4_0_k4096_n14336"]),
+        "q8_0_gemv_k4096_n14336": gemv_leg(q8, "q8_0", "q8_0_gemv_k4096_n14336",
+                                           ceil["stream_read_62.5MB_q8_0_k4096_n14336"]),
         "w8a8_gemm_m2048_k4096_n4096": w8a8_leg(w8[4096], 4096, "w8a8_int8_gemm_m2048_k4096_n4096"),
         "w8a8_gemm_m2048_k4096_n14336": w8a8_leg(w8[14336], 14336,
                                                  "w8a8_int8_gemm_m2048_k4096_n14336"),
@@ -721,6 +772,9 @@ def main():
                    "weight_bytes_per_step": head["weight_bytes"],
                    "parallelism": "single GPU"},
         "pct_hbm_peak": round(100.0 * head["gbs"] / HBM_PEAK_GBS, 2),
+        # a pure 16-byte-load read of the same 33.1 MB in this process (qc_hip_stream_read)
+        "stream_read_us": head_leg["stream_read_us"],
+        "pct_of_stream_read": head_leg["pct_of_stream_read"],
         "roofline": dict(head_leg["roofline"], kernel_us=round(head["gpu_ms"] * 1e3, 3)),
         "cpu_baseline": head_leg["cpu_baseline"],
         "check": head_leg["check"],

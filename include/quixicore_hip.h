@@ -271,6 +271,13 @@ int qc_hip_qgemm_w8a8(const int8_t* w, const int8_t* x, const float* ws, const f
 /* Test seam: the exact int32 accumulators sum_k W[n][k]*X[m][k] into
  * acc[m][n] (k <= 131071).  No reference counterpart (the reference's
  * accumulators are internal to kernels/quantization/int8_gemm_*.cpp). */
+/* Measurement seam with no reference counterpart: reads `bytes` (a multiple
+ * of 16) of device memory with 16-byte loads as fast as the chip allows and
+ * stores one XOR word per thread into out (grid * 256 words).  bench.py times
+ * it at the GEMV's footprint to give the streaming ceiling that the GEMV's
+ * HBM efficiency is judged against. */
+int qc_hip_stream_read(const void* p, long long bytes, uint32_t* out, int grid, void* stream);
+
 int qc_hip_int8_gemm_i32(const int8_t* w, const int8_t* x, int32_t* acc, long long m,
                          long long n, long long k, void* stream);
 

@@ -286,6 +286,12 @@ int qc_hip_int8_gemm_i32(const int8_t* w, const int8_t* x, int32_t* acc, long lo
                                      n, k, false, nullptr, as_stream(stream), g_int8_route));
 }
 
+int qc_hip_stream_read(const void* p, long long bytes, uint32_t* out, int grid, void* stream) {
+  if (bytes <= 0 || bytes % 16 != 0 || grid <= 0) return QC_INVALID_SHAPE;
+  if (p == nullptr || out == nullptr) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_stream_read(p, bytes, out, grid, as_stream(stream)));
+}
+
 int qc_hip_nonfinite_scan(const float* x, long long count, int* dev_flag, void* stream) {
   if (count <= 0) return QC_INVALID_SHAPE;
   if (x == nullptr || dev_flag == nullptr) return QC_INVALID_ARGUMENT;

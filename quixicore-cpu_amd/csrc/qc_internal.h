@@ -132,6 +132,11 @@ hipError_t launch_dequantize_int8_asymmetric(const int8_t* codes, const float* s
                                              const int* zero_points, float* out, long long rows,
                                              long long dim, hipStream_t s);
 
+// Streaming read of `bytes` (multiple of 16) by `grid` workgroups of 256
+// threads; out receives grid * 256 words (measurement seam).
+hipError_t launch_stream_read(const void* p, long long bytes, uint32_t* out, int grid,
+                              hipStream_t s);
+
 // *flag = 1 if any of x[0..count) is NaN or +-inf (flag must start at 0).
 hipError_t launch_nonfinite_scan(const float* x, long long count, int* flag, hipStream_t s);
 

@@ -296,4 +296,33 @@ hipError_t launch_unpack(int fmt, const void* packed, float* w, long long n, lon
   return hipGetLastError();
 }
 
+// Streaming-read ceiling: reads `bytes` (a multiple of 16) with 16-byte loads,
+// all sixteen of a 64 KB slab in flight per thread, the workgroups taking
+// interleaved slabs; each thread stores the XOR of what it read (so nothing
+// is optimised away).  A measurement seam: the GEMV's HBM efficiency is
+// judged against it.
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, long long n16,
+                                                          uint32_t* __restrict__ out) {
+  constexpr long long kSlab = 4096;                // 16-byte units per slab (64 KB)
+  uint32_t x = 0;
+  for (long long base = static_cast<long long>(blockIdx.x) * kSlab; base < n16;
+       base += static_cast<long long>(gridDim.x) * kSlab) {
+    uint4 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const long long i = base + threadIdx.x + 256LL * u;
+      v[u] = i < n16 ? p[i] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  out[static_cast<long long>(blockIdx.x) * 256 + threadIdx.x] = x;
+}
+
+hipError_t launch_stream_read(const void* p, long long bytes, uint32_t* out, int grid,
+                              hipStream_t s) {
+  stream_read_kernel<<<grid, 256, 0, s>>>(static_cast<const uint4*>(p), bytes / 16, out);
+  return hipGetLastError();
+}
+
 }  // namespace qc

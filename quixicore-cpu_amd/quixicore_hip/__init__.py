@@ -65,6 +65,7 @@ _SIGS = {
     "qc_hip_set_norm_sequential_sum": ([_I], _I),
     "qc_hip_set_qgemm_panel": ([_I], _I),
     "qc_hip_set_qgemm_rows": ([_I], _I),
+    "qc_hip_stream_read": ([_P, _LL, _P, _I, _P], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
