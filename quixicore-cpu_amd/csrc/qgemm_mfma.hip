@@ -807,16 +807,21 @@ hipError_t launch_nw(int nst, const uint8_t* W, const uint8_t* xf, const float* 
 // Workgroup width (NW wavefronts = 16 NW rows) and stages per workgroup
 // (NST; K is split ceil(nstages / NST) ways) from a simple cost model of
 // this kernel on gfx950: one workgroup per CU at a time (LDS), a CU streams
-// at most ~37 GB/s on its own and the chip ~5.2 TB/s, a workgroup costs
-// ~1.5 us of latency, and a K split beyond two ways costs a reduction kernel
-// (~3.5 us).
+// at most ~37 GB/s on its own and the chip ~5.2 TB/s, a stage costs a wave
+// c(XL) of compute (0.67 / 1.25 / 1.4 / 2.15 us for 4 / 8 / 16 / 32
+// activation rows, fitted on MI355X; 1.4x that for an 8-wave workgroup,
+// whose two waves per SIMD share it), a workgroup costs ~1.5 us of latency,
+// and a K split beyond two ways costs a reduction kernel (~3.5 us).  The
+// compute term is what makes N = 4096 with 8-32 rows split K four ways
+// (6-20% faster than two).
 struct Plan {
   int nw, nst, ks;
 };
 // max_ks > 0 limits the K split to max(max_ks, the fewest ranges possible),
 // which bounds the partial-sum scratch.
 template <int FMT>
-Plan plan_for(int n, int nstages, int cus, int max_ks = 0) {
+Plan plan_for(int n, int nstages, int cus, int max_ks = 0, int xl = 4) {
+  const double c_stage = xl <= 4 ? 0.67e-6 : xl <= 8 ? 1.25e-6 : xl <= 16 ? 1.4e-6 : 2.15e-6;
   Plan best{8, 16, (nstages + 15) / 16};
   double best_t = 1e30;
   const int ks_cap = max_ks > 0 ? std::max(max_ks, (nstages + 15) / 16) : nstages;
@@ -824,13 +829,17 @@ Plan plan_for(int n, int nstages, int cus, int max_ks = 0) {
     const int nslabs = (n + 16 * nw - 1) / (16 * nw);
     for (int nst : {16, 8, 4, 2, 1}) {
       const int ks = (nstages + nst - 1) / nst;
-      if (ks > ks_cap) continue;
+      // for K <= 4096, more than four K ranges measured slower (the
+      // reduction reads ks partial sets)
+      if (ks > ks_cap || (nstages <= 16 && ks > 4)) continue;
       const long long wgs = static_cast<long long>(nslabs) * ks;
       const long long active = wgs < cus ? wgs : cus;
       const long long rounds = (wgs + cus - 1) / cus;
       const double rate = std::min(37e9, 5.2e12 / static_cast<double>(active));
       const double wg_bytes = 16.0 * nw * nst * kStagePairs * PairLayout<FMT>::bytes;
-      const double t = rounds * (wg_bytes / rate + 1.5e-6) + (ks > 2 ? 3.5e-6 : 0.0);
+      const double wg_compute = nst * c_stage * (nw == 8 ? 1.4 : 1.0);
+      const double t = rounds * (std::max(wg_bytes / rate, wg_compute) + 1.5e-6) +
+                       (ks > 2 ? 3.5e-6 : 0.0);
       if (t < best_t * 0.999) {
         best_t = t;
         best = Plan{nw, nst, ks};
@@ -846,7 +855,7 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const int nb = k / 32;
   const int nstages = (nb + kStageBlocks - 1) / kStageBlocks;
   const int nbp = nstages * kStageBlocks;
-  Plan plan = plan_for<FMT>(n, nstages, device_cu_count(), scratch.max_ks);
+  Plan plan = plan_for<FMT>(n, nstages, device_cu_count(), scratch.max_ks, XL);
   if (waves) plan.nw = waves;                      // test / tuning overrides
   if (stages) {
     plan.nst = stages;
