@@ -49,7 +49,7 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", choices=["headline", "all", "copy", "stream", "w8a8", "qgemm", "prefill",
-                                      "legs"],
+                                      "legs", "cint8"],
                    default="all",
                    help="copy: a plain 64 MiB device copy, the calibration kernel for "
                         "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm / prefill / legs: "
@@ -261,6 +261,40 @@ def qgemm_case(qc, n, k, m, steps, warmup, seed, fmt=0):
     return {"m": m, "n": n, "k": k, "bytes": alg, "wall_ms": wall, "gpu_ms": gpu,
             "gbs": alg / (wall * 1e-3) / 1e9, "kernel_gbs": alg / (gpu * 1e-3) / 1e9,
             "kernel_tflops": flops / (gpu * 1e-3) / 1e12}
+
+
+def cint8_case(qc, n, k, m, steps, warmup, groups=1, mode=0):
+    """Prepared storage projection over canonical int8 weights (C ABI
+    qc_hip_cint8_project): f32 x [m][k], f32 y; mode 1 = SwiGLU over two
+    [n][k] matrices.  Rotated weight copies; bytes = codes + scales + x + y."""
+    import torch
+    dev = torch.device("cuda:0")
+    nw = 2 if mode == 1 else 1
+    wbytes = nw * (n * k + 4 * n * groups)
+    copies = rotation(wbytes)
+    g = torch.Generator(device=dev).manual_seed(31)
+    mats = []
+    for _ in range(copies):
+        ws = []
+        for _ in range(nw):
+            codes = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+            scales = torch.rand(n * groups, generator=g, device=dev) * 1e-3 + 1e-5
+            ws.append((codes, scales))
+        mats.append(ws)
+    structs = [[qc.cint8_weights(c, s_, None, n, k, groups) for c, s_ in ws] for ws in mats]
+    x = torch.randn((m, k), generator=g, device=dev)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+
+    def launch(i):
+        st = qc.cint8_project_raw(mode, structs[i % copies], x, 0, m, [y], [0])
+        if st:
+            raise RuntimeError(f"cint8 status {st}")
+
+    wall, gpu = time_steps(launch, steps, warmup)
+    alg = wbytes + 4 * m * k + 4 * m * n
+    return {"m": m, "n": n, "k": k, "groups": groups, "bytes": alg, "copies": copies,
+            "wall_ms": wall, "gpu_ms": gpu, "gbs": alg / (wall * 1e-3) / 1e9,
+            "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
 
 
 def quant_case(qc, m, k, steps, warmup):
@@ -633,7 +667,7 @@ def main():
         print_cases(stream_ceiling(qc, args.steps, args.warmup))
         return
     K, W = args.steps, args.warmup
-    if args.only in ("w8a8", "qgemm", "prefill", "legs"):
+    if args.only in ("w8a8", "qgemm", "prefill", "legs", "cint8"):
         s = {}
         if args.only == "legs":
             # the metric's legs in the order the JSON line lists them
@@ -648,6 +682,11 @@ def main():
                 for m in (512, 2048):
                     s[f"{name}_qgemm_m{m}_k4096_n14336"] = qgemm_case(qc, 14336, 4096, m, K, W,
                                                                      seed=8 + m, fmt=fmt)
+        elif args.only == "cint8":
+            s["cint8_channel_m1_k4096_n14336"] = cint8_case(qc, 14336, 4096, 1, K, W)
+            s["cint8_group128_m1_k4096_n14336"] = cint8_case(qc, 14336, 4096, 1, K, W, groups=32)
+            s["cint8_channel_m4_k4096_n14336"] = cint8_case(qc, 14336, 4096, 4, K, W)
+            s["cint8_swiglu_m1_k4096_n2x14336"] = cint8_case(qc, 14336, 4096, 1, K, W, mode=1)
         elif args.only == "w8a8":
             s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
             s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
@@ -694,6 +733,11 @@ def main():
                 s[f"q8_0_qgemm_m{m}_k4096_n{n_}"] = qgemm_case(qc, n_, 4096, m, K, W, seed=4 + m)
         s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
         s["quantize_int8_asymmetric_m2048_k4096"] = asym_case(qc, 2048, 4096, K, W)
+        # prepared storage projections over canonical int8 weights (f32 x and y)
+        s["cint8_channel_m1_k4096_n14336"] = cint8_case(qc, 14336, 4096, 1, K, W)
+        s["cint8_group128_m1_k4096_n14336"] = cint8_case(qc, 14336, 4096, 1, K, W, groups=32)
+        s["cint8_channel_m4_k4096_n14336"] = cint8_case(qc, 14336, 4096, 4, K, W)
+        s["cint8_swiglu_m1_k4096_n2x14336"] = cint8_case(qc, 14336, 4096, 1, K, W, mode=1)
         for key, r in layer_sweep(qc, max(20, K // 4), W).items():
             s[f"decoder_layer_{key}"] = r
         print_cases(s)

@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "qc_device.h"
 #include "qc_internal.h"
 
@@ -158,6 +160,12 @@ __device__ __forceinline__ void unpack16(const uint4& c, float* q) {
 // 2^gshift columns (else per row, applied once at the end); AFF: zero points.
 // The activations of a K chunk (kc columns, a multiple of 1024) are staged in
 // LDS as f32.  Requires k % 16 == 0 and 16-byte aligned codes.
+//
+// When K fits one chunk the grid is persistent: a workgroup stages x once
+// and takes row groups blockIdx.x, + gridDim.x, ... (kWaves * RW logical
+// rows each), the first codes of its first group in flight before the
+// staging and those of the next group before the current one finishes.
+// Otherwise each workgroup takes one row group and restages x per chunk.
 template <int MB, int RW, bool GRP, bool AFF>
 __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const void* __restrict__ x,
                                                          int xtype, long long ldx, int m0, int mrows,
@@ -166,124 +174,199 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int total = segs.start[segs.nseg];
-  const int g0 = (blockIdx.x * kWaves + wave) * RW;
-  const int8_t* wrow[RW];
-  const float* srow[RW];
-  const float* zrow[RW];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const RowRef rr = logical_row(segs, min(g0 + r, total - 1));
-    wrow[r] = segs.w[rr.seg] + static_cast<long long>(rr.row) * k;
-    srow[r] = segs.scale[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
-    zrow[r] = AFF ? segs.zero[rr.seg] + static_cast<long long>(rr.row) * segs.groups : nullptr;
-  }
-  float acc[RW][MB];
-  float sx[MB];
-#pragma unroll
-  for (int r = 0; r < RW; ++r)
-#pragma unroll
-    for (int mm = 0; mm < MB; ++mm) acc[r][mm] = 0.f;
-#pragma unroll
-  for (int mm = 0; mm < MB; ++mm) sx[mm] = 0.f;
+  const int groups = (total + kWaves * RW - 1) / (kWaves * RW);
 
-  for (int c0 = 0; c0 < k; c0 += kc) {
-    const int clen = min(kc, k - c0);
-    if (c0) __syncthreads();
+  // row pointers of row group g: codes, scales, zero points; returns its first logical row
+  auto rows_of = [&](int g, const int8_t* (&w)[RW], const float* (&sp)[RW],
+                     const float* (&zp)[RW]) {
+    const int g0 = (g * kWaves + wave) * RW;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const RowRef rr = logical_row(segs, min(g0 + r, total - 1));
+      w[r] = segs.w[rr.seg] + static_cast<long long>(rr.row) * k;
+      sp[r] = segs.scale[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
+      zp[r] = AFF ? segs.zero[rr.seg] + static_cast<long long>(rr.row) * segs.groups : nullptr;
+    }
+    return g0;
+  };
+  // x of chunk [c0, c0 + clen) into LDS as f32: four loads in flight per
+  // thread (consecutive threads, consecutive elements), then their stores
+  auto stage_x = [&](int c0, int clen) {
+    constexpr int kBatch = 4;
     for (int mm = 0; mm < MB; ++mm) {
       const int mrow = m0 + mm;
-      for (int i = threadIdx.x; i < clen; i += kThreads)
-        xs[mm * kc + i] = mrow < mrows ? load_x(x, mrow * ldx + c0 + i, xtype) : 0.f;
-    }
-    __syncthreads();
-    const int items = (clen + 1023) >> 10;
-    uint4 cur[RW], nxt[RW];
-    auto fetch = [&](uint4* dst, int j) {
-      const int e = min(c0 + 16 * (lane + 64 * j), k - 16);
+      const bool live = mrow < mrows;
+      for (int base = 0; base < clen; base += kBatch * kThreads) {
+        float v[kBatch];
 #pragma unroll
-      for (int r = 0; r < RW; ++r) dst[r] = *reinterpret_cast<const uint4*>(wrow[r] + e);
-    };
-    fetch(cur, 0);
-    for (int j = 0; j < items; ++j) {
-      if (j + 1 < items) fetch(nxt, j + 1);
-      const int e = c0 + 16 * (lane + 64 * j);
-      if (e < c0 + clen) {
-        float xv[MB][16];
-#pragma unroll
-        for (int mm = 0; mm < MB; ++mm) {
-          const float4* p = reinterpret_cast<const float4*>(xs + mm * kc + (e - c0));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float4 t = p[i];
-            xv[mm][4 * i] = t.x; xv[mm][4 * i + 1] = t.y; xv[mm][4 * i + 2] = t.z; xv[mm][4 * i + 3] = t.w;
-          }
-        }
-        float s16[MB];
-        if constexpr (AFF) {
-#pragma unroll
-          for (int mm = 0; mm < MB; ++mm) {
-            float t = 0.f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) t += xv[mm][i];
-            s16[mm] = t;
-            if constexpr (!GRP) sx[mm] += t;
-          }
+        for (int u = 0; u < kBatch; ++u) {
+          const int i = base + threadIdx.x + u * kThreads;
+          v[u] = live && i < clen ? load_x(x, mrow * ldx + c0 + i, xtype) : 0.f;
         }
 #pragma unroll
-        for (int r = 0; r < RW; ++r) {
-          float q[16];
-          unpack16(cur[r], q);
-          float sc = 1.f, zp = 0.f;
-          if constexpr (GRP) {
-            sc = srow[r][e >> segs.gshift];
-            if constexpr (AFF) zp = zrow[r][e >> segs.gshift];
-          }
-#pragma unroll
-          for (int mm = 0; mm < MB; ++mm) {
-            float t = 0.f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) t = fmaf(q[i], xv[mm][i], t);
-            if constexpr (GRP) {
-              if constexpr (AFF) t = fmaf(-zp, s16[mm], t);
-              acc[r][mm] = fmaf(sc, t, acc[r][mm]);
-            } else {
-              acc[r][mm] += t;
-            }
-          }
+        for (int u = 0; u < kBatch; ++u) {
+          const int i = base + threadIdx.x + u * kThreads;
+          if (i < clen) xs[mm * kc + i] = v[u];
         }
       }
-#pragma unroll
-      for (int r = 0; r < RW; ++r) cur[r] = nxt[r];
     }
-  }
-  // wave sums, returned to every lane; then lane (r * MB + mm) finishes one
-  // value, or (paired modes) one row pair
-  float tot[RW][MB];
+  };
+  // a unit: columns [c, c + 4096) of one row (up to 4 steps of 1024), loaded
+  // as one contiguous 4 KB run per wave (lane: 16 bytes per step)
+  // (GRP: with the group scales and zero points of its four 16-column steps)
+  struct Unit {
+    uint4 c[4];
+    float s[4], z[4];
+  };
+  auto fetch = [&](Unit& u, const int8_t* row, const float* sp, const float* zp, int c) {
 #pragma unroll
-  for (int r = 0; r < RW; ++r)
+    for (int i = 0; i < 4; ++i) {
+      const int e = min(c + 16 * (lane + 64 * i), k - 16);
+      u.c[i] = *reinterpret_cast<const uint4*>(row + e);
+      if constexpr (GRP) {
+        u.s[i] = sp[e >> segs.gshift];
+        if constexpr (AFF) u.z[i] = zp[e >> segs.gshift];
+      }
+    }
+  };
+  // 16 codes of one row at column e against the staged activations
+  auto step = [&](const uint4& c, float sc, float zv, int c0, int e, float (&acc)[MB],
+                  float (&sx)[MB], bool count_x) {
+    float xv[MB][16];
 #pragma unroll
     for (int mm = 0; mm < MB; ++mm) {
-      float v = wave_sum(acc[r][mm]);
-      if constexpr (!GRP) {
-        const float sc = srow[r][0];
-        if constexpr (AFF) v = fmaf(-zrow[r][0], wave_sum(sx[mm]), v);
-        v = sc * v;
+      const float4* p = reinterpret_cast<const float4*>(xs + mm * kc + (e - c0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 t = p[i];
+        xv[mm][4 * i] = t.x; xv[mm][4 * i + 1] = t.y; xv[mm][4 * i + 2] = t.z; xv[mm][4 * i + 3] = t.w;
       }
-      tot[r][mm] = v;
     }
-  if (segs.mode == 0) {
+    float s16[MB];
+    if constexpr (AFF) {
+#pragma unroll
+      for (int mm = 0; mm < MB; ++mm) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t += xv[mm][i];
+        s16[mm] = t;
+        if constexpr (!GRP)
+          if (count_x) sx[mm] += t;
+      }
+    }
+    float q[16];
+    unpack16(c, q);
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t = fmaf(q[i], xv[mm][i], t);
+      if constexpr (GRP) {
+        if constexpr (AFF) t = fmaf(-zv, s16[mm], t);
+        acc[mm] = fmaf(sc, t, acc[mm]);
+      } else {
+        acc[mm] += t;
+      }
+    }
+  };
+  // wave sums, returned to every lane; then lane (r * MB + mm) finishes one
+  // value, or (paired modes) one row pair
+  auto finish = [&](int g0, const float* const (&sp)[RW], const float* const (&zp)[RW],
+                    float (&acc)[RW][MB], float (&sx)[MB]) {
+    float tot[RW][MB];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
-      for (int mm = 0; mm < MB; ++mm)
-        if (lane == r * MB + mm && g0 + r < total && m0 + mm < mrows)
-          epilogue(segs, g0 + r, m0 + mm, tot[r][mm], 0.f);
-  } else {
+      for (int mm = 0; mm < MB; ++mm) {
+        float v = wave_sum(acc[r][mm]);
+        if constexpr (!GRP) {
+          const float sc = sp[r][0];
+          if constexpr (AFF) v = fmaf(-zp[r][0], wave_sum(sx[mm]), v);
+          v = sc * v;
+        }
+        tot[r][mm] = v;
+      }
+    if (segs.mode == 0) {
 #pragma unroll
-    for (int r = 0; r + 1 < RW; r += 2)
+      for (int r = 0; r < RW; ++r)
 #pragma unroll
-      for (int mm = 0; mm < MB; ++mm)
-        if (lane == r * MB + mm && g0 + r < total && m0 + mm < mrows)
-          epilogue(segs, g0 + r, m0 + mm, tot[r][mm], tot[r + 1][mm]);
+        for (int mm = 0; mm < MB; ++mm)
+          if (lane == r * MB + mm && g0 + r < total && m0 + mm < mrows)
+            epilogue(segs, g0 + r, m0 + mm, tot[r][mm], 0.f);
+    } else {
+#pragma unroll
+      for (int r = 0; r + 1 < RW; r += 2)
+#pragma unroll
+        for (int mm = 0; mm < MB; ++mm)
+          if (lane == r * MB + mm && g0 + r < total && m0 + mm < mrows)
+            epilogue(segs, g0 + r, m0 + mm, tot[r][mm], tot[r + 1][mm]);
+    }
+  };
+
+  float acc[RW][MB];
+  float sx[MB];
+  const int8_t* w[RW];
+  const float* sp[RW];
+  const float* zp[RW];
+  const bool single = k <= kc;
+  int g = blockIdx.x;
+  int g0 = rows_of(g, w, sp, zp);
+  Unit cur, nxt;
+  if (single) {
+    fetch(cur, w[0], sp[0], zp[0], 0);
+    stage_x(0, k);
+    __syncthreads();
+  }
+  for (;;) {
+    const int gn = single ? g + static_cast<int>(gridDim.x) : groups;
+    const int8_t* wn[RW];
+    const float* sn[RW];
+    const float* zn[RW];
+    const int gn0 = rows_of(min(gn, groups - 1), wn, sn, zn);
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int mm = 0; mm < MB; ++mm) acc[r][mm] = 0.f;
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) sx[mm] = 0.f;
+    for (int c0 = 0; c0 < k; c0 += kc) {
+      const int clen = min(kc, k - c0);
+      if (!single) {
+        fetch(cur, w[0], sp[0], zp[0], c0);
+        if (c0) __syncthreads();
+        stage_x(c0, clen);
+        __syncthreads();
+      }
+      // rows in order, each in 4096-column units; the next unit (of this
+      // row, the next row, or the next row group's first row) is in flight
+      // while the current one is computed
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        for (int c = c0; c < c0 + clen; c += 4096) {
+          const int rn = r + 1 < RW ? r + 1 : r;
+          if (c + 4096 < c0 + clen) fetch(nxt, w[r], sp[r], zp[r], c + 4096);
+          else if (r + 1 < RW) fetch(nxt, w[rn], sp[rn], zp[rn], c0);
+          else if (!single && c0 + kc < k) fetch(nxt, w[0], sp[0], zp[0], c0 + kc);
+          else if (gn < groups) fetch(nxt, wn[0], sn[0], zn[0], 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = c + 16 * (lane + 64 * i);
+            if (e < c0 + clen) step(cur.c[i], cur.s[i], cur.z[i], c0, e, acc[r], sx, r == 0);
+          }
+          cur = nxt;
+        }
+      }
+    }
+    finish(g0, sp, zp, acc, sx);
+    if (gn >= groups) break;
+    g = gn;
+    g0 = gn0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      w[r] = wn[r];
+      sp[r] = sn[r];
+      zp[r] = zn[r];
+    }
   }
 }
 
@@ -333,8 +416,18 @@ hipError_t launch_fast(const CSegs& sg, const void* x, int xtype, long long ldx,
                        hipStream_t s) {
   const int total = sg.start[sg.nseg];
   const int kc = min(((k + 1023) / 1024) * 1024, 16384 / MB);
-  const unsigned grid = static_cast<unsigned>((total + kWaves * RW - 1) / (kWaves * RW));
+  const long long groups = (total + kWaves * RW - 1) / (kWaves * RW);
   const size_t lds = sizeof(float) * MB * kc;
+  // one chunk: a persistent grid of what fits on the chip at once, rounded
+  // so that every workgroup takes the same number of row groups
+  long long g = groups;
+  if (k <= kc) {
+    const long long per_cu = std::max<long long>(1, std::min<long long>(160 * 1024 / lds, 8));
+    const long long most = static_cast<long long>(device_cu_count()) * per_cu;
+    const long long rounds = (groups + most - 1) / most;
+    g = (groups + rounds - 1) / rounds;
+  }
+  const unsigned grid = static_cast<unsigned>(g);
   for (int m0 = 0; m0 < m; m0 += MB) {
     cint8_kernel<MB, RW, GRP, AFF><<<grid, kThreads, lds, s>>>(sg, x, xtype, ldx, m0, m, k, kc);
     const hipError_t e = hipGetLastError();
@@ -397,7 +490,8 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
     fast = fast && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
   if (fast) {
     const int cus = device_cu_count();
-    const bool four = (total + kWaves * 4 - 1) / (kWaves * 4) >= 2 * cus;
+    const bool four = L.rows_per_wave ? L.rows_per_wave == 4
+                                       : (total + kWaves * 4 - 1) / (kWaves * 4) >= 2 * cus;
     if (m == 1)
       return four ? launch_mb<1, 4>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s)
                   : launch_mb<1, 2>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s);

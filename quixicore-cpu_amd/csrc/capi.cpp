@@ -526,6 +526,7 @@ int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void
     L.rope_cos = rope_cos;
     L.rope_sin = rope_sin;
   }
+  L.rows_per_wave = g_tuning.rows_per_wave == 2 || g_tuning.rows_per_wave == 4 ? g_tuning.rows_per_wave : 0;
   return finish(qc::launch_cint8(L, as_stream(stream)));
 }
 

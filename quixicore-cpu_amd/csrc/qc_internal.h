@@ -103,6 +103,7 @@ struct CInt8Launch {
   int nrope = 0;
   const float* rope_cos = nullptr;
   const float* rope_sin = nullptr;
+  int rows_per_wave = 0;        // 2 or 4 (0: from the shape)
 };
 hipError_t launch_cint8(const CInt8Launch& launch, hipStream_t s);
 
