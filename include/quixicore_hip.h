@@ -327,6 +327,14 @@ int qc_hip_set_qgemm_panel(int mode);
  * 1 = always.  Tuning and test knob with no reference counterpart. */
 int qc_hip_set_qgemm_rows(int mode);
 
+/* Small-batch MFMA kernels with int8 digit activations (2 <= m <= 8 per
+ * pass): 0 (default) = the GEMM kernel builds each stage's digits from x
+ * itself where it can (K % 256 == 0, x 16-byte aligned, K not split in two),
+ * saving the separate digit-prep launch; -1 = always run the prep launch.
+ * Both give the same bits.  Tuning and test knob with no reference
+ * counterpart. */
+int qc_hip_set_qgemm_fold(int mode);
+
 /* on != 0: qc_hip_rms_norm_add_quant_int8 replays the element-order sum of
  * squares for every row instead of only for rows whose float norm the
  * parallel sum cannot settle (process-wide; results are identical either

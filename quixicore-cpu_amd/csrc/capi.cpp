@@ -650,6 +650,12 @@ int qc_hip_set_qgemm_rows(int mode) {
   return QC_OK;
 }
 
+int qc_hip_set_qgemm_fold(int mode) {
+  if (mode < -1 || mode > 0) return QC_INVALID_ARGUMENT;
+  g_tuning.qgemm_fold = mode;
+  return QC_OK;
+}
+
 int qc_hip_set_norm_sequential_sum(int on) {
   g_norm_sequential = on != 0;
   return QC_OK;

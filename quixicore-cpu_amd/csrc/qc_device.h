@@ -61,6 +61,25 @@ __device__ __forceinline__ int dpp_i32(int v) {
 __device__ __forceinline__ float xor1_f32(float v) { return dpp_f32<0xB1>(v); }
 __device__ __forceinline__ int xor1_i32(int v) { return dpp_i32<0xB1>(v); }
 
+// Reductions over each aligned group of 8 lanes, returned to all 8 (quad
+// perms [1,0,3,2] = 0xB1 and [2,3,0,1] = 0x4E, then row_half_mirror = 0x141,
+// which pairs lane i of a group with lane 7 - i, in the other quad).
+__device__ __forceinline__ float group8_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  return fmaxf(v, dpp_f32<0x141>(v));
+}
+__device__ __forceinline__ int group8_sum(int v) {
+  v += dpp_i32<0xB1>(v);
+  v += dpp_i32<0x4E>(v);
+  return v + dpp_i32<0x141>(v);
+}
+__device__ __forceinline__ int group8_and(int v) {
+  v &= dpp_i32<0xB1>(v);
+  v &= dpp_i32<0x4E>(v);
+  return v & dpp_i32<0x141>(v);
+}
+
 // Sum over the 64 lanes of a wavefront, valid in lane 63 only (the AMD DPP
 // reduction: partial sums within each 16-lane row, then row broadcasts).
 // Summation order is fixed, so results are deterministic.

@@ -18,6 +18,7 @@ struct GemvTuning {
   int qgemm_stages = 0;   // small-batch GEMM K stages per workgroup (1..16; 0 = from the shape)
   int qgemm_panel = 0;    // 2-D GEMM route: 0 = for m >= 64, -1 = never, 1 / 2 = always (K ranges)
   int qgemm_rows = 0;     // exact-digit rows route for 2 <= m <= 8: 0 = by shape, -1 = never, 1 = always
+  int qgemm_fold = 0;     // digit-layout GEMM builds its own digits: 0 = where it can, -1 = never
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
@@ -70,10 +71,11 @@ hipError_t launch_qgemv_w8a8(int fmt, const void* W, const float* x, float* y, l
 // for up to 8 rows per pass, bf16 hi/lo above; for m >= 64 one 2-D tiled
 // kernel (the panel route) instead of passes of 32 rows.  waves / stages:
 // small-batch plan override (0 = from the shape); panel: 0 = from m, -1 =
-// never, 1 / 2 = always (one / two K ranges).
+// never, 1 / 2 = always (one / two K ranges).  fold: 0 = the digit-layout
+// GEMM builds its own digits where it can (no prep launch), -1 = never.
 hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
                              int k, hipStream_t s, int waves = 0, int stages = 0,
-                             int panel = 0);
+                             int panel = 0, int fold = 0);
 
 // launch_qgemm_mfma without allocating: the scratch is a fixed device
 // array of kQgemmNoAllocScratchBytes per GPU, shared by every such call on

@@ -325,6 +325,68 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
     zero_y[i] = 0.0f;
 }
 
+// The digits of one 4-element part of a 32-element block of activation row m
+// (the 8 parts of a (block, row) sit in an aligned group of 8 lanes, part =
+// lane & 7, and every lane of the wave calls this together), written into the
+// block's record `rec` (XBlock layout) when `write`.  The digits are those of
+// the M = 1 path: e = frexp exponent of max|x_b| - 21, q = rint(x * 2^-e) clamped to
+// [-2^21, 2^21), q = 2^14 d0 + 2^7 d1 + d2; a block with a non-finite value
+// gets gate NaN and zero digits.
+template <int XL, bool BIAS>
+__device__ __forceinline__ void digit_part(const float (&v)[4], int m, int part, bool write,
+                                           uint8_t* rec) {
+  using XB = XBlock<XL, BIAS>;
+  float mx = 0.f;
+  int fin = 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    mx = fmaxf(mx, fabsf(v[i]));
+    fin &= isfinite(v[i]) ? 1 : 0;
+  }
+  mx = group8_max(mx);
+  fin = group8_and(fin);
+  int ex = 0;
+  (void)frexpf(mx, &ex);                           // mx < 2^ex
+  const int e = fin ? ex - 21 : 0;
+  uint32_t pk[3] = {0u, 0u, 0u};
+  int sum[3] = {0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int q = fin ? __float2int_rn(ldexpf(v[i], -e)) : 0;   // |x * 2^-e| <= 2^21
+    q = q > 2097151 ? 2097151 : q;
+    const int dg[3] = {q >> 14, (q >> 7) & 127, q & 127};
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      pk[d] |= static_cast<uint32_t>(dg[d] & 0xFF) << (8 * i);
+      sum[d] += dg[d];
+    }
+  }
+  if (write) {
+    // operand row r = 4 (m & 3) + d, k = 4 part + i: lane r + 16 (part >> 1),
+    // bytes 4 (part & 1) .. +3 of its 8
+    uint8_t* a = rec + (m >> 2) * 512 + 4 * (part & 1);
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      *reinterpret_cast<uint32_t*>(a + 8 * (4 * (m & 3) + d + 16 * (part >> 1))) = d < 3 ? pk[d] : 0u;
+  }
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int d = 0; d < 3; ++d) sum[d] = group8_sum(sum[d]);
+  }
+  if (write && part == 0) {
+    int* meta = reinterpret_cast<int*>(rec + XB::meta_off) + 2 * m;
+    meta[0] = e;
+    meta[1] = __float_as_int(fin ? 1.0f : __builtin_nanf(""));
+    if constexpr (BIAS) {
+      int* c = reinterpret_cast<int*>(rec + XB::bias_off) + 4 * m;
+      c[0] = -8 * sum[0];
+      c[1] = -8 * sum[1];
+      c[2] = -8 * sum[2];
+      c[3] = 0;
+    }
+  }
+}
+
 // Digit fragments of the compact layouts (M <= 8): one 64-thread workgroup
 // per block.  Block 0 also copies the weights' last row's short final stage
 // (`tail` bytes from `tail_src`) into the zero-padded `tail_pad`
@@ -342,9 +404,7 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
   const int l = threadIdx.x;
   const int nb = K / 32;
   {
-    // Thread l: row m = l >> 3, elements 4 (l & 7) .. +3 of block b.  The
-    // digits are those of the M = 1 path: e = frexp exponent of max|x_b| - 21,
-    // q = rint(x * 2^-e) clamped to [-2^21, 2^21), q = 2^14 d0 + 2^7 d1 + d2.
+    // Thread l: row m = l >> 3, elements 4 (l & 7) .. +3 of block b.
     const int b = blockIdx.x;
     const int m = l >> 3, part = l & 7;
     const bool row_ok = m < XL;
@@ -353,61 +413,7 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = live ? src[i] : 0.0f;
-    float mx = 0.f;
-    int fin = 1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      mx = fmaxf(mx, fabsf(v[i]));
-      fin &= isfinite(v[i]) ? 1 : 0;
-    }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-      mx = fmaxf(mx, __shfl_xor(mx, o));
-      fin &= __shfl_xor(fin, o);
-    }
-    int ex = 0;
-    (void)frexpf(mx, &ex);                           // mx < 2^ex
-    const int e = fin ? ex - 21 : 0;
-    uint32_t pk[3] = {0u, 0u, 0u};
-    int sum[3] = {0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int q = fin ? __float2int_rn(ldexpf(v[i], -e)) : 0;   // |x * 2^-e| <= 2^21
-      q = q > 2097151 ? 2097151 : q;
-      const int dg[3] = {q >> 14, (q >> 7) & 127, q & 127};
-#pragma unroll
-      for (int d = 0; d < 3; ++d) {
-        pk[d] |= static_cast<uint32_t>(dg[d] & 0xFF) << (8 * i);
-        sum[d] += dg[d];
-      }
-    }
-    uint8_t* rec = xf + static_cast<long long>(b) * XB::bytes;
-    if (row_ok) {
-      // operand row r = 4 (m & 3) + d, k = 4 part + i: lane r + 16 (part >> 1),
-      // bytes 4 (part & 1) .. +3 of its 8
-      uint8_t* a = rec + (m >> 2) * 512 + 4 * (part & 1);
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        *reinterpret_cast<uint32_t*>(a + 8 * (4 * (m & 3) + d + 16 * (part >> 1))) = d < 3 ? pk[d] : 0u;
-    }
-    if constexpr (BIAS) {
-#pragma unroll
-      for (int d = 0; d < 3; ++d)
-#pragma unroll
-        for (int o = 1; o < 8; o <<= 1) sum[d] += __shfl_xor(sum[d], o);
-    }
-    if (row_ok && part == 0) {
-      int* meta = reinterpret_cast<int*>(rec + XB::meta_off) + 2 * m;
-      meta[0] = e;
-      meta[1] = __float_as_int(fin ? 1.0f : __builtin_nanf(""));
-      if constexpr (BIAS) {
-        int* c = reinterpret_cast<int*>(rec + XB::bias_off) + 4 * m;
-        c[0] = -8 * sum[0];
-        c[1] = -8 * sum[1];
-        c[2] = -8 * sum[2];
-        c[3] = 0;
-      }
-    }
+    digit_part<XL, BIAS>(v, m, part, row_ok, xf + static_cast<long long>(b) * XB::bytes);
   }
   // y is accumulated with two atomic adds when K is split in two: clear it.
   for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
@@ -462,18 +468,28 @@ struct StageLayout {
 };
 
 // NW wavefronts per workgroup, 16 weight rows each.
-template <int FMT, int XL, int NW, int NST>
+//
+// FOLD (digit layouts, K % 256 == 0, x 16-byte aligned): no prep launch.  The
+// workgroup builds each stage's digit records itself, from x: the x values
+// of stage s + S - 1 are loaded into registers (before that stage's weight
+// loads, so waiting for them leaves the weights in flight) while stage s is
+// computed, then turned into digits (digit_part, the prep kernel's own
+// arithmetic, so the records are the same bytes) and written into the free
+// ring slot, which the next barriers publish.
+template <int FMT, int XL, int NW, int NST, bool FOLD>
 __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
-    const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
-    float* __restrict__ y, float* __restrict__ partial, const uint8_t* __restrict__ tail_pad,
-    const int* __restrict__ rexp, int M, int N, int K, int nslabs, int ks_count, int nstages) {
+    const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ x,
+    const float* __restrict__ bias, float* __restrict__ y, float* __restrict__ partial,
+    const uint8_t* __restrict__ tail_pad, const int* __restrict__ rexp, int M, int N, int K,
+    int nslabs, int ks_count, int nstages) {
   using L = StageLayout<FMT, XL, NW>;
   using XB = typename L::XB;
   using WS = WStage<FMT>;
+  static_assert(!FOLD || XB::digits, "only the digit layouts are built in the GEMM");
   constexpr int T = XB::T;
   constexpr int kSlab = 16 * NW;
   constexpr int S = L::ring;
-  constexpr int G = L::g;
+  constexpr int G = FOLD ? WS::loads : L::g;   // ring loads per wave per stage
   constexpr int kBiasPerWave = L::bias_bytes / NW;
   static_assert(L::bias_bytes % (16 * NW) == 0, "bias split");
   static_assert(G * (S - 1) < 64, "vmcnt range");
@@ -542,12 +558,14 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
         if (q + 1 < WS::loads || lane < WS::last_lanes) dma16(W, wrow_off[q] + seg + wchunk[q], dst);
       }
     }
-    const uint8_t* xs = xf + static_cast<long long>(st) * L::x_bytes;
+    if constexpr (!FOLD) {
+      const uint8_t* xs = xf + static_cast<long long>(st) * L::x_bytes;
 #pragma unroll
-    for (int i = 0; i < L::gx; ++i) {
-      const int c = 64 * i + lane;   // chunk wave * cpw + c of the stage
-      if (c < L::cpw && wave * L::cpw + c < L::xc)
-        dma16(xs, xoff + i * 1024, base + L::w_bytes + 16 * (wave * L::cpw + 64 * i));
+      for (int i = 0; i < L::gx; ++i) {
+        const int c = 64 * i + lane;   // chunk wave * cpw + c of the stage
+        if (c < L::cpw && wave * L::cpw + c < L::xc)
+          dma16(xs, xoff + i * 1024, base + L::w_bytes + 16 * (wave * L::cpw + 64 * i));
+      }
     }
     if constexpr (L::bias_bytes > 0) {
       // Wave w moves bias bytes [w, w+1) * kBiasPerWave of the stage with
@@ -556,6 +574,55 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
                           static_cast<long long>(st) * L::bias_bytes;
       if (lane < kBiasPerWave / 16)
         dma16(bs, boff, base + L::w_bytes + L::x_bytes + wave * kBiasPerWave);
+    }
+  };
+
+  // FOLD: task tau = tid + NT * t of a stage is (block b, row m, part p) with
+  // p = tau & 7, m = (tau >> 3) % XL, b = (tau >> 3) / XL: 64 XL tasks, each
+  // 16 bytes of x; a workgroup with more threads leaves its last waves idle.
+  // The x bytes of a stage are copied into `xstage` (task tau at byte 16 tau)
+  // by global->LDS loads like the weights', so every load in flight stays
+  // invisible to the compiler and every wait explicit; rows past M read row
+  // 0 and are zeroed when the digits are built.
+  constexpr int kTasks = 64 * XL, kThreadsWg = 64 * NW;
+  constexpr int TPT = kTasks >= kThreadsWg ? kTasks / kThreadsWg : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t xstage[FOLD ? 16 * kTasks : 16];
+  const bool xtask = kTasks >= kThreadsWg || wave * 64 < kTasks;   // wave-uniform
+  uint32_t xsrc[TPT];
+#pragma unroll
+  for (int t = 0; t < TPT; ++t) {
+    const int tau = static_cast<int>(threadIdx.x) + kThreadsWg * t;
+    const int g = tau >> 3, m = g % XL, b = g / XL;
+    xsrc[t] = static_cast<uint32_t>(4 * (static_cast<long long>(m < M ? m : 0) * K + 32 * b +
+                                         4 * (tau & 7)));
+  }
+  auto load_x = [&](int stage) {
+    if constexpr (FOLD) {
+      const int st = stage < st1 ? stage : st1 - 1;
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(x) +
+                            static_cast<long long>(st) * (4 * 32 * kStageBlocks);
+      if (xtask) {
+#pragma unroll
+        for (int t = 0; t < TPT; ++t)
+          dma16(base, xsrc[t], xstage + 16 * (kThreadsWg * t + 64 * wave));
+      }
+    }
+  };
+  auto build_x = [&](int slot) {
+    if constexpr (FOLD) {
+      uint8_t* rec0 = slot_base(slot) + L::w_bytes;
+      if (xtask) {
+#pragma unroll
+        for (int t = 0; t < TPT; ++t) {
+          const int tau = static_cast<int>(threadIdx.x) + kThreadsWg * t;
+          const int g = tau >> 3, m = g % XL, b = g / XL;
+          const bool live = m < M;
+          const f32x4 xv = *reinterpret_cast<const f32x4*>(xstage + 16 * tau);
+          const float v[4] = {live ? xv[0] : 0.f, live ? xv[1] : 0.f, live ? xv[2] : 0.f,
+                              live ? xv[3] : 0.f};
+          digit_part<XL, FMT == kQ4_0>(v, m, tau & 7, true, rec0 + b * XB::bytes);
+        }
+      }
     }
   };
 
@@ -643,9 +710,30 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
   // next issue overwrites is no longer read), issues the loads S-1 stages
   // ahead and then computes, so S-1 stages are in flight during the
   // compute.  Stages past st1 only issue (clamped) loads.
+  //
+  // FOLD: each stage's x loads go out just before its ring loads, and are
+  // waited for (vmcnt <= G: the ring loads issued after them may stay in
+  // flight) once the current stage is computed; the digits then go into the
+  // stage's slot.  In-order retirement makes that wait also cover every
+  // earlier stage's ring loads, so at a step's start only the most recent
+  // stage's ring loads can be outstanding and the stage wait below stays
+  // exact.
 #pragma unroll
   for (int i = 0; i < S - 1; ++i)
-    if (i < NST) issue(st0 + i, i);
+    if (i < NST) {
+      if constexpr (FOLD) {
+        if (i > 0) {   // every wave is done reading xstage
+          wait_lgkmcnt0();
+          ring_barrier();
+        }
+      }
+      load_x(st0 + i);
+      issue(st0 + i, i);
+      if constexpr (FOLD) {
+        wait_vmcnt<G>();
+        build_x(i);
+      }
+    }
 #pragma unroll
   for (int i = 0; i < NST; ++i) {
     const int cur = st0 + i;
@@ -654,8 +742,17 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     wait_stages<G, S - 2>(NST - 1 - i);
     wait_lgkmcnt0();
     ring_barrier();
-    if (i + S - 1 < NST) issue(cur + S - 1, (i + S - 1) % S);
+    if (i + S - 1 < NST) {
+      load_x(cur + S - 1);
+      issue(cur + S - 1, (i + S - 1) % S);
+    }
     compute(cur, i % S, cur < st1);
+    if constexpr (FOLD) {
+      if (i + S - 1 < NST) {
+        wait_vmcnt<G>();
+        build_x((i + S - 1) % S);
+      }
+    }
     // Materialise the accumulators here: otherwise the compiler sinks the
     // scale FMAs of every stage into the (conditional) store block and keeps
     // all MFMA results of the workgroup live until then.
@@ -745,6 +842,7 @@ struct Scratch {
   uint8_t* fixed = nullptr;
   size_t fixed_split = 0, fixed_bytes = 0;
   int max_ks = 0;   // > 0: K split limit for the small-batch plan (see plan_for)
+  int fold = 0;     // digit layouts: 0 = build the digits in the GEMM where it can, -1 = never
 
   hipError_t get(hipStream_t s, size_t bytes, void** out, int tag = 0) {
     if (w == nullptr) {
@@ -782,25 +880,34 @@ struct Scratch {
   }
 };
 
-template <int FMT, int XL, int NW, int NST>
-hipError_t launch_nst(const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
-                      float* partial, const uint8_t* tail_pad, const int* rexp, int m, int n, int k,
-                      int nslabs, int ks, int nstages, hipStream_t s) {
-  qgemm_mfma<FMT, XL, NW, NST><<<nslabs * ks, 64 * NW, 0, s>>>(W, xf, bias, y, partial, tail_pad,
-                                                              rexp, m, n, k, nslabs, ks, nstages);
+struct MfmaArgs {
+  const uint8_t* W;
+  const uint8_t* xf;
+  const float* x;
+  const float* bias;
+  float* y;
+  float* partial;
+  const uint8_t* tail_pad;
+  const int* rexp;
+  int m, n, k, nslabs, ks, nstages;
+};
+
+template <int FMT, int XL, int NW, int NST, bool FOLD>
+hipError_t launch_nst(const MfmaArgs& a, hipStream_t s) {
+  qgemm_mfma<FMT, XL, NW, NST, FOLD><<<a.nslabs * a.ks, 64 * NW, 0, s>>>(
+      a.W, a.xf, a.x, a.bias, a.y, a.partial, a.tail_pad, a.rexp, a.m, a.n, a.k, a.nslabs, a.ks,
+      a.nstages);
   return hipGetLastError();
 }
 
-template <int FMT, int XL, int NW>
-hipError_t launch_nw(int nst, const uint8_t* W, const uint8_t* xf, const float* bias, float* y,
-                     float* partial, const uint8_t* tail_pad, const int* rexp, int m, int n, int k,
-                     int nslabs, int ks, int nstages, hipStream_t s) {
+template <int FMT, int XL, int NW, bool FOLD>
+hipError_t launch_nw(int nst, const MfmaArgs& a, hipStream_t s) {
   switch (nst) {
-    case 16: return launch_nst<FMT, XL, NW, 16>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
-    case 8: return launch_nst<FMT, XL, NW, 8>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
-    case 4: return launch_nst<FMT, XL, NW, 4>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
-    case 2: return launch_nst<FMT, XL, NW, 2>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
-    default: return launch_nst<FMT, XL, NW, 1>(W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
+    case 16: return launch_nst<FMT, XL, NW, 16, FOLD>(a, s);
+    case 8: return launch_nst<FMT, XL, NW, 8, FOLD>(a, s);
+    case 4: return launch_nst<FMT, XL, NW, 4, FOLD>(a, s);
+    case 2: return launch_nst<FMT, XL, NW, 2, FOLD>(a, s);
+    default: return launch_nst<FMT, XL, NW, 1, FOLD>(a, s);
   }
 }
 
@@ -866,7 +973,13 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   using XB = XBlock<XL, FMT == kQ4_0>;
   // the bf16 / f16 layouts store and apply per-row exponents
   if (!XB::digits && rexp == nullptr) return hipErrorInvalidValue;
-  const size_t xf_bytes = static_cast<size_t>(nbp) * XB::bytes;
+  // Digit layouts without the prep launch: the GEMM builds the digits (no
+  // short last stage to pad, x loadable in 16-byte pieces, and no y to clear
+  // for a two-way K split).
+  const bool fold = XB::digits && scratch.fold >= 0 && k % (32 * kStageBlocks) == 0 &&
+                    reinterpret_cast<uintptr_t>(x) % 16 == 0 && ks != 2 &&
+                    static_cast<long long>(m) * k * 4 < (1LL << 32);
+  const size_t xf_bytes = fold ? 0 : static_cast<size_t>(nbp) * XB::bytes;
   const size_t bias_bytes = static_cast<size_t>(nbp) * XB::bias_bytes;
   const size_t part_bytes = ks > 2 ? static_cast<size_t>(ks) * m * n * sizeof(float) : 0;
   const size_t pad_bytes = WStage<FMT>::row_bytes;
@@ -883,19 +996,29 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const long long row_bytes = static_cast<long long>(nb) * PairLayout<FMT>::bytes / 2;
   const int tail = (k / 64) % kStagePairs * PairLayout<FMT>::bytes;
   const uint8_t* tail_src = W + (n - 1) * row_bytes + static_cast<long long>(nstages - 1) * WStage<FMT>::row_bytes;
-  if constexpr (XB::digits)
-    qgemm_prep<XL, FMT == kQ4_0><<<nbp, 64, 0, s>>>(x, m, k, xf, y, ks == 2 ? outs : 0, tail_src,
-                                                    tail, tail_pad, static_cast<int>(pad_bytes));
-  else
-    prep_rows<false, FMT == kQ4_0><<<XL, 256, 0, s>>>(x, m, k, nbp, XB::T, xf, bias, rexp, y,
-                                                      ks == 2 ? outs : 0, tail_src, tail, tail_pad,
-                                                      static_cast<int>(pad_bytes));
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (plan.nw == 8)
-    e = launch_nw<FMT, XL, 8>(plan.nst, W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
-  else
-    e = launch_nw<FMT, XL, 4>(plan.nst, W, xf, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages, s);
+  if (!fold) {
+    if constexpr (XB::digits)
+      qgemm_prep<XL, FMT == kQ4_0><<<nbp, 64, 0, s>>>(x, m, k, xf, y, ks == 2 ? outs : 0, tail_src,
+                                                      tail, tail_pad, static_cast<int>(pad_bytes));
+    else
+      prep_rows<false, FMT == kQ4_0><<<XL, 256, 0, s>>>(x, m, k, nbp, XB::T, xf, bias, rexp, y,
+                                                        ks == 2 ? outs : 0, tail_src, tail, tail_pad,
+                                                        static_cast<int>(pad_bytes));
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const MfmaArgs a{W, xf, x, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages};
+  if constexpr (XB::digits) {
+    if (fold)
+      e = plan.nw == 8 ? launch_nw<FMT, XL, 8, true>(plan.nst, a, s)
+                       : launch_nw<FMT, XL, 4, true>(plan.nst, a, s);
+    else
+      e = plan.nw == 8 ? launch_nw<FMT, XL, 8, false>(plan.nst, a, s)
+                       : launch_nw<FMT, XL, 4, false>(plan.nst, a, s);
+  } else {
+    e = plan.nw == 8 ? launch_nw<FMT, XL, 8, false>(plan.nst, a, s)
+                     : launch_nw<FMT, XL, 4, false>(plan.nst, a, s);
+  }
   if (e != hipSuccess || ks <= 2) return e;
   const long long blocks = (outs + 255) / 256;
   qgemm_reduce<<<static_cast<unsigned>(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(partial, y, outs, ks);
@@ -1259,13 +1382,14 @@ hipError_t qgemm_mfma_with(int fmt, const void* W, const float* x, float* y, int
 }  // namespace
 
 hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, int m, int n,
-                             int k, hipStream_t s, int waves, int stages, int panel) {
+                             int k, hipStream_t s, int waves, int stages, int panel, int fold) {
   StreamWorkspace* ws = nullptr;
   const hipError_t e = stream_workspace(s, &ws);
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> hold(ws->call);   // until the call's last launch
   Scratch scratch;
   scratch.w = ws;
+  scratch.fold = fold;
   return qgemm_mfma_with(fmt, W, x, y, m, n, k, s, waves, stages, panel, scratch);
 }
 

@@ -283,7 +283,7 @@ hipError_t launch_fmt(const uint8_t* W, const float* x, float* y, int m, int n, 
   if (k % 64 == 0 && w_bytes + 4096 < (1LL << 32))
     return noalloc ? launch_qgemm_mfma_noalloc(FMT, W, x, y, m, n, k, s)
                    : launch_qgemm_mfma(FMT, W, x, y, m, n, k, s, t.qgemm_waves, t.qgemm_stages,
-                                       t.qgemm_panel);
+                                       t.qgemm_panel, t.qgemm_fold);
   const int grid = (n + kWaves - 1) / kWaves;
   for (int m0 = 0; m0 < m; m0 += 8) {
     const int mt = m - m0 < 8 ? m - m0 : 8;

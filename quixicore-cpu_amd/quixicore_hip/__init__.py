@@ -65,6 +65,7 @@ _SIGS = {
     "qc_hip_set_norm_sequential_sum": ([_I], _I),
     "qc_hip_set_qgemm_panel": ([_I], _I),
     "qc_hip_set_qgemm_rows": ([_I], _I),
+    "qc_hip_set_qgemm_fold": ([_I], _I),
     "qc_hip_stream_read": ([_P, _LL, _P, _I, _P], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
@@ -316,6 +317,12 @@ def set_qgemm_rows(mode=0):
     M = 2, and M <= 4 with N <= 8192, at K <= 4096), -1 = never (MFMA
     small-batch kernels), 1 = always."""
     _check(lib.qc_hip_set_qgemm_rows(mode), "set_qgemm_rows")
+
+
+def set_qgemm_fold(mode=0):
+    """Digit-layout small-batch GEMM: 0 = builds its own digits where it can
+    (no prep launch), -1 = always runs the prep launch (same bits)."""
+    _check(lib.qc_hip_set_qgemm_fold(mode), "set_qgemm_fold")
 
 
 def set_norm_sequential_sum(on):

@@ -295,3 +295,45 @@ def test_qgemm_dense_activation_range(qc, oracle, synth, dev, fmt, m, off):
     Y = Y.cpu().numpy()
     for r in range(m):
         _check_rows(oracle, fmt, packed, x[r], Y[r], n, k)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("m,n,k,waves,stages,x_off", [
+    (3, 300, 2304, 4, 1, 0), (4, 14336, 4096, 0, 0, 0), (5, 4096, 4096, 0, 0, 0),
+    (8, 4096, 4096, 8, 4, 0), (6, 1000, 14336, 0, 0, 0), (7, 300, 2304, 8, 2, 0),
+    (8, 260, 256, 4, 1, 0), (2, 520, 4096, 8, 16, 0), (5, 300, 4096, 4, 8, 3),
+    (8, 129, 2304, 4, 8, 0)])
+def test_qgemm_fold_bitwise_prep(qc, oracle, synth, dev, fmt, m, n, k, waves, stages, x_off):
+    """The digit-layout GEMM that builds its own digits from x (no prep
+    launch) gives the same bits as the prep launch + GEMM, for XL = 4 / 8,
+    4- and 8-wave workgroups, one K range, two (which keeps the prep launch
+    to clear y) and more (partial sums), ragged N, M < XL, and x off 16-byte
+    alignment (prep launch); a non-finite activation poisons its row the
+    same way in both."""
+    import torch
+    print(f"qgemm fold fmt={fmt} m={m} n={n} k={k} plan={waves},{stages} x_off={x_off}", flush=True)
+    packed, _ = _case(oracle, synth, fmt, n, k, 700 + m)
+    x = synth.normal_fast(800 + m + k, m * k).reshape(m, k)
+    x[1, 37] = np.inf if m > 2 else x[1, 37]
+    P = torch.from_numpy(packed).to(dev)
+    buf = torch.zeros(m * k + x_off, dtype=torch.float32, device=dev)
+    buf[x_off:] = torch.from_numpy(x.reshape(-1)).to(dev)
+    X = buf[x_off:].view(m, k)
+    out = {}
+    qc.set_qgemm_rows(-1)
+    qc.set_qgemm_plan(waves, stages)
+    try:
+        for fold in (-1, 0):
+            qc.set_qgemm_fold(fold)
+            Y = torch.full((m * n,), 7.0, dtype=torch.float32, device=dev)
+            assert qc.qgemm_raw(fmt, P, X, Y, m, n, k) == 0
+            out[fold] = Y.cpu().numpy().reshape(m, n)
+    finally:
+        qc.set_qgemm_fold(0)
+        qc.set_qgemm_plan(0, 0)
+        qc.set_qgemm_rows(0)
+    assert np.array_equal(out[0].view(np.uint32), out[-1].view(np.uint32))
+    for r in (0, m - 1):
+        _check_rows(oracle, fmt, packed, x[r], out[0][r], n, k)
+    if m > 2:
+        assert not np.isfinite(out[0][1]).any()
