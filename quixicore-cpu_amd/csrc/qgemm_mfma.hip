@@ -24,7 +24,8 @@
 // Data flow.  A prep kernel (qgemm_prep for the digit layouts, prep_rows
 // for f16 / bf16) writes the activation fragments in the MFMA operand layout
 // ([block][m-tile][hi | lo][64 lanes][16 B]) plus the q4 bias, and zeroes y
-// when two K halves will add into it.  The GEMM workgroup (4 or
+// when two K halves will add into it; for the digit layouts the GEMM usually
+// builds them itself instead (FOLD, below).  The GEMM workgroup (4 or
 // 8 wavefronts, 16 weight rows each) runs a ring of LDS stages, each
 // holding 4 block pairs (256 K) of its weight rows -- whole row segments,
 // copied with global_load_lds_dwordx4, so every weight byte crosses the
@@ -76,7 +77,9 @@ constexpr int kFragBytes = 2048;
 //    planes of each row as v_mfma_i32_16x16x32_i8 A operands, [tile][64
 //    lanes][8 B] with operand row 4 (m & 3) + d holding digit d of row m (d = 3
 //    is zero); then per row {int32 e, f32 gate}; then (q4_0) per row the
-//    int32 C input {-8 sum_k digit_d, d = 0..3}.
+//    int32 C input {-8 sum_k digit_d, d = 0..3}.  The digits of a row share
+//    one exponent per stage of 8 blocks; every block record of the stage
+//    holds it.
 template <int XL, bool BIAS>
 struct XBlock {
   static constexpr bool digits = XL <= 8;
@@ -86,6 +89,7 @@ struct XBlock {
   static constexpr int bytes = digits ? bias_off + (BIAS ? 16 * XL : 0) : T * kFragBytes;
   static constexpr int bias_bytes = digits || !BIAS ? 0 : T * 64;    // separate array
   static constexpr int prep_groups = digits ? 1 : T;                 // prep workgroups per block
+  static constexpr int stage_bytes = kStageBlocks * bytes;           // x bytes of a ring stage
   static_assert(bytes % 16 == 0, "whole 16-byte chunks");
 };
 
@@ -325,17 +329,20 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
     zero_y[i] = 0.0f;
 }
 
-// The digits of one 4-element part of a 32-element block of activation row m
-// (the 8 parts of a (block, row) sit in an aligned group of 8 lanes, part =
-// lane & 7, and every lane of the wave calls this together), written into the
-// block's record `rec` (XBlock layout) when `write`.  The digits are those of
-// the M = 1 path: e = frexp exponent of max|x_b| - 21, q = rint(x * 2^-e) clamped to
-// [-2^21, 2^21), q = 2^14 d0 + 2^7 d1 + d2; a block with a non-finite value
-// gets gate NaN and zero digits.
+// The digits of activation row m over one stage of 8 blocks, built by one
+// whole wavefront: lane l holds elements 4 (l & 7) .. +3 of block l >> 3
+// (v, zero past K or M), and the records go to the stage's x area
+// `stage_rec` (XBlock layout) when `write`.  The row shares one exponent
+// over the stage: e = frexp exponent of max |x| over its 256 elements - 21,
+// q = rint(x * 2^-e) clamped to [-2^21, 2^21), q = 2^14 d0 + 2^7 d1 + d2, so
+// each element is held to within 2^-22 of the stage maximum.  A stage row
+// with a non-finite value gets gate NaN and zero digits.
 template <int XL, bool BIAS>
-__device__ __forceinline__ void digit_part(const float (&v)[4], int m, int part, bool write,
-                                           uint8_t* rec) {
+__device__ __forceinline__ void digit_stage_row(const float (&v)[4], int m, bool write,
+                                                uint8_t* stage_rec) {
   using XB = XBlock<XL, BIAS>;
+  const int lane = threadIdx.x & 63;
+  const int part = lane & 7, b = lane >> 3;
   float mx = 0.f;
   int fin = 1;
 #pragma unroll
@@ -343,8 +350,8 @@ __device__ __forceinline__ void digit_part(const float (&v)[4], int m, int part,
     mx = fmaxf(mx, fabsf(v[i]));
     fin &= isfinite(v[i]) ? 1 : 0;
   }
-  mx = group8_max(mx);
-  fin = group8_and(fin);
+  mx = wave_max_nonneg(mx);                        // NaN lanes are caught by fin
+  fin = __all(fin) ? 1 : 0;
   int ex = 0;
   (void)frexpf(mx, &ex);                           // mx < 2^ex
   const int e = fin ? ex - 21 : 0;
@@ -361,6 +368,7 @@ __device__ __forceinline__ void digit_part(const float (&v)[4], int m, int part,
       sum[d] += dg[d];
     }
   }
+  uint8_t* rec = stage_rec + b * XB::bytes;
   if (write) {
     // operand row r = 4 (m & 3) + d, k = 4 part + i: lane r + 16 (part >> 1),
     // bytes 4 (part & 1) .. +3 of its 8
@@ -388,9 +396,10 @@ __device__ __forceinline__ void digit_part(const float (&v)[4], int m, int part,
 }
 
 // Digit fragments of the compact layouts (M <= 8): one 64-thread workgroup
-// per block.  Block 0 also copies the weights' last row's short final stage
-// (`tail` bytes from `tail_src`) into the zero-padded `tail_pad`
-// (pad_bytes), which the GEMM reads instead of running past the end of W.
+// per (stage, row), stage records of XBlock::stage_bytes.  Workgroup 0 also
+// copies the weights' last row's short final stage (`tail` bytes from
+// `tail_src`) into the zero-padded `tail_pad` (pad_bytes), which the GEMM
+// reads instead of running past the end of W.
 template <int XL, bool BIAS>
 __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, int M, int K,
                                                  uint8_t* __restrict__ xf, float* zero_y,
@@ -404,16 +413,16 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
   const int l = threadIdx.x;
   const int nb = K / 32;
   {
-    // Thread l: row m = l >> 3, elements 4 (l & 7) .. +3 of block b.
-    const int b = blockIdx.x;
-    const int m = l >> 3, part = l & 7;
-    const bool row_ok = m < XL;
-    const bool live = row_ok && m < M && b < nb;
-    const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * b : 0) + 4 * part;
+    // lane l: elements 4 (l & 7) .. +3 of block 8 st + (l >> 3) of row m
+    const int st = blockIdx.x / XL, m = blockIdx.x % XL;
+    const int blk = kStageBlocks * st + (l >> 3);
+    const bool live = m < M && blk < nb;
+    const float* src = x + static_cast<long long>(live ? m : 0) * K + (live ? 32 * blk : 0) +
+                       4 * (l & 7);
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = live ? src[i] : 0.0f;
-    digit_part<XL, BIAS>(v, m, part, row_ok, xf + static_cast<long long>(b) * XB::bytes);
+    digit_stage_row<XL, BIAS>(v, m, true, xf + static_cast<long long>(st) * XB::stage_bytes);
   }
   // y is accumulated with two atomic adds when K is split in two: clear it.
   for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
@@ -452,7 +461,7 @@ struct StageLayout {
   using XB = XBlock<XL, FMT == kQ4_0>;
   static constexpr bool bias = FMT == kQ4_0;
   static constexpr int w_bytes = NW * WStage<FMT>::wave_bytes;
-  static constexpr int x_bytes = kStageBlocks * XB::bytes;
+  static constexpr int x_bytes = XB::stage_bytes;
   static constexpr int bias_bytes = kStageBlocks * XB::bias_bytes;   // dense q4_0 only
   static constexpr int bytes = w_bytes + x_bytes + bias_bytes;
   // Ring depth: three stages when they fit the 160 KB LDS, else two (deeper
@@ -473,7 +482,7 @@ struct StageLayout {
 // workgroup builds each stage's digit records itself, from x: the x values
 // of stage s + S - 1 are loaded into registers (before that stage's weight
 // loads, so waiting for them leaves the weights in flight) while stage s is
-// computed, then turned into digits (digit_part, the prep kernel's own
+// computed, then turned into digits (digit_stage_row, the prep kernel's own
 // arithmetic, so the records are the same bytes) and written into the free
 // ring slot, which the next barriers publish.
 template <int FMT, int XL, int NW, int NST, bool FOLD>
@@ -577,9 +586,10 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     }
   };
 
-  // FOLD: task tau = tid + NT * t of a stage is (block b, row m, part p) with
-  // p = tau & 7, m = (tau >> 3) % XL, b = (tau >> 3) / XL: 64 XL tasks, each
-  // 16 bytes of x; a workgroup with more threads leaves its last waves idle.
+  // FOLD: task tau = tid + NT * t of a stage is (row m, block b, part p) with
+  // m = tau >> 6, b = (tau >> 3) & 7, p = tau & 7 -- one wavefront per row --
+  // each 16 bytes of x; a workgroup with more threads leaves its last waves
+  // idle.
   // The x bytes of a stage are copied into `xstage` (task tau at byte 16 tau)
   // by global->LDS loads like the weights', so every load in flight stays
   // invisible to the compiler and every wait explicit; rows past M read row
@@ -592,9 +602,8 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
 #pragma unroll
   for (int t = 0; t < TPT; ++t) {
     const int tau = static_cast<int>(threadIdx.x) + kThreadsWg * t;
-    const int g = tau >> 3, m = g % XL, b = g / XL;
-    xsrc[t] = static_cast<uint32_t>(4 * (static_cast<long long>(m < M ? m : 0) * K + 32 * b +
-                                         4 * (tau & 7)));
+    const int m = tau >> 6;
+    xsrc[t] = static_cast<uint32_t>(4 * (static_cast<long long>(m < M ? m : 0) * K + 4 * lane));
   }
   auto load_x = [&](int stage) {
     if constexpr (FOLD) {
@@ -615,12 +624,12 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
 #pragma unroll
         for (int t = 0; t < TPT; ++t) {
           const int tau = static_cast<int>(threadIdx.x) + kThreadsWg * t;
-          const int g = tau >> 3, m = g % XL, b = g / XL;
+          const int m = tau >> 6;
           const bool live = m < M;
           const f32x4 xv = *reinterpret_cast<const f32x4*>(xstage + 16 * tau);
           const float v[4] = {live ? xv[0] : 0.f, live ? xv[1] : 0.f, live ? xv[2] : 0.f,
                               live ? xv[3] : 0.f};
-          digit_part<XL, FMT == kQ4_0>(v, m, tau & 7, true, rec0 + b * XB::bytes);
+          digit_stage_row<XL, FMT == kQ4_0>(v, m, true, rec0);
         }
       }
     }
@@ -642,6 +651,9 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     const uint8_t* base = slot_base(slot);
     const uint8_t* row = base + wave * WS::wave_bytes + (lane & 15) * WS::row_bytes;
     const uint8_t* xs = base + L::w_bytes;
+    float sacc[T];    // digit mode: this stage's sum, before its exponent
+#pragma unroll
+    for (int t = 0; t < T; ++t) sacc[t] = 0.f;
 #pragma unroll
     for (int pp = 0; pp < kStagePairs; ++pp) {
       const bool valid = live && stage * kStagePairs + pp < npairs;   // wave-uniform
@@ -665,7 +677,7 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
             w1 = (c1 >> sh) & 0x0F0F0F0Fu;
           }
           const long wq = static_cast<long>(w0) | (static_cast<long>(w1) << 32);
-          const float dw = half_bits_to_float(dbits);
+          const float dw = valid ? half_bits_to_float(dbits) : 0.0f;
           const uint8_t* rec = xs + blk * XB::bytes;
 #pragma unroll
           for (int t = 0; t < T; ++t) {
@@ -675,13 +687,11 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
               c = *reinterpret_cast<const i32x4*>(rec + XB::bias_off + 16 * (4 * t + j));
             // D lane (n, j): digit sums S_0..S_3 of row m = 4t + j (S_3 = 0)
             c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wq, c, 0, 0, 0);
-            const int2 me = *reinterpret_cast<const int2*>(rec + XB::meta_off + 8 * (4 * t + j));
             // 2^7 S1 + S2 is exact in int32 (|S| < 2^20), and its float
             // conversion is the same single rounding as fmaf(S1, 128, S2)
             const float f = fmaf(static_cast<float>(c[0]), 16384.f,
                                  static_cast<float>((c[1] << 7) + c[2]));
-            const float blk_dot = ldexpf((dw * __int_as_float(me.y)) * f, me.x);
-            accd[t] += valid ? blk_dot : 0.0f;
+            sacc[t] = fmaf(dw, f, sacc[t]);
           }
         } else {
           using Op = typename OpType<FMT>::T;
@@ -701,6 +711,17 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
             for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(c[e], d, acc[t][e]);
           }
         }
+      }
+    }
+    if constexpr (XB::digits) {
+      // the stage's exponent and gate of row m = 4t + j, from block 0's
+      // record (a clamped reload of a stage past the workgroup's range adds
+      // nothing, whatever its gate)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int2 me = *reinterpret_cast<const int2*>(xs + XB::meta_off + 8 * (4 * t + j));
+        const float v = ldexpf(sacc[t] * __int_as_float(me.y), me.x);
+        accd[t] += live ? v : 0.0f;
       }
     }
   };
@@ -979,7 +1000,7 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const bool fold = XB::digits && scratch.fold >= 0 && k % (32 * kStageBlocks) == 0 &&
                     reinterpret_cast<uintptr_t>(x) % 16 == 0 && ks != 2 &&
                     static_cast<long long>(m) * k * 4 < (1LL << 32);
-  const size_t xf_bytes = fold ? 0 : static_cast<size_t>(nbp) * XB::bytes;
+  const size_t xf_bytes = fold ? 0 : static_cast<size_t>(nstages) * XB::stage_bytes;
   const size_t bias_bytes = static_cast<size_t>(nbp) * XB::bias_bytes;
   const size_t part_bytes = ks > 2 ? static_cast<size_t>(ks) * m * n * sizeof(float) : 0;
   const size_t pad_bytes = WStage<FMT>::row_bytes;
@@ -998,8 +1019,9 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   const uint8_t* tail_src = W + (n - 1) * row_bytes + static_cast<long long>(nstages - 1) * WStage<FMT>::row_bytes;
   if (!fold) {
     if constexpr (XB::digits)
-      qgemm_prep<XL, FMT == kQ4_0><<<nbp, 64, 0, s>>>(x, m, k, xf, y, ks == 2 ? outs : 0, tail_src,
-                                                      tail, tail_pad, static_cast<int>(pad_bytes));
+      qgemm_prep<XL, FMT == kQ4_0><<<nstages * XL, 64, 0, s>>>(x, m, k, xf, y, ks == 2 ? outs : 0,
+                                                               tail_src, tail, tail_pad,
+                                                               static_cast<int>(pad_bytes));
     else
       prep_rows<false, FMT == kQ4_0><<<XL, 256, 0, s>>>(x, m, k, nbp, XB::T, xf, bias, rexp, y,
                                                         ks == 2 ? outs : 0, tail_src, tail, tail_pad,
