@@ -643,6 +643,49 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     accd[t] = 0.f;
   }
 
+  // The LDS operands of one block pair: the lane's code bytes and scales and,
+  // per block and tile, the activation operand (digit planes, or hi / lo)
+  // and the q4_0 C input.  compute() loads pair pp + 1 before it computes
+  // pair pp, so the LDS latency is covered by a pair's MFMAs and VALU work.
+  using Op = typename OpType<FMT>::T;
+  struct PairOps {
+    u32x3_a4 b0;
+    u32x2_a4 b1;
+    uint32_t s0, s1;
+    long a[2][T];       // digit mode
+    i32x4 cb[2][T];     // digit mode, q4_0
+    Op xh[2][T], xl[2][T];
+    f32x4 bb[2][T];     // dense mode, q4_0
+  };
+  auto load_ops = [&](const uint8_t* row, const uint8_t* xs, int pp) {
+    PairOps o;
+    const uint32_t* pr = reinterpret_cast<const uint32_t*>(row + pp * PairLayout<FMT>::bytes);
+    o.b0 = *reinterpret_cast<const u32x3_a4*>(pr + PairLayout<FMT>::blk0_dword(j));
+    o.b1 = *reinterpret_cast<const u32x2_a4*>(pr + PairLayout<FMT>::blk1_dword(j));
+    o.s0 = pr[0];
+    o.s1 = pr[PairLayout<FMT>::scale1_dword];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int blk = 2 * pp + h;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if constexpr (XB::digits) {
+          const uint8_t* rec = xs + blk * XB::bytes;
+          o.a[h][t] = *reinterpret_cast<const long*>(rec + t * 512 + 8 * lane);
+          if constexpr (L::bias)
+            o.cb[h][t] = *reinterpret_cast<const i32x4*>(rec + XB::bias_off + 16 * (4 * t + j));
+        } else {
+          const uint8_t* f = xs + (blk * T + t) * kFragBytes + lane * 16;
+          o.xh[h][t] = *reinterpret_cast<const Op*>(f);
+          o.xl[h][t] = *reinterpret_cast<const Op*>(f + 1024);
+          if constexpr (L::bias)
+            o.bb[h][t] = *reinterpret_cast<const f32x4*>(xs + L::x_bytes + (blk * T + t) * 64 + 16 * j);
+        }
+      }
+    }
+    return o;
+  };
+
   // Branch-free, so the compiler can overlap the pairs' LDS reads, code
   // conversions and MFMAs.  A pair past K or a stage past st1 (clamped
   // reloads) adds c * 0: its codes are finite integers and its activation
@@ -654,19 +697,18 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     float sacc[T];    // digit mode: this stage's sum, before its exponent
 #pragma unroll
     for (int t = 0; t < T; ++t) sacc[t] = 0.f;
+    PairOps cur = load_ops(row, xs, 0);
 #pragma unroll
     for (int pp = 0; pp < kStagePairs; ++pp) {
+      PairOps nxt;
+      if (pp + 1 < kStagePairs) nxt = load_ops(row, xs, pp + 1);
+      __builtin_amdgcn_sched_barrier(0);
       const bool valid = live && stage * kStagePairs + pp < npairs;   // wave-uniform
-      const uint32_t* pr = reinterpret_cast<const uint32_t*>(row + pp * PairLayout<FMT>::bytes);
-      const u32x3_a4 b0 = *reinterpret_cast<const u32x3_a4*>(pr + PairLayout<FMT>::blk0_dword(j));
-      const u32x2_a4 b1 = *reinterpret_cast<const u32x2_a4*>(pr + PairLayout<FMT>::blk1_dword(j));
-      const uint32_t s0 = pr[0], s1 = pr[PairLayout<FMT>::scale1_dword];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const uint32_t c0 = h == 0 ? __builtin_amdgcn_alignbyte(b0.y, b0.x, 2) : b1.x;
-        const uint32_t c1 = h == 0 ? __builtin_amdgcn_alignbyte(b0.z, b0.y, 2) : b1.y;
-        const uint32_t dbits = h == 0 ? (s0 & 0xFFFFu) : (s1 >> 16);
-        const int blk = 2 * pp + h;
+        const uint32_t c0 = h == 0 ? __builtin_amdgcn_alignbyte(cur.b0.y, cur.b0.x, 2) : cur.b1.x;
+        const uint32_t c1 = h == 0 ? __builtin_amdgcn_alignbyte(cur.b0.z, cur.b0.y, 2) : cur.b1.y;
+        const uint32_t dbits = h == 0 ? (cur.s0 & 0xFFFFu) : (cur.s1 >> 16);
         if constexpr (XB::digits) {
           // B operand: the lane's 8 codes as int8 (q8_0 as stored; q4_0
           // nibbles 0..15, the -8 entering through the C input).
@@ -678,15 +720,12 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
           }
           const long wq = static_cast<long>(w0) | (static_cast<long>(w1) << 32);
           const float dw = valid ? half_bits_to_float(dbits) : 0.0f;
-          const uint8_t* rec = xs + blk * XB::bytes;
 #pragma unroll
           for (int t = 0; t < T; ++t) {
-            const long a = *reinterpret_cast<const long*>(rec + t * 512 + 8 * lane);
             i32x4 c = {0, 0, 0, 0};
-            if constexpr (L::bias)
-              c = *reinterpret_cast<const i32x4*>(rec + XB::bias_off + 16 * (4 * t + j));
+            if constexpr (L::bias) c = cur.cb[h][t];
             // D lane (n, j): digit sums S_0..S_3 of row m = 4t + j (S_3 = 0)
-            c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wq, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.a[h][t], wq, c, 0, 0, 0);
             // 2^7 S1 + S2 is exact in int32 (|S| < 2^20), and its float
             // conversion is the same single rounding as fmaf(S1, 128, S2)
             const float f = fmaf(static_cast<float>(c[0]), 16384.f,
@@ -694,24 +733,20 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
             sacc[t] = fmaf(dw, f, sacc[t]);
           }
         } else {
-          using Op = typename OpType<FMT>::T;
           const Op wv = codes_op<FMT>(c0, c1, j);
           const float d = valid ? half_bits_to_float(dbits) : 0.0f;
 #pragma unroll
           for (int t = 0; t < T; ++t) {
-            const uint8_t* f = xs + (blk * T + t) * kFragBytes + lane * 16;
-            const Op xh = *reinterpret_cast<const Op*>(f);
-            const Op xl = *reinterpret_cast<const Op*>(f + 1024);
             f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (L::bias)
-              c = *reinterpret_cast<const f32x4*>(xs + L::x_bytes + (blk * T + t) * 64 + 16 * j);
-            c = mfma_op(xh, wv, c);
-            c = mfma_op(xl, wv, c);
+            if constexpr (L::bias) c = cur.bb[h][t];
+            c = mfma_op(cur.xh[h][t], wv, c);
+            c = mfma_op(cur.xl[h][t], wv, c);
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[t][e] = fmaf(c[e], d, acc[t][e]);
           }
         }
       }
+      if (pp + 1 < kStagePairs) cur = nxt;
     }
     if constexpr (XB::digits) {
       // the stage's exponent and gate of row m = 4t + j, from block 0's
