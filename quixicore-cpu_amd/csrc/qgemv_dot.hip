@@ -210,9 +210,42 @@ __device__ __forceinline__ float block_acc(float acc, uint32_t dbits, float gate
   return acc + ldexpf(t, e);
 }
 
-// acc += contribution of one pair (two blocks) of one row.
+// The f32 dot of block h (0 / 1) of a pair (its bytes at `wp` in global
+// memory) with the block's 32 values of x, summed in element order
+// (kernels/quantization/qgemv_ref.cpp:70-76); only for blocks of x that hold
+// NaN or +-inf, where it gives the reference's per-row inf / NaN.  A rolled
+// loop over memory in a function of its own: the rare form adds little
+// register pressure to the fast one.
 template <int FMT>
-__device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g, float acc) {
+__device__ __noinline__ float block_f32(const uint8_t* wp, int h, const float* xb) {
+  float s = 0.0f;
+#pragma unroll 1
+  for (int j = 0; j < 32; ++j) {
+    int q;
+    if constexpr (FMT == kQ8_0) {
+      q = static_cast<int8_t>(wp[(h == 0 ? 2 : 36) + j]);   // codes follow each fp16 scale
+    } else {
+      const uint8_t b = wp[(h == 0 ? 2 : 20) + (j & 15)];   // code j low, j + 16 high nibble
+      q = static_cast<int>(j < 16 ? (b & 0xF) : (b >> 4)) - 8;
+    }
+    s += static_cast<float>(q) * xb[j];
+  }
+  return s;
+}
+
+// True when a block of the pair holds a non-finite value of x (gate NaN).
+__device__ __forceinline__ bool pair_special(const PairDigits& g) {
+  return !(g.gate[0] == 1.0f && g.gate[1] == 1.0f);
+}
+
+// acc += contribution of one pair (two blocks) of one row.  SLOW: a block
+// whose gate is not 1 (non-finite x) adds d_w times the f32 dot of the
+// pair's bytes `wp` with its x values `xp` instead; every other block is
+// computed as in the fast form, bit for bit.
+template <int FMT, bool SLOW = false>
+__device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g, float acc,
+                                          const float* xp = nullptr,
+                                          const uint8_t* wp = nullptr) {
   if constexpr (FMT == kQ8_0) {
     int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
@@ -226,8 +259,15 @@ __device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g
       b1 = __builtin_amdgcn_sdot4(e, static_cast<int>(g.d[1][8 + i]), b1, false);
       b2 = __builtin_amdgcn_sdot4(e, static_cast<int>(g.d[2][8 + i]), b2, false);
     }
-    acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
-    acc = block_acc(acc, w[8] >> 16, g.gate[1], g.e[1], b0, b1, b2);
+    if constexpr (SLOW) {
+      acc = g.gate[0] == 1.0f ? block_acc(acc, w[0] & 0xFFFFu, 1.0f, g.e[0], a0, a1, a2)
+                              : acc + half_bits_to_float(w[0] & 0xFFFFu) * block_f32<FMT>(wp, 0, xp);
+      acc = g.gate[1] == 1.0f ? block_acc(acc, w[8] >> 16, 1.0f, g.e[1], b0, b1, b2)
+                              : acc + half_bits_to_float(w[8] >> 16) * block_f32<FMT>(wp, 1, xp + 32);
+    } else {
+      acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
+      acc = block_acc(acc, w[8] >> 16, g.gate[1], g.e[1], b0, b1, b2);
+    }
   } else {
     int a0 = g.off[0][0], a1 = g.off[0][1], a2 = g.off[0][2];
     int b0 = g.off[1][0], b1 = g.off[1][1], b2 = g.off[1][2];
@@ -252,8 +292,15 @@ __device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g
       b1 = __builtin_amdgcn_sdot4(hi1, static_cast<int>(g.d[1][12 + i]), b1, false);
       b2 = __builtin_amdgcn_sdot4(hi1, static_cast<int>(g.d[2][12 + i]), b2, false);
     }
-    acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
-    acc = block_acc(acc, w[4] >> 16, g.gate[1], g.e[1], b0, b1, b2);
+    if constexpr (SLOW) {
+      acc = g.gate[0] == 1.0f ? block_acc(acc, w[0] & 0xFFFFu, 1.0f, g.e[0], a0, a1, a2)
+                              : acc + half_bits_to_float(w[0] & 0xFFFFu) * block_f32<FMT>(wp, 0, xp);
+      acc = g.gate[1] == 1.0f ? block_acc(acc, w[4] >> 16, 1.0f, g.e[1], b0, b1, b2)
+                              : acc + half_bits_to_float(w[4] >> 16) * block_f32<FMT>(wp, 1, xp + 32);
+    } else {
+      acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
+      acc = block_acc(acc, w[4] >> 16, g.gate[1], g.e[1], b0, b1, b2);
+    }
   }
   return acc;
 }
@@ -392,11 +439,18 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
       const int p = p0 + 64 * j;
       PairDigits g;
       read_digits<FMT>(g, lds, min(p, pend - 1) - pbeg, kc);
+      // a non-finite x value in some lane's pair: that wave takes the form
+      // with the reference's per-row inf / NaN (rare; wave-uniform branch)
+      const bool slow = __any(p < pend && pair_special(g));
+      const float* xp = x + 64LL * min(p, pend - 1);
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int t = j * RB + r;
         if (t + WIN < T) issue(t + WIN);
-        if (p < pend) acc[r] = pair_dot<FMT>(w[t], g, acc[r]);
+        if (p < pend)
+          acc[r] = slow ? pair_dot<FMT, true>(w[t], g, acc[r], xp,
+                                              wrow[r] + static_cast<long long>(p) * (2 * BB))
+                        : pair_dot<FMT>(w[t], g, acc[r]);
       }
     }
   }
@@ -567,8 +621,14 @@ __global__ __launch_bounds__(64 * NW) void qgemm_rows_kernel(const uint8_t* __re
         for (int mm = 0; mm < MB; ++mm) {
           PairDigits dg;
           read_digits<FMT>(dg, lds + mm * lsz, p, kc);
+          // rows past m have no digits built: never their slow form
+          const bool slow = mm < m && __any(pair_special(dg));
+          const float* xp = x + static_cast<long long>(mm < m ? mm : 0) * k + 64 * p;
 #pragma unroll
-          for (int r = 0; r < RB; ++r) acc[r][mm] = pair_dot<FMT>(w[r], dg, acc[r][mm]);
+          for (int r = 0; r < RB; ++r)
+            acc[r][mm] = slow ? pair_dot<FMT, true>(w[r], dg, acc[r][mm], xp,
+                                                    wr[r] + static_cast<long long>(p) * (2 * BB))
+                              : pair_dot<FMT>(w[r], dg, acc[r][mm]);
         }
       }
       store(row0, acc);
@@ -610,8 +670,13 @@ __global__ __launch_bounds__(64 * NW) void qgemm_rows_kernel(const uint8_t* __re
       for (int mm = 0; mm < MB; ++mm) {
         PairDigits dg;
         read_digits<FMT>(dg, lds + mm * lsz, p - pbeg, kc);
+        const bool slow = mm < m && __any(pair_special(dg));
+        const float* xp = x + static_cast<long long>(mm < m ? mm : 0) * k + 64LL * p;
 #pragma unroll
-        for (int r = 0; r < RB; ++r) acc[r][mm] = pair_dot<FMT>(w[r], dg, acc[r][mm]);
+        for (int r = 0; r < RB; ++r)
+          acc[r][mm] = slow ? pair_dot<FMT, true>(w[r], dg, acc[r][mm], xp,
+                                                  wrow[r] + static_cast<long long>(p) * (2 * BB))
+                            : pair_dot<FMT>(w[r], dg, acc[r][mm]);
       }
     }
   }

@@ -337,3 +337,62 @@ def test_qgemm_fold_bitwise_prep(qc, oracle, synth, dev, fmt, m, n, k, waves, st
         _check_rows(oracle, fmt, packed, x[r], out[0][r], n, k)
     if m > 2:
         assert not np.isfinite(out[0][1]).any()
+
+
+def _classes(y):
+    return np.isnan(y), np.isposinf(y), np.isneginf(y)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("k,x_off", [(4096, 0), (14336, 0), (2048, 1)])
+def test_qgemv_nonfinite_activations(qc, oracle, synth, dev, fmt, k, x_off):
+    """x holding +-inf or NaN gives each row the reference's f32 result
+    class (kernels/quantization/qgemv_ref.cpp:62-80, qgemv_gguf_avx2.cpp:
+    295-318: y = sum_b d_b * sum_j q_j x_j): +inf / -inf by the signs of the
+    products, NaN where a zero weight meets an infinity, opposite infinities
+    meet, or x holds NaN.  The M = 2..4 rows route gives the same bits row
+    for row."""
+    import torch
+    n = 200
+    packed, _ = _case(oracle, synth, fmt, n, k, 1200 + k)
+    w64 = oracle.unpack(fmt, packed, n, k).astype(np.float64)
+    rng = np.random.default_rng(k + fmt)
+    base = rng.standard_normal(k).astype(np.float32)
+    cases = []
+    x = base.copy(); x[97] = np.inf; cases.append(x)
+    x = base.copy(); x[k - 5] = -np.inf; cases.append(x)                  # last block
+    x = base.copy(); x[40] = np.inf; x[k // 2 + 3] = -np.inf; cases.append(x)
+    x = base.copy(); x[300] = np.nan; cases.append(x)
+    x = base.copy(); x[0:32] = np.inf; cases.append(x)                    # a whole block
+    P = torch.from_numpy(packed).to(dev)
+    for i, x in enumerate(cases):
+        print(f"nonfinite fmt={fmt} k={k} x_off={x_off} case={i}", flush=True)
+        buf = torch.zeros(k + x_off, dtype=torch.float32, device=dev)
+        buf[x_off:] = torch.from_numpy(x).to(dev)
+        X = buf[x_off:]
+        y = torch.empty(n, dtype=torch.float32, device=dev)
+        assert qc.qgemv_raw(fmt, P, X, y, n, k) == 0
+        y = y.cpu().numpy()
+        with np.errstate(invalid="ignore", over="ignore"):
+            y64 = (w64 * x.astype(np.float64)[None, :]).sum(axis=1)
+        for got, want in zip(_classes(y), _classes(y64)):
+            assert np.array_equal(got, want), (i, np.flatnonzero(got != want)[:5])
+        assert not np.isfinite(y).any()
+    # rows route: every row bit-identical to qgemv of that row
+    m = 3
+    xm = np.stack([cases[0], base, cases[2]]).astype(np.float32)
+    buf = torch.zeros(m * k + x_off, dtype=torch.float32, device=dev)
+    buf[x_off:] = torch.from_numpy(xm.reshape(-1)).to(dev)
+    X = buf[x_off:].view(m, k)
+    qc.set_qgemm_rows(1)
+    try:
+        Y = torch.empty(m * n, dtype=torch.float32, device=dev)
+        assert qc.qgemm_raw(fmt, P, X, Y, m, n, k) == 0
+    finally:
+        qc.set_qgemm_rows(0)
+    Y = Y.cpu().numpy().reshape(m, n)
+    for r in range(m):
+        yr = torch.empty(n, dtype=torch.float32, device=dev)
+        assert qc.qgemv_raw(fmt, P, X[r], yr, n, k) == 0
+        assert np.array_equal(Y[r].view(np.uint32), yr.cpu().numpy().view(np.uint32)), r
+    assert np.all(np.isfinite(Y[1]))
