@@ -21,6 +21,7 @@
 #include <algorithm>
 
 #include "qc_device.h"
+#include "qc_digits.h"
 #include "qc_internal.h"
 
 namespace qc {
@@ -229,9 +230,10 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
       }
     }
   };
-  // 16 codes of one row at column e against the staged activations
-  auto step = [&](const uint4& c, float sc, float zv, int c0, int e, float (&acc)[MB],
-                  float (&sx)[MB], bool count_x) {
+  // 16 codes of one row at column e against the staged activations; affine
+  // codes enter as (q - z), the reference's decode, so an infinite x meets
+  // each weight's own sign (sum q x - z sum x could give inf - inf)
+  auto step = [&](const uint4& c, float sc, float zv, int c0, int e, float (&acc)[MB]) {
     float xv[MB][16];
 #pragma unroll
     for (int mm = 0; mm < MB; ++mm) {
@@ -242,48 +244,31 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
         xv[mm][4 * i] = t.x; xv[mm][4 * i + 1] = t.y; xv[mm][4 * i + 2] = t.z; xv[mm][4 * i + 3] = t.w;
       }
     }
-    float s16[MB];
-    if constexpr (AFF) {
-#pragma unroll
-      for (int mm = 0; mm < MB; ++mm) {
-        float t = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) t += xv[mm][i];
-        s16[mm] = t;
-        if constexpr (!GRP)
-          if (count_x) sx[mm] += t;
-      }
-    }
     float q[16];
     unpack16(c, q);
+    if constexpr (AFF) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) q[i] -= zv;
+    }
 #pragma unroll
     for (int mm = 0; mm < MB; ++mm) {
       float t = 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) t = fmaf(q[i], xv[mm][i], t);
-      if constexpr (GRP) {
-        if constexpr (AFF) t = fmaf(-zv, s16[mm], t);
-        acc[mm] = fmaf(sc, t, acc[mm]);
-      } else {
-        acc[mm] += t;
-      }
+      if constexpr (GRP) acc[mm] = fmaf(sc, t, acc[mm]);
+      else acc[mm] += t;
     }
   };
   // wave sums, returned to every lane; then lane (r * MB + mm) finishes one
   // value, or (paired modes) one row pair
-  auto finish = [&](int g0, const float* const (&sp)[RW], const float* const (&zp)[RW],
-                    float (&acc)[RW][MB], float (&sx)[MB]) {
+  auto finish = [&](int g0, const float* const (&sp)[RW], float (&acc)[RW][MB]) {
     float tot[RW][MB];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
       for (int mm = 0; mm < MB; ++mm) {
         float v = wave_sum(acc[r][mm]);
-        if constexpr (!GRP) {
-          const float sc = sp[r][0];
-          if constexpr (AFF) v = fmaf(-zp[r][0], wave_sum(sx[mm]), v);
-          v = sc * v;
-        }
+        if constexpr (!GRP) v = sp[r][0] * v;
         tot[r][mm] = v;
       }
     if (segs.mode == 0) {
@@ -304,7 +289,6 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
   };
 
   float acc[RW][MB];
-  float sx[MB];
   const int8_t* w[RW];
   const float* sp[RW];
   const float* zp[RW];
@@ -327,8 +311,6 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
     for (int r = 0; r < RW; ++r)
 #pragma unroll
       for (int mm = 0; mm < MB; ++mm) acc[r][mm] = 0.f;
-#pragma unroll
-    for (int mm = 0; mm < MB; ++mm) sx[mm] = 0.f;
     for (int c0 = 0; c0 < k; c0 += kc) {
       const int clen = min(kc, k - c0);
       if (!single) {
@@ -348,16 +330,18 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
           else if (r + 1 < RW) fetch(nxt, w[rn], sp[rn], zp[rn], c0);
           else if (!single && c0 + kc < k) fetch(nxt, w[0], sp[0], zp[0], c0 + kc);
           else if (gn < groups) fetch(nxt, wn[0], sn[0], zn[0], 0);
+          // affine row zero points: one per row
+          const float zr = AFF && !GRP ? zp[r][0] : 0.f;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = c + 16 * (lane + 64 * i);
-            if (e < c0 + clen) step(cur.c[i], cur.s[i], cur.z[i], c0, e, acc[r], sx, r == 0);
+            if (e < c0 + clen) step(cur.c[i], cur.s[i], GRP ? cur.z[i] : zr, c0, e, acc[r]);
           }
           cur = nxt;
         }
       }
     }
-    finish(g0, sp, zp, acc, sx);
+    finish(g0, sp, acc);
     if (gn >= groups) break;
     g = gn;
     g0 = gn0;
@@ -367,6 +351,177 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
       sp[r] = sn[r];
       zp[r] = zn[r];
     }
+  }
+}
+
+// sum_j (code_j - z) * x_j in f32, element order, over the 32 codes at
+// `codes` and x[xi ..]: the rare form for a block of x that holds NaN or
+// +-inf, whose per-element products give the reference's inf / NaN classes
+// (the split into sum q x - z sum x could turn +-inf into NaN).
+__device__ __noinline__ float cint8_block_f32(const int8_t* codes, const void* x, long long xi,
+                                              int xtype, float z) {
+  float s = 0.0f;
+#pragma unroll 1
+  for (int j = 0; j < 32; ++j) s += (static_cast<float>(codes[j]) - z) * load_x(x, xi + j, xtype);
+  return s;
+}
+
+// M = 1 with exact digit dots (the GEMV's encoding of x, qc_digits.h):
+// k % 64 == 0, 16-byte aligned codes, GRP groups a power of two >= 32.
+// Wave w of workgroup b owns logical rows (b * kWaves + w) * RB + r; lane l
+// the block pair p = l (mod 64) of each row in every chunk of up to 4096
+// columns, its 64 codes in four 16-byte loads issued after the thread's x
+// values and before the chunk's digit build.  Per block: f = 2^e (2^14 S0 + 2^7 S1 + S2) ~ sum_j q_j x_j
+// (three v_dot4 sums per 4 codes) and, for affine weights, xs = 2^e (2^14
+// D0 + 2^7 D1 + D2) ~ sum_j x_j over the same encoded x.  Group scales add
+// s_g (f - z_g xs) per block; row scales finish as s (sum f - z sum xs).
+template <int RB, bool GRP, bool AFF>
+__global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
+                                                             const void* __restrict__ x,
+                                                             int xtype, int k, bool xvec) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int kc = 4096;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int total = segs.start[segs.nseg];
+  const int g0 = (blockIdx.x * kWaves + wave) * RB;
+  const int8_t* w[RB];
+  const float* sp[RB];
+  const float* zp[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const RowRef rr = logical_row(segs, min(g0 + r, total - 1));
+    w[r] = segs.w[rr.seg] + static_cast<long long>(rr.row) * k;
+    sp[r] = segs.scale[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
+    zp[r] = AFF ? segs.zero[rr.seg] + static_cast<long long>(rr.row) * segs.groups : nullptr;
+  }
+  float acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = 0.f;
+  float sxs = 0.f;   // affine row scales: this lane's sum of xs (finite blocks)
+  for (int c0 = 0; c0 < k; c0 += kc) {
+    const int clen = min(kc, k - c0);
+    const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
+    const int p = first_pair(pbeg, lane);
+    const bool live = p < pend;
+    const int pc = min(p, pend - 1);
+    // 1. this thread's half-block of x (16 values; past the chunk it re-reads
+    // the last one, which is not built), issued before the codes so that
+    // waiting for it does not wait for them (loads retire in order); no
+    // branch around it, which would make the compiler wait at the join
+    const int nh = clen >> 4;
+    const int hx = min(static_cast<int>(threadIdx.x), nh - 1);
+    float v[16];
+    {
+      const long long xi = c0 + 16LL * hx;
+      if (xvec && xtype == QC_STORAGE_F32) {
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(&v[4 * i]) = src[i];
+      } else if (xvec) {
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + xi);
+        const uint4 a = src[0], b = src[1];
+        const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint16_t lo = static_cast<uint16_t>(wd[i]), hi = static_cast<uint16_t>(wd[i] >> 16);
+          if (xtype == QC_STORAGE_F16) {
+            v[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+            v[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+          } else {
+            v[2 * i] = __uint_as_float(static_cast<uint32_t>(lo) << 16);
+            v[2 * i + 1] = __uint_as_float(static_cast<uint32_t>(hi) << 16);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = load_x(x, xi + i, xtype);
+      }
+    }
+    // 2. the codes of this lane's pair of every row (and group scales)
+    uint4 cw[RB][4];
+    float gs[RB][2], gz[RB][2];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        cw[r][i] = *reinterpret_cast<const uint4*>(w[r] + 64LL * pc + 16 * i);
+      if constexpr (GRP) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int gi = (64 * pc + 32 * h) >> segs.gshift;
+          gs[r][h] = sp[r][gi];
+          gz[r][h] = AFF ? zp[r][gi] : 0.f;
+        }
+      }
+    }
+    // digits of this chunk of x (half-block h = thread; the two halves of a
+    // block sit in lanes t and t ^ 1, both inside or both past the chunk)
+    // 3. the chunk's digits
+    if (c0) lds_barrier();
+    if (static_cast<int>(threadIdx.x) < nh) build_half<AFF>(lds, v, threadIdx.x, kc);
+    lds_barrier();
+    if (live) {
+      PairDigits g;
+      read_digits<kQ8_0>(g, lds, p - pbeg, kc);
+      float xs[2] = {0.f, 0.f};
+      if constexpr (AFF) {
+        int ds[2][3];
+        read_digit_sums(ds, lds, p - pbeg, kc);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) xs[h] = ldexpf(combine(ds[h][0], ds[h][1], ds[h][2]), g.e[h]);
+        if constexpr (!GRP) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            if (g.gate[h] == 1.0f) sxs += xs[h];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        int sd[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint4 q4 = cw[r][i >> 2];
+          const uint32_t q = (i & 3) == 0 ? q4.x : (i & 3) == 1 ? q4.y : (i & 3) == 2 ? q4.z : q4.w;
+          const int hb = i >> 3;
+#pragma unroll
+          for (int t = 0; t < 3; ++t)
+            sd[hb][t] = __builtin_amdgcn_sdot4(static_cast<int>(q), static_cast<int>(g.d[t][i]),
+                                               sd[hb][t], false);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (g.gate[h] == 1.0f) {
+            const float f = ldexpf(combine(sd[h][0], sd[h][1], sd[h][2]), g.e[h]);
+            if constexpr (GRP) acc[r] = fmaf(gs[r][h], AFF ? fmaf(-gz[r][h], xs[h], f) : f, acc[r]);
+            else acc[r] += f;
+          } else {
+            const float z = AFF ? (GRP ? gz[r][h] : zp[r][0]) : 0.f;
+            const float b = cint8_block_f32(w[r] + 64LL * p + 32 * h, x, c0 + 64LL * (p - pbeg) + 32 * h,
+                                            xtype, z);
+            acc[r] += GRP ? gs[r][h] * b : b;
+          }
+        }
+      }
+    }
+  }
+  // wave sums; lane r finishes row r (paired modes: lane r the pair r, r + 1)
+  float tot[RB];
+  const float sx = AFF && !GRP ? wave_sum(sxs) : 0.f;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    float v = wave_sum(acc[r]);
+    if constexpr (!GRP) v = sp[r][0] * (AFF ? fmaf(-zp[r][0], sx, v) : v);
+    tot[r] = v;
+  }
+  if (segs.mode == 0) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      if (lane == r && g0 + r < total) epilogue(segs, g0 + r, 0, tot[r], 0.f);
+  } else {
+#pragma unroll
+    for (int r = 0; r + 1 < RB; r += 2)
+      if (lane == r && g0 + r < total) epilogue(segs, g0 + r, 0, tot[r], tot[r + 1]);
   }
 }
 
@@ -436,6 +591,26 @@ hipError_t launch_fast(const CSegs& sg, const void* x, int xtype, long long ldx,
   return hipSuccess;
 }
 
+template <int RB, bool GRP, bool AFF>
+hipError_t launch_dot(const CSegs& sg, const void* x, int xtype, int k, hipStream_t s) {
+  const int total = sg.start[sg.nseg];
+  const unsigned grid = static_cast<unsigned>((total + kWaves * RB - 1) / (kWaves * RB));
+  // x read in 16-byte pieces when it is 16-byte aligned (every half-block
+  // then is: k % 64 == 0)
+  const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  cint8_dot_kernel<RB, GRP, AFF><<<grid, kThreads, lds_size(4096), s>>>(sg, x, xtype, k, xvec);
+  return hipGetLastError();
+}
+
+template <bool GRP, bool AFF>
+hipError_t launch_dot_rb(const CSegs& sg, const void* x, int xtype, int k, int rb, hipStream_t s) {
+  switch (rb) {
+    case 8: return launch_dot<8, GRP, AFF>(sg, x, xtype, k, s);
+    case 4: return launch_dot<4, GRP, AFF>(sg, x, xtype, k, s);
+    default: return launch_dot<2, GRP, AFF>(sg, x, xtype, k, s);
+  }
+}
+
 template <int MB, int RW>
 hipError_t launch_mb(const CSegs& sg, bool grp, bool aff, const void* x, int xtype, long long ldx,
                      int m, int k, hipStream_t s) {
@@ -488,10 +663,23 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   bool fast = k % 16 == 0 && (!grp || (sg.gsize >= 16 && (1 << sg.gshift) == sg.gsize));
   for (int i = 0; i < L.nw; ++i)
     fast = fast && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
+  // M = 1: exact digit dots over 64-column block pairs, two rows per wave
+  // (K=4096, 14336 rows: 13.9 us against 15.3 / 16.6 us with 4 / 8 rows;
+  // SwiGLU over 2 x 14336 rows 22.3 against 23.7 / 27.3 us).
+  if (fast && m == 1 && k % 64 == 0 && (!grp || sg.gsize >= 32) && L.dot >= 0) {
+    int rb = 2;
+    if (L.rows_per_wave == 2 || L.rows_per_wave == 4 || L.rows_per_wave == 8) rb = L.rows_per_wave;
+    if (grp)
+      return aff ? launch_dot_rb<true, true>(sg, L.x, L.xtype, k, rb, s)
+                 : launch_dot_rb<true, false>(sg, L.x, L.xtype, k, rb, s);
+    return aff ? launch_dot_rb<false, true>(sg, L.x, L.xtype, k, rb, s)
+               : launch_dot_rb<false, false>(sg, L.x, L.xtype, k, rb, s);
+  }
   if (fast) {
     const int cus = device_cu_count();
-    const bool four = L.rows_per_wave ? L.rows_per_wave == 4
-                                       : (total + kWaves * 4 - 1) / (kWaves * 4) >= 2 * cus;
+    const bool four = L.rows_per_wave == 2 || L.rows_per_wave == 4
+                          ? L.rows_per_wave == 4
+                          : (total + kWaves * 4 - 1) / (kWaves * 4) >= 2 * cus;
     if (m == 1)
       return four ? launch_mb<1, 4>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s)
                   : launch_mb<1, 2>(sg, grp, aff, L.x, L.xtype, L.ldx, m, k, s);

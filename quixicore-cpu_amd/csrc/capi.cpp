@@ -526,7 +526,9 @@ int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void
     L.rope_cos = rope_cos;
     L.rope_sin = rope_sin;
   }
-  L.rows_per_wave = g_tuning.rows_per_wave == 2 || g_tuning.rows_per_wave == 4 ? g_tuning.rows_per_wave : 0;
+  const int rw = g_tuning.rows_per_wave;
+  L.rows_per_wave = rw == 2 || rw == 4 || rw == 8 ? rw : 0;
+  L.dot = g_tuning.cint8_dot;
   return finish(qc::launch_cint8(L, as_stream(stream)));
 }
 
@@ -647,6 +649,12 @@ int qc_hip_set_qgemm_panel(int mode) {
 int qc_hip_set_qgemm_rows(int mode) {
   if (mode < -1 || mode > 1) return QC_INVALID_ARGUMENT;
   g_tuning.qgemm_rows = mode;
+  return QC_OK;
+}
+
+int qc_hip_set_cint8_dot(int mode) {
+  if (mode < -1 || mode > 0) return QC_INVALID_ARGUMENT;
+  g_tuning.cint8_dot = mode;
   return QC_OK;
 }
 

@@ -19,6 +19,7 @@ struct GemvTuning {
   int qgemm_panel = 0;    // 2-D GEMM route: 0 = for m >= 64, -1 = never, 1 / 2 = always (K ranges)
   int qgemm_rows = 0;     // exact-digit rows route for 2 <= m <= 8: 0 = by shape, -1 = never, 1 = always
   int qgemm_fold = 0;     // digit-layout GEMM builds its own digits: 0 = where it can, -1 = never
+  int cint8_dot = 0;      // canonical int8, M = 1: digit-dot kernel 0 = where it applies, -1 = never
 };
 
 // y[m][n] = dequant(W)[n][:] . x[m][:]  (W canonical q8_0/q4_0 blocks).
@@ -105,7 +106,8 @@ struct CInt8Launch {
   int nrope = 0;
   const float* rope_cos = nullptr;
   const float* rope_sin = nullptr;
-  int rows_per_wave = 0;        // 2 or 4 (0: from the shape)
+  int rows_per_wave = 0;        // 2, 4 or (M = 1 digit kernel) 8; 0: from the shape
+  int dot = 0;                  // M = 1 digit-dot kernel: 0 where it applies, -1 never
 };
 hipError_t launch_cint8(const CInt8Launch& launch, hipStream_t s);
 

@@ -66,6 +66,7 @@ _SIGS = {
     "qc_hip_set_qgemm_panel": ([_I], _I),
     "qc_hip_set_qgemm_rows": ([_I], _I),
     "qc_hip_set_qgemm_fold": ([_I], _I),
+    "qc_hip_set_cint8_dot": ([_I], _I),
     "qc_hip_stream_read": ([_P, _LL, _P, _I, _P], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
@@ -317,6 +318,12 @@ def set_qgemm_rows(mode=0):
     M = 2, and M <= 4 with N <= 8192, at K <= 4096), -1 = never (MFMA
     small-batch kernels), 1 = always."""
     _check(lib.qc_hip_set_qgemm_rows(mode), "set_qgemm_rows")
+
+
+def set_cint8_dot(mode=0):
+    """Canonical int8 projections with one activation row: 0 = exact
+    digit-dot kernel where it applies, -1 = always the f32 kernel."""
+    _check(lib.qc_hip_set_cint8_dot(mode), "set_cint8_dot")
 
 
 def set_qgemm_fold(mode=0):

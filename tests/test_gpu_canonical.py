@@ -67,19 +67,32 @@ def _dev(qc, dev, arr, offset=0):
     return t[offset:]
 
 
-@pytest.mark.parametrize("rows,cols,groups,affine,m,offset", [
-    (14336, 4096, 1, False, 1, 0),     # SmoothQuant-style channel scales, decode
-    (4096, 4096, 32, True, 1, 0),      # affine, groups of 128
-    (4096, 14336, 1, False, 2, 0),
-    (1024, 4096, 64, False, 7, 0),     # passes of 4 activation rows
-    (300, 4008, 1, True, 3, 0),        # K % 16 != 0: byte-loading route
-    (256, 1024, 4, False, 2, 4),       # misaligned codes: byte-loading route
-    (130, 96, 3, True, 5, 0),          # groups of 32 over K = 96
+@pytest.mark.parametrize("rows,cols,groups,affine,m,offset,dot", [
+    (14336, 4096, 1, False, 1, 0, 0),     # SmoothQuant-style channel scales, decode
+    (14336, 4096, 1, False, 1, 0, -1),    # the same on the f32 multiply-add kernel
+    (4096, 4096, 32, True, 1, 0, 0),      # affine, groups of 128
+    (4096, 4096, 32, True, 1, 0, -1),
+    (1000, 14336, 1, True, 1, 0, 0),      # affine channel scales, K in 4 chunks
+    (600, 4096, 128, True, 1, 0, 0),      # groups of 32
+    (4096, 14336, 1, False, 2, 0, 0),
+    (1024, 4096, 64, False, 7, 0, 0),     # passes of 4 activation rows
+    (300, 4008, 1, True, 3, 0, 0),        # K % 16 != 0: byte-loading route
+    (256, 1024, 4, False, 2, 4, 0),       # misaligned codes: byte-loading route
+    (130, 96, 3, True, 5, 0, 0),          # groups of 32 over K = 96
 ])
-def test_cint8_project_contract(qc, oracle, synth, dev, rows, cols, groups, affine, m, offset):
+def test_cint8_project_contract(qc, oracle, synth, dev, rows, cols, groups, affine, m, offset, dot):
     import torch
-    print(f"cint8 rows={rows} cols={cols} groups={groups} affine={affine} m={m} off={offset}",
-          flush=True)
+    print(f"cint8 rows={rows} cols={cols} groups={groups} affine={affine} m={m} off={offset} "
+          f"dot={dot}", flush=True)
+    qc.set_cint8_dot(dot)
+    try:
+        _contract_case(qc, oracle, synth, dev, rows, cols, groups, affine, m, offset)
+    finally:
+        qc.set_cint8_dot(0)
+
+
+def _contract_case(qc, oracle, synth, dev, rows, cols, groups, affine, m, offset):
+    import torch
     codes, scales, zeros = _tensor(synth, rows + cols, rows, cols, groups, affine)
     x = synth.normal_fast(7 + m, m * cols).reshape(m, cols)
     C = _dev(qc, dev, codes, offset)
@@ -109,6 +122,59 @@ def test_cint8_project_contract(qc, oracle, synth, dev, rows, cols, groups, affi
     XB = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
     assert qc.cint8_project_raw(0, [w], XB, 2, m, [yb], [0]) == 0
     assert np.array_equal(yb.cpu().numpy().view(np.uint32), yd.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("groups,affine,x_type", [(1, False, 0), (1, True, 0), (32, True, 2),
+                                                  (32, False, 1)])
+def test_cint8_nonfinite_activations(qc, oracle, synth, dev, groups, affine, x_type):
+    """One activation row holding +-inf or NaN: every output gets the
+    reference's f32 class (decode w = s * (q - z), then sum w x;
+    kernels/quantization/qgemm_canonical.cpp:125-176): +-inf by the signs of
+    the products, NaN where a zero weight meets an infinity, opposite
+    infinities meet, or x holds NaN; on both M = 1 kernels."""
+    import torch
+    rows, cols = 300, 4096
+    codes, scales, zeros = _tensor(synth, 77 + groups, rows, cols, groups, affine)
+    codes[:, 200] = 0                                   # zero codes meet the infinity
+    if zeros is not None:
+        zeros[::5] = 0.0
+    keep = [_dev(qc, dev, a) for a in (codes, scales, zeros)]
+    w = qc.cint8_weights(keep[0], keep[1], keep[2], rows, cols, groups)
+    what = oracle.cint8_dequant(codes, scales, zeros, rows, cols, groups).astype(np.float64)
+    rng = np.random.default_rng(groups)
+    base = rng.standard_normal(cols).astype(np.float32)
+    cases = []
+    x = base.copy(); x[200] = np.inf; cases.append(x)
+    x = base.copy(); x[77] = -np.inf; x[3000] = np.inf; cases.append(x)
+    x = base.copy(); x[1234] = np.nan; cases.append(x)
+    x = base.copy(); x[4000] = np.inf; cases.append(x)
+    for dot in (0, -1):
+        qc.set_cint8_dot(dot)
+        try:
+            for i, x in enumerate(cases):
+                print(f"cint8 nonfinite groups={groups} affine={affine} x_type={x_type} dot={dot} "
+                      f"case={i}", flush=True)
+                if x_type == 0:
+                    X = torch.from_numpy(x).to(dev)
+                    xd = x
+                elif x_type == 1:
+                    xh = x.astype(np.float16)
+                    X = torch.from_numpy(xh.view(np.int16).copy()).to(dev)
+                    xd = xh.astype(np.float32)
+                else:
+                    xb = _bf16_bits(x)
+                    X = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+                    xd = (xb.astype(np.uint32) << 16).view(np.float32)
+                y = torch.empty(rows, dtype=torch.float32, device=dev)
+                assert qc.cint8_project_raw(0, [w], X, x_type, 1, [y], [0]) == 0
+                y = y.cpu().numpy()
+                with np.errstate(invalid="ignore", over="ignore"):
+                    y64 = (what * xd.astype(np.float64)[None, :]).sum(axis=1)
+                for got, want in ((np.isnan(y), np.isnan(y64)), (np.isposinf(y), np.isposinf(y64)),
+                                  (np.isneginf(y), np.isneginf(y64))):
+                    assert np.array_equal(got, want), (i, np.flatnonzero(got != want)[:5])
+        finally:
+            qc.set_cint8_dot(0)
 
 
 def test_cint8_fused_decode_shapes(qc, oracle, synth, dev):
