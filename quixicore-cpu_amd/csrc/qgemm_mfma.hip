@@ -456,7 +456,9 @@ struct WStage {
   static constexpr int wave_bytes = 16 * row_bytes;
 };
 
-template <int FMT, int XL, int NW>
+// KG: K ranges sharing one workgroup (one ring per range); FOLD: x staging
+// area of the digit build.
+template <int FMT, int XL, int NW, int KG = 1, bool FOLD = false>
 struct StageLayout {
   using XB = XBlock<XL, FMT == kQ4_0>;
   static constexpr bool bias = FMT == kQ4_0;
@@ -466,7 +468,8 @@ struct StageLayout {
   static constexpr int bytes = w_bytes + x_bytes + bias_bytes;
   // Ring depth: three stages when they fit the 160 KB LDS, else two (deeper
   // rings measured slower on MI355X).
-  static constexpr int ring = 3 * bytes <= 160 * 1024 ? 3 : 2;
+  static constexpr int xstage_bytes = FOLD ? 16 * 64 * XL : 0;
+  static constexpr int ring = KG * (3 * bytes + xstage_bytes) <= 160 * 1024 ? 3 : 2;
   // The x bytes of a stage are xc 16-byte chunks; wave w copies chunks
   // [w * cpw, (w + 1) * cpw) with gx loads (the last ones partial).
   static constexpr int xc = x_bytes / 16;
@@ -485,16 +488,23 @@ struct StageLayout {
 // computed, then turned into digits (digit_stage_row, the prep kernel's own
 // arithmetic, so the records are the same bytes) and written into the free
 // ring slot, which the next barriers publish.
-template <int FMT, int XL, int NW, int NST, bool FOLD>
-__global__ __launch_bounds__(64 * NW) void qgemm_mfma(
+//
+// KG = 2 (digit layouts): the two K ranges of a row slab run in one
+// workgroup, NW waves each with a ring of their own, and meet in LDS at the
+// end (range 0 + range 1, always in that order): no atomics, so y needs no
+// clearing and, with FOLD, the call no prep launch (the q8_0 4-row layout:
+// see run()).
+template <int FMT, int XL, int NW, int NST, bool FOLD, int KG = 1>
+__global__ __launch_bounds__(64 * NW * KG) void qgemm_mfma(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ x,
     const float* __restrict__ bias, float* __restrict__ y, float* __restrict__ partial,
     const uint8_t* __restrict__ tail_pad, const int* __restrict__ rexp, int M, int N, int K,
     int nslabs, int ks_count, int nstages) {
-  using L = StageLayout<FMT, XL, NW>;
+  using L = StageLayout<FMT, XL, NW, KG, FOLD>;
   using XB = typename L::XB;
   using WS = WStage<FMT>;
   static_assert(!FOLD || XB::digits, "only the digit layouts are built in the GEMM");
+  static_assert(KG == 1 || (KG == 2 && XB::digits), "K ranges meet in LDS in digit mode");
   constexpr int T = XB::T;
   constexpr int kSlab = 16 * NW;
   constexpr int S = L::ring;
@@ -505,16 +515,22 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
   // One LDS array per ring slot: slot indices are compile-time after
   // unrolling, so the compiler can tell the reads of one slot from the
   // global->LDS writes into another and adds no waits of its own.
-  __shared__ __attribute__((aligned(1024))) uint8_t ring0[L::bytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t ring1[L::bytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t ring2[S > 2 ? L::bytes : 16];
-  auto slot_base = [&](int slot) -> uint8_t* { return slot == 0 ? ring0 : slot == 1 ? ring1 : ring2; };
+  __shared__ __attribute__((aligned(1024))) uint8_t ring0[KG * L::bytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring1[KG * L::bytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring2[S > 2 ? KG * L::bytes : 16];
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // kgrp: this wave's K range within the workgroup; wave: its index there
+  const int wall = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kgrp = KG == 1 ? 0 : wall / NW;
+  const int wave = KG == 1 ? wall : wall % NW;
+  const int tid = static_cast<int>(threadIdx.x) - kgrp * 64 * NW;
+  auto slot_base = [&](int slot) -> uint8_t* {
+    return (slot == 0 ? ring0 : slot == 1 ? ring1 : ring2) + kgrp * L::bytes;
+  };
   const int j = lane >> 4;
   const int slab = blockIdx.x % nslabs;
-  const int ks = blockIdx.x / nslabs;
+  const int ks = (blockIdx.x / nslabs) * KG + kgrp;
   // NST stages per workgroup (the last K range may hold fewer).
   const int st0 = ks * NST;
   const int st1 = st0 + NST < nstages ? st0 + NST : nstages;
@@ -596,12 +612,13 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
   // 0 and are zeroed when the digits are built.
   constexpr int kTasks = 64 * XL, kThreadsWg = 64 * NW;
   constexpr int TPT = kTasks >= kThreadsWg ? kTasks / kThreadsWg : 1;
-  __shared__ __attribute__((aligned(16))) uint8_t xstage[FOLD ? 16 * kTasks : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t xstage_all[FOLD ? KG * 16 * kTasks : 16];
+  uint8_t* const xstage = xstage_all + (FOLD ? kgrp * 16 * kTasks : 0);
   const bool xtask = kTasks >= kThreadsWg || wave * 64 < kTasks;   // wave-uniform
   uint32_t xsrc[TPT];
 #pragma unroll
   for (int t = 0; t < TPT; ++t) {
-    const int tau = static_cast<int>(threadIdx.x) + kThreadsWg * t;
+    const int tau = tid + kThreadsWg * t;
     const int m = tau >> 6;
     xsrc[t] = static_cast<uint32_t>(4 * (static_cast<long long>(m < M ? m : 0) * K + 4 * lane));
   }
@@ -623,7 +640,7 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
       if (xtask) {
 #pragma unroll
         for (int t = 0; t < TPT; ++t) {
-          const int tau = static_cast<int>(threadIdx.x) + kThreadsWg * t;
+          const int tau = tid + kThreadsWg * t;
           const int m = tau >> 6;
           const bool live = m < M;
           const f32x4 xv = *reinterpret_cast<const f32x4*>(xstage + 16 * tau);
@@ -819,6 +836,22 @@ __global__ __launch_bounds__(64 * NW) void qgemm_mfma(
     }
   }
   wait_vmcnt<0>();   // no global->LDS load may outlive the workgroup's LDS
+  if constexpr (KG == 2) {
+    // range 1's sums to LDS (the rings are no longer read), then range 0
+    // adds them and stores
+    float* ex = reinterpret_cast<float*>(ring0);
+    wait_lgkmcnt0();
+    ring_barrier();
+    if (kgrp == 1) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) ex[t * 64 * NW + tid] = accd[t];
+    }
+    wait_lgkmcnt0();
+    ring_barrier();
+    if (kgrp == 1) return;
+#pragma unroll
+    for (int t = 0; t < T; ++t) accd[t] = accd[t] + ex[t * 64 * NW + tid];
+  }
 
   // acc[t][e] is output (m = 16t + 4j + e, n).  One K range: store.  Two:
   // both add into the zeroed y (0 + a + b == 0 + b + a, so the result does
@@ -948,22 +981,24 @@ struct MfmaArgs {
   int m, n, k, nslabs, ks, nstages;
 };
 
-template <int FMT, int XL, int NW, int NST, bool FOLD>
+// KG = 2: a.ks must be 2; one workgroup of 2 NW waves per row slab, which
+// stores y itself (ks_count 1).
+template <int FMT, int XL, int NW, int NST, bool FOLD, int KG = 1>
 hipError_t launch_nst(const MfmaArgs& a, hipStream_t s) {
-  qgemm_mfma<FMT, XL, NW, NST, FOLD><<<a.nslabs * a.ks, 64 * NW, 0, s>>>(
-      a.W, a.xf, a.x, a.bias, a.y, a.partial, a.tail_pad, a.rexp, a.m, a.n, a.k, a.nslabs, a.ks,
-      a.nstages);
+  qgemm_mfma<FMT, XL, NW, NST, FOLD, KG><<<a.nslabs * (a.ks / KG), 64 * NW * KG, 0, s>>>(
+      a.W, a.xf, a.x, a.bias, a.y, a.partial, a.tail_pad, a.rexp, a.m, a.n, a.k, a.nslabs,
+      KG == 2 ? 1 : a.ks, a.nstages);
   return hipGetLastError();
 }
 
-template <int FMT, int XL, int NW, bool FOLD>
+template <int FMT, int XL, int NW, bool FOLD, int KG = 1>
 hipError_t launch_nw(int nst, const MfmaArgs& a, hipStream_t s) {
   switch (nst) {
-    case 16: return launch_nst<FMT, XL, NW, 16, FOLD>(a, s);
-    case 8: return launch_nst<FMT, XL, NW, 8, FOLD>(a, s);
-    case 4: return launch_nst<FMT, XL, NW, 4, FOLD>(a, s);
-    case 2: return launch_nst<FMT, XL, NW, 2, FOLD>(a, s);
-    default: return launch_nst<FMT, XL, NW, 1, FOLD>(a, s);
+    case 16: return launch_nst<FMT, XL, NW, 16, FOLD, KG>(a, s);
+    case 8: return launch_nst<FMT, XL, NW, 8, FOLD, KG>(a, s);
+    case 4: return launch_nst<FMT, XL, NW, 4, FOLD, KG>(a, s);
+    case 2: return launch_nst<FMT, XL, NW, 2, FOLD, KG>(a, s);
+    default: return launch_nst<FMT, XL, NW, 1, FOLD, KG>(a, s);
   }
 }
 
@@ -1032,9 +1067,16 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   // Digit layouts without the prep launch: the GEMM builds the digits (no
   // short last stage to pad, x loadable in 16-byte pieces, and no y to clear
   // for a two-way K split).
-  const bool fold = XB::digits && scratch.fold >= 0 && k % (32 * kStageBlocks) == 0 &&
-                    reinterpret_cast<uintptr_t>(x) % 16 == 0 && ks != 2 &&
-                    static_cast<long long>(m) * k * 4 < (1LL << 32);
+  // A two-way K split either keeps the prep launch (which clears y for the
+  // two atomic halves) or, for q8_0 with up to 4 rows, runs both ranges in
+  // one workgroup, meeting in LDS (K=4096 N=14336 M=4: 18.4 -> 17.0 us).
+  // With 8 rows, or q4_0's half-size weights, the digit builds the paired
+  // workgroup repeats cost more than the launch (q4_0 M=8 17.8 -> 22.5 us).
+  const bool can_fold = XB::digits && scratch.fold >= 0 && k % (32 * kStageBlocks) == 0 &&
+                        reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                        static_cast<long long>(m) * k * 4 < (1LL << 32);
+  const bool paired = can_fold && ks == 2 && XL == 4 && FMT == kQ8_0;
+  const bool fold = can_fold && (ks != 2 || paired);
   const size_t xf_bytes = fold ? 0 : static_cast<size_t>(nstages) * XB::stage_bytes;
   const size_t bias_bytes = static_cast<size_t>(nbp) * XB::bias_bytes;
   const size_t part_bytes = ks > 2 ? static_cast<size_t>(ks) * m * n * sizeof(float) : 0;
@@ -1066,7 +1108,14 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
   }
   const MfmaArgs a{W, xf, x, bias, y, partial, tail_pad, rexp, m, n, k, nslabs, ks, nstages};
   if constexpr (XB::digits) {
-    if (fold)
+    if (paired) {
+      // the same waves per row slab as the plan: 4 per K range
+      if constexpr (XL == 4 && FMT == kQ8_0) {
+        MfmaArgs p = a;
+        p.nslabs = (n + 63) / 64;
+        e = launch_nw<FMT, XL, 4, true, 2>(plan.nst, p, s);
+      }
+    } else if (fold)
       e = plan.nw == 8 ? launch_nw<FMT, XL, 8, true>(plan.nst, a, s)
                        : launch_nw<FMT, XL, 4, true>(plan.nst, a, s);
     else
