@@ -19,9 +19,9 @@
 // int32 sums of int8 x int8 products (v_dot4_i32_i8, 4 MACs per instruction):
 //   sum_j w_j x_j ~= 2^e_b * d_w * (2^14 S0 + 2^7 S1 + S2),  S_t = sum_j c_j d_t,j
 // with c_j the q8_0 code, or the q4_0 nibble n_j with the -8 offset folded in
-// exactly as S_t -= 8 * sum_j d_t,j.  A block of x holding NaN or +-inf is
-// computed in f32 instead (pair_dot's SLOW form), which gives each row the
-// reference's inf or NaN.  Blocks are accumulated in f32 in a fixed per-lane order
+// exactly as S_t -= 8 * sum_j d_t,j.  When x holds NaN or +-inf, every row is
+// recomputed after the main loop in the reference's f32 form (row_f32), which
+// gives each output the reference's inf or NaN.  Blocks are accumulated in f32 in a fixed per-lane order
 // and reduced across the wave in a fixed butterfly, so results are
 // deterministic.
 //
@@ -86,12 +86,9 @@ __device__ __forceinline__ float block_acc(float acc, uint32_t dbits, float gate
 
 // The f32 dot of block h (0 / 1) of a pair (its bytes at `wp` in global
 // memory) with the block's 32 values of x, summed in element order
-// (kernels/quantization/qgemv_ref.cpp:70-76); only for blocks of x that hold
-// NaN or +-inf, where it gives the reference's per-row inf / NaN.  A rolled
-// loop over memory in a function of its own: the rare form adds little
-// register pressure to the fast one.
+// (kernels/quantization/qgemv_ref.cpp:70-76).
 template <int FMT>
-__device__ __noinline__ float block_f32(const uint8_t* wp, int h, const float* xb) {
+__device__ __forceinline__ float block_f32(const uint8_t* wp, int h, const float* xb) {
   float s = 0.0f;
 #pragma unroll 1
   for (int j = 0; j < 32; ++j) {
@@ -107,19 +104,36 @@ __device__ __noinline__ float block_f32(const uint8_t* wp, int h, const float* x
   return s;
 }
 
+// One row's sum over this lane's block pairs p = lane (mod 64) in f32, from
+// memory: sum_b d_b * sum_j q_j x_j as the reference forms it
+// (kernels/quantization/qgemv_ref.cpp:62-80).  Used for the rows whose x
+// holds NaN or +-inf: every output of such an activation row is +-inf or
+// NaN, set by its non-finite products alone, and this gives the reference's
+// class (the digit path would give NaN throughout).  Rare, so a rolled loop
+// after the main one, which keeps it out of the fast loop's code.
+template <int FMT>
+__device__ __forceinline__ float row_f32(const uint8_t* wrow, const float* x, int k, int lane) {
+  constexpr int BB = Fmt<FMT>::block_bytes;
+  float acc = 0.0f;
+#pragma unroll 1
+  for (int p = lane; p < (k >> 6); p += 64) {
+    const uint8_t* wp = wrow + static_cast<long long>(p) * (2 * BB);
+    const uint16_t d0 = *reinterpret_cast<const uint16_t*>(wp);
+    const uint16_t d1 = *reinterpret_cast<const uint16_t*>(wp + BB);
+    acc += half_bits_to_float(d0) * block_f32<FMT>(wp, 0, x + 64LL * p);
+    acc += half_bits_to_float(d1) * block_f32<FMT>(wp, 1, x + 64LL * p + 32);
+  }
+  return acc;
+}
+
 // True when a block of the pair holds a non-finite value of x (gate NaN).
 __device__ __forceinline__ bool pair_special(const PairDigits& g) {
   return !(g.gate[0] == 1.0f && g.gate[1] == 1.0f);
 }
 
-// acc += contribution of one pair (two blocks) of one row.  SLOW: a block
-// whose gate is not 1 (non-finite x) adds d_w times the f32 dot of the
-// pair's bytes `wp` with its x values `xp` instead; every other block is
-// computed as in the fast form, bit for bit.
-template <int FMT, bool SLOW = false>
-__device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g, float acc,
-                                          const float* xp = nullptr,
-                                          const uint8_t* wp = nullptr) {
+// acc += contribution of one pair (two blocks) of one row.
+template <int FMT>
+__device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g, float acc) {
   if constexpr (FMT == kQ8_0) {
     int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
@@ -133,15 +147,8 @@ __device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g
       b1 = __builtin_amdgcn_sdot4(e, static_cast<int>(g.d[1][8 + i]), b1, false);
       b2 = __builtin_amdgcn_sdot4(e, static_cast<int>(g.d[2][8 + i]), b2, false);
     }
-    if constexpr (SLOW) {
-      acc = g.gate[0] == 1.0f ? block_acc(acc, w[0] & 0xFFFFu, 1.0f, g.e[0], a0, a1, a2)
-                              : acc + half_bits_to_float(w[0] & 0xFFFFu) * block_f32<FMT>(wp, 0, xp);
-      acc = g.gate[1] == 1.0f ? block_acc(acc, w[8] >> 16, 1.0f, g.e[1], b0, b1, b2)
-                              : acc + half_bits_to_float(w[8] >> 16) * block_f32<FMT>(wp, 1, xp + 32);
-    } else {
-      acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
-      acc = block_acc(acc, w[8] >> 16, g.gate[1], g.e[1], b0, b1, b2);
-    }
+    acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
+    acc = block_acc(acc, w[8] >> 16, g.gate[1], g.e[1], b0, b1, b2);
   } else {
     int a0 = g.off[0][0], a1 = g.off[0][1], a2 = g.off[0][2];
     int b0 = g.off[1][0], b1 = g.off[1][1], b2 = g.off[1][2];
@@ -166,15 +173,8 @@ __device__ __forceinline__ float pair_dot(const uint32_t* w, const PairDigits& g
       b1 = __builtin_amdgcn_sdot4(hi1, static_cast<int>(g.d[1][12 + i]), b1, false);
       b2 = __builtin_amdgcn_sdot4(hi1, static_cast<int>(g.d[2][12 + i]), b2, false);
     }
-    if constexpr (SLOW) {
-      acc = g.gate[0] == 1.0f ? block_acc(acc, w[0] & 0xFFFFu, 1.0f, g.e[0], a0, a1, a2)
-                              : acc + half_bits_to_float(w[0] & 0xFFFFu) * block_f32<FMT>(wp, 0, xp);
-      acc = g.gate[1] == 1.0f ? block_acc(acc, w[4] >> 16, 1.0f, g.e[1], b0, b1, b2)
-                              : acc + half_bits_to_float(w[4] >> 16) * block_f32<FMT>(wp, 1, xp + 32);
-    } else {
-      acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
-      acc = block_acc(acc, w[4] >> 16, g.gate[1], g.e[1], b0, b1, b2);
-    }
+    acc = block_acc(acc, w[0] & 0xFFFFu, g.gate[0], g.e[0], a0, a1, a2);
+    acc = block_acc(acc, w[4] >> 16, g.gate[1], g.e[1], b0, b1, b2);
   }
   return acc;
 }
@@ -287,6 +287,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
   float acc[RB];
 #pragma unroll
   for (int r = 0; r < RB; ++r) acc[r] = 0.f;
+  bool nonfinite = false;   // some block of x is NaN or +-inf (every row's output then is)
 
   for (int c0 = 0; c0 < k; c0 += kc) {
     const int clen = min(kc, k - c0);
@@ -313,20 +314,19 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
       const int p = p0 + 64 * j;
       PairDigits g;
       read_digits<FMT>(g, lds, min(p, pend - 1) - pbeg, kc);
-      // a non-finite x value in some lane's pair: that wave takes the form
-      // with the reference's per-row inf / NaN (rare; wave-uniform branch)
-      const bool slow = __any(p < pend && pair_special(g));
-      const float* xp = x + 64LL * min(p, pend - 1);
+      nonfinite = nonfinite || __any(p < pend && pair_special(g));
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int t = j * RB + r;
         if (t + WIN < T) issue(t + WIN);
-        if (p < pend)
-          acc[r] = slow ? pair_dot<FMT, true>(w[t], g, acc[r], xp,
-                                              wrow[r] + static_cast<long long>(p) * (2 * BB))
-                        : pair_dot<FMT>(w[t], g, acc[r]);
+        if (p < pend) acc[r] = pair_dot<FMT>(w[t], g, acc[r]);
       }
     }
+  }
+  // x held NaN or +-inf (wave-uniform, rare): the reference's f32 form
+  if (nonfinite) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) acc[r] = row_f32<FMT>(wrow[r], x, k, lane);
   }
   if constexpr (!MULTI) {
 #pragma unroll
@@ -385,6 +385,27 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
       const bool in2 = three && g >= s2, in1 = g >= s1;
       float* const out = in2 ? y2 : in1 ? y1 : y0;
       out[g - (in2 ? s2 : in1 ? s1 : 0)] = t[r];
+    }
+  }
+}
+
+// For the rows kernel, after its main loop, when some activation row in
+// `mask` held a non-finite x value: the outputs of those activation rows for
+// weight rows [row0, row0 + rb) are stored again in the reference's f32 form
+// (qgemv's own row_f32 and reduction, so each stays bit-identical to qgemv of
+// its row).  Out of line and called after the main loop, so the loop keeps
+// its code and registers.
+template <int FMT>
+__device__ __noinline__ void rows_fix_group(const uint8_t* W, const float* x, float* y, int n,
+                                            int k, int mb, int row0, int rb, uint32_t mask) {
+  const int lane = threadIdx.x & 63;
+  const long long row_bytes = static_cast<long long>(k >> 5) * Fmt<FMT>::block_bytes;
+  for (int mm = 0; mm < mb; ++mm) {
+    if (!((mask >> mm) & 1u)) continue;
+    for (int r = 0; r < rb; ++r) {
+      const uint8_t* wr = W + static_cast<long long>(min(row0 + r, n - 1)) * row_bytes;
+      const float t = wave_sum_lane63(row_f32<FMT>(wr, x + static_cast<long long>(mm) * k, k, lane));
+      if (lane == 63 && row0 + r < n) y[static_cast<long long>(mm) * n + row0 + r] = t;
     }
   }
 }
@@ -467,10 +488,29 @@ __global__ __launch_bounds__(64 * NW) void qgemm_rows_kernel(const uint8_t* __re
       }
   };
 
+  // Bit mm: some lane's pair of activation row mm holds a non-finite x value
+  // in the chunk just built (wave-uniform; rows past m have no digits).
+  auto slow_rows = [&](int pend, int pbeg) {
+    const int p = first_pair(pbeg, lane);
+    const int pl = min(p, pend - 1) - pbeg;
+    uint32_t mask = 0;
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) {
+      const float2 gv = *reinterpret_cast<const float2*>(lds + mm * lsz + gate_off(kc) + 8 * pl);
+      const bool sp = p < pend && mm < m && !(gv.x == 1.0f && gv.y == 1.0f);
+      if (__any(sp)) mask |= 1u << mm;
+    }
+    return mask;
+  };
+  auto fix_group = [&](uint32_t mask, int g) {
+    rows_fix_group<FMT>(W, x, y, n, k, MB, (g * NW + wave) * RB, RB, mask);
+  };
+
   if (single) {
     // one chunk: digits once, then a stream of row groups; two register sets
     // of weights alternate (statically, so neither leaves registers): one is
     // computed while the next group's loads fill the other
+    uint32_t badbits = 0;   // bit mm: this lane's pair of row mm holds a non-finite x
     const int pend = k >> 6;
     const int p = lane;                            // this lane's only pair
     const int G = gridDim.x;
@@ -495,14 +535,9 @@ __global__ __launch_bounds__(64 * NW) void qgemm_rows_kernel(const uint8_t* __re
         for (int mm = 0; mm < MB; ++mm) {
           PairDigits dg;
           read_digits<FMT>(dg, lds + mm * lsz, p, kc);
-          // rows past m have no digits built: never their slow form
-          const bool slow = mm < m && __any(pair_special(dg));
-          const float* xp = x + static_cast<long long>(mm < m ? mm : 0) * k + 64 * p;
+          badbits |= pair_special(dg) ? 1u << mm : 0u;
 #pragma unroll
-          for (int r = 0; r < RB; ++r)
-            acc[r][mm] = slow ? pair_dot<FMT, true>(w[r], dg, acc[r][mm], xp,
-                                                    wr[r] + static_cast<long long>(p) * (2 * BB))
-                              : pair_dot<FMT>(w[r], dg, acc[r][mm]);
+          for (int r = 0; r < RB; ++r) acc[r][mm] = pair_dot<FMT>(w[r], dg, acc[r][mm]);
         }
       }
       store(row0, acc);
@@ -518,10 +553,20 @@ __global__ __launch_bounds__(64 * NW) void qgemm_rows_kernel(const uint8_t* __re
       if (g + 2 * G < groups) issue(wa, g + 2 * G);
       compute(wb, g + G);
     }
+    // did any lane meet a non-finite x value (rows past m have no digits)?
+    uint32_t slowmask = 0;
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm)
+      if (mm < m && __any((badbits >> mm) & 1u)) slowmask |= 1u << mm;
+    if (slowmask != 0) {
+#pragma unroll 1
+      for (int gg = blockIdx.x; gg < groups; gg += G) fix_group(slowmask, gg);
+    }
     return;
   }
 
   // several chunks: one row group per workgroup, digits rebuilt per chunk
+  uint32_t slowmask = 0;
   const uint8_t* wrow[RB];
   const int row0 = rows_of(blockIdx.x, wrow);
   float acc[RB][MB];
@@ -544,17 +589,14 @@ __global__ __launch_bounds__(64 * NW) void qgemm_rows_kernel(const uint8_t* __re
       for (int mm = 0; mm < MB; ++mm) {
         PairDigits dg;
         read_digits<FMT>(dg, lds + mm * lsz, p - pbeg, kc);
-        const bool slow = mm < m && __any(pair_special(dg));
-        const float* xp = x + static_cast<long long>(mm < m ? mm : 0) * k + 64LL * p;
 #pragma unroll
-        for (int r = 0; r < RB; ++r)
-          acc[r][mm] = slow ? pair_dot<FMT, true>(w[r], dg, acc[r][mm], xp,
-                                                  wrow[r] + static_cast<long long>(p) * (2 * BB))
-                            : pair_dot<FMT>(w[r], dg, acc[r][mm]);
+        for (int r = 0; r < RB; ++r) acc[r][mm] = pair_dot<FMT>(w[r], dg, acc[r][mm]);
       }
     }
+    slowmask |= slow_rows(pend, pbeg);
   }
   store(row0, acc);
+  if (slowmask != 0) fix_group(slowmask, blockIdx.x);
 }
 
 // ------------------------------------------------------------ qgemv_w8a8
