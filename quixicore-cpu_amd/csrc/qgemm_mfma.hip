@@ -38,9 +38,11 @@
 // few workgroups.  With ks = 2 both halves add atomically into a y that the
 // prep kernel zeroed (two addends onto zero: order-independent); with
 // ks > 2 the partial sums go to a workspace and a small kernel adds them in
-// index order.  Results are deterministic either way.  (A per-workgroup
-// device-scope fence, as a "last workgroup reduces" scheme needs, writes
-// back the XCD's whole L2 and costs far more than the extra launch.)
+// index order.  Results are deterministic either way.  Having the slab's
+// last workgroup add the partial sums instead (a per-slab counter behind a
+// device-scope fence) measured slower than the extra launch: +2.4 to +17 us
+// at N=4096, M=8..32; with agent-scope write-through stores and loads and no
+// L2 writeback, equal at M=8 and +2 to +10 us at M=16 / 32.
 #include <algorithm>
 #include <memory>
 #include <mutex>
