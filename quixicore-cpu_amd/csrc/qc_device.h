@@ -115,4 +115,50 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
 // 4-byte-aligned 128-bit load (global_load_dwordx4 accepts dword alignment).
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
+// The f32 dot of block h (0 / 1) of a pair (its bytes at `wp` in global
+// memory) with the block's 32 values of x, summed in element order
+// (kernels/quantization/qgemv_ref.cpp:70-76).
+template <int FMT>
+__device__ __forceinline__ float block_f32(const uint8_t* wp, int h, const float* xb) {
+  float s = 0.0f;
+#pragma unroll 1
+  for (int j = 0; j < 32; ++j) {
+    int q;
+    if constexpr (FMT == kQ8_0) {
+      q = static_cast<int8_t>(wp[(h == 0 ? 2 : 36) + j]);   // codes follow each fp16 scale
+    } else {
+      const uint8_t b = wp[(h == 0 ? 2 : 20) + (j & 15)];   // code j low, j + 16 high nibble
+      q = static_cast<int>(j < 16 ? (b & 0xF) : (b >> 4)) - 8;
+    }
+    s += static_cast<float>(q) * xb[j];
+  }
+  return s;
+}
+
+// For an activation row x holding NaN or +-inf: the sum over blocks
+// [b0, b1) of W row `wrow` of d_b * sum_j q_j x_j in f32, taken over the
+// blocks whose 32 values of x hold NaN or +-inf only.  Each such block gives
+// +-inf or NaN (the reference's class: +-inf by the signs of its products,
+// NaN where a zero weight or scale meets an infinity, opposite infinities
+// meet, or x holds NaN), and the finite blocks the reference adds to them do
+// not change the result, so this is the reference's value of a K range in
+// which x is not finite; ranges added together keep that class.  A rare
+// path: callers reach it from one rolled loop after their main work.
+template <int FMT>
+__device__ __forceinline__ float nonfinite_blocks_f32(const uint8_t* wrow, const float* xr, int b0,
+                                                   int b1) {
+  constexpr int BB = Fmt<FMT>::block_bytes;
+  float acc = 0.0f;
+  for (int b = b0; b < b1; ++b) {
+    const float* xb = xr + 32LL * b;
+    bool special = false;
+    for (int j = 0; j < 32; ++j) special = special || !(fabsf(xb[j]) <= 3.402823466e38f);
+    if (!special) continue;
+    const uint8_t* wp = wrow + static_cast<long long>(b >> 1) * (2 * BB);
+    const uint16_t d = *reinterpret_cast<const uint16_t*>(wp + (b & 1) * BB);
+    acc += half_bits_to_float(d) * block_f32<FMT>(wp, b & 1, xb);
+  }
+  return acc;
+}
+
 }  // namespace qc

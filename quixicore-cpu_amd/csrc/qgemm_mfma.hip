@@ -206,7 +206,9 @@ __device__ __forceinline__ void ring_barrier() {
 // so that the row's largest element is in [0.5, 1) (bf16) or [2^14, 2^15)
 // (f16): no element that matters is subnormal in the operand type (which
 // would leave it a few bits) and no product overflows; rexp[m] = e(m), and
-// outputs are scaled back by 2^e(m), exactly.
+// outputs are scaled back by 2^e(m), exactly.  A row holding NaN or +-inf
+// gets rexp[m] = kRowNonfinite instead, and the GEMMs recompute its outputs
+// in the reference's f32 form (nonfinite_blocks_f32).
 //
 // One 256-thread workgroup per row of the layout (rows past M are zero): the
 // row's maximum, then its fragments, in one launch.  Thread t converts the
@@ -215,6 +217,8 @@ __device__ __forceinline__ void ring_barrier() {
 // 8-element chunk sums.  Workgroup 0 also copies the weights' short final
 // stage into `tail_pad` (small-batch passes), and all of them clear y when
 // two K ranges add into it.
+constexpr int kRowNonfinite = 0x40000000;   // no exponent takes this value
+
 template <bool PANEL, bool BIAS>
 __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, int M, int K,
                                                  int nbo, int T, uint8_t* __restrict__ xf,
@@ -224,6 +228,7 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
                                                  const uint8_t* __restrict__ tail_src, int tail,
                                                  uint8_t* __restrict__ tail_pad, int pad_bytes) {
   __shared__ float smax[4];
+  __shared__ int sbad[4];
   // Workgroups are dealt to the 8 XCDs in turn (id mod 8), and each 128-byte
   // line of a fragment holds 8 consecutive rows: give those rows to one XCD
   // (ids 8q + c of each group of 64 take rows 8c + q), so each line is
@@ -238,8 +243,19 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
   if (blockIdx.x == 0 && tail > 0)
     for (int i = tid; i < pad_bytes; i += 256) tail_pad[i] = i < tail ? tail_src[i] : 0;
 
-  // max |x[m][:]|, four independent loads in flight per step
-  float mx = 0.f;
+  // max |x[m][:]|, four independent loads in flight per step; z stays 0
+  // unless an element is NaN or +-inf (0 * x is then NaN)
+  float mx = 0.f, z = 0.f;
+  auto see = [&](float v) {
+    mx = fmaxf(mx, fabsf(v));
+    z = fmaf(0.0f, v, z);
+  };
+  auto see4 = [&](const float4& a) {
+    see(a.x);
+    see(a.y);
+    see(a.z);
+    see(a.w);
+  };
   if (live) {
     int i = tid;
     if (reinterpret_cast<uintptr_t>(xr) % 16 == 0) {
@@ -247,32 +263,39 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
       const int n4 = K / 4;
       for (; i + 768 < n4; i += 1024) {
         const float4 a = x4[i], b = x4[i + 256], c = x4[i + 512], d = x4[i + 768];
-        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                             fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
-        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
-                             fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
+        see4(a);
+        see4(b);
+        see4(c);
+        see4(d);
       }
-      for (; i < n4; i += 256) {
-        const float4 a = x4[i];
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
-      }
+      for (; i < n4; i += 256) see4(x4[i]);
     } else {
-      for (; i + 768 < K; i += 1024)
-        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xr[i]), fabsf(xr[i + 256]))),
-                   fmaxf(fabsf(xr[i + 512]), fabsf(xr[i + 768])));
-      for (; i < K; i += 256) mx = fmaxf(mx, fabsf(xr[i]));
+      for (; i + 768 < K; i += 1024) {
+        const float a = xr[i], b = xr[i + 256], c = xr[i + 512], d = xr[i + 768];
+        see(a);
+        see(b);
+        see(c);
+        see(d);
+      }
+      for (; i < K; i += 256) see(xr[i]);
     }
   }
   mx = wave_max_nonneg(mx);
-  if ((tid & 63) == 0) smax[tid >> 6] = mx;
+  const int wbad = __any(z != 0.0f) ? 1 : 0;
+  if ((tid & 63) == 0) {
+    smax[tid >> 6] = mx;
+    sbad[tid >> 6] = wbad;
+  }
   __syncthreads();
   mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+  const bool bad = (sbad[0] | sbad[1] | sbad[2] | sbad[3]) != 0;
   int e = 0;
   if (mx > 0.f && mx <= 3.402823466e38f) (void)frexpf(mx, &e);
   // q4_0 (bf16): largest element in [0.5, 1); q8_0 (f16): in [2^14, 2^15), so
   // that only elements below 2^-28 of the row's maximum reach f16 subnormals
   if constexpr (!BIAS) e -= 15;
-  if (live && tid == 0) rexp[m] = e;
+  if (live && tid == 0) rexp[m] = bad ? kRowNonfinite : e;
+  if (bad) e = 0;
 
   const int t = m >> 4, r = m & 15;
   const int nh = 2 * nbo;                          // half blocks of the layout's row
@@ -656,6 +679,7 @@ __global__ __launch_bounds__(64 * NW * KG) void qgemm_mfma(
 
   f32x4 acc[T];     // bf16 mode: output (m = 16t + 4j + e, n)
   float accd[T];    // digit mode: output (m = 4t + j, n)
+  uint32_t badrows = 0u;   // digit mode: bit t when row 4t + j met a non-finite stage
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -776,6 +800,7 @@ __global__ __launch_bounds__(64 * NW * KG) void qgemm_mfma(
         const int2 me = *reinterpret_cast<const int2*>(xs + XB::meta_off + 8 * (4 * t + j));
         const float v = ldexpf(sacc[t] * __int_as_float(me.y), me.x);
         accd[t] += live ? v : 0.0f;
+        badrows |= live && me.y != __float_as_int(1.0f) ? 1u << t : 0u;
       }
     }
   };
@@ -838,6 +863,26 @@ __global__ __launch_bounds__(64 * NW * KG) void qgemm_mfma(
     }
   }
   wait_vmcnt<0>();   // no global->LDS load may outlive the workgroup's LDS
+  // Blocks [b0, b1) of this K range.  An activation row holding NaN or +-inf
+  // (digit mode: a stage gate NaN; the f16 / bf16 layouts: rexp marked) has
+  // its outputs recomputed in the reference's f32 form.
+  const int b0 = st0 * kStageBlocks;
+  const int b1 = st1 * kStageBlocks < K / 32 ? st1 * kStageBlocks : K / 32;
+  const uint8_t* const wrow_n = W + static_cast<long long>(n < N ? n : N - 1) * row_bytes;
+  if constexpr (XB::digits) {
+    if (__any(badrows != 0u)) {
+#pragma unroll 1
+      for (int t = 0; t < T; ++t) {
+        const int m = 4 * t + j;
+        if (((badrows >> t) & 1u) != 0u && n < N && m < M) {
+          const float v = nonfinite_blocks_f32<FMT>(wrow_n, x + static_cast<long long>(m) * K, b0, b1);
+#pragma unroll
+          for (int u = 0; u < T; ++u)
+            if (u == t) accd[u] = v;
+        }
+      }
+    }
+  }
   if constexpr (KG == 2) {
     // range 1's sums to LDS (the rings are no longer read), then range 0
     // adds them and stores
@@ -860,13 +905,24 @@ __global__ __launch_bounds__(64 * NW * KG) void qgemm_mfma(
   // not depend on which finishes first).  More: partial sums for the
   // reduction kernel.
   if (n >= N) return;
-  auto put = [&](int m, float v) {
-    if (m >= M) return;
-    if constexpr (!XB::digits) v = ldexpf(v, rexp[m]);   // undo the row scale
+  auto store = [&](int m, float v) {
     const long long o = static_cast<long long>(m) * N + n;
     if (ks_count == 1) y[o] = v;
     else if (ks_count == 2) atomicAdd(y + o, v);
     else partial[static_cast<long long>(ks) * M * N + o] = v;
+  };
+  bool special = false;   // f16 / bf16 layouts: a row of this lane holds NaN or +-inf
+  auto put = [&](int m, float v) {
+    if (m >= M) return;
+    if constexpr (!XB::digits) {
+      const int r = rexp[m];
+      if (r == kRowNonfinite) {   // stored by the loop below
+        special = true;
+        return;
+      }
+      v = ldexpf(v, r);   // undo the row scale
+    }
+    store(m, v);
   };
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -875,6 +931,16 @@ __global__ __launch_bounds__(64 * NW * KG) void qgemm_mfma(
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) put(16 * t + 4 * j + e, acc[t][e]);
+    }
+  }
+  if constexpr (!XB::digits) {
+    if (__any(special)) {
+#pragma unroll 1
+      for (int q = 0; q < 4 * T; ++q) {
+        const int m = 16 * (q >> 2) + 4 * j + (q & 3);
+        if (m < M && rexp[m] == kRowNonfinite)
+          store(m, nonfinite_blocks_f32<FMT>(wrow_n, x + static_cast<long long>(m) * K, b0, b1));
+      }
     }
   }
 }
@@ -1182,8 +1248,8 @@ struct PanelStage {
 template <int FMT, int TM>
 __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
     const uint8_t* __restrict__ W, const uint8_t* __restrict__ xf, const float* __restrict__ bias,
-    float* __restrict__ y, const int* __restrict__ rexp, int M, int N, int K,
-    int pairs_per_split, int ks_count) {
+    float* __restrict__ y, const int* __restrict__ rexp, const float* __restrict__ x, int M,
+    int N, int K, int pairs_per_split, int ks_count) {
   using PS = PanelStage<FMT, TM>;
   constexpr int PB = PairLayout<FMT>::bytes;
   constexpr int G = PS::g;
@@ -1367,6 +1433,7 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
 
   // acc[tm][tn][e] is output (m = 16 (mt0 + 4 wm + tm) + 4 j + e,
   // n = n0 + 64 wn + 16 tn + (lane & 15)).
+  bool special = false;
 #pragma unroll
   for (int tn = 0; tn < kPTN; ++tn) {
     const int n = n0 + wn * 64 + tn * 16 + (lane & 15);
@@ -1378,10 +1445,30 @@ __global__ __launch_bounds__(64 * kPWaves, 1) void qgemm_panel(
         const int m = 16 * (mt0 + wm * TM + tm) + 4 * j + e;
         if (m >= M) continue;
         const long long o = static_cast<long long>(m) * N + n;
-        const float v = ldexpf(acc[tm][tn][e], rexp[m]);   // undo the row scale
+        const int r = rexp[m];
+        if (r == kRowNonfinite) {   // stored by the loop below
+          special = true;
+          continue;
+        }
+        const float v = ldexpf(acc[tm][tn][e], r);   // undo the row scale
         if (ks_count == 1) y[o] = v;
         else atomicAdd(y + o, v);
       }
+    }
+  }
+  // Rows holding NaN or +-inf: the reference's f32 form over this K range.
+  if (__any(special)) {
+#pragma unroll 1
+    for (int q = 0; q < kPTN * TM * 4; ++q) {
+      const int tn = q / (TM * 4), tm = (q / 4) % TM, e = q % 4;
+      const int n = n0 + wn * 64 + tn * 16 + (lane & 15);
+      const int m = 16 * (mt0 + wm * TM + tm) + 4 * j + e;
+      if (n >= N || m >= M || rexp[m] != kRowNonfinite) continue;
+      const float v = nonfinite_blocks_f32<FMT>(W + static_cast<long long>(n) * row_bytes,
+                                                x + static_cast<long long>(m) * K, 2 * p0, 2 * p1);
+      const long long o = static_cast<long long>(m) * N + n;
+      if (ks_count == 1) y[o] = v;
+      else atomicAdd(y + o, v);
     }
   }
 }
@@ -1439,7 +1526,7 @@ hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, i
   if (e != hipSuccess) return e;
   const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(mblocks),
                   static_cast<unsigned>(ks));
-  qgemm_panel<FMT, TM><<<grid, 64 * kPWaves, 0, s>>>(W, xf, bias, y, rexp, m, n, k, per, ks);
+  qgemm_panel<FMT, TM><<<grid, 64 * kPWaves, 0, s>>>(W, xf, bias, y, rexp, x, m, n, k, per, ks);
   return hipGetLastError();
 }
 

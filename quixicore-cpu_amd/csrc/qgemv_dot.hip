@@ -84,26 +84,6 @@ __device__ __forceinline__ float block_acc(float acc, uint32_t dbits, float gate
   return acc + ldexpf(t, e);
 }
 
-// The f32 dot of block h (0 / 1) of a pair (its bytes at `wp` in global
-// memory) with the block's 32 values of x, summed in element order
-// (kernels/quantization/qgemv_ref.cpp:70-76).
-template <int FMT>
-__device__ __forceinline__ float block_f32(const uint8_t* wp, int h, const float* xb) {
-  float s = 0.0f;
-#pragma unroll 1
-  for (int j = 0; j < 32; ++j) {
-    int q;
-    if constexpr (FMT == kQ8_0) {
-      q = static_cast<int8_t>(wp[(h == 0 ? 2 : 36) + j]);   // codes follow each fp16 scale
-    } else {
-      const uint8_t b = wp[(h == 0 ? 2 : 20) + (j & 15)];   // code j low, j + 16 high nibble
-      q = static_cast<int>(j < 16 ? (b & 0xF) : (b >> 4)) - 8;
-    }
-    s += static_cast<float>(q) * xb[j];
-  }
-  return s;
-}
-
 // One row's sum over this lane's block pairs p = lane (mod 64) in f32, from
 // memory: sum_b d_b * sum_j q_j x_j as the reference forms it
 // (kernels/quantization/qgemv_ref.cpp:62-80).  Used for the rows whose x

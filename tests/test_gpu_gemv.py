@@ -396,3 +396,67 @@ def test_qgemv_nonfinite_activations(qc, oracle, synth, dev, fmt, k, x_off):
         assert qc.qgemv_raw(fmt, P, X[r], yr, n, k) == 0
         assert np.array_equal(Y[r].view(np.uint32), yr.cpu().numpy().view(np.uint32)), r
     assert np.all(np.isfinite(Y[1]))
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("m,k,n,panel", [
+    (3, 4096, 200, 0),      # digit layout, 4 rows
+    (4, 4096, 300, -2),     # digit layout, K split in two (q8_0: both ranges in one workgroup)
+    (6, 4096, 4096, 0),     # digit layout, 8 rows, K split four ways
+    (8, 14336, 1000, 0),    # digit layout, long K
+    (16, 4096, 200, 0),     # f16 / bf16 layout
+    (32, 2048, 4096, 0),    # f16 / bf16 layout, 32 rows
+    (70, 2048, 300, 1),     # 2-D panel GEMM, one K range
+    (70, 4096, 300, 2),     # 2-D panel GEMM, two K ranges (atomic halves)
+])
+def test_qgemm_mfma_nonfinite_activations(qc, oracle, synth, dev, fmt, m, k, n, panel):
+    """The MFMA routes (digit, f16 / bf16 and panel layouts, every K split):
+    an activation row holding +-inf or NaN gives each output the reference's
+    f32 result class (kernels/quantization/qgemm_ref.cpp:156-162 runs the
+    row's qgemv; qgemv_ref.cpp:62-80), and the finite rows are bit-identical
+    to the same call with the non-finite rows zeroed."""
+    import torch
+    packed, _ = _case(oracle, synth, fmt, n, k, 1500 + m + k)
+    w64 = oracle.unpack(fmt, packed, n, k).astype(np.float64)
+    rng = np.random.default_rng(m * 7 + k + fmt)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    bad = {0: [(97, np.inf)], m - 1: [(k - 5, -np.inf)],
+           m // 2: [(40, np.inf), (k // 2 + 3, -np.inf), (300, np.nan)]}
+    if m > 4:
+        bad[1] = [(slice(0, 32), np.inf)]
+        bad[3] = [(k - 1, np.nan)]
+    xb = x.copy()
+    for r, items in bad.items():
+        for c, v in items:
+            xb[r, c] = v
+    P = torch.from_numpy(packed).to(dev)
+
+    def run(xa):
+        X = torch.from_numpy(xa).to(dev)
+        Y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        assert qc.qgemm_raw(fmt, P, X, Y, m, n, k) == 0
+        return Y.cpu().numpy()
+
+    print(f"qgemm nonfinite fmt={fmt} m={m} k={k} n={n} panel={panel}", flush=True)
+    qc.set_qgemm_panel(panel if panel > 0 else -1)
+    qc.set_qgemm_rows(-1)
+    if panel == -2:
+        qc.set_qgemm_plan(4, 8)   # 16 stages in two K ranges
+    try:
+        y = run(xb)
+        xz = xb.copy()
+        xz[sorted(bad)] = 0.0
+        yz = run(xz)
+    finally:
+        qc.set_qgemm_panel(0)
+        qc.set_qgemm_rows(0)
+        qc.set_qgemm_plan(0, 0)
+    for r in range(m):
+        if r in bad:
+            with np.errstate(invalid="ignore", over="ignore"):
+                y64 = (w64 * xb[r].astype(np.float64)[None, :]).sum(axis=1)
+            for got, want in zip(_classes(y[r]), _classes(y64)):
+                assert np.array_equal(got, want), (r, np.flatnonzero(got != want)[:5])
+            assert not np.isfinite(y[r]).any(), r
+        else:
+            assert np.array_equal(y[r].view(np.uint32), yz[r].view(np.uint32)), r
