@@ -116,7 +116,7 @@ STREAM_SIZES = (("17.9MB_q8_0_k4096_n4096", 17858560), ("33.1MB_q4_0_k4096_n1433
 
 def stream_ceiling(qc, steps, warmup, sizes=STREAM_SIZES, wpcs=(1, 2, 4, 8, 16)):
     """The streaming-read ceiling at the GEMV footprints: qc_hip_stream_read
-    (16-byte loads, sixteen in flight per thread) over rotated buffers of
+    (16-byte non-temporal loads, sixteen in flight per thread) over rotated buffers of
     each size, one launch per step, timed like the GEMV; best over 1-16
     workgroups per CU."""
     import torch

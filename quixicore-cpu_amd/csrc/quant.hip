@@ -300,7 +300,10 @@ hipError_t launch_unpack(int fmt, const void* packed, float* w, long long n, lon
 // all sixteen of a 64 KB slab in flight per thread, the workgroups taking
 // interleaved slabs; each thread stores the XOR of what it read (so nothing
 // is optimised away).  A measurement seam: the GEMV's HBM efficiency is
-// judged against it.
+// judged against it.  The loads carry the non-temporal hint, which measured
+// 6-11% faster for this whole-line pattern on MI355X (256 MB: 47-48 ->
+// 42.4 us).
+typedef uint32_t u32x4nt __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, long long n16,
                                                           uint32_t* __restrict__ out) {
   constexpr long long kSlab = 4096;                // 16-byte units per slab (64 KB)
@@ -311,7 +314,9 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const long long i = base + threadIdx.x + 256LL * u;
-      v[u] = i < n16 ? p[i] : make_uint4(0, 0, 0, 0);
+      const u32x4nt t = i < n16 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4nt*>(p) + i)
+                                : u32x4nt{0, 0, 0, 0};
+      v[u] = make_uint4(t.x, t.y, t.z, t.w);
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
