@@ -209,6 +209,22 @@ __device__ __forceinline__ float fused_activation(float v, int act) {
                   : v / (1.0f + expf(-v));
 }
 
+// q8_0 items with one pair per lane (NPM = 1: 64 consecutive block pairs of
+// one row, 4352 bytes) are read in whole lines -- lane l takes the 16-byte
+// chunks l + 64 i (i < 4) and the dword 1024 + l -- and handed to the lanes
+// through a per-wave LDS staging area, one item at a time: a lane's own
+// 68-byte pair straddles cache lines, and five loads per lane of such records
+// keep re-requesting the same lines (a read of the same rows took 13.1-14.2
+// us as records, 12.0-12.2 us as chunks restaged through LDS).  17 dwords per
+// lane and item, as for the records, but the staging adds ~20 VGPRs, which
+// costs occupancy from 4 rows per wave on: taken for 1-2 rows per wave only
+// (q8_0 4096 x 4096, 8 waves x 2 rows: 5.93-6.09 -> 5.75-5.85 us; 4096 ->
+// 14336 with 4 rows per wave was 2-5% slower chunked, so it keeps the records).
+constexpr int kQ8Item = 64 * 68;
+template <int FMT, int NPM, int RB>
+constexpr bool q8_chunked() { return FMT == kQ8_0 && NPM == 1 && RB <= 2; }
+__host__ __device__ constexpr size_t q8_stage_off(int kc) { return (lds_size(kc) + 15) / 16 * 16; }
+
 // NW wavefronts of RB rows each, up to NPM pairs per lane per K chunk.  The (pair j,
 // row r) items of a chunk are loaded in j-major order with at most WIN items
 // in flight: item t + WIN is issued just before item t is computed, so the
@@ -231,6 +247,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
   constexpr int T = NPM * RB;
   constexpr int NT = 64 * NW;
   constexpr int HPT = (NPM * 256 + NT - 1) / NT;   // half-blocks of x per thread
+  constexpr bool CHUNKED = q8_chunked<FMT, NPM, RB>();   // see kQ8Item
   const int lane = threadIdx.x & 63;
   const long long row_bytes = static_cast<long long>(k >> 5) * BB;
   const uint8_t* wrow[RB];
@@ -277,10 +294,33 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
     float xv[HPT][16];
     load_x<HPT, NT, VEC>(xv, x + c0, clen);
     uint32_t w[T][PD];
+    // chunked items: pairs [q0c, q0c + nbytes / 68) of the row (one clamped
+    // pair past the chunk); a chunk that would run past them is moved back
+    // to end with them (its overlap rewrites the same bytes)
+    auto span = [&](int j, int& q0c, int& nbytes) {
+      const int q0 = pbeg + 64 * j;
+      q0c = min(q0, pend - 1);
+      nbytes = (q0 < pend ? min(64, pend - q0) : 1) * 68;
+    };
     auto issue = [&](int t) {
       const int j = t / RB, r = t % RB;
-      const int p = min(p0 + 64 * j, pend - 1);
-      load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
+      if constexpr (CHUNKED) {
+        int q0c, nbytes;
+        span(j, q0c, nbytes);
+        const uint8_t* base = wrow[r] + static_cast<long long>(q0c) * 68;
+        // every lane loads (a lane past the item re-reads its last bytes), so
+        // no register waits on a condition
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int off = min(16 * (lane + 64 * i), nbytes - 16);
+          const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(base + off);
+          w[t][4 * i] = v.x; w[t][4 * i + 1] = v.y; w[t][4 * i + 2] = v.z; w[t][4 * i + 3] = v.w;
+        }
+        w[t][16] = *reinterpret_cast<const uint32_t*>(base + min(4096 + 4 * lane, nbytes - 4));
+      } else {
+        const int p = min(p0 + 64 * j, pend - 1);
+        load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
+      }
     };
 #pragma unroll
     for (int t = 0; t < T && t < WIN; ++t) issue(t);
@@ -299,7 +339,26 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
       for (int r = 0; r < RB; ++r) {
         const int t = j * RB + r;
         if (t + WIN < T) issue(t + WIN);
-        if (p < pend) acc[r] = pair_dot<FMT>(w[t], g, acc[r]);
+        if constexpr (CHUNKED) {
+          // the item's bytes into the wave's staging area, then this lane's pair
+          uint8_t* const stage = lds + q8_stage_off(kc) + (threadIdx.x >> 6) * kQ8Item;
+          int q0c, nbytes;
+          span(j, q0c, nbytes);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int off = 16 * (lane + 64 * i);
+            if (off < nbytes)
+              *reinterpret_cast<u32x4_a4*>(stage + min(off, nbytes - 16)) =
+                  u32x4_a4{w[t][4 * i], w[t][4 * i + 1], w[t][4 * i + 2], w[t][4 * i + 3]};
+          }
+          if (4096 + 4 * lane < nbytes)
+            *reinterpret_cast<uint32_t*>(stage + 4096 + 4 * lane) = w[t][16];
+          const uint32_t* rec =
+              reinterpret_cast<const uint32_t*>(stage + (min(p, pend - 1) - q0c) * 68);
+          if (p < pend) acc[r] = pair_dot<FMT>(rec, g, acc[r]);
+        } else {
+          if (p < pend) acc[r] = pair_dot<FMT>(w[t], g, acc[r]);
+        }
       }
     }
   }
@@ -849,14 +908,17 @@ hipError_t launch_one(const GemvSegs& sg, const float* x, int k, int* status, hi
   const int kc = NPM * 4096 < k ? NPM * 4096 : k;
   const unsigned grid = static_cast<unsigned>((static_cast<long long>(n) + NW * RB - 1) / (NW * RB));
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  // digit records, then (chunked q8_0 items) each wave's item staging area
+  const size_t dlds = q8_chunked<FMT, NPM, RB>() ? q8_stage_off(kc) + static_cast<size_t>(NW) * kQ8Item
+                                                 : lds_size(kc);
   if constexpr (KIND == 0) {
     if (vec)
-      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true, false><<<grid, 64 * NW, lds_size(kc), s>>>(sg, x, k, kc);
+      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true, false><<<grid, 64 * NW, dlds, s>>>(sg, x, k, kc);
     else
-      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, false, false><<<grid, 64 * NW, lds_size(kc), s>>>(sg, x, k, kc);
+      qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, false, false><<<grid, 64 * NW, dlds, s>>>(sg, x, k, kc);
   } else if constexpr (KIND == 2) {
     // the caller guarantees a 16-byte aligned x
-    qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true, true><<<grid, 64 * NW, lds_size(kc), s>>>(sg, x, k, kc);
+    qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true, true><<<grid, 64 * NW, dlds, s>>>(sg, x, k, kc);
   } else {
     const size_t lds = w8_lds_size(kc, NW, RB);
     if (vec)
