@@ -211,13 +211,34 @@ __device__ __forceinline__ void ring_barrier() {
 // in the reference's f32 form (nonfinite_blocks_f32).
 //
 // One 256-thread workgroup per row of the layout (rows past M are zero): the
-// row's maximum, then its fragments, in one launch.  Thread t converts the
+// row's maximum, then its fragments, in one launch; workgroups `rows` and up
+// only clear y (zero_count floats), beside the row work rather than after it.  Thread t converts the
 // half blocks h = t + 256 i; the two halves of a block sit in lanes t, t ^ 1,
 // and the bias sum keeps the order ((s0 + s1) + (s2 + s3)) of the four
 // 8-element chunk sums.  Workgroup 0 also copies the weights' short final
 // stage into `tail_pad` (small-batch passes), and all of them clear y when
 // two K ranges add into it.
 constexpr int kRowNonfinite = 0x40000000;   // no exponent takes this value
+
+// p[0..count) = 0 by `stride` threads, this one being thread `first`: 16-byte
+// stores when p is 16-byte aligned.
+__device__ __forceinline__ void clear_floats(float* p, long long count, long long first,
+                                             long long stride) {
+  long long done = 0;
+  if (reinterpret_cast<uintptr_t>(p) % 16 == 0) {
+    const long long n4 = count / 4;
+    for (long long i = first; i < n4; i += stride)
+      reinterpret_cast<float4*>(p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    done = 4 * n4;
+  }
+  for (long long i = done + first; i < count; i += stride) p[i] = 0.0f;
+}
+
+// Workgroups of prep_rows that only clear y (about 16 floats per thread).
+inline int clear_workgroups(long long count) {
+  const long long w = (count + 256 * 16 - 1) / (256 * 16);
+  return static_cast<int>(w < 512 ? w : 512);
+}
 
 template <bool PANEL, bool BIAS>
 __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, int M, int K,
@@ -226,14 +247,20 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
                                                  int* __restrict__ rexp, float* zero_y,
                                                  long long zero_count,
                                                  const uint8_t* __restrict__ tail_src, int tail,
-                                                 uint8_t* __restrict__ tail_pad, int pad_bytes) {
+                                                 uint8_t* __restrict__ tail_pad, int pad_bytes,
+                                                 int rows) {
+  if (static_cast<int>(blockIdx.x) >= rows) {
+    clear_floats(zero_y, zero_count, static_cast<long long>(blockIdx.x - rows) * 256 + threadIdx.x,
+                 static_cast<long long>(gridDim.x - rows) * 256);
+    return;
+  }
   __shared__ float smax[4];
   __shared__ int sbad[4];
   // Workgroups are dealt to the 8 XCDs in turn (id mod 8), and each 128-byte
   // line of a fragment holds 8 consecutive rows: give those rows to one XCD
   // (ids 8q + c of each group of 64 take rows 8c + q), so each line is
   // assembled in one L2 instead of being written back in pieces from eight.
-  const int m = gridDim.x % 64 == 0
+  const int m = rows % 64 == 0
                     ? (blockIdx.x & ~63) | ((blockIdx.x & 7) << 3) | ((blockIdx.x >> 3) & 7)
                     : static_cast<int>(blockIdx.x);
   const int tid = threadIdx.x;
@@ -349,9 +376,6 @@ __global__ __launch_bounds__(256) void prep_rows(const float* __restrict__ x, in
       if (h < nh && half == 0) bias[f * 16 + r] = -8.0f * sp;
     }
   }
-  for (long long i = static_cast<long long>(blockIdx.x) * 256 + tid; i < zero_count;
-       i += static_cast<long long>(gridDim.x) * 256)
-    zero_y[i] = 0.0f;
 }
 
 // The digits of activation row m over one stage of 8 blocks, built by one
@@ -450,9 +474,8 @@ __global__ __launch_bounds__(64) void qgemm_prep(const float* __restrict__ x, in
     digit_stage_row<XL, BIAS>(v, m, true, xf + static_cast<long long>(st) * XB::stage_bytes);
   }
   // y is accumulated with two atomic adds when K is split in two: clear it.
-  for (long long i = static_cast<long long>(blockIdx.x) * 64 + l; i < zero_count;
-       i += static_cast<long long>(gridDim.x) * 64)
-    zero_y[i] = 0.0f;
+  clear_floats(zero_y, zero_count, static_cast<long long>(blockIdx.x) * 64 + l,
+               static_cast<long long>(gridDim.x) * 64);
 }
 
 // Sum of the ks partial results in index order (K split more than twice).
@@ -1168,9 +1191,10 @@ hipError_t run(const uint8_t* W, const float* x, float* y, int m, int n, int k, 
                                                                tail_src, tail, tail_pad,
                                                                static_cast<int>(pad_bytes));
     else
-      prep_rows<false, FMT == kQ4_0><<<XL, 256, 0, s>>>(x, m, k, nbp, XB::T, xf, bias, rexp, y,
-                                                        ks == 2 ? outs : 0, tail_src, tail, tail_pad,
-                                                        static_cast<int>(pad_bytes));
+      prep_rows<false, FMT == kQ4_0>
+          <<<XL + (ks == 2 ? clear_workgroups(outs) : 0), 256, 0, s>>>(
+              x, m, k, nbp, XB::T, xf, bias, rexp, y, ks == 2 ? outs : 0, tail_src, tail,
+              tail_pad, static_cast<int>(pad_bytes), XL);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1520,8 +1544,10 @@ hipError_t run_panel(const uint8_t* W, const float* x, float* y, int m, int n, i
   uint8_t* xf = static_cast<uint8_t*>(ws);
   float* bias = reinterpret_cast<float*>(xf + xf_bytes);
   const long long outs = static_cast<long long>(m) * n;
-  prep_rows<true, FMT == kQ4_0><<<static_cast<unsigned>(16 * mtiles), 256, 0, s>>>(
-      x, m, k, nb, 0, xf, bias, rexp, y, ks == 2 ? outs : 0, nullptr, 0, nullptr, 0);
+  prep_rows<true, FMT == kQ4_0>
+      <<<static_cast<unsigned>(16 * mtiles + (ks == 2 ? clear_workgroups(outs) : 0)), 256, 0, s>>>(
+          x, m, k, nb, 0, xf, bias, rexp, y, ks == 2 ? outs : 0, nullptr, 0, nullptr, 0,
+          16 * mtiles);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(mblocks),
