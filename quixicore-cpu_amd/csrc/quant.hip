@@ -11,6 +11,8 @@
 #include "qc_internal.h"
 
 namespace qc {
+// 16-byte vector for the non-temporal loads of the streaming kernels.
+typedef uint32_t u32x4nt __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int kThreads = 256;
@@ -78,7 +80,10 @@ __global__ __launch_bounds__(NT) void quantize_rows_regs(const float* __restrict
   for (int i = 0; i < V; ++i) {
     const int idx = threadIdx.x + i * NT;
     if (idx < n4) {
-      v[i] = xr[idx];
+      // x is read once and the codes written once: non-temporal loads and
+      // stores measured 5.5% faster at M=2048 K=4096 (9.52-9.68 -> 8.97-9.04 us)
+      const u32x4nt t = __builtin_nontemporal_load(reinterpret_cast<const u32x4nt*>(xr) + idx);
+      v[i] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
       bad |= !finite4(v[i]);
       m = abs_max4(v[i], m);
     }
@@ -93,7 +98,7 @@ __global__ __launch_bounds__(NT) void quantize_rows_regs(const float* __restrict
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = threadIdx.x + i * NT;
-    if (idx < n4) cr[idx] = quant4(v[i], inv);
+    if (idx < n4) __builtin_nontemporal_store(quant4(v[i], inv), cr + idx);
   }
   if (threadIdx.x == 0) scales[row] = scale;
 }
@@ -303,7 +308,6 @@ hipError_t launch_unpack(int fmt, const void* packed, float* w, long long n, lon
 // judged against it.  The loads carry the non-temporal hint, which measured
 // 6-11% faster for this whole-line pattern on MI355X (256 MB: 47-48 ->
 // 42.4 us).
-typedef uint32_t u32x4nt __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, long long n16,
                                                           uint32_t* __restrict__ out) {
   constexpr long long kSlab = 4096;                // 16-byte units per slab (64 KB)
