@@ -254,7 +254,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
   int row0, total;
   if constexpr (!MULTI) {
     total = segs.start[1];
-    row0 = (blockIdx.x * NW + (threadIdx.x >> 6)) * RB;
+    row0 = (blockIdx.x * NW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RB;
 #pragma unroll
     for (int r = 0; r < RB; ++r) wrow[r] = segs.w[0] + min(row0 + r, total - 1) * row_bytes;
   } else {
@@ -309,14 +309,16 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
         span(j, q0c, nbytes);
         const uint8_t* base = wrow[r] + static_cast<long long>(q0c) * 68;
         // every lane loads (a lane past the item re-reads its last bytes), so
-        // no register waits on a condition
+        // no register waits on a condition; a whole item needs no clamping
+        const bool whole = nbytes == kQ8Item;   // wave-uniform
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int off = min(16 * (lane + 64 * i), nbytes - 16);
+          const int off = whole ? 16 * lane + 1024 * i : min(16 * (lane + 64 * i), nbytes - 16);
           const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(base + off);
           w[t][4 * i] = v.x; w[t][4 * i + 1] = v.y; w[t][4 * i + 2] = v.z; w[t][4 * i + 3] = v.w;
         }
-        w[t][16] = *reinterpret_cast<const uint32_t*>(base + min(4096 + 4 * lane, nbytes - 4));
+        w[t][16] = *reinterpret_cast<const uint32_t*>(
+            base + (whole ? 4096 + 4 * lane : min(4096 + 4 * lane, nbytes - 4)));
       } else {
         const int p = min(p0 + 64 * j, pend - 1);
         load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
@@ -344,15 +346,23 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
           uint8_t* const stage = lds + q8_stage_off(kc) + (threadIdx.x >> 6) * kQ8Item;
           int q0c, nbytes;
           span(j, q0c, nbytes);
+          if (nbytes == kQ8Item) {   // a whole item (wave-uniform)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int off = 16 * (lane + 64 * i);
-            if (off < nbytes)
-              *reinterpret_cast<u32x4_a4*>(stage + min(off, nbytes - 16)) =
+            for (int i = 0; i < 4; ++i)
+              *reinterpret_cast<u32x4_a4*>(stage + 16 * lane + 1024 * i) =
                   u32x4_a4{w[t][4 * i], w[t][4 * i + 1], w[t][4 * i + 2], w[t][4 * i + 3]};
-          }
-          if (4096 + 4 * lane < nbytes)
             *reinterpret_cast<uint32_t*>(stage + 4096 + 4 * lane) = w[t][16];
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int off = 16 * (lane + 64 * i);
+              if (off < nbytes)
+                *reinterpret_cast<u32x4_a4*>(stage + min(off, nbytes - 16)) =
+                    u32x4_a4{w[t][4 * i], w[t][4 * i + 1], w[t][4 * i + 2], w[t][4 * i + 3]};
+            }
+            if (4096 + 4 * lane < nbytes)
+              *reinterpret_cast<uint32_t*>(stage + 4096 + 4 * lane) = w[t][16];
+          }
           const uint32_t* rec =
               reinterpret_cast<const uint32_t*>(stage + (min(p, pend - 1) - q0c) * 68);
           if (p < pend) acc[r] = pair_dot<FMT>(rec, g, acc[r]);
