@@ -375,12 +375,18 @@ __device__ __noinline__ float cint8_block_f32(const int8_t* codes, const void* x
 // (three v_dot4 sums per 4 codes) and, for affine weights, xs = 2^e (2^14
 // D0 + 2^7 D1 + D2) ~ sum_j x_j over the same encoded x.  Group scales add
 // s_g (f - z_g xs) per block; row scales finish as s (sum f - z sum xs).
-template <int RB, bool GRP, bool AFF>
+// MB > 1: activation rows m0 .. m0 + MB - 1 (those below m) in one pass, one
+// digit record of x each in LDS; a lane's codes are loaded once and dotted
+// with every row's digits.
+template <int RB, bool GRP, bool AFF, int MB = 1>
 __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
                                                              const void* __restrict__ x,
-                                                             int xtype, int k, bool xvec) {
+                                                             int xtype, int k, bool xvec,
+                                                             long long ldx, int m0, int m) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int kc = 4096;
+  constexpr int LS = static_cast<int>(lds_size(kc));
+  const int mrows = min(MB, m - m0);   // wave-uniform
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int total = segs.start[segs.nseg];
@@ -395,10 +401,14 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
     sp[r] = segs.scale[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
     zp[r] = AFF ? segs.zero[rr.seg] + static_cast<long long>(rr.row) * segs.groups : nullptr;
   }
-  float acc[RB];
+  float acc[RB][MB];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) acc[r] = 0.f;
-  float sxs = 0.f;   // affine row scales: this lane's sum of xs (finite blocks)
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) acc[r][mm] = 0.f;
+  float sxs[MB];   // affine row scales: this lane's sum of xs (finite blocks)
+#pragma unroll
+  for (int mm = 0; mm < MB; ++mm) sxs[mm] = 0.f;
   for (int c0 = 0; c0 < k; c0 += kc) {
     const int clen = min(kc, k - c0);
     const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
@@ -411,13 +421,15 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
     // branch around it, which would make the compiler wait at the join
     const int nh = clen >> 4;
     const int hx = min(static_cast<int>(threadIdx.x), nh - 1);
-    float v[16];
-    {
-      const long long xi = c0 + 16LL * hx;
+    float v[MB][16];
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) {
+      // rows past m re-read row m0 (not built)
+      const long long xi = static_cast<long long>(m0 + (mm < mrows ? mm : 0)) * ldx + c0 + 16LL * hx;
       if (xvec && xtype == QC_STORAGE_F32) {
         const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xi);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(&v[4 * i]) = src[i];
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(&v[mm][4 * i]) = src[i];
       } else if (xvec) {
         const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + xi);
         const uint4 a = src[0], b = src[1];
@@ -426,16 +438,16 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
         for (int i = 0; i < 8; ++i) {
           const uint16_t lo = static_cast<uint16_t>(wd[i]), hi = static_cast<uint16_t>(wd[i] >> 16);
           if (xtype == QC_STORAGE_F16) {
-            v[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
-            v[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+            v[mm][2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+            v[mm][2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
           } else {
-            v[2 * i] = __uint_as_float(static_cast<uint32_t>(lo) << 16);
-            v[2 * i + 1] = __uint_as_float(static_cast<uint32_t>(hi) << 16);
+            v[mm][2 * i] = __uint_as_float(static_cast<uint32_t>(lo) << 16);
+            v[mm][2 * i + 1] = __uint_as_float(static_cast<uint32_t>(hi) << 16);
           }
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = load_x(x, xi + i, xtype);
+        for (int i = 0; i < 16; ++i) v[mm][i] = load_x(x, xi + i, xtype);
       }
     }
     // 2. the codes of this lane's pair of every row (and group scales)
@@ -459,21 +471,28 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
     // block sit in lanes t and t ^ 1, both inside or both past the chunk)
     // 3. the chunk's digits
     if (c0) lds_barrier();
-    if (static_cast<int>(threadIdx.x) < nh) build_half<AFF>(lds, v, threadIdx.x, kc);
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm)
+      if (mm < mrows && static_cast<int>(threadIdx.x) < nh)
+        build_half<AFF>(lds + mm * LS, v[mm], threadIdx.x, kc);
     lds_barrier();
-    if (live) {
+#pragma unroll
+    for (int mm = 0; mm < MB; ++mm) {
+      if (!live || mm >= mrows) continue;
+      const uint8_t* const rec = lds + mm * LS;
+      const long long xrow = static_cast<long long>(m0 + mm) * ldx;
       PairDigits g;
-      read_digits<kQ8_0>(g, lds, p - pbeg, kc);
+      read_digits<kQ8_0>(g, rec, p - pbeg, kc);
       float xs[2] = {0.f, 0.f};
       if constexpr (AFF) {
         int ds[2][3];
-        read_digit_sums(ds, lds, p - pbeg, kc);
+        read_digit_sums(ds, rec, p - pbeg, kc);
 #pragma unroll
         for (int h = 0; h < 2; ++h) xs[h] = ldexpf(combine(ds[h][0], ds[h][1], ds[h][2]), g.e[h]);
         if constexpr (!GRP) {
 #pragma unroll
           for (int h = 0; h < 2; ++h)
-            if (g.gate[h] == 1.0f) sxs += xs[h];
+            if (g.gate[h] == 1.0f) sxs[mm] += xs[h];
         }
       }
 #pragma unroll
@@ -493,35 +512,39 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
         for (int h = 0; h < 2; ++h) {
           if (g.gate[h] == 1.0f) {
             const float f = ldexpf(combine(sd[h][0], sd[h][1], sd[h][2]), g.e[h]);
-            if constexpr (GRP) acc[r] = fmaf(gs[r][h], AFF ? fmaf(-gz[r][h], xs[h], f) : f, acc[r]);
-            else acc[r] += f;
+            if constexpr (GRP) acc[r][mm] = fmaf(gs[r][h], AFF ? fmaf(-gz[r][h], xs[h], f) : f, acc[r][mm]);
+            else acc[r][mm] += f;
           } else {
             const float z = AFF ? (GRP ? gz[r][h] : zp[r][0]) : 0.f;
-            const float b = cint8_block_f32(w[r] + 64LL * p + 32 * h, x, c0 + 64LL * (p - pbeg) + 32 * h,
-                                            xtype, z);
-            acc[r] += GRP ? gs[r][h] * b : b;
+            const float b = cint8_block_f32(w[r] + 64LL * p + 32 * h, x,
+                                            xrow + c0 + 64LL * (p - pbeg) + 32 * h, xtype, z);
+            acc[r][mm] += GRP ? gs[r][h] * b : b;
           }
         }
       }
     }
   }
   // wave sums; lane r finishes row r (paired modes: lane r the pair r, r + 1)
-  float tot[RB];
-  const float sx = AFF && !GRP ? wave_sum(sxs) : 0.f;
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    float v = wave_sum(acc[r]);
-    if constexpr (!GRP) v = sp[r][0] * (AFF ? fmaf(-zp[r][0], sx, v) : v);
-    tot[r] = v;
-  }
-  if (segs.mode == 0) {
+  for (int mm = 0; mm < MB; ++mm) {
+    if (mm >= mrows) continue;
+    float tot[RB];
+    const float sx = AFF && !GRP ? wave_sum(sxs[mm]) : 0.f;
 #pragma unroll
-    for (int r = 0; r < RB; ++r)
-      if (lane == r && g0 + r < total) epilogue(segs, g0 + r, 0, tot[r], 0.f);
-  } else {
+    for (int r = 0; r < RB; ++r) {
+      float v = wave_sum(acc[r][mm]);
+      if constexpr (!GRP) v = sp[r][0] * (AFF ? fmaf(-zp[r][0], sx, v) : v);
+      tot[r] = v;
+    }
+    if (segs.mode == 0) {
 #pragma unroll
-    for (int r = 0; r + 1 < RB; r += 2)
-      if (lane == r && g0 + r < total) epilogue(segs, g0 + r, 0, tot[r], tot[r + 1]);
+      for (int r = 0; r < RB; ++r)
+        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, m0 + mm, tot[r], 0.f);
+    } else {
+#pragma unroll
+      for (int r = 0; r + 1 < RB; r += 2)
+        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, m0 + mm, tot[r], tot[r + 1]);
+    }
   }
 }
 
@@ -591,23 +614,34 @@ hipError_t launch_fast(const CSegs& sg, const void* x, int xtype, long long ldx,
   return hipSuccess;
 }
 
-template <int RB, bool GRP, bool AFF>
-hipError_t launch_dot(const CSegs& sg, const void* x, int xtype, int k, hipStream_t s) {
+template <int RB, bool GRP, bool AFF, int MB>
+hipError_t launch_dot(const CSegs& sg, const void* x, int xtype, long long ldx, int m, int k,
+                      hipStream_t s) {
   const int total = sg.start[sg.nseg];
   const unsigned grid = static_cast<unsigned>((total + kWaves * RB - 1) / (kWaves * RB));
-  // x read in 16-byte pieces when it is 16-byte aligned (every half-block
-  // then is: k % 64 == 0)
-  const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
-  cint8_dot_kernel<RB, GRP, AFF><<<grid, kThreads, lds_size(4096), s>>>(sg, x, xtype, k, xvec);
-  return hipGetLastError();
+  // x read in 16-byte pieces when every row starts 16-byte aligned (every
+  // half-block then is: k % 64 == 0)
+  const long long row_bytes = ldx * (xtype == QC_STORAGE_F32 ? 4 : 2);
+  const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (m == 1 || row_bytes % 16 == 0);
+  for (int m0 = 0; m0 < m; m0 += MB) {
+    cint8_dot_kernel<RB, GRP, AFF, MB><<<grid, kThreads, MB * lds_size(4096), s>>>(
+        sg, x, xtype, k, xvec, ldx, m0, m);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 template <bool GRP, bool AFF>
-hipError_t launch_dot_rb(const CSegs& sg, const void* x, int xtype, int k, int rb, hipStream_t s) {
+hipError_t launch_dot_rb(const CSegs& sg, const void* x, int xtype, long long ldx, int m, int k,
+                         int rb, hipStream_t s) {
+  if (m > 1)   // passes of up to 4 activation rows, two weight rows per wave
+    return m == 2 ? launch_dot<2, GRP, AFF, 2>(sg, x, xtype, ldx, m, k, s)
+                  : launch_dot<2, GRP, AFF, 4>(sg, x, xtype, ldx, m, k, s);
   switch (rb) {
-    case 8: return launch_dot<8, GRP, AFF>(sg, x, xtype, k, s);
-    case 4: return launch_dot<4, GRP, AFF>(sg, x, xtype, k, s);
-    default: return launch_dot<2, GRP, AFF>(sg, x, xtype, k, s);
+    case 8: return launch_dot<8, GRP, AFF, 1>(sg, x, xtype, ldx, m, k, s);
+    case 4: return launch_dot<4, GRP, AFF, 1>(sg, x, xtype, ldx, m, k, s);
+    default: return launch_dot<2, GRP, AFF, 1>(sg, x, xtype, ldx, m, k, s);
   }
 }
 
@@ -663,17 +697,18 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   bool fast = k % 16 == 0 && (!grp || (sg.gsize >= 16 && (1 << sg.gshift) == sg.gsize));
   for (int i = 0; i < L.nw; ++i)
     fast = fast && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
-  // M = 1: exact digit dots over 64-column block pairs, two rows per wave
-  // (K=4096, 14336 rows: 13.9 us against 15.3 / 16.6 us with 4 / 8 rows;
-  // SwiGLU over 2 x 14336 rows 22.3 against 23.7 / 27.3 us).
-  if (fast && m == 1 && k % 64 == 0 && (!grp || sg.gsize >= 32) && L.dot >= 0) {
+  // M = 1..4: exact digit dots over 64-column block pairs, two rows per wave
+  // (M = 1, K=4096, 14336 rows: 13.9 us against 15.3 / 16.6 us with 4 / 8
+  // rows; SwiGLU over 2 x 14336 rows 22.3 against 23.7 / 27.3 us; M = 2 / 4:
+  // 22 / 41 us against 37 / 61 us on the f32 kernel).
+  if (fast && m <= 4 && k % 64 == 0 && (!grp || sg.gsize >= 32) && L.dot >= 0) {
     int rb = 2;
     if (L.rows_per_wave == 2 || L.rows_per_wave == 4 || L.rows_per_wave == 8) rb = L.rows_per_wave;
     if (grp)
-      return aff ? launch_dot_rb<true, true>(sg, L.x, L.xtype, k, rb, s)
-                 : launch_dot_rb<true, false>(sg, L.x, L.xtype, k, rb, s);
-    return aff ? launch_dot_rb<false, true>(sg, L.x, L.xtype, k, rb, s)
-               : launch_dot_rb<false, false>(sg, L.x, L.xtype, k, rb, s);
+      return aff ? launch_dot_rb<true, true>(sg, L.x, L.xtype, L.ldx, m, k, rb, s)
+                 : launch_dot_rb<true, false>(sg, L.x, L.xtype, L.ldx, m, k, rb, s);
+    return aff ? launch_dot_rb<false, true>(sg, L.x, L.xtype, L.ldx, m, k, rb, s)
+               : launch_dot_rb<false, false>(sg, L.x, L.xtype, L.ldx, m, k, rb, s);
   }
   if (fast) {
     const int cus = device_cu_count();

@@ -74,7 +74,11 @@ def _dev(qc, dev, arr, offset=0):
     (4096, 4096, 32, True, 1, 0, -1),
     (1000, 14336, 1, True, 1, 0, 0),      # affine channel scales, K in 4 chunks
     (600, 4096, 128, True, 1, 0, 0),      # groups of 32
-    (4096, 14336, 1, False, 2, 0, 0),
+    (4096, 14336, 1, False, 2, 0, 0),     # 2-4 rows: digit dots, codes loaded once per pass
+    (2048, 4096, 32, True, 3, 0, 0),      # affine groups of 128, 3 rows
+    (1000, 14336, 1, True, 4, 0, 0),      # affine channel scales, 4 rows, K in 4 chunks
+    (1000, 14336, 1, True, 4, 0, -1),     # the same on the f32 multiply-add kernel
+    (600, 4096, 128, True, 2, 0, 0),      # groups of 32, 2 rows
     (1024, 4096, 64, False, 7, 0, 0),     # passes of 4 activation rows
     (300, 4008, 1, True, 3, 0, 0),        # K % 16 != 0: byte-loading route
     (256, 1024, 4, False, 2, 4, 0),       # misaligned codes: byte-loading route
