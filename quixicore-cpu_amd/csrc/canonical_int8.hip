@@ -375,17 +375,171 @@ __device__ __noinline__ float cint8_block_f32(const int8_t* codes, const void* x
 // (three v_dot4 sums per 4 codes) and, for affine weights, xs = 2^e (2^14
 // D0 + 2^7 D1 + D2) ~ sum_j x_j over the same encoded x.  Group scales add
 // s_g (f - z_g xs) per block; row scales finish as s (sum f - z sum xs).
+template <int RB, bool GRP, bool AFF>
+__global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
+                                                             const void* __restrict__ x,
+                                                             int xtype, int k, bool xvec) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int kc = 4096;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int total = segs.start[segs.nseg];
+  const int g0 = (blockIdx.x * kWaves + wave) * RB;
+  const int8_t* w[RB];
+  const float* sp[RB];
+  const float* zp[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const RowRef rr = logical_row(segs, min(g0 + r, total - 1));
+    w[r] = segs.w[rr.seg] + static_cast<long long>(rr.row) * k;
+    sp[r] = segs.scale[rr.seg] + static_cast<long long>(rr.row) * segs.groups;
+    zp[r] = AFF ? segs.zero[rr.seg] + static_cast<long long>(rr.row) * segs.groups : nullptr;
+  }
+  float acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = 0.f;
+  float sxs = 0.f;   // affine row scales: this lane's sum of xs (finite blocks)
+  for (int c0 = 0; c0 < k; c0 += kc) {
+    const int clen = min(kc, k - c0);
+    const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
+    const int p = first_pair(pbeg, lane);
+    const bool live = p < pend;
+    const int pc = min(p, pend - 1);
+    // 1. this thread's half-block of x (16 values; past the chunk it re-reads
+    // the last one, which is not built), issued before the codes so that
+    // waiting for it does not wait for them (loads retire in order); no
+    // branch around it, which would make the compiler wait at the join
+    const int nh = clen >> 4;
+    const int hx = min(static_cast<int>(threadIdx.x), nh - 1);
+    float v[16];
+    {
+      const long long xi = c0 + 16LL * hx;
+      if (xvec && xtype == QC_STORAGE_F32) {
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(&v[4 * i]) = src[i];
+      } else if (xvec) {
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + xi);
+        const uint4 a = src[0], b = src[1];
+        const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint16_t lo = static_cast<uint16_t>(wd[i]), hi = static_cast<uint16_t>(wd[i] >> 16);
+          if (xtype == QC_STORAGE_F16) {
+            v[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+            v[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+          } else {
+            v[2 * i] = __uint_as_float(static_cast<uint32_t>(lo) << 16);
+            v[2 * i + 1] = __uint_as_float(static_cast<uint32_t>(hi) << 16);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = load_x(x, xi + i, xtype);
+      }
+    }
+    // 2. the codes of this lane's pair of every row (and group scales)
+    uint4 cw[RB][4];
+    float gs[RB][2], gz[RB][2];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        cw[r][i] = *reinterpret_cast<const uint4*>(w[r] + 64LL * pc + 16 * i);
+      if constexpr (GRP) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int gi = (64 * pc + 32 * h) >> segs.gshift;
+          gs[r][h] = sp[r][gi];
+          gz[r][h] = AFF ? zp[r][gi] : 0.f;
+        }
+      }
+    }
+    // digits of this chunk of x (half-block h = thread; the two halves of a
+    // block sit in lanes t and t ^ 1, both inside or both past the chunk)
+    // 3. the chunk's digits
+    if (c0) lds_barrier();
+    if (static_cast<int>(threadIdx.x) < nh) build_half<AFF>(lds, v, threadIdx.x, kc);
+    lds_barrier();
+    if (live) {
+      PairDigits g;
+      read_digits<kQ8_0>(g, lds, p - pbeg, kc);
+      float xs[2] = {0.f, 0.f};
+      if constexpr (AFF) {
+        int ds[2][3];
+        read_digit_sums(ds, lds, p - pbeg, kc);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) xs[h] = ldexpf(combine(ds[h][0], ds[h][1], ds[h][2]), g.e[h]);
+        if constexpr (!GRP) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            if (g.gate[h] == 1.0f) sxs += xs[h];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        int sd[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint4 q4 = cw[r][i >> 2];
+          const uint32_t q = (i & 3) == 0 ? q4.x : (i & 3) == 1 ? q4.y : (i & 3) == 2 ? q4.z : q4.w;
+          const int hb = i >> 3;
+#pragma unroll
+          for (int t = 0; t < 3; ++t)
+            sd[hb][t] = __builtin_amdgcn_sdot4(static_cast<int>(q), static_cast<int>(g.d[t][i]),
+                                               sd[hb][t], false);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (g.gate[h] == 1.0f) {
+            const float f = ldexpf(combine(sd[h][0], sd[h][1], sd[h][2]), g.e[h]);
+            if constexpr (GRP) acc[r] = fmaf(gs[r][h], AFF ? fmaf(-gz[r][h], xs[h], f) : f, acc[r]);
+            else acc[r] += f;
+          } else {
+            const float z = AFF ? (GRP ? gz[r][h] : zp[r][0]) : 0.f;
+            const float b = cint8_block_f32(w[r] + 64LL * p + 32 * h, x, c0 + 64LL * (p - pbeg) + 32 * h,
+                                            xtype, z);
+            acc[r] += GRP ? gs[r][h] * b : b;
+          }
+        }
+      }
+    }
+  }
+  // wave sums; lane r finishes row r (paired modes: lane r the pair r, r + 1)
+  float tot[RB];
+  const float sx = AFF && !GRP ? wave_sum(sxs) : 0.f;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    float v = wave_sum(acc[r]);
+    if constexpr (!GRP) v = sp[r][0] * (AFF ? fmaf(-zp[r][0], sx, v) : v);
+    tot[r] = v;
+  }
+  if (segs.mode == 0) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      if (lane == r && g0 + r < total) epilogue(segs, g0 + r, 0, tot[r], 0.f);
+  } else {
+#pragma unroll
+    for (int r = 0; r + 1 < RB; r += 2)
+      if (lane == r && g0 + r < total) epilogue(segs, g0 + r, 0, tot[r], tot[r + 1]);
+  }
+}
+
 // MB > 1: activation rows m0 .. m0 + MB - 1 (those below m) in one pass, one
 // digit record of x each in LDS; a lane's codes are loaded once and dotted
-// with every row's digits.
-template <int RB, bool GRP, bool AFF, int MB = 1>
-__global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
+// with every row's digits.  (One row keeps its own kernel above: the row
+// offsets and counts cost it 2-4%.)
+template <int RB, bool GRP, bool AFF, int MB>
+__global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs segs,
                                                              const void* __restrict__ x,
                                                              int xtype, int k, bool xvec,
                                                              long long ldx, int m0, int m) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int kc = 4096;
   constexpr int LS = static_cast<int>(lds_size(kc));
+  static_assert(MB == 2 || MB == 4, "one activation row takes cint8_dot_kernel");
+  const int mbase = m0;
+  const long long ldxe = ldx;
   const int mrows = min(MB, m - m0);   // wave-uniform
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -425,7 +579,7 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
 #pragma unroll
     for (int mm = 0; mm < MB; ++mm) {
       // rows past m re-read row m0 (not built)
-      const long long xi = static_cast<long long>(m0 + (mm < mrows ? mm : 0)) * ldx + c0 + 16LL * hx;
+      const long long xi = static_cast<long long>(mbase + (mm < mrows ? mm : 0)) * ldxe + c0 + 16LL * hx;
       if (xvec && xtype == QC_STORAGE_F32) {
         const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xi);
 #pragma unroll
@@ -480,7 +634,7 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
     for (int mm = 0; mm < MB; ++mm) {
       if (!live || mm >= mrows) continue;
       const uint8_t* const rec = lds + mm * LS;
-      const long long xrow = static_cast<long long>(m0 + mm) * ldx;
+      const long long xrow = static_cast<long long>(mbase + mm) * ldxe;
       PairDigits g;
       read_digits<kQ8_0>(g, rec, p - pbeg, kc);
       float xs[2] = {0.f, 0.f};
@@ -539,11 +693,11 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
     if (segs.mode == 0) {
 #pragma unroll
       for (int r = 0; r < RB; ++r)
-        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, m0 + mm, tot[r], 0.f);
+        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, mbase + mm, tot[r], 0.f);
     } else {
 #pragma unroll
       for (int r = 0; r + 1 < RB; r += 2)
-        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, m0 + mm, tot[r], tot[r + 1]);
+        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, mbase + mm, tot[r], tot[r + 1]);
     }
   }
 }
@@ -623,13 +777,18 @@ hipError_t launch_dot(const CSegs& sg, const void* x, int xtype, long long ldx, 
   // half-block then is: k % 64 == 0)
   const long long row_bytes = ldx * (xtype == QC_STORAGE_F32 ? 4 : 2);
   const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (m == 1 || row_bytes % 16 == 0);
-  for (int m0 = 0; m0 < m; m0 += MB) {
-    cint8_dot_kernel<RB, GRP, AFF, MB><<<grid, kThreads, MB * lds_size(4096), s>>>(
-        sg, x, xtype, k, xvec, ldx, m0, m);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+  if constexpr (MB == 1) {
+    cint8_dot_kernel<RB, GRP, AFF><<<grid, kThreads, lds_size(4096), s>>>(sg, x, xtype, k, xvec);
+    return hipGetLastError();
+  } else {
+    for (int m0 = 0; m0 < m; m0 += MB) {
+      cint8_dot_rows_kernel<RB, GRP, AFF, MB><<<grid, kThreads, MB * lds_size(4096), s>>>(
+          sg, x, xtype, k, xvec, ldx, m0, m);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
   }
-  return hipSuccess;
 }
 
 template <bool GRP, bool AFF>

@@ -181,6 +181,41 @@ def test_cint8_nonfinite_activations(qc, oracle, synth, dev, groups, affine, x_t
             qc.set_cint8_dot(0)
 
 
+@pytest.mark.parametrize("groups,affine,x_type,m", [(1, False, 0, 2), (1, True, 0, 3), (32, True, 2, 4),
+                                                    (32, False, 1, 4)])
+def test_cint8_rows_match_one_row(qc, oracle, synth, dev, groups, affine, x_type, m):
+    """2-4 activation rows on the digit-dot kernel: every output row is
+    bit-identical to the one-row call on that row (same digits, order and
+    finish), finite rows and rows holding +-inf or NaN alike."""
+    import torch
+    rows, cols = 300, 4096
+    codes, scales, zeros = _tensor(synth, 91 + groups, rows, cols, groups, affine)
+    codes[:, 200] = 0
+    keep = [_dev(qc, dev, a) for a in (codes, scales, zeros)]
+    w = qc.cint8_weights(keep[0], keep[1], keep[2], rows, cols, groups)
+    rng = np.random.default_rng(m + groups)
+    xs = rng.standard_normal((m, cols)).astype(np.float32)
+    xs[0, 200] = np.inf
+    xs[m - 1, 1234] = np.nan
+    if x_type == 0:
+        X = torch.from_numpy(xs).to(dev)
+    elif x_type == 1:
+        X = torch.from_numpy(xs.astype(np.float16).view(np.int16).copy()).to(dev)
+    else:
+        X = torch.from_numpy(_bf16_bits(xs).view(np.int16).copy()).to(dev)
+    print(f"cint8 rows vs one row groups={groups} affine={affine} x_type={x_type} m={m}", flush=True)
+    Y = torch.empty((m, rows), dtype=torch.float32, device=dev)
+    assert qc.cint8_project_raw(0, [w], X, x_type, m, [Y], [0]) == 0
+    Y = Y.cpu().numpy()
+    for r in range(m):
+        y1 = torch.empty(rows, dtype=torch.float32, device=dev)
+        assert qc.cint8_project_raw(0, [w], X[r].contiguous(), x_type, 1, [y1], [0]) == 0
+        assert np.array_equal(Y[r].view(np.uint32), y1.cpu().numpy().view(np.uint32)), r
+    assert not np.isfinite(Y[0]).any()
+    if m > 2:
+        assert np.isfinite(Y[1]).all()
+
+
 def test_cint8_fused_decode_shapes(qc, oracle, synth, dev):
     """SwiGLU and RoPE Q/K/V at a decoder's shapes: bit-identical to the f32
     epilogue applied to the plain projections of the same launch family."""
