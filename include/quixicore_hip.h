@@ -327,8 +327,8 @@ int qc_hip_set_qgemm_panel(int mode);
  * 1 = always.  Tuning and test knob with no reference counterpart. */
 int qc_hip_set_qgemm_rows(int mode);
 
-/* Canonical int8 projections (qc_hip_cint8_project) with one to four
- * activation rows: 0 (default) = the kernel with exact int8 digit dots (the
+/* Canonical int8 projections (qc_hip_cint8_project), any number of
+ * activation rows: 0 (default) = the kernels with exact int8 digit dots (the
  * GEMV's encoding of x) where it applies (K % 64 == 0, codes 16-byte aligned,
  * row scales or groups of >= 32 columns), -1 = always the f32 multiply-add
  * kernel.  Both stay within the contract tolerance.  Tuning and test knob

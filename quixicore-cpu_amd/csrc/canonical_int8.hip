@@ -856,11 +856,12 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   bool fast = k % 16 == 0 && (!grp || (sg.gsize >= 16 && (1 << sg.gshift) == sg.gsize));
   for (int i = 0; i < L.nw; ++i)
     fast = fast && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
-  // M = 1..4: exact digit dots over 64-column block pairs, two rows per wave
+  // Exact digit dots over 64-column block pairs, two rows per wave, passes of
+  // up to four activation rows
   // (M = 1, K=4096, 14336 rows: 13.9 us against 15.3 / 16.6 us with 4 / 8
-  // rows; SwiGLU over 2 x 14336 rows 22.3 against 23.7 / 27.3 us; M = 2 / 4:
-  // 22 / 41 us against 37 / 61 us on the f32 kernel).
-  if (fast && m <= 4 && k % 64 == 0 && (!grp || sg.gsize >= 32) && L.dot >= 0) {
+  // rows; SwiGLU over 2 x 14336 rows 22.3 against 23.7 / 27.3 us; M = 2 / 4 /
+  // 8: 22 / 41 / 82 us against 37 / 61 / 121 us on the f32 kernel).
+  if (fast && k % 64 == 0 && (!grp || sg.gsize >= 32) && L.dot >= 0) {
     int rb = 2;
     if (L.rows_per_wave == 2 || L.rows_per_wave == 4 || L.rows_per_wave == 8) rb = L.rows_per_wave;
     if (grp)
