@@ -525,21 +525,20 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
   }
 }
 
-// MB > 1: activation rows m0 .. m0 + MB - 1 (those below m) in one pass, one
-// digit record of x each in LDS; a lane's codes are loaded once and dotted
-// with every row's digits.  (One row keeps its own kernel above: the row
-// offsets and counts cost it 2-4%.)
+// The same digit dots for several activation rows: rows m0 .. m0 + MB - 1
+// (those below m) in one pass, with one digit record of x each in LDS; a
+// lane's codes are loaded once and dotted with every row's digits, so each
+// output row is bit-identical to the one-row kernel's.  (One row keeps its
+// own kernel above: the row offset and count as arguments cost it 2-4%.)
 template <int RB, bool GRP, bool AFF, int MB>
 __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs segs,
-                                                             const void* __restrict__ x,
-                                                             int xtype, int k, bool xvec,
-                                                             long long ldx, int m0, int m) {
+                                                                  const void* __restrict__ x,
+                                                                  int xtype, int k, bool xvec,
+                                                                  long long ldx, int m0, int m) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int kc = 4096;
   constexpr int LS = static_cast<int>(lds_size(kc));
   static_assert(MB == 2 || MB == 4, "one activation row takes cint8_dot_kernel");
-  const int mbase = m0;
-  const long long ldxe = ldx;
   const int mrows = min(MB, m - m0);   // wave-uniform
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -579,7 +578,7 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs se
 #pragma unroll
     for (int mm = 0; mm < MB; ++mm) {
       // rows past m re-read row m0 (not built)
-      const long long xi = static_cast<long long>(mbase + (mm < mrows ? mm : 0)) * ldxe + c0 + 16LL * hx;
+      const long long xi = static_cast<long long>(m0 + (mm < mrows ? mm : 0)) * ldx + c0 + 16LL * hx;
       if (xvec && xtype == QC_STORAGE_F32) {
         const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(x) + xi);
 #pragma unroll
@@ -634,7 +633,7 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs se
     for (int mm = 0; mm < MB; ++mm) {
       if (!live || mm >= mrows) continue;
       const uint8_t* const rec = lds + mm * LS;
-      const long long xrow = static_cast<long long>(mbase + mm) * ldxe;
+      const long long xrow = static_cast<long long>(m0 + mm) * ldx;
       PairDigits g;
       read_digits<kQ8_0>(g, rec, p - pbeg, kc);
       float xs[2] = {0.f, 0.f};
@@ -693,11 +692,11 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs se
     if (segs.mode == 0) {
 #pragma unroll
       for (int r = 0; r < RB; ++r)
-        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, mbase + mm, tot[r], 0.f);
+        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, m0 + mm, tot[r], 0.f);
     } else {
 #pragma unroll
       for (int r = 0; r + 1 < RB; r += 2)
-        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, mbase + mm, tot[r], tot[r + 1]);
+        if (lane == r && g0 + r < total) epilogue(segs, g0 + r, m0 + mm, tot[r], tot[r + 1]);
     }
   }
 }
