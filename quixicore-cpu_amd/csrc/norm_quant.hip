@@ -125,7 +125,7 @@ __device__ __forceinline__ void block_max_any(float& m, int& bad, float* smax, i
 // One workgroup of NT threads per row, the row in registers (V float4 per
 // thread; float4 index t + i * NT).  G4 = group size / 4 for groups of 4..256
 // columns (a group is G4 adjacent lanes), 0 for one group per row.  Requires
-// hidden % 4 == 0, hidden <= 4 * NT * V, 16-byte aligned x / residual /
+// hidden % 4 == 0, 4 <= hidden <= 4 * NT * V, 16-byte aligned x / residual /
 // weight / residual_out and 4-byte aligned codes.  residual_out may alias x
 // or residual (each element is read before it is written, by one thread).
 template <int V, int NT, int G4>
@@ -147,11 +147,15 @@ __global__ __launch_bounds__(NT) void rms_norm_quant_rows(
   const int n4 = hidden >> 2;
   const int t = threadIdx.x;
 
+  // Every lane issues all 2V loads (a lane past the row re-reads the row's
+  // last float4 and ignores it), so they are in flight together: a load
+  // inside `if (idx < n4)` was waited for before the next one was issued.
   float4 v[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = t + i * NT;
-    if (idx < n4) v[i] = add4(x4[idx], r4[idx]);
+    const int li = idx < n4 ? idx : n4 - 1;
+    v[i] = add4(x4[li], r4[li]);
   }
   double ss = 0.0;
 #pragma unroll
@@ -313,18 +317,46 @@ __device__ __forceinline__ int x86_int(double d) {
   return (d > -2147483649.0 && d < 2147483648.0) ? static_cast<int>(d) : INT_MIN;
 }
 
-__device__ __forceinline__ int8_t asym_code(float v, double sv, int zero) {
-  int q = static_cast<int>(static_cast<uint32_t>(x86_int(rint(static_cast<double>(v) / sv))) +
-                           static_cast<uint32_t>(zero));
-  q = q < -128 ? -128 : (q > 127 ? 127 : q);
-  return static_cast<int8_t>(q);
+// rint(v / sv) as the reference rounds it (the IEEE double quotient, half to
+// even), mostly without a division.  With rs = f32(RN(1 / sv)), the f32
+// product t = v * rs is (v / sv)(1 + e) with |e| <= 2^-23 (1 + 2^-22) (two f32
+// roundings and one double), and the double quotient D is (v / sv)(1 + e')
+// with |e'| <= 2^-53, so |t - D| < 2^-22.9 |t|.  Where t lies farther than
+// 2^-21 |t| from every half-integer, no half-integer separates t from D and
+// rintf(t) == rint(D); below |t| = 1/8 both round to zero.  Exact ties
+// (v / sv = k + 1/2), |t| >= 2^21 and a non-finite t (1 / sv beyond the f32
+// range) fail the test and take the division.  f32 denormals are kept on
+// this target, so subnormal v and t stay within the bound.
+__device__ __forceinline__ bool asym_fast(float v, float rs, int& q) {
+  const float t = v * rs;
+  const float r = rintf(t);
+  const bool ok = fabsf(t - r) < 0.5f - fabsf(t) * 0x1p-21f;
+  q = ok ? static_cast<int>(r) : 0;
+  return ok;
 }
 
-__device__ __forceinline__ uint32_t asym_codes4(float4 v, double sv, int zero) {
-  return static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.x, sv, zero))) |
-         (static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.y, sv, zero))) << 8) |
-         (static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.z, sv, zero))) << 16) |
-         (static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.w, sv, zero))) << 24);
+__device__ __forceinline__ int asym_exact(float v, double sv) {
+  return x86_int(rint(static_cast<double>(v) / sv));
+}
+
+// The code of rounded quotient q: q + zero with 32-bit wrap, saturated to int8.
+__device__ __forceinline__ uint32_t asym_byte(int q, int zero) {
+  int c = static_cast<int>(static_cast<uint32_t>(q) + static_cast<uint32_t>(zero));
+  c = c < -128 ? -128 : (c > 127 ? 127 : c);
+  return static_cast<uint8_t>(static_cast<int8_t>(c));
+}
+
+__device__ __forceinline__ int8_t asym_code(float v, double sv, float rs, int zero) {
+  int q;
+  if (!asym_fast(v, rs, q)) q = asym_exact(v, sv);
+  return static_cast<int8_t>(asym_byte(q, zero));
+}
+
+__device__ __forceinline__ uint32_t asym_codes4(float4 v, double sv, float rs, int zero) {
+  return static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.x, sv, rs, zero))) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.y, sv, rs, zero))) << 8) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.z, sv, rs, zero))) << 16) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(asym_code(v.w, sv, rs, zero))) << 24);
 }
 
 constexpr int kAsymThreads = 256;
@@ -396,6 +428,7 @@ __global__ __launch_bounds__(kAsymThreads) void quantize_asym_rows(
     sv = a < 1e-7 ? 1e-7 : a;
   }
   const int zero = x86_int(rint(-128.0 - minimum / sv));
+  const float rs = static_cast<float>(1.0 / sv);
   if (t == 0) {
     scales[row] = static_cast<float>(sv);
     zero_points[row] = zero;
@@ -406,16 +439,16 @@ __global__ __launch_bounds__(kAsymThreads) void quantize_asym_rows(
     uint32_t* c4 = reinterpret_cast<uint32_t*>(cr);
     for (long long i = t; i < dim / 4; i += kAsymThreads) {
       const float4 v = x4[i];
-      c4[i] = asym_codes4(v, sv, zero);
+      c4[i] = asym_codes4(v, sv, rs, zero);
     }
   } else {
-    for (long long i = t; i < dim; i += kAsymThreads) cr[i] = asym_code(xr[i], sv, zero);
+    for (long long i = t; i < dim; i += kAsymThreads) cr[i] = asym_code(xr[i], sv, rs, zero);
   }
 }
 
 
 // The same with the row held in registers (V float4 per thread): one read
-// of x.  Requires dim % 4 == 0, dim <= 4 * NT * V, x 16-byte and codes
+// of x.  Requires dim % 4 == 0, 4 <= dim <= 4 * NT * V, x 16-byte and codes
 // 4-byte aligned.
 template <int V, int NT>
 __global__ __launch_bounds__(NT) void quantize_asym_rows_regs(
@@ -431,11 +464,20 @@ __global__ __launch_bounds__(NT) void quantize_asym_rows_regs(
   float4 v[V];
   float lo = INFINITY, hi = -INFINITY;
   int bad = 0;
+  // All V loads in flight together, as in quantize_rows_regs (a lane past the
+  // row re-reads its last float4 and ignores it); x is read once and the
+  // codes written once: non-temporal loads and stores.
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = t + i * NT;
-    if (idx < n4) {
-      v[i] = x4[idx];
+    const u32x4nt u = __builtin_nontemporal_load(reinterpret_cast<const u32x4nt*>(x4) +
+                                                 (idx < n4 ? idx : n4 - 1));
+    v[i] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                       __uint_as_float(u.w));
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    if (t + i * NT < n4) {
       bad |= !finite4(v[i]);
       lo = fminf(fminf(lo, v[i].x), fminf(v[i].y, fminf(v[i].z, v[i].w)));
       hi = fmaxf(fmaxf(hi, v[i].x), fmaxf(v[i].y, fmaxf(v[i].z, v[i].w)));
@@ -476,14 +518,42 @@ __global__ __launch_bounds__(NT) void quantize_asym_rows_regs(
     sv = a < 1e-7 ? 1e-7 : a;
   }
   const int zero = x86_int(rint(-128.0 - minimum / sv));
+  const float rs = static_cast<float>(1.0 / sv);
   if (t == 0) {
     scales[row] = static_cast<float>(sv);
     zero_points[row] = zero;
   }
+  // The f32 estimate for every value first; the few that fail its test (one
+  // bit each in slow) take the division in one branch per thread.
+  int q[V][4];
+  uint32_t slow = 0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    q[i][0] = q[i][1] = q[i][2] = q[i][3] = 0;
+    if (t + i * NT < n4) {
+      slow |= (asym_fast(v[i].x, rs, q[i][0]) ? 0u : 1u) << (4 * i);
+      slow |= (asym_fast(v[i].y, rs, q[i][1]) ? 0u : 2u) << (4 * i);
+      slow |= (asym_fast(v[i].z, rs, q[i][2]) ? 0u : 4u) << (4 * i);
+      slow |= (asym_fast(v[i].w, rs, q[i][3]) ? 0u : 8u) << (4 * i);
+    }
+  }
+  if (slow != 0) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      if (slow & (1u << (4 * i))) q[i][0] = asym_exact(v[i].x, sv);
+      if (slow & (2u << (4 * i))) q[i][1] = asym_exact(v[i].y, sv);
+      if (slow & (4u << (4 * i))) q[i][2] = asym_exact(v[i].z, sv);
+      if (slow & (8u << (4 * i))) q[i][3] = asym_exact(v[i].w, sv);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = t + i * NT;
-    if (idx < n4) c4[idx] = asym_codes4(v[i], sv, zero);
+    if (idx < n4)
+      __builtin_nontemporal_store(asym_byte(q[i][0], zero) | (asym_byte(q[i][1], zero) << 8) |
+                                      (asym_byte(q[i][2], zero) << 16) |
+                                      (asym_byte(q[i][3], zero) << 24),
+                                  c4 + idx);
   }
 }
 
@@ -534,7 +604,8 @@ hipError_t launch_rms_norm_add_quant_int8(const float* x, const float* residual,
   // groups of 4..256 columns that are a power of two, or one group per row
   const long long g4 = group == hidden ? 0 : group / 4;
   const bool small_group = group % 4 == 0 && g4 >= 1 && g4 <= 64 && (g4 & (g4 - 1)) == 0;
-  const bool fast = hidden % 4 == 0 && hidden <= 32768 && (group == hidden || small_group) &&
+  const bool fast = hidden % 4 == 0 && hidden >= 4 && hidden <= 32768 &&
+                    (group == hidden || small_group) &&
                     aligned16(x) && aligned16(residual) && aligned16(weight) &&
                     aligned16(residual_out) && reinterpret_cast<uintptr_t>(codes) % 4 == 0 &&
                     rows <= 0x7FFFFFFFLL;
@@ -565,7 +636,7 @@ hipError_t launch_quantize_int8_asymmetric(const float* x, int8_t* codes, float*
   if (rows > 0x7FFFFFFFLL) return hipErrorInvalidValue;
   const unsigned grid = static_cast<unsigned>(rows);
   const bool vec = dim % 4 == 0 && aligned16(x) && reinterpret_cast<uintptr_t>(codes) % 4 == 0;
-  if (vec && dim <= 32768) {
+  if (vec && dim >= 4 && dim <= 32768) {
     const int d = static_cast<int>(dim);
     if (dim <= 1024)
       quantize_asym_rows_regs<1, 256><<<grid, 256, 0, s>>>(x, codes, scales, zero_points, d, status);

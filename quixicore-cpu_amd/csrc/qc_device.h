@@ -114,6 +114,8 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
 
 // 4-byte-aligned 128-bit load (global_load_dwordx4 accepts dword alignment).
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+// 16-byte vector for the non-temporal loads of the streaming kernels.
+typedef uint32_t u32x4nt __attribute__((ext_vector_type(4)));
 
 // The f32 dot of block h (0 / 1) of a pair (its bytes at `wp` in global
 // memory) with the block's 32 values of x, summed in element order

@@ -11,8 +11,6 @@
 #include "qc_internal.h"
 
 namespace qc {
-// 16-byte vector for the non-temporal loads of the streaming kernels.
-typedef uint32_t u32x4nt __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int kThreads = 256;
@@ -62,8 +60,8 @@ __device__ __forceinline__ void block_max_or(float& m, int& bad) {
 }
 
 // One workgroup of NT threads per row, the row held in registers: V float4
-// per thread.  Requires dim % 4 == 0, x 16-byte aligned, codes 4-byte
-// aligned and dim <= 4 * NT * V.
+// per thread.  Requires dim % 4 == 0, 4 <= dim <= 4 * NT * V, x 16-byte
+// aligned and codes 4-byte aligned.
 template <int V, int NT>
 __global__ __launch_bounds__(NT) void quantize_rows_regs(const float* __restrict__ x,
                                                                int8_t* __restrict__ codes,
@@ -76,14 +74,21 @@ __global__ __launch_bounds__(NT) void quantize_rows_regs(const float* __restrict
   float4 v[V];
   float m = 0.f;
   int bad = 0;
+  // Every lane issues all V loads (a lane past the row re-reads its last
+  // float4 and ignores it), so they are in flight together: a load inside
+  // `if (idx < n4)` was waited for before the next one was issued.  x is read
+  // once and the codes written once: non-temporal loads and stores measured
+  // 5.5% faster at M=2048 K=4096 (9.52-9.68 -> 8.97-9.04 us).
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = threadIdx.x + i * NT;
-    if (idx < n4) {
-      // x is read once and the codes written once: non-temporal loads and
-      // stores measured 5.5% faster at M=2048 K=4096 (9.52-9.68 -> 8.97-9.04 us)
-      const u32x4nt t = __builtin_nontemporal_load(reinterpret_cast<const u32x4nt*>(xr) + idx);
-      v[i] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
+    const u32x4nt t = __builtin_nontemporal_load(reinterpret_cast<const u32x4nt*>(xr) +
+                                                 (idx < n4 ? idx : n4 - 1));
+    v[i] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    if (static_cast<int>(threadIdx.x) + i * NT < n4) {
       bad |= !finite4(v[i]);
       m = abs_max4(v[i], m);
     }
@@ -248,7 +253,7 @@ hipError_t launch_quantize_int8(const float* x, int8_t* codes, float* scales, lo
   const bool per_row = group == dim;
   const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(codes) % 4 == 0 && dim % 4 == 0;
-  if (per_row && aligned && dim <= 32768 && rows <= 0x7FFFFFFFLL) {
+  if (per_row && aligned && dim >= 4 && dim <= 32768 && rows <= 0x7FFFFFFFLL) {
     const unsigned grid = static_cast<unsigned>(rows);
     if (dim <= 1024)
       quantize_rows_regs<1, 256><<<grid, 256, 0, s>>>(x, codes, scales, (int)dim, status);

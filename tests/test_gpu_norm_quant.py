@@ -221,6 +221,38 @@ def test_asym_edges(qc, oracle, dev):
     _asym_check(qc, oracle, dev, np.stack(rows))
 
 
+def test_asym_large_quotients_and_near_ties(qc, oracle, dev):
+    """Rows whose quotients x / scale run to ~2^32 (a large offset over a tiny
+    spread), quotients within 1e-7 relative of a half-integer, 1-ulp spreads
+    over every binade and subnormal rows: the codes are rint of the IEEE
+    double quotient even where a product with the reciprocal scale rounds the
+    other way."""
+    print("quantize_int8_asymmetric large quotients / near ties", flush=True)
+    rng = np.random.default_rng(11)
+    rows = []
+    for _ in range(96):
+        base = 10.0 ** rng.uniform(-30, 30) * rng.choice([-1.0, 1.0])
+        spread = abs(base) * 10.0 ** rng.uniform(-7.5, 2.0)
+        rows.append(base + rng.standard_normal(1024) * spread)
+    for _ in range(96):
+        s = 10.0 ** rng.uniform(-10, 10)
+        k = rng.integers(0, 255, 1022)
+        near = (k + 0.5) * s * (1.0 + rng.uniform(-1e-7, 1e-7, 1022))
+        rows.append(np.concatenate([[0.0, 255.0 * s], near]))
+    for _ in range(64):
+        b = np.float32(10.0 ** rng.uniform(-20, 20))
+        b1 = np.nextafter(b, np.float32(np.inf))
+        rows.append(np.array([b, b1, np.nextafter(b1, np.float32(np.inf)), b1] * 256))
+    for _ in range(16):
+        # subnormal rows (1 / scale beyond the f32 range), and subnormal values
+        # under a normal extreme (quotients 0 .. ~60 of subnormal x)
+        rows.append(rng.uniform(0.0, 1.0, 1024) * 1e-39)
+        top = 10.0 ** rng.uniform(-37, -35)
+        rows.append(np.concatenate([[0.0, top], rng.uniform(0.0, 1.0, 1022) * 1.1e-38]))
+        rows.append(np.concatenate([[-top, 0.0], -rng.uniform(0.0, 1.0, 1022) * 1.1e-38]))
+    _asym_check(qc, oracle, dev, np.stack(rows).astype(np.float32))
+
+
 def test_asym_nonfinite(qc, dev):
     import torch
     x = np.ones((4, 1024), np.float32)
