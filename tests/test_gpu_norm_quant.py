@@ -221,13 +221,14 @@ def test_asym_edges(qc, oracle, dev):
     _asym_check(qc, oracle, dev, np.stack(rows))
 
 
-def test_asym_large_quotients_and_near_ties(qc, oracle, dev):
+@pytest.mark.parametrize("off", [0, 1])    # 1: misaligned x, the generic kernel
+def test_asym_large_quotients_and_near_ties(qc, oracle, dev, off):
     """Rows whose quotients x / scale run to ~2^32 (a large offset over a tiny
     spread), quotients within 1e-7 relative of a half-integer, 1-ulp spreads
     over every binade and subnormal rows: the codes are rint of the IEEE
     double quotient even where a product with the reciprocal scale rounds the
     other way."""
-    print("quantize_int8_asymmetric large quotients / near ties", flush=True)
+    print(f"quantize_int8_asymmetric large quotients / near ties off={off}", flush=True)
     rng = np.random.default_rng(11)
     rows = []
     for _ in range(96):
@@ -250,7 +251,7 @@ def test_asym_large_quotients_and_near_ties(qc, oracle, dev):
         top = 10.0 ** rng.uniform(-37, -35)
         rows.append(np.concatenate([[0.0, top], rng.uniform(0.0, 1.0, 1022) * 1.1e-38]))
         rows.append(np.concatenate([[-top, 0.0], -rng.uniform(0.0, 1.0, 1022) * 1.1e-38]))
-    _asym_check(qc, oracle, dev, np.stack(rows).astype(np.float32))
+    _asym_check(qc, oracle, dev, np.stack(rows).astype(np.float32), off)
 
 
 def test_asym_nonfinite(qc, dev):
