@@ -25,6 +25,8 @@
 // quantize_int8_asymmetric restates kernels/quantization/quantization_ref.cpp:
 // 190-226 in double, with static_cast<int> of an out-of-range double giving
 // INT_MIN and int additions wrapping, as the reference's x86-64 build does.
+// Each code's rint(x / scale) comes from an f32 product wherever that provably
+// equals the double quotient's rounding (asym_fast), else from the division.
 #include "qc_device.h"
 #include "qc_internal.h"
 
