@@ -484,8 +484,20 @@ __global__ __launch_bounds__(256) void qgemm_reduce(const float* __restrict__ pa
                                                     int ks) {
   for (long long o = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; o < count;
        o += static_cast<long long>(gridDim.x) * 256) {
-    float sum = partial[o];
-    for (int q = 1; q < ks; ++q) sum += partial[static_cast<long long>(q) * count + o];
+    // Four partial sums in flight at once (indices clamped to the last set,
+    // so every load is in bounds), added in index order as before: with one
+    // load per loop trip each was waited for before the next was issued.
+    float sum = 0.0f;
+    for (int q0 = 0; q0 < ks; q0 += 4) {
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[j] = partial[static_cast<long long>(min(q0 + j, ks - 1)) * count + o];
+      sum = q0 == 0 ? v[0] : sum + v[0];
+#pragma unroll
+      for (int j = 1; j < 4; ++j)
+        if (q0 + j < ks) sum += v[j];
+    }
     y[o] = sum;
   }
 }
