@@ -89,6 +89,7 @@ def time_steps(launch, steps, warmup):
             end.record(stream)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
+        LAST_SAMPLES.clear()
         return (t1 - t0) * 1e3 / steps, start.elapsed_time(end) / steps
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
@@ -106,8 +107,66 @@ def time_steps(launch, steps, warmup):
         t1 = time.perf_counter()
     wall_ms = (t1 - t0) * 1e3 / steps
     gpu_ms = start.elapsed_time(end) / steps
+    # the reference harness's statistic (median of >= 20 samples after warmup,
+    # benchmarks/harness/timing.cpp:19-85): 20 more replays of the same graph,
+    # each bracketed by events; per-step GPU time of each replay
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(SAMPLES)]
+    with torch.cuda.stream(stream):
+        for a, b in evs:
+            a.record(stream)
+            graph.replay()
+            b.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) / steps for a, b in evs)
+    LAST_SAMPLES.clear()
+    LAST_SAMPLES.update({"gpu_ms_median": per[len(per) // 2], "gpu_ms_p20": per[len(per) // 5],
+                         "gpu_ms_p80": per[(4 * len(per)) // 5], "samples": len(per)})
     del graph
     return wall_ms, gpu_ms
+
+
+SAMPLES = 20
+LAST_SAMPLES = {}
+
+
+def samples():
+    """Median / p20 / p80 per-step GPU time of the replays after the last
+    time_steps call (empty for eager timing)."""
+    return dict(LAST_SAMPLES)
+
+
+def contract_gate(qc, fmt, packed, X, Y, n, k, rows):
+    """Correctness gate of one GPU result before it is timed: the given
+    activation rows of Y against the f64 contract |y - y64| <= 1e-4 *
+    ||x||_2 * ||w_hat_row||_2 (tests/correctness/test_qgemv.cpp:278-303).
+    The weights are dequantized by the library's unpack kernel (bit-exact with
+    the reference's unpackers, tested) and multiplied in float64 on the GPU."""
+    import torch
+    w = qc.unpack(fmt, packed, n, k).double()
+    wn = w.norm(dim=1)
+    xr = X.reshape(-1, k)[rows].double()
+    y64 = xr @ w.T.contiguous()
+    del w
+    err = (Y.reshape(-1, n)[rows].double() - y64).abs()
+    bound = 1e-4 * xr.norm(dim=1, keepdim=True) * wn[None, :]
+    worst = float((err / bound.clamp_min(1e-300)).max()) * 1e-4
+    torch.cuda.synchronize()
+    return {"pass": bool((err <= bound).all()), "rows_checked": len(rows),
+            "max_norm_err_vs_f64": worst}
+
+
+def w8a8_gate(w, x, ws, as_, y, rows):
+    """Bit-exact gate of int8_gemm outputs on the given rows: the int32 dots
+    from a float64 product (exact: every partial sum is an integer below
+    2^53) and the reference's epilogue (float(dot) * ws[n]) * as[m]
+    (kernels/quantization/int8_gemm_ref.cpp:9-32) as two separately rounded
+    f32 multiplies."""
+    import torch
+    acc = x[rows].double() @ w.double().T.contiguous()
+    want = (acc.float() * ws[None, :]) * as_[rows, None]
+    ok = torch.equal(y[rows].view(torch.int32), want.view(torch.int32))
+    return {"pass": bool(ok), "rows_checked": len(rows), "bit_exact": True}
 
 
 STREAM_SIZES = (("17.9MB_q8_0_k4096_n4096", 17858560), ("33.1MB_q4_0_k4096_n14336", 33103872),
@@ -139,7 +198,7 @@ def stream_ceiling(qc, steps, warmup, sizes=STREAM_SIZES, wpcs=(1, 2, 4, 8, 16))
                     raise RuntimeError(f"stream_read status {st}")
 
             wall, gpu = time_steps(launch, steps, warmup)
-            r = {"bytes": nb, "copies": copies, "grid": grid, "wall_ms": wall, "gpu_ms": gpu,
+            r = {"bytes": nb, "copies": copies, "grid": grid, "wall_ms": wall, "gpu_ms": gpu, **samples(),
                  "gbs": nb / (wall * 1e-3) / 1e9, "kernel_gbs": nb / (gpu * 1e-3) / 1e9}
             if best is None or r["gpu_ms"] < best["gpu_ms"]:
                 best = r
@@ -148,8 +207,10 @@ def stream_ceiling(qc, steps, warmup, sizes=STREAM_SIZES, wpcs=(1, 2, 4, 8, 16))
     return cases
 
 
-def gemv_case(qc, fmt, n, k, steps, warmup, seed):
-    """Rotated copies of packed weights; returns timing and one output."""
+def gemv_case(qc, fmt, n, k, steps, warmup, seed, gate=False):
+    """Rotated copies of packed weights; returns timing and one output.  With
+    `gate`, every output of one launch is checked against the f64 contract
+    before timing."""
     import torch
     dev = torch.device("cuda:0")
     bb = qc.BLOCK_BYTES[fmt]
@@ -169,11 +230,18 @@ def gemv_case(qc, fmt, n, k, steps, warmup, seed):
         if st:
             raise RuntimeError(f"qgemv status {st}")
 
+    check = None
+    if gate:
+        launch(0)
+        check = contract_gate(qc, fmt, packs[0], x, y, n, k, [0])
     wall, gpu = time_steps(launch, steps, warmup)
     alg = wbytes + 4 * k + 4 * n
-    return {"bytes": alg, "weight_bytes": wbytes, "copies": copies, "wall_ms": wall,
-            "gpu_ms": gpu, "gbs": alg / (wall * 1e-3) / 1e9,
-            "kernel_gbs": alg / (gpu * 1e-3) / 1e9}, packs[0], x, y
+    r = {"bytes": alg, "weight_bytes": wbytes, "copies": copies, "wall_ms": wall,
+         "gpu_ms": gpu, **samples(), "gbs": alg / (wall * 1e-3) / 1e9,
+         "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
+    if gate:
+        r["check"] = check
+    return r, packs[0], x, y
 
 
 def gemv_w8a8_case(qc, fmt, n, k, steps, warmup, seed):
@@ -201,13 +269,14 @@ def gemv_w8a8_case(qc, fmt, n, k, steps, warmup, seed):
     wall, gpu = time_steps(launch, steps, warmup)
     alg = wbytes + 4 * k + 4 * n
     return {"bytes": alg, "weight_bytes": wbytes, "copies": copies, "wall_ms": wall,
-            "gpu_ms": gpu, "gbs": alg / (wall * 1e-3) / 1e9,
+            "gpu_ms": gpu, **samples(), "gbs": alg / (wall * 1e-3) / 1e9,
             "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
 
 
-def fused_case(qc, kind, fmt, rows, k, steps, warmup, seed):
+def fused_case(qc, kind, fmt, rows, k, steps, warmup, seed, gate=False):
     """One fused decode launch over one x: kind "up_gate" (rows = (n, n)) or
-    "qkv" (rows = (q, kv, kv)), rotated weight copies."""
+    "qkv" (rows = (q, kv, kv)), rotated weight copies.  With `gate`, every
+    projection of one launch is checked against the f64 contract first."""
     import torch
     dev = torch.device("cuda:0")
     bb = qc.BLOCK_BYTES[fmt]
@@ -234,13 +303,25 @@ def fused_case(qc, kind, fmt, rows, k, steps, warmup, seed):
         if st:
             raise RuntimeError(f"{kind} status {st}")
 
+    check = None
+    if gate:
+        launch(0)
+        parts = [contract_gate(qc, fmt, p, x, y, r, k, [0]) for p, y, r in zip(sets[0], ys, rows)]
+        check = {"pass": all(p["pass"] for p in parts), "rows_checked": 1,
+                 "max_norm_err_vs_f64": max(p["max_norm_err_vs_f64"] for p in parts)}
     wall, gpu = time_steps(launch, steps, warmup)
     alg = wbytes + 4 * k + 4 * sum(rows)
-    return {"bytes": alg, "copies": copies, "wall_ms": wall, "gpu_ms": gpu,
-            "gbs": alg / (wall * 1e-3) / 1e9, "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
+    r = {"bytes": alg, "copies": copies, "wall_ms": wall, "gpu_ms": gpu, **samples(),
+         "gbs": alg / (wall * 1e-3) / 1e9, "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
+    if gate:
+        r["check"] = check
+    return r
 
 
-def qgemm_case(qc, n, k, m, steps, warmup, seed, fmt=0):
+def qgemm_case(qc, n, k, m, steps, warmup, seed, fmt=0, gate=False):
+    """Small-batch / prefill qgemm on rotated weight copies.  With `gate`, the
+    first and last activation rows of one launch (and a middle one) are
+    checked against the f64 contract before timing."""
     import torch
     dev = torch.device("cuda:0")
     wbytes = n * (k // 32) * qc.BLOCK_BYTES[fmt]
@@ -255,12 +336,19 @@ def qgemm_case(qc, n, k, m, steps, warmup, seed, fmt=0):
         if st:
             raise RuntimeError(f"qgemm status {st}")
 
+    check = None
+    if gate:
+        launch(0)
+        check = contract_gate(qc, fmt, packs[0], x, y, n, k, sorted({0, m // 2, m - 1}))
     wall, gpu = time_steps(launch, steps, warmup)
     alg = wbytes + 4 * m * k + 4 * m * n
     flops = 2.0 * m * n * k
-    return {"m": m, "n": n, "k": k, "bytes": alg, "wall_ms": wall, "gpu_ms": gpu,
-            "gbs": alg / (wall * 1e-3) / 1e9, "kernel_gbs": alg / (gpu * 1e-3) / 1e9,
-            "kernel_tflops": flops / (gpu * 1e-3) / 1e12}
+    r = {"m": m, "n": n, "k": k, "bytes": alg, "wall_ms": wall, "gpu_ms": gpu, **samples(),
+         "gbs": alg / (wall * 1e-3) / 1e9, "kernel_gbs": alg / (gpu * 1e-3) / 1e9,
+         "kernel_tflops": flops / (gpu * 1e-3) / 1e12}
+    if gate:
+        r["check"] = check
+    return r
 
 
 def cint8_case(qc, n, k, m, steps, warmup, groups=1, mode=0):
@@ -293,7 +381,7 @@ def cint8_case(qc, n, k, m, steps, warmup, groups=1, mode=0):
     wall, gpu = time_steps(launch, steps, warmup)
     alg = wbytes + 4 * m * k + 4 * m * n
     return {"m": m, "n": n, "k": k, "groups": groups, "bytes": alg, "copies": copies,
-            "wall_ms": wall, "gpu_ms": gpu, "gbs": alg / (wall * 1e-3) / 1e9,
+            "wall_ms": wall, "gpu_ms": gpu, **samples(), "gbs": alg / (wall * 1e-3) / 1e9,
             "kernel_gbs": alg / (gpu * 1e-3) / 1e9}
 
 
@@ -313,7 +401,7 @@ def quant_case(qc, m, k, steps, warmup):
             raise RuntimeError(f"quantize status {st}")
 
     wall, gpu = time_steps(launch, steps, warmup)
-    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu,
+    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu, **samples(),
             "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
 
 
@@ -339,7 +427,7 @@ def norm_quant_case(qc, m, k, steps, warmup):
             raise RuntimeError(f"rms_norm_add_quant status {st}")
 
     wall, gpu = time_steps(launch, steps, warmup)
-    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu,
+    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu, **samples(),
             "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
 
 
@@ -360,7 +448,7 @@ def asym_case(qc, m, k, steps, warmup):
             raise RuntimeError(f"quantize_int8_asymmetric status {st}")
 
     wall, gpu = time_steps(launch, steps, warmup)
-    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu,
+    return {"m": m, "k": k, "bytes": fp, "wall_ms": wall, "gpu_ms": gpu, **samples(),
             "gbs": fp / (wall * 1e-3) / 1e9, "kernel_gbs": fp / (gpu * 1e-3) / 1e9}
 
 
@@ -380,7 +468,10 @@ def w8a8_operands(qc, m, n, k, seed=7):
     return w, x, ws.reshape(-1), as_.reshape(-1)
 
 
-def w8a8_case(qc, m, n, k, steps, warmup, keep=False):
+def w8a8_case(qc, m, n, k, steps, warmup, keep=False, gate=False):
+    """int8_gemm over config 3's operand distribution.  With `gate`, 64
+    output rows spread over every m-tile of one launch are checked bit for
+    bit before timing."""
     import torch
     dev = torch.device("cuda:0")
     w, x, ws, as_ = w8a8_operands(qc, m, n, k)
@@ -392,10 +483,17 @@ def w8a8_case(qc, m, n, k, steps, warmup, keep=False):
         if st:
             raise RuntimeError(f"int8_gemm status {st}")
 
+    check = None
+    if gate:
+        launch(0)
+        rows = torch.linspace(0, m - 1, 64, device=dev).round().long().unique()
+        check = w8a8_gate(w, x, ws, as_, y, rows)
     wall, gpu = time_steps(launch, steps, warmup)
     ops = 2.0 * m * n * k
-    r = {"m": m, "n": n, "k": k, "ops": ops, "wall_ms": wall, "gpu_ms": gpu,
+    r = {"m": m, "n": n, "k": k, "ops": ops, "wall_ms": wall, "gpu_ms": gpu, **samples(),
          "tops": ops / (wall * 1e-3) / 1e12, "kernel_tops": ops / (gpu * 1e-3) / 1e12}
+    if gate:
+        r["check"] = check
     return (r, (w, x, ws, as_, y)) if keep else r
 
 
@@ -409,57 +507,78 @@ def layer_sweep(qc, steps, warmup):
     at M=1 (GEMV), M=8 (small-batch GEMM) and M=512 (prefill, the 2-D GEMM);
     W8A8 at M=512 and M=2048
     (per-token activation quantization + int8 GEMM).  Each matmul is timed on
-    its own (same graph discipline, rotated weight copies)."""
+    its own (same graph discipline, rotated weight copies), after one launch
+    of it passed its correctness gate (f64 contract for q4_0 rows, bit-exact
+    int8 GEMM rows); every regime reports its gates' outcome in `check`."""
     out = {}
+
+    def gates(parts):
+        return {"pass": all(p["pass"] for p in parts), "matmuls_checked": len(parts)}
+
     for m in (1, 8, 512):
-        us, wbytes = 0.0, 0
+        us, wbytes, checks = 0.0, 0, []
         for cnt, n, k in LAYER:
             if m == 1:
-                r, *_ = gemv_case(qc, 1, n, k, steps, warmup, seed=100 + n + k)
+                r, *_ = gemv_case(qc, 1, n, k, steps, warmup, seed=100 + n + k, gate=True)
             else:
-                r = qgemm_case(qc, n, k, m, steps, warmup, seed=200 + n + k, fmt=1)
+                r = qgemm_case(qc, n, k, m, steps, warmup, seed=200 + n + k, fmt=1, gate=True)
+            checks.append(r["check"])
             us += cnt * r["gpu_ms"] * 1e3
             wbytes += cnt * n * (k // 32) * 18
         flops = sum(cnt * 2.0 * m * n * k for cnt, n, k in LAYER)
         out[f"q4_0_m{m}"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
                              "weight_gbs": wbytes / (us * 1e-6) / 1e9,
-                             "tflops": flops / (us * 1e-6) / 1e12}
+                             "tflops": flops / (us * 1e-6) / 1e12, "check": gates(checks)}
     # M = 1 with the fused decode seams: Q/K/V in one launch (4096 x 3 rows),
     # O alone, gate/up in one launch, down alone.
-    us, wbytes = 0.0, 0
-    r = fused_case(qc, "qkv", 1, (4096, 4096, 4096), 4096, steps, warmup, seed=301)
+    us, checks = 0.0, []
+    r = fused_case(qc, "qkv", 1, (4096, 4096, 4096), 4096, steps, warmup, seed=301, gate=True)
     us += r["gpu_ms"] * 1e3
-    r, *_ = gemv_case(qc, 1, 4096, 4096, steps, warmup, seed=302)
+    checks.append(r["check"])
+    r, *_ = gemv_case(qc, 1, 4096, 4096, steps, warmup, seed=302, gate=True)
     us += r["gpu_ms"] * 1e3
-    r = fused_case(qc, "up_gate", 1, (14336, 14336), 4096, steps, warmup, seed=303)
+    checks.append(r["check"])
+    r = fused_case(qc, "up_gate", 1, (14336, 14336), 4096, steps, warmup, seed=303, gate=True)
     us += r["gpu_ms"] * 1e3
-    r, *_ = gemv_case(qc, 1, 4096, 14336, steps, warmup, seed=304)
+    checks.append(r["check"])
+    r, *_ = gemv_case(qc, 1, 4096, 14336, steps, warmup, seed=304, gate=True)
     us += r["gpu_ms"] * 1e3
+    checks.append(r["check"])
     wbytes = sum(cnt * n * (k // 32) * 18 for cnt, n, k in LAYER)
     out["q4_0_m1_fused"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
-                            "weight_gbs": wbytes / (us * 1e-6) / 1e9}
+                            "weight_gbs": wbytes / (us * 1e-6) / 1e9, "check": gates(checks)}
     for m in (512, 2048):
-        us, ops = 0.0, 0.0
+        us, ops, checks = 0.0, 0.0, []
         for cnt, n, k in LAYER:
             q = quant_case(qc, m, k, steps, warmup)
-            g = w8a8_case(qc, m, n, k, max(10, steps // 4), warmup)
+            g = w8a8_case(qc, m, n, k, max(10, steps // 4), warmup, gate=True)
+            checks.append(g["check"])
             us += cnt * (q["gpu_ms"] + g["gpu_ms"]) * 1e3
             ops += cnt * 2.0 * m * n * k
         out[f"w8a8_m{m}"] = {"layer_us": us, "model_ms_32_layers": 32 * us / 1e3,
-                             "tops": ops / (us * 1e-6) / 1e12}
+                             "tops": ops / (us * 1e-6) / 1e12, "check": gates(checks)}
     return out
 
 
 def profiled_traffic(name):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE runs,
     scaled by the copy-kernel calibration, from the committed summary
-    profiles/<name>.txt (None if absent)."""
+    profiles/<name>.txt (None if absent).  Not measured in this run: the
+    counters need their own profiler passes."""
     import re
     path = os.path.join(ROOT, "profiles", name + ".txt")
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read())
     return float(m.group(1)) if m else None
+
+
+def traffic_source(name):
+    """Where roofline.traffic comes from (it is read, not measured here)."""
+    if profiled_traffic(name) is None:
+        return None
+    return (f"profiles/{name}.txt: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes of the same "
+            "kernel, copy-calibrated; read from the committed summary, not measured in this run")
 
 
 def host_cpu():
@@ -619,17 +738,39 @@ def w8a8_baseline(ref, oracle, cpu, w_dev, x_dev, ws_dev, as_dev, y_dev, sample_
 
 def quant_baseline(ref, oracle, cpu, m, k, seconds):
     """The reference's quantize_int8 (kernels/quantization/quantization_ref.cpp:
-    143-168, scalar per row) over config 3's whole M x K activation matrix."""
+    143-168, scalar per row) over config 3's whole M x K activation matrix,
+    plus the bit-exact gate of the GPU quantizer on the same matrix (codes
+    and scale bits against the reference's)."""
     import numpy as np
+    import torch
+    import quixicore_hip as qc
     from quixicore_hip import synth
     x = synth.activations_outliers_fast(3, m, k)
+    codes_gpu, scales_gpu = qc.quantize_int8(torch.from_numpy(x).to("cuda:0"))
+    st, codes_ref, scales_ref = ref.quantize_int8(x)
+    gate = {"pass": bool(st == 0
+                         and np.array_equal(codes_gpu.cpu().numpy(), codes_ref)
+                         and np.array_equal(scales_gpu.cpu().numpy().view(np.uint32),
+                                            scales_ref.view(np.uint32))),
+            "rows_checked": m, "bit_exact": True}
     codes = np.empty((m, k), dtype=np.int8)
     scales = np.empty(m, dtype=np.float32)
     args = (oracle._ptr(x), oracle._ptr(codes), oracle._ptr(scales), m, k, 0)
     fp = 4 * m * k + m * k + 4 * m
-    return cpu_legs(ref, oracle, cpu, seconds,
+    base = cpu_legs(ref, oracle, cpu, seconds,
                     lambda: (lambda: ref.lib.qcref_quantize_int8(*args), fp), "GB/s",
                     f"reference quantize_int8 M={m} K={k} (config 3 activations)")
+    return base, gate
+
+
+def median_fields(r):
+    """The median (p20, p80) per-step kernel time over the 20 replays that
+    follow a case's timed replay, in microseconds."""
+    if "gpu_ms_median" not in r:
+        return {}
+    return {"kernel_us_median": round(r["gpu_ms_median"] * 1e3, 3),
+            "kernel_us_p20_p80": [round(r["gpu_ms_p20"] * 1e3, 3), round(r["gpu_ms_p80"] * 1e3, 3)],
+            "samples": r["samples"]}
 
 
 def print_cases(cases):
@@ -753,7 +894,7 @@ def main():
         for n_ in (4096, 14336):
             bases[n_] = w8a8_baseline(ref, oracle, cpu, w8ops[n_][0], w8ops[n_][1], w8ops[n_][2],
                                       w8ops[n_][3], w8ops[n_][4], 64, sec * 0.5)
-        bases["quant"] = (quant_baseline(ref, oracle, cpu, 2048, 4096, sec * 0.3), None)
+        bases["quant"] = quant_baseline(ref, oracle, cpu, 2048, 4096, sec * 0.3)
         ref.set_threads(1)
     del w8ops
 
@@ -766,20 +907,24 @@ def main():
         return {"value": round(r["gbs"], 2), "unit": "GB/s", **extra,
                 "pct_hbm_peak": round(100.0 * r["gbs"] / HBM_PEAK_GBS, 2),
                 "kernel_us": round(r["gpu_ms"] * 1e3, 3), "bytes_per_step": r["bytes"],
+                **median_fields(r),
                 "roofline": {"bound": "hbm", "achieved": round(r["kernel_gbs"], 2),
                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                             "traffic": profiled_traffic(name)},
+                             "traffic": profiled_traffic(name),
+                             "traffic_source": traffic_source(name)},
                 "cpu_baseline": base, "check": gate}
 
     def w8a8_leg(r, key, name):
         base, gate = bases.get(key, (None, None))
         return {"value": round(r["tops"], 2), "unit": "TOPS",
                 "kernel_us": round(r["gpu_ms"] * 1e3, 3), "ops_per_step": r["ops"],
+                **median_fields(r),
                 "roofline": {"bound": "mfma", "achieved": round(r["kernel_tops"], 2),
                              "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                              "frac": round(r["kernel_tops"] / INT8_PEAK_TOPS, 4),
-                             "traffic": profiled_traffic(name)},
+                             "traffic": profiled_traffic(name),
+                             "traffic_source": traffic_source(name)},
                 "cpu_baseline": base, "check": gate}
 
     legs = {

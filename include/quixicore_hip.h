@@ -86,8 +86,11 @@ int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long 
  * (activation fragments, partial sums, row exponents) lives in a fixed
  * device array of QC_QGEMM_NOALLOC_SCRATCH_BYTES per GPU, held until the
  * process ends, instead of memory the library allocates.  Every call on a
- * GPU shares that GPU's array, so calls that overlap on one GPU (any
- * streams, any threads) race: serialize them.  M >= 2 runs passes of at
+ * GPU shares that GPU's array.  A per-GPU host lock is held from a call's
+ * first launch to its last, so calls from several host threads on ONE stream
+ * are safe (their launch sequences queue one after the other); calls on
+ * different streams of one GPU can overlap on the device and race: serialize
+ * those.  M >= 2 runs passes of at
  * most 32 rows (never the 2-D M >= 64 route, whose scratch grows with m) with
  * the fewest K splits.  Limits: m <= QC_QGEMM_NOALLOC_MAX_M and
  * k <= QC_QGEMM_NOALLOC_MAX_K, else 1 (QC_INVALID_SHAPE) with a message in
@@ -268,9 +271,6 @@ int qc_hip_qgemm_w8a8(const int8_t* w, const int8_t* x, const float* ws, const f
                       float* y, long long m, long long n, long long k, int* dev_status,
                       void* stream);
 
-/* Test seam: the exact int32 accumulators sum_k W[n][k]*X[m][k] into
- * acc[m][n] (k <= 131071).  No reference counterpart (the reference's
- * accumulators are internal to kernels/quantization/int8_gemm_*.cpp). */
 /* Measurement seam with no reference counterpart: reads `bytes` (a multiple
  * of 16) of device memory with 16-byte loads as fast as the chip allows and
  * stores one XOR word per thread into out (grid * 256 words).  bench.py times
@@ -278,6 +278,9 @@ int qc_hip_qgemm_w8a8(const int8_t* w, const int8_t* x, const float* ws, const f
  * HBM efficiency is judged against. */
 int qc_hip_stream_read(const void* p, long long bytes, uint32_t* out, int grid, void* stream);
 
+/* Test seam: the exact int32 accumulators sum_k W[n][k]*X[m][k] into
+ * acc[m][n] (k <= 131071).  No reference counterpart (the reference's
+ * accumulators are internal to kernels/quantization/int8_gemm_*.cpp). */
 int qc_hip_int8_gemm_i32(const int8_t* w, const int8_t* x, int32_t* acc, long long m,
                          long long n, long long k, void* stream);
 

@@ -399,6 +399,12 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
 #pragma unroll
   for (int r = 0; r < RB; ++r) acc[r] = 0.f;
   float sxs = 0.f;   // affine row scales: this lane's sum of xs (finite blocks)
+  // affine row scales with an integral zero point: (c - z) summed exactly per
+  // block (affine_block), so sxs is not needed for that row
+  int rzi[RB];
+  bool rzint[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) rzint[r] = AFF && !GRP && integral_zero(zp[r][0], rzi[r]);
   for (int c0 = 0; c0 < k; c0 += kc) {
     const int clen = min(kc, k - c0);
     const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
@@ -465,8 +471,8 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
       PairDigits g;
       read_digits<kQ8_0>(g, lds, p - pbeg, kc);
       float xs[2] = {0.f, 0.f};
+      int ds[2][3] = {{0, 0, 0}, {0, 0, 0}};
       if constexpr (AFF) {
-        int ds[2][3];
         read_digit_sums(ds, lds, p - pbeg, kc);
 #pragma unroll
         for (int h = 0; h < 2; ++h) xs[h] = ldexpf(combine(ds[h][0], ds[h][1], ds[h][2]), g.e[h]);
@@ -493,8 +499,18 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
         for (int h = 0; h < 2; ++h) {
           if (g.gate[h] == 1.0f) {
             const float f = ldexpf(combine(sd[h][0], sd[h][1], sd[h][2]), g.e[h]);
-            if constexpr (GRP) acc[r] = fmaf(gs[r][h], AFF ? fmaf(-gz[r][h], xs[h], f) : f, acc[r]);
-            else acc[r] += f;
+            if constexpr (GRP && AFF) {
+              int zi;
+              const float t = integral_zero(gz[r][h], zi) ? affine_block(sd[h], ds[h], zi, g.e[h])
+                                                          : fmaf(-gz[r][h], xs[h], f);
+              acc[r] = fmaf(gs[r][h], t, acc[r]);
+            } else if constexpr (GRP) {
+              acc[r] = fmaf(gs[r][h], f, acc[r]);
+            } else if constexpr (AFF) {
+              acc[r] += rzint[r] ? affine_block(sd[h], ds[h], rzi[r], g.e[h]) : f;
+            } else {
+              acc[r] += f;
+            }
           } else {
             const float z = AFF ? (GRP ? gz[r][h] : zp[r][0]) : 0.f;
             const float b = cint8_block_f32(w[r] + 64LL * p + 32 * h, x, c0 + 64LL * (p - pbeg) + 32 * h,
@@ -511,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
     float v = wave_sum(acc[r]);
-    if constexpr (!GRP) v = sp[r][0] * (AFF ? fmaf(-zp[r][0], sx, v) : v);
+    if constexpr (!GRP) v = sp[r][0] * (AFF && !rzint[r] ? fmaf(-zp[r][0], sx, v) : v);
     tot[r] = v;
   }
   if (segs.mode == 0) {
@@ -562,6 +578,10 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs se
   float sxs[MB];   // affine row scales: this lane's sum of xs (finite blocks)
 #pragma unroll
   for (int mm = 0; mm < MB; ++mm) sxs[mm] = 0.f;
+  int rzi[RB];      // integral row zero points (affine_block), as in the one-row kernel
+  bool rzint[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) rzint[r] = AFF && !GRP && integral_zero(zp[r][0], rzi[r]);
   for (int c0 = 0; c0 < k; c0 += kc) {
     const int clen = min(kc, k - c0);
     const int pbeg = c0 >> 6, pend = (c0 + clen) >> 6;
@@ -637,8 +657,8 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs se
       PairDigits g;
       read_digits<kQ8_0>(g, rec, p - pbeg, kc);
       float xs[2] = {0.f, 0.f};
+      int ds[2][3] = {{0, 0, 0}, {0, 0, 0}};
       if constexpr (AFF) {
-        int ds[2][3];
         read_digit_sums(ds, rec, p - pbeg, kc);
 #pragma unroll
         for (int h = 0; h < 2; ++h) xs[h] = ldexpf(combine(ds[h][0], ds[h][1], ds[h][2]), g.e[h]);
@@ -665,8 +685,18 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs se
         for (int h = 0; h < 2; ++h) {
           if (g.gate[h] == 1.0f) {
             const float f = ldexpf(combine(sd[h][0], sd[h][1], sd[h][2]), g.e[h]);
-            if constexpr (GRP) acc[r][mm] = fmaf(gs[r][h], AFF ? fmaf(-gz[r][h], xs[h], f) : f, acc[r][mm]);
-            else acc[r][mm] += f;
+            if constexpr (GRP && AFF) {
+              int zi;
+              const float t = integral_zero(gz[r][h], zi) ? affine_block(sd[h], ds[h], zi, g.e[h])
+                                                          : fmaf(-gz[r][h], xs[h], f);
+              acc[r][mm] = fmaf(gs[r][h], t, acc[r][mm]);
+            } else if constexpr (GRP) {
+              acc[r][mm] = fmaf(gs[r][h], f, acc[r][mm]);
+            } else if constexpr (AFF) {
+              acc[r][mm] += rzint[r] ? affine_block(sd[h], ds[h], rzi[r], g.e[h]) : f;
+            } else {
+              acc[r][mm] += f;
+            }
           } else {
             const float z = AFF ? (GRP ? gz[r][h] : zp[r][0]) : 0.f;
             const float b = cint8_block_f32(w[r] + 64LL * p + 32 * h, x,
@@ -686,7 +716,7 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_rows_kernel(const CSegs se
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       float v = wave_sum(acc[r][mm]);
-      if constexpr (!GRP) v = sp[r][0] * (AFF ? fmaf(-zp[r][0], sx, v) : v);
+      if constexpr (!GRP) v = sp[r][0] * (AFF && !rzint[r] ? fmaf(-zp[r][0], sx, v) : v);
       tot[r] = v;
     }
     if (segs.mode == 0) {

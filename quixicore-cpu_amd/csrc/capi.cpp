@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdlib>
@@ -20,9 +21,39 @@
 namespace {
 
 thread_local std::string g_last_error;
-qc::GemvTuning g_tuning;
-int g_int8_route = qc::kInt8Auto;
-bool g_norm_sequential = false;
+
+// Process-wide routing knobs (the qc_hip_set_* calls).  Each is an atomic and
+// every call reads them once, into a snapshot, so a setter that races with
+// calls on other threads is well defined: each call sees the old value or
+// the new one.  The qgemm plan (waves, stages) is one word, so a call never
+// sees half of a plan.
+struct Knobs {
+  std::atomic<int> rows_per_wave{0};
+  std::atomic<int> qgemm_plan{0};   // waves | stages << 8
+  std::atomic<int> qgemm_panel{0};
+  std::atomic<int> qgemm_rows{0};
+  std::atomic<int> qgemm_fold{0};
+  std::atomic<int> cint8_dot{0};
+  std::atomic<int> int8_route{qc::kInt8Auto};
+  std::atomic<bool> norm_sequential{false};
+};
+Knobs g_knobs;
+
+qc::GemvTuning tuning() {
+  constexpr auto r = std::memory_order_relaxed;
+  qc::GemvTuning t;
+  t.rows_per_wave = g_knobs.rows_per_wave.load(r);
+  const int plan = g_knobs.qgemm_plan.load(r);
+  t.qgemm_waves = plan & 0xFF;
+  t.qgemm_stages = plan >> 8;
+  t.qgemm_panel = g_knobs.qgemm_panel.load(r);
+  t.qgemm_rows = g_knobs.qgemm_rows.load(r);
+  t.qgemm_fold = g_knobs.qgemm_fold.load(r);
+  t.cint8_dot = g_knobs.cint8_dot.load(r);
+  return t;
+}
+
+int int8_route() { return g_knobs.int8_route.load(std::memory_order_relaxed); }
 
 int device_error(hipError_t e) {
   g_last_error = hipGetErrorString(e);
@@ -184,7 +215,7 @@ int qc_hip_qgemv(int format, const void* packed, const float* x, float* y, long 
   size_t ignored = 0;
   if (packed_bytes(format, n, k, &ignored) != QC_OK) return QC_INVALID_SHAPE;
   if (packed == nullptr || x == nullptr || y == nullptr) return QC_INVALID_ARGUMENT;
-  return finish(qc::launch_qgemm(format, packed, x, y, 1, n, k, as_stream(stream), g_tuning));
+  return finish(qc::launch_qgemm(format, packed, x, y, 1, n, k, as_stream(stream), tuning()));
 }
 
 // kernels/quantization/qgemm_ref.cpp:141-164: shape products first, then the
@@ -197,7 +228,7 @@ int qc_hip_qgemm(int format, const void* packed, const float* x, float* y, long 
   size_t size = 0;
   const int st = qc_hip_qgemv_packed_size(format, n, k, &size);
   if (st != QC_OK) return st;
-  return finish(qc::launch_qgemm(format, packed, x, y, m, n, k, as_stream(stream), g_tuning));
+  return finish(qc::launch_qgemm(format, packed, x, y, m, n, k, as_stream(stream), tuning()));
 }
 
 // qc_hip_qgemm without allocating: the same validation and kernels, with the
@@ -218,7 +249,7 @@ int qc_hip_qgemm_noalloc(int format, const void* packed, const float* x, float* 
   const int st = qc_hip_qgemv_packed_size(format, n, k, &size);
   if (st != QC_OK) return st;
   const hipError_t e = qc::launch_qgemm(format, packed, x, y, m, n, k, as_stream(stream),
-                                        g_tuning, /*noalloc=*/true);
+                                        tuning(), /*noalloc=*/true);
   if (e == hipErrorOutOfMemory) {
     g_last_error = "qgemm_noalloc: this shape needs more than the fixed scratch of " +
                    std::to_string(qc::kQgemmNoAllocScratchBytes) + " bytes";
@@ -257,7 +288,7 @@ int qc_hip_int8_gemm(const int8_t* w, const int8_t* x, const float* ws, const fl
   const hipStream_t s = as_stream(stream);
   if (dev_status != nullptr)
     return finish(qc::launch_int8_gemm(w, x, ws, as, row_sum, zp, y, nullptr, m, n, k,
-                                       asymmetric != 0, dev_status, s, g_int8_route));
+                                       asymmetric != 0, dev_status, s, int8_route()));
   bool finite = false;
   int st = all_finite(ws, n, s, &finite);
   if (st != QC_OK) return st;
@@ -266,7 +297,7 @@ int qc_hip_int8_gemm(const int8_t* w, const int8_t* x, const float* ws, const fl
   if (st != QC_OK) return st;
   if (!finite) return QC_INVALID_ARGUMENT;
   hipError_t e = qc::launch_int8_gemm(w, x, ws, as, row_sum, zp, y, nullptr, m, n, k,
-                                      asymmetric != 0, nullptr, s, g_int8_route);
+                                      asymmetric != 0, nullptr, s, int8_route());
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   return finish(e);
 }
@@ -283,7 +314,7 @@ int qc_hip_int8_gemm_i32(const int8_t* w, const int8_t* x, int32_t* acc, long lo
   if (k > 131071) return QC_INVALID_SHAPE;
   if (w == nullptr || x == nullptr || acc == nullptr) return QC_INVALID_ARGUMENT;
   return finish(qc::launch_int8_gemm(w, x, nullptr, nullptr, nullptr, nullptr, nullptr, acc, m,
-                                     n, k, false, nullptr, as_stream(stream), g_int8_route));
+                                     n, k, false, nullptr, as_stream(stream), int8_route()));
 }
 
 int qc_hip_stream_read(const void* p, long long bytes, uint32_t* out, int grid, void* stream) {
@@ -308,7 +339,7 @@ const char* qc_hip_int8_gemm_variant(void) { return "hip_gfx950_mfma_i8"; }
 int qc_hip_set_gemv_rows_per_wave(int rows) {
   if (rows != 0 && rows != 1 && rows != 2 && rows != 4 && rows != 7 && rows != 8 && rows != 14)
     return QC_INVALID_ARGUMENT;
-  g_tuning.rows_per_wave = rows;
+  g_knobs.rows_per_wave.store(rows, std::memory_order_relaxed);
   return QC_OK;
 }
 
@@ -332,9 +363,10 @@ int fused_gemv(int format, int nseg, const void* const* w, float* const* y,
     for (int i = 0; i < nseg; ++i) r[i] = static_cast<int>(rows[i]);
     return finish(qc::launch_qgemv_multi(format, nseg, w, y, r, act, x, static_cast<int>(k), s));
   }
+  const qc::GemvTuning t = tuning();
   if (act < 0) {
     for (int i = 0; i < nseg; ++i) {
-      const hipError_t e = qc::launch_qgemm(format, w[i], x, y[i], 1, rows[i], k, s, g_tuning);
+      const hipError_t e = qc::launch_qgemm(format, w[i], x, y[i], 1, rows[i], k, s, t);
       if (e != hipSuccess) return device_error(e);
     }
     return QC_OK;
@@ -342,8 +374,8 @@ int fused_gemv(int format, int nseg, const void* const* w, float* const* y,
   float* up = nullptr;
   hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&up), sizeof(float) * rows[0], s);
   if (e != hipSuccess) return device_error(e);
-  e = qc::launch_qgemm(format, w[0], x, up, 1, rows[0], k, s, g_tuning);
-  if (e == hipSuccess) e = qc::launch_qgemm(format, w[1], x, y[0], 1, rows[0], k, s, g_tuning);
+  e = qc::launch_qgemm(format, w[0], x, up, 1, rows[0], k, s, t);
+  if (e == hipSuccess) e = qc::launch_qgemm(format, w[1], x, y[0], 1, rows[0], k, s, t);
   if (e == hipSuccess) {
     e = qc::launch_fused_activation(y[0], up, rows[0], act, s);
   }
@@ -454,15 +486,16 @@ int qc_hip_qgemv_qkv_rope_kv(int format, const void* packed_q, const void* packe
                                             static_cast<int>(kv_rows), static_cast<int>(half),
                                             rc, rs, x, static_cast<int>(input_dim), s));
   if (half > INT_MAX) return QC_INVALID_SHAPE;   // this library's dimension limit
-  hipError_t e = qc::launch_qgemm(format, packed_q, x, q, 1, query_dim, input_dim, s, g_tuning);
+  const qc::GemvTuning t = tuning();
+  hipError_t e = qc::launch_qgemm(format, packed_q, x, q, 1, query_dim, input_dim, s, t);
   if (e == hipSuccess)
     e = qc::launch_rope_pairs(q, query_heads, static_cast<int>(half), rc, rs, s);
   if (e == hipSuccess && slot >= 0) {
-    e = qc::launch_qgemm(format, packed_k, x, kc, 1, kv_dim, input_dim, s, g_tuning);
+    e = qc::launch_qgemm(format, packed_k, x, kc, 1, kv_dim, input_dim, s, t);
     if (e == hipSuccess)
       e = qc::launch_rope_pairs(kc, kv_heads, static_cast<int>(half), rc, rs, s);
     if (e == hipSuccess)
-      e = qc::launch_qgemm(format, packed_v, x, vc, 1, kv_dim, input_dim, s, g_tuning);
+      e = qc::launch_qgemm(format, packed_v, x, vc, 1, kv_dim, input_dim, s, t);
   }
   return finish(e);
 }
@@ -526,9 +559,10 @@ int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void
     L.rope_cos = rope_cos;
     L.rope_sin = rope_sin;
   }
-  const int rw = g_tuning.rows_per_wave;
+  const qc::GemvTuning t = tuning();
+  const int rw = t.rows_per_wave;
   L.rows_per_wave = rw == 2 || rw == 4 || rw == 8 ? rw : 0;
-  L.dot = g_tuning.cint8_dot;
+  L.dot = t.cint8_dot;
   return finish(qc::launch_cint8(L, as_stream(stream)));
 }
 
@@ -554,13 +588,13 @@ int qc_hip_qgemv_w8a8(int format, const void* packed, const float* x, float* y, 
   if (packed == nullptr || x == nullptr || y == nullptr) return QC_INVALID_ARGUMENT;
   const hipStream_t s = as_stream(stream);
   if (dev_status != nullptr)
-    return finish(qc::launch_qgemv_w8a8(format, packed, x, y, n, k, g_tuning.rows_per_wave,
+    return finish(qc::launch_qgemv_w8a8(format, packed, x, y, n, k, tuning().rows_per_wave,
                                         dev_status, s));
   bool finite = false;
   const int fst = all_finite(x, k, s, &finite);
   if (fst != QC_OK) return fst;
   if (!finite) return QC_INVALID_ARGUMENT;
-  hipError_t e = qc::launch_qgemv_w8a8(format, packed, x, y, n, k, g_tuning.rows_per_wave,
+  hipError_t e = qc::launch_qgemv_w8a8(format, packed, x, y, n, k, tuning().rows_per_wave,
                                        nullptr, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   return finish(e);
@@ -575,8 +609,7 @@ int qc_hip_set_qgemm_plan(int waves, int stages) {
   if (waves != 0 && waves != 4 && waves != 8) return QC_INVALID_ARGUMENT;
   if (stages != 0 && stages != 1 && stages != 2 && stages != 4 && stages != 8 && stages != 16)
     return QC_INVALID_ARGUMENT;
-  g_tuning.qgemm_waves = waves;
-  g_tuning.qgemm_stages = stages;
+  g_knobs.qgemm_plan.store(waves | stages << 8, std::memory_order_relaxed);
   return QC_OK;
 }
 
@@ -596,7 +629,7 @@ int qc_hip_rms_norm_add_quant_int8(const float* x, const float* residual, const 
   if (!x || !residual || !weight || !codes || !residual_out || !scales)
     return QC_INVALID_ARGUMENT;
   const hipStream_t s = as_stream(stream);
-  const bool seq = g_norm_sequential;
+  const bool seq = g_knobs.norm_sequential.load(std::memory_order_relaxed);
   if (dev_status != nullptr)
     return finish(qc::launch_rms_norm_add_quant_int8(x, residual, weight, codes, residual_out,
                                                      scales, rows, hidden, eps, group_size,
@@ -642,36 +675,36 @@ int qc_hip_dequantize_int8_asymmetric(const int8_t* codes, const float* scales,
 
 int qc_hip_set_qgemm_panel(int mode) {
   if (mode < -1 || mode > 2) return QC_INVALID_ARGUMENT;
-  g_tuning.qgemm_panel = mode;
+  g_knobs.qgemm_panel.store(mode, std::memory_order_relaxed);
   return QC_OK;
 }
 
 int qc_hip_set_qgemm_rows(int mode) {
   if (mode < -1 || mode > 1) return QC_INVALID_ARGUMENT;
-  g_tuning.qgemm_rows = mode;
+  g_knobs.qgemm_rows.store(mode, std::memory_order_relaxed);
   return QC_OK;
 }
 
 int qc_hip_set_cint8_dot(int mode) {
   if (mode < -1 || mode > 0) return QC_INVALID_ARGUMENT;
-  g_tuning.cint8_dot = mode;
+  g_knobs.cint8_dot.store(mode, std::memory_order_relaxed);
   return QC_OK;
 }
 
 int qc_hip_set_qgemm_fold(int mode) {
   if (mode < -1 || mode > 0) return QC_INVALID_ARGUMENT;
-  g_tuning.qgemm_fold = mode;
+  g_knobs.qgemm_fold.store(mode, std::memory_order_relaxed);
   return QC_OK;
 }
 
 int qc_hip_set_norm_sequential_sum(int on) {
-  g_norm_sequential = on != 0;
+  g_knobs.norm_sequential.store(on != 0, std::memory_order_relaxed);
   return QC_OK;
 }
 
 int qc_hip_set_int8_gemm_route(int route) {
   if (route < qc::kInt8Auto || route > qc::kInt8Simple) return QC_INVALID_ARGUMENT;
-  g_int8_route = route;
+  g_knobs.int8_route.store(route, std::memory_order_relaxed);
   return QC_OK;
 }
 

@@ -35,6 +35,17 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Orders one wavefront's LDS accesses across lanes (stores of some lanes
+// before loads of them by others, or loads before later stores): a fence at
+// wavefront scope plus a wave barrier.  The hardware already runs a wave's
+// LDS operations in order, so this emits no instruction; it keeps the
+// compiler from reordering the accesses.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 // LDS layout of one chunk of kc elements (kc a multiple of 64):
 //   [kc/64 pair records of kRec bytes][kc/32 int32 exponents e_b]
 //   [kc/32 f32 gates: 1, or NaN for a non-finite block][3 x kc/32 int32 digit sums]
@@ -147,6 +158,23 @@ __device__ __forceinline__ void read_digits(PairDigits& g, const uint8_t* lds, i
 
 __device__ __forceinline__ float combine(int s0, int s1, int s2) {
   return fmaf(static_cast<float>(s0), 16384.f, fmaf(static_cast<float>(s1), 128.f, static_cast<float>(s2)));
+}
+
+// An integral zero point z with |z| <= 2^16, as an int (false otherwise: NaN,
+// fractional or larger zero points keep the f32 form f - z * xs).
+__device__ __forceinline__ bool integral_zero(float z, int& zi) {
+  zi = __float2int_rn(z);   // saturates; NaN gives 0, which then differs from z
+  return static_cast<float>(zi) == z && zi >= -65536 && zi <= 65536;
+}
+
+// The affine block dot sum_j (c_j - z) x_j for an integral zero point, from
+// the code-digit sums sd[t] = sum_j c_j d_t,j and the digit-plane sums
+// ds[t] = sum_j d_t,j: each plane's sum_j (c_j - z) d_t,j = sd[t] - z ds[t] is
+// an exact int32 (|sd| <= 2^19, |z ds| <= 2^28), so a row or group whose codes
+// all equal z gives exactly 0, as the reference's per-element decode
+// scale * (code - zero) does.
+__device__ __forceinline__ float affine_block(const int (&sd)[3], const int (&ds)[3], int zi, int e) {
+  return ldexpf(combine(sd[0] - zi * ds[0], sd[1] - zi * ds[1], sd[2] - zi * ds[2]), e);
 }
 
 // The digit-plane sums of pair pl's two blocks: s[b][t] = sum_j d_t,j.

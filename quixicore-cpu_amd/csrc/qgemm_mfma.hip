@@ -1634,41 +1634,50 @@ hipError_t launch_qgemm_mfma(int fmt, const void* W, const float* x, float* y, i
 // held until the process ends.  Host code uses the address that
 // hipGetSymbolAddress returns for the current device (the array's name is
 // only a host-side handle).  Every no-allocation call on a GPU shares that
-// GPU's array, so such calls must not overlap on one GPU.  Nothing in it
-// has to start at zero: each call's prep kernels write every byte its GEMM
-// kernels read.
+// GPU's array.  A per-device host mutex is held from a call's first launch to
+// its last, so calls from several host threads on one stream queue their
+// launch sequences one after the other; calls on different streams of one GPU
+// can still overlap on the device and race.  Nothing in it has to start at
+// zero: each call's prep kernels write every byte its GEMM kernels read.
 static __device__ __align__(256) uint8_t noalloc_scratch[kQgemmNoAllocScratchBytes];
 
-static hipError_t noalloc_scratch_base(void** out) {
+struct NoAllocDevice {
+  void* base = nullptr;   // hipGetSymbolAddress of noalloc_scratch on this device
+  std::mutex call;        // held by one call's launch sequence
+};
+
+static hipError_t noalloc_device(NoAllocDevice** out) {
   static std::mutex mu;
-  static std::vector<void*> base;   // [device], resolved once per device
+  static std::vector<std::unique_ptr<NoAllocDevice>> devices;   // [device], resolved once
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lock(mu);
-  if (static_cast<int>(base.size()) <= dev) base.resize(dev + 1, nullptr);
-  if (base[dev] == nullptr) {
+  if (static_cast<int>(devices.size()) <= dev) devices.resize(dev + 1);
+  if (devices[dev] == nullptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
     if (e != hipSuccess) return e;
-    base[dev] = p;
+    devices[dev].reset(new NoAllocDevice);
+    devices[dev]->base = p;
   }
-  *out = base[dev];
+  *out = devices[dev].get();
   return hipSuccess;
 }
 
 hipError_t launch_qgemm_mfma_noalloc(int fmt, const void* W, const float* x, float* y, int m,
                                      int n, int k, hipStream_t s) {
-  void* base = nullptr;
-  const hipError_t e = noalloc_scratch_base(&base);
+  NoAllocDevice* d = nullptr;
+  const hipError_t e = noalloc_device(&d);
   if (e != hipSuccess) return e;
   Scratch scratch;
-  scratch.fixed = static_cast<uint8_t*>(base);
+  scratch.fixed = static_cast<uint8_t*>(d->base);
   // region 1: the row exponents; region 0: one pass's fragments and partials
   scratch.fixed_split = (sizeof(int) * static_cast<size_t>(m) + 256 + 255) / 256 * 256;
   scratch.fixed_bytes = kQgemmNoAllocScratchBytes;
   scratch.max_ks = 2;
   if (scratch.fixed_split >= scratch.fixed_bytes) return hipErrorOutOfMemory;
+  std::lock_guard<std::mutex> hold(d->call);   // until the call's last launch
   // passes of at most 32 rows: the panel route's fragments grow with m
   return qgemm_mfma_with(fmt, W, x, y, m, n, k, s, 0, 0, -1, scratch);
 }

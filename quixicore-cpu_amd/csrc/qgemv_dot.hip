@@ -343,9 +343,13 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
         if (t + WIN < T) issue(t + WIN);
         if constexpr (CHUNKED) {
           // the item's bytes into the wave's staging area, then this lane's pair
+          // (lanes read what other lanes stored: wave_lds_sync orders the
+          // previous item's reads before these stores, and the stores before
+          // this item's reads)
           uint8_t* const stage = lds + q8_stage_off(kc) + (threadIdx.x >> 6) * kQ8Item;
           int q0c, nbytes;
           span(j, q0c, nbytes);
+          wave_lds_sync();
           if (nbytes == kQ8Item) {   // a whole item (wave-uniform)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -363,6 +367,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
             if (4096 + 4 * lane < nbytes)
               *reinterpret_cast<uint32_t*>(stage + 4096 + 4 * lane) = w[t][16];
           }
+          wave_lds_sync();
           const uint32_t* rec =
               reinterpret_cast<const uint32_t*>(stage + (min(p, pend - 1) - q0c) * 68);
           if (p < pend) acc[r] = pair_dot<FMT>(rec, g, acc[r]);

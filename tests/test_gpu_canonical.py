@@ -284,3 +284,42 @@ def test_cint8_validation(qc, synth, dev):
     assert call(0, [qc.cint8_weights(C, None, None, 64, 128, 1)], x, 0, 1, [y], [0]) == 3
     torch.cuda.synchronize()
     assert np.all(y.cpu().numpy() == 3.0)
+
+
+@pytest.mark.parametrize("groups", [1, 32])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("fractional", [False, True])
+def test_cint8_affine_codes_at_zero_point(qc, oracle, synth, dev, groups, m, fractional):
+    """kInt8Affine rows (and groups) whose codes all equal the zero point
+    decode to exact zeros in the reference (scale * (code - zero),
+    kernels/quantization/qgemm_canonical.cpp:168-174), so such an output
+    row is exactly 0 -- the contract bound is 0 there -- and a zeroed group
+    adds nothing.  Integral zero points take the digit kernels' exact
+    integer form; fractional ones (no code can equal them) the f32 form,
+    checked against the same contract."""
+    import torch
+    rows, cols = 160, 4096
+    codes, scales, zeros = _tensor(synth, 313 + groups, rows, cols, groups, True)
+    if fractional:
+        zeros = (zeros + np.float32(0.375)).astype(np.float32)
+    z = zeros.reshape(rows, groups)
+    g = cols // groups
+    if not fractional:
+        for r in (3, 64, 159):                    # whole rows at their zero points
+            codes[r] = np.repeat(z[r], g).astype(np.int8)
+        if groups > 1:                            # one group of row 9
+            codes[9, 7 * g:8 * g] = np.int8(z[9, 7])
+    keep = [_dev(qc, dev, a) for a in (codes, scales, zeros)]
+    w = qc.cint8_weights(keep[0], keep[1], keep[2], rows, cols, groups)
+    x = synth.normal_fast(17 + m + groups, m * cols).reshape(m, cols)
+    print(f"cint8 affine at zero point groups={groups} m={m} fractional={fractional}", flush=True)
+    Y = torch.full((m, rows), float("nan"), dtype=torch.float32, device=dev)
+    assert qc.cint8_project_raw(0, [w], torch.from_numpy(x).to(dev), 0, m, [Y], [0]) == 0
+    yf = Y.cpu().numpy()
+    what = oracle.cint8_dequant(codes, scales, zeros, rows, cols, groups)
+    y64, wn = oracle.cint8_project_f64(x, what)
+    xn = np.linalg.norm(x.astype(np.float64), axis=1)[:, None]
+    assert np.all(np.abs(yf - y64) <= TOL * xn * wn[None, :])
+    if not fractional:
+        for r in (3, 64, 159):
+            assert np.all(yf[:, r] == 0.0), r

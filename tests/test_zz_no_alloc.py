@@ -90,3 +90,60 @@ def test_noalloc_rejects_beyond_limits(qc, dev):
     assert b"fixed scratch" in qc.lib.qc_hip_last_error()
     torch.cuda.synchronize()
     assert torch.all(y == 5.0) and torch.all(y2 == 5.0)
+
+
+def test_noalloc_threads_share_one_stream(qc, oracle, synth, dev):
+    """Several host threads calling the no-allocation entry on one stream at
+    once: the per-GPU lock queues each call's launch sequence (prep, GEMM,
+    reduce) as a whole, so every result is bit-identical to the same call
+    made alone, although all calls share the one fixed array."""
+    import threading
+
+    import torch
+    fmt, n, k = 0, 2048, 4096
+    print(f"qgemm_noalloc threads fmt={fmt} n={n} k={k}", flush=True)
+    w = synth.normal_fast(91, n * k, 0.02).reshape(n, k)
+    st, packed = oracle.pack(fmt, w)
+    assert st == 0
+    P = torch.from_numpy(packed).to(dev)
+    # digit mode (M=4, 6), dense tiles (M=24) and passes of 32 rows (M=40)
+    ms = (4, 6, 24, 40)
+    xs = {m: synth.normal_fast(990 + m, m * k).reshape(m, k) for m in ms}
+    X = {m: torch.from_numpy(xs[m]).to(dev) for m in ms}
+    stream = torch.cuda.Stream()          # default priority
+    alone = {}
+    for m in ms:
+        alone[m] = torch.full((m, n), float("nan"), device=dev)
+        assert qc.qgemm_noalloc_raw(fmt, P, X[m], alone[m], m, n, k, stream=stream.cuda_stream) == 0
+    torch.cuda.synchronize()
+    iters = 10
+    outs = {m: [torch.full((m, n), float("nan"), device=dev) for _ in range(iters)] for m in ms}
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(m):
+        try:
+            for i in range(iters):
+                stt = qc.qgemm_noalloc_raw(fmt, P, X[m], outs[m][i], m, n, k,
+                                           stream=stream.cuda_stream)
+                if stt != 0:
+                    errors.append((m, i, stt))
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append((m, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(m,)) for m in ms]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for m in ms:
+        want = alone[m].cpu().numpy()
+        for i in range(iters):
+            got = outs[m][i].cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, i)
+        y64, wn = oracle.qgemm_f64(fmt, packed, xs[m], n, k)
+        for r in (0, m - 1):
+            ok, worst = oracle.within_contract(want[r], y64[r], wn, xs[m][r], TOL)
+            assert ok, (m, r, worst)
