@@ -127,3 +127,14 @@ def test_product_does_not_reference_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 for needle in needles:
                     assert needle not in text, (f, needle)
+
+
+def test_integration_binding_is_the_compiled_one():
+    """The reference-side binding printed in INTEGRATION.md is the text of
+    tests/cpp/reference_binding.h, which reference_binding_check compiles
+    and tests/test_gpu_reference_binding.py runs: the document cannot drift
+    from the code that is tested."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    header = open(os.path.join(root, "tests", "cpp", "reference_binding.h")).read()
+    doc = open(os.path.join(root, "INTEGRATION.md")).read()
+    assert "```cpp\n" + header + "```\n" in doc
