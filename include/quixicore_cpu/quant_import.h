@@ -5,6 +5,9 @@
 // into device memory in CpuPackedWeights::prepare.
 //
 // Provided: the container, validate_canonical_quant_tensor,
+// quantize_canonical / dequantize_canonical for the two int8 layouts (on the
+// GPU quantizers and decode kernel; the other layouts return
+// kUnsupportedFormat after the reference's validation),
 // import_smoothquant_w8a8 and quant_import_provenance_name.  The AWQ, GPTQ,
 // AutoRound and BitNet importers of the reference build layouts other than
 // int8 (int4 / fp8 / fp4 / ternary), which this GPU path does not compute.
@@ -14,6 +17,7 @@
 #include <cstdint>
 #include <vector>
 
+#include "quixicore_cpu/float_storage.h"
 #include "quixicore_cpu/quant_contract.h"
 
 namespace quixicore_cpu {
@@ -42,6 +46,23 @@ struct CanonicalQuantTensor {
 };
 
 Status validate_canonical_quant_tensor(const CanonicalQuantTensor& tensor);
+
+// Canonical pack / unpack (reference :42-45,53-54;
+// kernels/quantization/quant_import_ref.cpp:552-681,717-838).
+// kInt8Symmetric: quantize_int8 with group_size (0 = one scale per row), codes
+// and f32 scales bit-identical to the reference's.  kInt8Affine (group_size 0
+// or columns): quantize_int8_asymmetric per row, integer zero points.  The
+// input may be f32, f16 or bf16 storage (decoded exactly), host or device
+// memory; the tensor's tables are host vectors.  Other layouts:
+// kUnsupportedFormat after the reference's checks (scale_2d is NVFP4's).
+Status quantize_canonical(FloatStorageInput input, long long rows, long long columns,
+                          CanonicalQuantLayout layout, long long group_size,
+                          CanonicalQuantTensor* tensor, bool scale_2d = false);
+// output[r][c] = scale * (code - zero) in f32, bit-identical to the
+// reference's decode, for the int8 layouts; output may be host or device
+// memory of exactly rows * columns floats.
+Status dequantize_canonical(const CanonicalQuantTensor& tensor, float* output,
+                            long long output_count);
 
 // SmoothQuant W8A8 export: int8 weights [rows, columns], one f32 scale per
 // output row, activation scales (and optionally zero points, for the AZP

@@ -196,6 +196,25 @@ int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void
                          int activation, const float* rope_cos, const float* rope_sin,
                          long long head_dim, void* stream);
 
+/* Decode of canonical int8 weights to f32 [rows][cols]:
+ * out[r][c] = scale(r, g) * (float(code[r][c]) - zero(r, g)), each step
+ * rounded in f32 (zero = 0 when w->zero_points is NULL), with
+ * g = group_index[c] when group_index is not NULL (a column -> group table of
+ * w->groups groups per row), else c / (cols / groups).  The int8 branch of
+ * dequantize_canonical (include/quixicore_cpu/quant_import.h:53-54;
+ * kernels/quantization/quant_import_ref.cpp:753-770).  Status: 1 when rows,
+ * cols or groups is not positive or, without a group index, groups does not
+ * divide cols; 3 for NULL codes, scales or out. */
+int qc_hip_cint8_dequantize(const qc_cint8_weights* w, const int* group_index, float* out,
+                            void* stream);
+
+/* out[i] = x[i] for i < count, decoded exactly from QC_STORAGE_F32 / F16 /
+ * BF16 (float_storage_to_f32, kernels/utils/float_storage_ref.cpp): the
+ * staging step of quantize_canonical's FloatStorageInput
+ * (kernels/quantization/quant_import_ref.cpp:154-172).  Status: 1 for
+ * count <= 0, 2 for an unknown type, 3 for NULL pointers. */
+int qc_hip_storage_to_f32(const void* x, int type, long long count, float* out, void* stream);
+
 /* Activation-quantizing GEMV: x is quantized per 32-element block to int8
  * (scale = max|x_b| / 127, round half to even, clamp +-127), each block dot is
  * an exact integer sum, and y[r] = sum_b (float(dot) * d_w) * d_x in block

@@ -366,6 +366,13 @@ class Reference:
         self.lib.qcref_storage_scenarios.argtypes = [ctypes.c_char_p]
         return self.lib.qcref_storage_scenarios(str(directory).encode())
 
+    def canonical_quant_scenarios(self, directory):
+        """Runs tests/cpp/canonical_quant_scenarios.h through the reference's
+        own quantize_canonical / dequantize_canonical, writing under
+        `directory`."""
+        self.lib.qcref_canonical_quant_scenarios.argtypes = [ctypes.c_char_p]
+        return self.lib.qcref_canonical_quant_scenarios(str(directory).encode())
+
     def pack(self, fmt, w):
         w = np.ascontiguousarray(w, dtype=np.float32)
         n, k = w.shape

@@ -16,6 +16,9 @@
 //   qgemv_qkv_rope_kv -> the public function (kernels/quantization/qgemv_fused_ref.cpp:342-443)
 //   qgemm_prepacked_*_storage -> the public functions (kernels/quantization/qgemm_canonical.cpp),
 //               run over tests/cpp/storage_scenarios.h
+//   quantize_canonical / dequantize_canonical -> the public functions
+//               (kernels/quantization/quant_import_ref.cpp), run over
+//               tests/cpp/canonical_quant_scenarios.h
 //   CpuPackedWeights::prepare (both overloads), info(), panel_data()
 //               -> src/memory/packed_weights.cpp:197-412
 #include <cstddef>
@@ -32,6 +35,7 @@
 #include "quixicore_cpu/quantization.h"
 #include "quixicore_cpu/threading.h"
 #include "../tests/cpp/storage_scenarios.h"
+#include "../tests/cpp/canonical_quant_scenarios.h"
 
 namespace qc = quixicore_cpu;
 
@@ -236,6 +240,16 @@ int qcref_storage_scenarios(const char* dir) {
   storage_scenarios::Sink sink(dir);
   if (sink.manifest == nullptr) return 1;
   storage_scenarios::run(sink);
+  return 0;
+}
+
+// The quantize_canonical / dequantize_canonical scenarios
+// (tests/cpp/canonical_quant_scenarios.h) through the reference's functions
+// (kernels/quantization/quant_import_ref.cpp:552-681,717-838).
+int qcref_canonical_quant_scenarios(const char* dir) {
+  storage_scenarios::Sink sink(dir);
+  if (sink.manifest == nullptr) return 2;
+  canonical_quant_scenarios::run(sink);
   return 0;
 }
 

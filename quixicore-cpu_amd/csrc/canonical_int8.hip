@@ -930,4 +930,61 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   return e != hipSuccess ? e : f;
 }
 
+// ---- Decode and storage conversion (model load / inspection, not the
+// projection path) -------------------------------------------------------
+
+namespace {
+
+// out[r][c] = scale(r, g) * (float(code[r][c]) - zero(r, g)): the int code
+// converted exactly, the zero point subtracted and the scale applied, each
+// rounded in f32 (kernels/quantization/quant_import_ref.cpp:753-770);
+// g = gidx[c] when a group index is given, else c / gsize.
+__global__ __launch_bounds__(kThreads) void cint8_dequant_kernel(
+    const int8_t* __restrict__ codes, const float* __restrict__ scales,
+    const float* __restrict__ zeros, const int* __restrict__ gidx, long long rows, long long cols,
+    long long groups, long long gsize, float* __restrict__ out) {
+  const long long total = rows * cols;
+  const long long step = static_cast<long long>(gridDim.x) * kThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+       i += step) {
+    const long long r = i / cols, c = i - r * cols;
+    const long long si = r * groups + (gidx != nullptr ? gidx[c] : c / gsize);
+    const float z = zeros != nullptr ? zeros[si] : 0.0f;
+    out[i] = scales[si] * (static_cast<float>(codes[i]) - z);
+  }
+}
+
+// f16 / bf16 / f32 storage to f32, exactly (float_storage_to_f32 of
+// kernels/utils/float_storage_ref.cpp).
+__global__ __launch_bounds__(kThreads) void storage_to_f32_kernel(const void* __restrict__ x,
+                                                                  int type, long long count,
+                                                                  float* __restrict__ out) {
+  const long long step = static_cast<long long>(gridDim.x) * kThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+       i += step)
+    out[i] = load_x(x, i, type);
+}
+
+unsigned elementwise_grid(long long count) {
+  const long long blocks = (count + kThreads - 1) / kThreads;
+  return static_cast<unsigned>(std::min<long long>(std::max<long long>(blocks, 1), 256LL * 16));
+}
+
+}  // namespace
+
+hipError_t launch_cint8_dequant(const int8_t* codes, const float* scales, const float* zeros,
+                                const int* group_index, long long rows, long long cols,
+                                long long groups, long long group_size, float* out,
+                                hipStream_t s) {
+  cint8_dequant_kernel<<<elementwise_grid(rows * cols), kThreads, 0, s>>>(
+      codes, scales, zeros, group_index, rows, cols, groups, group_size, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_storage_to_f32(const void* x, int type, long long count, float* out,
+                                 hipStream_t s) {
+  storage_to_f32_kernel<<<elementwise_grid(count), kThreads, 0, s>>>(x, type, count, out);
+  return hipGetLastError();
+}
+
 }  // namespace qc

@@ -566,6 +566,30 @@ int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void
   return finish(qc::launch_cint8(L, as_stream(stream)));
 }
 
+// The int8 branch of dequantize_canonical
+// (kernels/quantization/quant_import_ref.cpp:753-770).  The caller (the
+// drop-in) has run the reference's tensor validation; this checks what the
+// kernel relies on.
+int qc_hip_cint8_dequantize(const qc_cint8_weights* w, const int* group_index, float* out,
+                            void* stream) {
+  if (w == nullptr) return QC_INVALID_ARGUMENT;
+  if (!valid_product({w->rows, w->cols}) || w->groups < 1 ||
+      (group_index == nullptr && w->cols % w->groups != 0))
+    return QC_INVALID_SHAPE;
+  if (w->codes == nullptr || w->scales == nullptr || out == nullptr) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_cint8_dequant(w->codes, w->scales, w->zero_points, group_index,
+                                         w->rows, w->cols, w->groups, w->cols / w->groups, out,
+                                         as_stream(stream)));
+}
+
+int qc_hip_storage_to_f32(const void* x, int type, long long count, float* out, void* stream) {
+  if (count <= 0) return QC_INVALID_SHAPE;
+  if (type != QC_STORAGE_F32 && type != QC_STORAGE_F16 && type != QC_STORAGE_BF16)
+    return QC_UNSUPPORTED_FORMAT;
+  if (x == nullptr || out == nullptr) return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_storage_to_f32(x, type, count, out, as_stream(stream)));
+}
+
 // src/dispatch/qgemv_w8a8.cpp:108-125 (qgemv_w8a8_packed_size).
 int qc_hip_qgemv_w8a8_packed_size(int format, long long n, long long k, long long* bytes) {
   size_t size = 0;

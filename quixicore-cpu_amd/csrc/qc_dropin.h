@@ -54,6 +54,8 @@ class Staging {
   const void* in(const void* host_or_device, std::size_t bytes);
   void* out(void* host_or_device, std::size_t bytes);
   void* inout(void* host_or_device, std::size_t bytes);
+  // Device memory for the call's own use (freed with the staging).
+  void* scratch(std::size_t bytes) { return device(bytes); }
   Status finish(int capi_status);
   Status finish_written(int capi_status);
   Status status() const { return status_; }

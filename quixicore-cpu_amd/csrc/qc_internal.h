@@ -111,6 +111,17 @@ struct CInt8Launch {
 };
 hipError_t launch_cint8(const CInt8Launch& launch, hipStream_t s);
 
+// out[r][c] = scales[si] * (float(codes[r][c]) - zeros[si]) (zeros may be
+// NULL), si = r * groups + (group_index ? group_index[c] : c / group_size).
+hipError_t launch_cint8_dequant(const int8_t* codes, const float* scales, const float* zeros,
+                                const int* group_index, long long rows, long long cols,
+                                long long groups, long long group_size, float* out,
+                                hipStream_t s);
+
+// out[i] = x[i] decoded from QC_STORAGE_F32 / F16 / BF16, exactly.
+hipError_t launch_storage_to_f32(const void* x, int type, long long count, float* out,
+                                 hipStream_t s);
+
 // Per-group symmetric int8 quantization.  status == nullptr: caller has
 // already verified that x is finite.  Otherwise non-finite groups are left
 // unwritten and *status is set to 3 (kInvalidArgument).

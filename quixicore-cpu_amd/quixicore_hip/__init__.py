@@ -68,6 +68,8 @@ _SIGS = {
     "qc_hip_set_qgemm_fold": ([_I], _I),
     "qc_hip_set_cint8_dot": ([_I], _I),
     "qc_hip_stream_read": ([_P, _LL, _P, _I, _P], _I),
+    "qc_hip_cint8_dequantize": ([_P, _P, _P, _P], _I),
+    "qc_hip_storage_to_f32": ([_P, _I, _LL, _P, _P], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -168,6 +170,17 @@ def cint8_project_raw(mode, weights, x, x_type, m, ys, y_types, bias=None, activ
     return lib.qc_hip_cint8_project(mode, arr, len(weights), _ptr(x), x_type, m, yp, yt,
                                     _ptr(bias), activation, _ptr(rope_cos), _ptr(rope_sin),
                                     head_dim, _stream(stream))
+
+
+def cint8_dequantize_raw(weights, out, group_index=None, stream=None):
+    """qc_hip_cint8_dequantize: weights a CInt8Weights, out f32 [rows][cols]."""
+    return lib.qc_hip_cint8_dequantize(ctypes.byref(weights), _ptr(group_index), _ptr(out),
+                                       _stream(stream))
+
+
+def storage_to_f32_raw(x, x_type, count, out, stream=None):
+    """qc_hip_storage_to_f32: x of STORAGE type x_type, out f32 [count]."""
+    return lib.qc_hip_storage_to_f32(_ptr(x), x_type, count, _ptr(out), _stream(stream))
 
 
 def qgemm_raw(fmt, packed, x, y, m, n, k, stream=None):

@@ -43,7 +43,8 @@ def test_cpp_dropin_symbols_exported():
                 "quixicore_cpu::rms_norm_add_quant_int8(",
                 "quixicore_cpu::quantize_int8_asymmetric(",
                 "quixicore_cpu::dequantize_int8_asymmetric(",
-                "quixicore_cpu::Workspace::allocate("):
+                "quixicore_cpu::Workspace::allocate(", "quixicore_cpu::quantize_canonical(",
+                "quixicore_cpu::dequantize_canonical("):
         assert sym in out, sym
 
 
