@@ -8,6 +8,7 @@
 #include "quixicore_cpu/ops.h"
 #include "quixicore_cpu/packed_weights.h"
 #include "quixicore_cpu/qgemv.h"
+#include "quixicore_cpu/quant_import.h"
 #include "quixicore_cpu/workspace.h"
 
 namespace quixicore_cpu {
@@ -78,6 +79,19 @@ Status qgemm_prepacked_swiglu_storage(const CpuPackedWeights& gate_weights,
 Status qgemv_prepacked_swiglu_storage(const CpuPackedWeights& gate_weights,
                                       const CpuPackedWeights& up_weights, FloatStorageInput x,
                                       FloatStorageOutput output, Workspace* workspace = nullptr);
+
+// qgemm.h:118-127 -- canonical activations (e.g. from quantize_canonical)
+// projected against canonical prepared weights: activation [M, K] codes,
+// f32 y [M, N] (host or device memory).  Computed on the GPU for int8
+// weights x int8 activations (kInt8Symmetric / kInt8Affine, row or group
+// scales); other pairs return kUnsupportedFormat after the reference's
+// validation.  qgemv_prepacked_quantized requires M = 1.
+Status qgemm_prepacked_quantized(const CpuPackedWeights& weights,
+                                 const CanonicalQuantTensor& activation, float* y,
+                                 Workspace* workspace = nullptr);
+Status qgemv_prepacked_quantized(const CpuPackedWeights& weights,
+                                 const CanonicalQuantTensor& activation, float* y,
+                                 Workspace* workspace = nullptr);
 
 // qgemm.h:235 -- prequantized integer GEMM, X token-major [M,K], W [N,K].
 Status int8_gemm(const std::int8_t* weights, const std::int8_t* x, const float* weight_scale,

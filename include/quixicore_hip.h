@@ -196,6 +196,22 @@ int qc_hip_cint8_project(int mode, const qc_cint8_weights* w, int nw, const void
                          int activation, const float* rope_cos, const float* rope_sin,
                          long long head_dim, void* stream);
 
+/* y[m][n] = sum_c w(n, c) * a(m, c) for canonical int8 weights w ([n][cols])
+ * and canonical int8 activations a (a->rows = m, a->cols = w->cols), both
+ * decoded as scale * (code - zero): the int8 x int8 case of
+ * qgemm_prepacked_quantized / qgemv_prepacked_quantized
+ * (include/quixicore_cpu/qgemm.h:118-127; kernels/quantization/
+ * qgemm_canonical.cpp:5415-5507).  Symmetric weights with one scale per row,
+ * against activations with one scale per row and either no zero points or
+ * integer ones also passed as a_int_zero_points (int [m]), run as the int8
+ * MFMA GEMM: exact int32 dot, minus z * sum_c code_w(n, c) in int64, then
+ * (float * scale_w[n]) * scale_a[m].  Any other combination (group scales,
+ * affine weights, fractional activation zero points) is decoded in f32 and
+ * accumulated by FMA, one wave per output.  Status: 1 shapes (non-positive
+ * dims, groups not dividing cols, a->cols != w->cols), 3 NULL pointers. */
+int qc_hip_cint8_quantized_gemm(const qc_cint8_weights* w, const qc_cint8_weights* a,
+                                const int* a_int_zero_points, float* y, void* stream);
+
 /* Decode of canonical int8 weights to f32 [rows][cols]:
  * out[r][c] = scale(r, g) * (float(code[r][c]) - zero(r, g)), each step
  * rounded in f32 (zero = 0 when w->zero_points is NULL), with

@@ -965,6 +965,52 @@ __global__ __launch_bounds__(kThreads) void storage_to_f32_kernel(const void* __
     out[i] = load_x(x, i, type);
 }
 
+// y[m][n] = sum_c w(n, c) * a(m, c), each operand decoded as
+// scale * (float(code) - zero) in f32, the products accumulated per lane with
+// explicit FMAs and summed across the wave: the general canonical int8 x
+// int8 projection (group scales, affine weights, activation zero points that
+// are not integers), one wave per output.
+__global__ __launch_bounds__(kThreads) void cint8_dual_generic(
+    const int8_t* __restrict__ wc, const float* __restrict__ ws, const float* __restrict__ wz,
+    long long wgroups, const int8_t* __restrict__ ac, const float* __restrict__ as,
+    const float* __restrict__ az, long long agroups, long long m, long long n, long long k,
+    float* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const long long waves = static_cast<long long>(gridDim.x) * kWaves;
+  const long long wgs = k / wgroups, ags = k / agroups;
+  for (long long o = static_cast<long long>(blockIdx.x) * kWaves + (threadIdx.x >> 6); o < m * n;
+       o += waves) {
+    const long long mi = o / n, ni = o - mi * n;
+    const int8_t* wr = wc + ni * k;
+    const int8_t* ar = ac + mi * k;
+    float acc = 0.0f;
+    for (long long c = lane; c < k; c += 64) {
+      const long long gw = ni * wgroups + c / wgs, ga = mi * agroups + c / ags;
+      const float wv = ws[gw] * (static_cast<float>(wr[c]) - (wz != nullptr ? wz[gw] : 0.0f));
+      const float av = as[ga] * (static_cast<float>(ar[c]) - (az != nullptr ? az[ga] : 0.0f));
+      acc = fmaf(wv, av, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[o] = acc;
+  }
+}
+
+// out[r] = sum_c codes[r][c] in int32 (exact for cols < 2^24), one wave per row.
+__global__ __launch_bounds__(kThreads) void cint8_row_sums(const int8_t* __restrict__ codes,
+                                                           long long rows, long long cols,
+                                                           int32_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const long long waves = static_cast<long long>(gridDim.x) * kWaves;
+  for (long long r = static_cast<long long>(blockIdx.x) * kWaves + (threadIdx.x >> 6); r < rows;
+       r += waves) {
+    const int8_t* row = codes + r * cols;
+    int sum = 0;
+    for (long long c = lane; c < cols; c += 64) sum += row[c];
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if (lane == 0) out[r] = sum;
+  }
+}
+
 unsigned elementwise_grid(long long count) {
   const long long blocks = (count + kThreads - 1) / kThreads;
   return static_cast<unsigned>(std::min<long long>(std::max<long long>(blocks, 1), 256LL * 16));
@@ -979,6 +1025,38 @@ hipError_t launch_cint8_dequant(const int8_t* codes, const float* scales, const 
   cint8_dequant_kernel<<<elementwise_grid(rows * cols), kThreads, 0, s>>>(
       codes, scales, zeros, group_index, rows, cols, groups, group_size, out);
   return hipGetLastError();
+}
+
+hipError_t launch_cint8_dual(const qc_cint8_weights& w, const qc_cint8_weights& a,
+                             const int* a_int_zero_points, float* y, int int8_route,
+                             hipStream_t s) {
+  const long long m = a.rows, n = w.rows, k = w.cols;
+  const bool mfma = w.zero_points == nullptr && w.groups == 1 && a.groups == 1 &&
+                    (a.zero_points == nullptr || a_int_zero_points != nullptr);
+  if (!mfma) {
+    const long long waves = m * n;
+    const unsigned grid = static_cast<unsigned>(
+        std::min<long long>((waves + kWaves - 1) / kWaves, 256LL * 64));
+    cint8_dual_generic<<<grid, kThreads, 0, s>>>(w.codes, w.scales, w.zero_points, w.groups,
+                                                 a.codes, a.scales, a.zero_points, a.groups, m,
+                                                 n, k, y);
+    return hipGetLastError();
+  }
+  if (a.zero_points == nullptr)
+    return launch_int8_gemm(w.codes, a.codes, w.scales, a.scales, nullptr, nullptr, y, nullptr,
+                            m, n, k, false, nullptr, s, int8_route);
+  // affine activations: dot - z * row_sum(w), the weights' row sums summed here
+  int32_t* sums = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&sums), sizeof(int32_t) * n, s);
+  if (e != hipSuccess) return e;
+  const unsigned grid = static_cast<unsigned>(std::min<long long>((n + kWaves - 1) / kWaves, 4096));
+  cint8_row_sums<<<grid, kThreads, 0, s>>>(w.codes, n, k, sums);
+  e = hipGetLastError();
+  if (e == hipSuccess)
+    e = launch_int8_gemm(w.codes, a.codes, w.scales, a.scales, sums, a_int_zero_points, y,
+                         nullptr, m, n, k, true, nullptr, s, int8_route);
+  const hipError_t f = hipFreeAsync(sums, s);
+  return e != hipSuccess ? e : f;
 }
 
 hipError_t launch_storage_to_f32(const void* x, int type, long long count, float* out,

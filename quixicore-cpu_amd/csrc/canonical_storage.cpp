@@ -13,7 +13,9 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cmath>
 #include <initializer_list>
+#include <vector>
 
 #include "qc_dropin.h"
 #include "quixicore_cpu/qgemm.h"
@@ -344,6 +346,85 @@ Status qgemv_prepacked_qkv_rope_kv_storage(
   if (g.status() != Status::kOk) return g.status();
   return g.finish(qc_hip_cint8_project(2, w, nw, xd, type_id(x.type), 1, ys, yt, nullptr, 0, cd,
                                        sd, head_dim, g.stream()));
+}
+
+// qgemm_canonical.cpp:5415-5433 (qgemm_prepacked_quantized): the prepared
+// weights, the activation tensor, its layout, then K and the output.  This
+// route then computes int8 weights against int8 activations with row,
+// channel or group scales (others: kUnsupportedFormat).  Integer activation
+// zero points are passed as ints too, which lets symmetric row-scaled
+// weights take the int8 MFMA GEMM (qc_hip_cint8_quantized_gemm).
+Status qgemm_prepacked_quantized(const CpuPackedWeights& weights,
+                                 const CanonicalQuantTensor& activation, float* y,
+                                 Workspace* workspace) {
+  CpuPackedWeightsInfo info;
+  Status st = validate_prepared(weights, &info);
+  if (st != Status::kOk) return st;
+  st = validate_canonical_quant_tensor(activation);
+  if (st != Status::kOk) return st;
+  const QuantTensorMetadata& am = activation.metadata;
+  if (am.layout == CanonicalQuantLayout::kTurboQuantKey ||
+      am.layout == CanonicalQuantLayout::kTurboQuantValue)
+    return Status::kUnsupportedFormat;
+  const long long m = am.logical_rows;
+  if (am.logical_columns != info.columns) return Status::kInvalidShape;
+  if (!valid_product({m, info.rows}) || y == nullptr) return Status::kInvalidArgument;
+  qc_cint8_weights w{};
+  if ((st = device_weights(weights, info, &w)) != Status::kOk) return st;
+  const bool int8 = am.layout == CanonicalQuantLayout::kInt8Symmetric ||
+                    am.layout == CanonicalQuantLayout::kInt8Affine;
+  const bool row_like = am.scale_mode == QuantScaleMode::kRow ||
+                        am.scale_mode == QuantScaleMode::kChannel ||
+                        am.scale_mode == QuantScaleMode::kGroup;
+  if (!int8 || !row_like || !activation.group_index.empty() || !activation.act_order.empty())
+    return Status::kUnsupportedFormat;
+  long long agroups = 1;
+  if (am.scale_mode == QuantScaleMode::kGroup) {
+    agroups = static_cast<long long>(am.scale_count) / m;
+    if (agroups < 1 || am.logical_columns % agroups != 0) return Status::kUnsupportedFormat;
+  }
+  const std::size_t elements = static_cast<std::size_t>(m) * static_cast<std::size_t>(info.columns);
+  // zero points that are all integers in int range also go as ints
+  std::vector<int> int_zeros;
+  const bool affine = am.layout == CanonicalQuantLayout::kInt8Affine;
+  if (affine && agroups == 1) {
+    int_zeros.reserve(activation.zero_points.size());
+    for (const float z : activation.zero_points) {
+      if (!(z >= -2147483648.0f && z < 2147483648.0f) || z != std::nearbyint(z)) {
+        int_zeros.clear();
+        break;
+      }
+      int_zeros.push_back(static_cast<int>(z));
+    }
+  }
+  detail::WorkspaceFrame frame(workspace);
+  detail::Staging g(workspace);
+  qc_cint8_weights a{};
+  a.codes = static_cast<const int8_t*>(g.in(activation.data.data(), elements));
+  a.scales = static_cast<const float*>(
+      g.in(activation.scales.data(), activation.scales.size() * sizeof(float)));
+  a.zero_points = affine ? static_cast<const float*>(g.in(
+                               activation.zero_points.data(),
+                               activation.zero_points.size() * sizeof(float)))
+                         : nullptr;
+  a.rows = m;
+  a.cols = info.columns;
+  a.groups = agroups;
+  const int* zi = int_zeros.empty()
+                      ? nullptr
+                      : static_cast<const int*>(g.in(int_zeros.data(), int_zeros.size() * sizeof(int)));
+  float* yd = static_cast<float*>(
+      g.out(y, sizeof(float) * static_cast<std::size_t>(m) * static_cast<std::size_t>(info.rows)));
+  if (g.status() != Status::kOk) return g.status();
+  return g.finish(qc_hip_cint8_quantized_gemm(&w, &a, zi, yd, g.stream()));
+}
+
+// qgemm_canonical.cpp:5502-5507.
+Status qgemv_prepacked_quantized(const CpuPackedWeights& weights,
+                                 const CanonicalQuantTensor& activation, float* y,
+                                 Workspace* workspace) {
+  if (activation.metadata.logical_rows != 1) return Status::kInvalidShape;
+  return qgemm_prepacked_quantized(weights, activation, y, workspace);
 }
 
 }  // namespace quixicore_cpu

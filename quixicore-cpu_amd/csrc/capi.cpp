@@ -582,6 +582,20 @@ int qc_hip_cint8_dequantize(const qc_cint8_weights* w, const int* group_index, f
                                          as_stream(stream)));
 }
 
+int qc_hip_cint8_quantized_gemm(const qc_cint8_weights* w, const qc_cint8_weights* a,
+                                const int* a_int_zero_points, float* y, void* stream) {
+  if (w == nullptr || a == nullptr) return QC_INVALID_ARGUMENT;
+  if (!valid_product({w->rows, w->cols}) || !valid_product({a->rows, a->cols}) ||
+      !valid_product({a->rows, w->rows}) || a->cols != w->cols || w->groups < 1 ||
+      a->groups < 1 || w->cols % w->groups != 0 || a->cols % a->groups != 0)
+    return QC_INVALID_SHAPE;
+  if (w->codes == nullptr || w->scales == nullptr || a->codes == nullptr ||
+      a->scales == nullptr || y == nullptr)
+    return QC_INVALID_ARGUMENT;
+  return finish(qc::launch_cint8_dual(*w, *a, a_int_zero_points, y, int8_route(),
+                                      as_stream(stream)));
+}
+
 int qc_hip_storage_to_f32(const void* x, int type, long long count, float* out, void* stream) {
   if (count <= 0) return QC_INVALID_SHAPE;
   if (type != QC_STORAGE_F32 && type != QC_STORAGE_F16 && type != QC_STORAGE_BF16)

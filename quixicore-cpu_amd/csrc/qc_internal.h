@@ -118,6 +118,16 @@ hipError_t launch_cint8_dequant(const int8_t* codes, const float* scales, const 
                                 long long groups, long long group_size, float* out,
                                 hipStream_t s);
 
+// y[m][n] = sum_c w(n, c) * a(m, c) over canonical int8 weights w and
+// activations a (a.rows = m), both decoded as scale * (code - zero).  Symmetric
+// row-scaled weights against row-scaled activations whose zero points are
+// integers (given as a_int_zero_points, or none) run as the int8 MFMA GEMM
+// (exact int32 dot, dot - z * row_sum in int64, then (float * ws[n]) * as[m]);
+// anything else as f32 decode and FMA accumulation, one wave per output.
+hipError_t launch_cint8_dual(const qc_cint8_weights& w, const qc_cint8_weights& a,
+                             const int* a_int_zero_points, float* y, int int8_route,
+                             hipStream_t s);
+
 // out[i] = x[i] decoded from QC_STORAGE_F32 / F16 / BF16, exactly.
 hipError_t launch_storage_to_f32(const void* x, int type, long long count, float* out,
                                  hipStream_t s);

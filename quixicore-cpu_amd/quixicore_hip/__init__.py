@@ -69,6 +69,7 @@ _SIGS = {
     "qc_hip_set_cint8_dot": ([_I], _I),
     "qc_hip_stream_read": ([_P, _LL, _P, _I, _P], _I),
     "qc_hip_cint8_dequantize": ([_P, _P, _P, _P], _I),
+    "qc_hip_cint8_quantized_gemm": ([_P, _P, _P, _P, _P], _I),
     "qc_hip_storage_to_f32": ([_P, _I, _LL, _P, _P], _I),
 }
 for _name, (_args, _res) in _SIGS.items():
@@ -176,6 +177,12 @@ def cint8_dequantize_raw(weights, out, group_index=None, stream=None):
     """qc_hip_cint8_dequantize: weights a CInt8Weights, out f32 [rows][cols]."""
     return lib.qc_hip_cint8_dequantize(ctypes.byref(weights), _ptr(group_index), _ptr(out),
                                        _stream(stream))
+
+
+def cint8_quantized_gemm_raw(weights, activation, y, a_int_zero_points=None, stream=None):
+    """qc_hip_cint8_quantized_gemm: weights / activation CInt8Weights, y f32 [m][n]."""
+    return lib.qc_hip_cint8_quantized_gemm(ctypes.byref(weights), ctypes.byref(activation),
+                                           _ptr(a_int_zero_points), _ptr(y), _stream(stream))
 
 
 def storage_to_f32_raw(x, x_type, count, out, stream=None):

@@ -10,6 +10,9 @@
 // Names starting with "other_" use layouts this GPU path does not compute:
 // only their statuses are written (the reference's validation results must
 // match; where the reference computes, this path returns kUnsupportedFormat).
+// Names starting with "proj_" are qgemm_prepacked_quantized /
+// qgemv_prepacked_quantized outputs (f32 sums, not bit-identical across the
+// two libraries) and the decoded operands they are checked against.
 #pragma once
 
 #include <cmath>
@@ -20,6 +23,9 @@
 #include <vector>
 
 #include "quixicore_cpu/float_storage.h"
+#include "quixicore_cpu/packed_weights.h"
+#include "quixicore_cpu/qgemm.h"
+#include "quixicore_cpu/qgemv.h"
 #include "quixicore_cpu/quant_import.h"
 #include "storage_scenarios.h"
 
@@ -90,7 +96,98 @@ inline void round_trip(Sink& sink, const std::string& name, qc::FloatStorageInpu
   sink.data(name + "_dequant", out.data(), out.size() * 4, "f32");
 }
 
+// qgemm_prepacked_quantized / qgemv_prepacked_quantized
+// (qgemm_canonical.cpp:5415-5507): int8 weights (symmetric rows, symmetric
+// groups of 128, affine rows) against int8 activations (symmetric rows,
+// symmetric groups of 64, affine rows), every pair, plus the validation cases.
+inline void projections(Sink& sink) {
+  const long long n = 96, k = 512, m = 5;
+  const std::vector<float> wf = matrix(0x77, n, k);
+  const std::vector<float> af = matrix(0x99, m, k);
+  struct Op {
+    const char* name;
+    L layout;
+    long long group;
+  };
+  const Op wops[] = {{"wsym", L::kInt8Symmetric, 0}, {"wsymg", L::kInt8Symmetric, 128},
+                     {"waff", L::kInt8Affine, 0}};
+  const Op aops[] = {{"asym", L::kInt8Symmetric, 0}, {"asymg", L::kInt8Symmetric, 64},
+                     {"aaff", L::kInt8Affine, 0}};
+  qc::CpuPackedWeights prepared[3];
+  qc::CanonicalQuantTensor acts[3];
+  for (int i = 0; i < 3; ++i) {
+    qc::CanonicalQuantTensor t;
+    const std::string nm = std::string("proj_") + wops[i].name;
+    sink.status(nm, qc::quantize_canonical({wf.data(), qc::FloatStorageType::kF32, n * k}, n, k,
+                                           wops[i].layout, wops[i].group, &t));
+    std::vector<float> dec(static_cast<size_t>(n * k));
+    sink.status(nm + "_dequant", qc::dequantize_canonical(t, dec.data(), n * k));
+    sink.data(nm + "_dequant", dec.data(), dec.size() * 4, "f32");
+    sink.status(nm + "_prepare", prepared[i].prepare(t));
+  }
+  for (int j = 0; j < 3; ++j) {
+    const std::string nm = std::string("proj_") + aops[j].name;
+    sink.status(nm, qc::quantize_canonical({af.data(), qc::FloatStorageType::kF32, m * k}, m, k,
+                                           aops[j].layout, aops[j].group, &acts[j]));
+    std::vector<float> dec(static_cast<size_t>(m * k));
+    sink.status(nm + "_dequant", qc::dequantize_canonical(acts[j], dec.data(), m * k));
+    sink.data(nm + "_dequant", dec.data(), dec.size() * 4, "f32");
+  }
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      const std::string nm = std::string("proj_") + wops[i].name + "_" + aops[j].name;
+      std::vector<float> y(static_cast<size_t>(m * n), 7.0f);
+      sink.status(nm, qc::qgemm_prepacked_quantized(prepared[i], acts[j], y.data()));
+      sink.data(nm + "_y", y.data(), y.size() * 4, "f32");
+    }
+  // M = 1: the first activation row alone
+  for (int j = 0; j < 3; ++j) {
+    qc::CanonicalQuantTensor one;
+    const std::string nm = std::string("proj_gemv_") + aops[j].name;
+    sink.status(nm + "_source", qc::quantize_canonical({af.data(), qc::FloatStorageType::kF32, k},
+                                                       1, k, aops[j].layout, aops[j].group, &one));
+    std::vector<float> y(static_cast<size_t>(n), 7.0f);
+    sink.status(nm, qc::qgemv_prepacked_quantized(prepared[0], one, y.data()));
+    sink.data(nm + "_y", y.data(), y.size() * 4, "f32");
+  }
+  // validation: rows for the GEMV form, K, output, readiness, GGUF weights
+  std::vector<float> y(static_cast<size_t>(m * n), 7.0f);
+  sink.status("proj_gemv_rows5", qc::qgemv_prepacked_quantized(prepared[0], acts[0], y.data()));
+  qc::CanonicalQuantTensor narrow;
+  sink.status("proj_narrow_source",
+              qc::quantize_canonical({af.data(), qc::FloatStorageType::kF32, m * 256}, m, 256,
+                                     L::kInt8Symmetric, 0, &narrow));
+  sink.status("proj_k_mismatch", qc::qgemm_prepacked_quantized(prepared[0], narrow, y.data()));
+  sink.status("proj_null_y", qc::qgemm_prepacked_quantized(prepared[0], acts[0], nullptr));
+  qc::CpuPackedWeights empty;
+  sink.status("proj_unprepared", qc::qgemm_prepacked_quantized(empty, acts[0], y.data()));
+  std::size_t bytes = 0;
+  (void)qc::qgemv_packed_size(qc::QuantFormat::kQ8_0, n, k, &bytes);
+  std::vector<uint8_t> gguf(bytes);
+  sink.status("proj_gguf_pack", qc::qgemv_pack(qc::QuantFormat::kQ8_0, wf.data(), n, k, gguf.data()));
+  qc::CpuPackedWeights gw;
+  sink.status("proj_gguf_prepare", gw.prepare(qc::QuantFormat::kQ8_0, gguf.data(), n, k));
+  sink.status("proj_gguf_weights", qc::qgemm_prepacked_quantized(gw, acts[0], y.data()));
+  qc::CanonicalQuantTensor bad = acts[0];
+  bad.scales.pop_back();
+  sink.status("proj_invalid_activation", qc::qgemm_prepacked_quantized(prepared[0], bad, y.data()));
+  sink.data("proj_untouched", y.data(), y.size() * 4, "f32");
+  // an fp8 activation tensor (one tensor scale): computed by the reference only
+  qc::CanonicalQuantTensor f8;
+  f8.metadata.layout = L::kFP8E4M3FN;
+  f8.metadata.logical_rows = m;
+  f8.metadata.logical_columns = k;
+  f8.metadata.scale_mode = qc::QuantScaleMode::kTensor;
+  f8.metadata.scale_encoding = qc::QuantScaleEncoding::kFP32;
+  f8.metadata.scale_count = 1;
+  f8.data.assign(static_cast<size_t>(m * k), 0x38);
+  f8.scales.assign(1, 0.5f);
+  sink.status("other_proj_fp8_activation", qc::qgemm_prepacked_quantized(prepared[0], f8, y.data()));
+}
+
 inline void run(Sink& sink) {
+  projections(sink);
+
   const long long rows = 48, cols = 256;
   const size_t n = static_cast<size_t>(rows * cols);
   const std::vector<float> x = matrix(0x5eed, rows, cols);

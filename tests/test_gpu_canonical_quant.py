@@ -1,12 +1,17 @@
 """GPU: quantize_canonical / dequantize_canonical for the canonical int8
 layouts (include/quixicore_cpu/quant_import.h:42-45,53-54;
-kernels/quantization/quant_import_ref.cpp:552-681,717-838).
+kernels/quantization/quant_import_ref.cpp:552-681,717-838), and the
+canonical W8A8 projections qgemm_prepacked_quantized /
+qgemv_prepacked_quantized over them (include/quixicore_cpu/qgemm.h:118-127;
+kernels/quantization/qgemm_canonical.cpp:5415-5507).
 
 * The scenario list of tests/cpp/canonical_quant_scenarios.h runs through this
   library's C++ drop-in (quixicore-cpu_amd/lib/canonical_quant_check, host
   buffers) and through the reference's own functions (oracle/_ref).  Every
   status must be equal, and every int8 tensor table (codes, scales, zero
-  points, metadata) and decoded output byte-identical.  For the layouts this
+  points, metadata) and decoded output byte-identical; the projections of
+  every int8 weight x activation pair meet the 1e-4 normalised contract
+  against the f64 product of the decoded operands.  For the layouts this
   GPU path does not compute ("other_" scenarios), the reference's validation
   failures must be the same and where the reference computes, this library
   returns kUnsupportedFormat (2).
@@ -61,10 +66,34 @@ def test_canonical_quant_scenarios_match_reference(qc, ref, tmp_path):
     computed = [n for n, v in s_ref.items() if v == 0 and not n.startswith("other_")]
     assert len(computed) >= 16
     for name in d_ref:
+        if name.startswith("proj_") and name.endswith("_y"):
+            continue                      # f32 sums: checked against the contract below
         assert d_ours[name] == d_ref[name], name
     # the int8 round trips did run and produced data
     assert len(d_ref["sym_row_f32_codes"]) == 48 * 256
     assert len(d_ref["aff_row_f16_zeros"]) == 48 * 4
+    # qgemm_prepacked_quantized / qgemv_prepacked_quantized: both libraries'
+    # outputs against the f64 product of the decoded operands (byte-identical
+    # in both runs, checked above), |y - y64| <= 1e-4 * ||a_row|| * ||w_row||
+    n, k, m = 96, 512, 5
+    f32 = lambda name: np.frombuffer(d_ours[name], dtype=np.float32)   # noqa: E731
+    pairs = 0
+    for wname in ("wsym", "wsymg", "waff"):
+        w = f32(f"proj_{wname}_dequant").reshape(n, k).astype(np.float64)
+        wn = np.linalg.norm(w, axis=1)
+        for aname in ("asym", "asymg", "aaff"):
+            a = f32(f"proj_{aname}_dequant").reshape(m, k).astype(np.float64)
+            y64 = a @ w.T
+            bound = 1e-4 * np.linalg.norm(a, axis=1)[:, None] * wn[None, :]
+            for d in (d_ours, d_ref):
+                y = np.frombuffer(d[f"proj_{wname}_{aname}_y"], dtype=np.float32).reshape(m, n)
+                assert np.all(np.abs(y - y64) <= bound), (wname, aname, d is d_ours)
+            if wname == "wsym":
+                y = np.frombuffer(d_ours[f"proj_gemv_{aname}_y"], dtype=np.float32)
+                assert np.all(np.abs(y - y64[0]) <= bound[0]), ("gemv", aname)
+            pairs += 1
+    assert pairs == 9
+    assert np.all(np.frombuffer(d_ours["proj_untouched"], dtype=np.float32) == 7.0)
 
 
 @pytest.mark.parametrize("affine,groups,fractional", [(False, 1, False), (False, 8, False),
@@ -126,3 +155,77 @@ def test_new_entry_validation(qc, dev):
     assert qc.cint8_dequantize_raw(qc.cint8_weights(c, None, None, 8, 8, 1), t) == 3
     assert qc.cint8_dequantize_raw(ok, None) == 3
     assert qc.cint8_dequantize_raw(ok, t) == 0
+
+
+@pytest.mark.parametrize("m,n,k,affine", [(512, 4096, 4096, False), (512, 4096, 4096, True),
+                                          (1, 14336, 4096, False), (70, 300, 1024, True)])
+def test_quantized_gemm_mfma_route_is_int8_gemm(qc, oracle, synth, dev, m, n, k, affine):
+    """Symmetric row-scaled weights x row-scaled activations (no zero points,
+    or integer ones): qc_hip_cint8_quantized_gemm gives exactly int8_gemm's
+    bits on the same codes and scales (the AZP form with the weights' row
+    sums for affine activations), which the int8 GEMM tests pin bit for bit
+    against the reference."""
+    import torch
+    print(f"cint8 quantized gemm mfma m={m} n={n} k={k} affine={affine}", flush=True)
+    st, wq, ws = oracle.quantize_int8(synth.normal_fast(71 + n, n * k, 0.02).reshape(n, k))
+    x = synth.activations_outliers_fast(3, m, k)
+    W, WS = torch.from_numpy(wq).to(dev), torch.from_numpy(ws[:, 0].copy()).to(dev)
+    if affine:
+        codes, scales, zps = qc.quantize_int8_asymmetric(torch.from_numpy(x).to(dev))
+        zf = zps.float()
+    else:
+        codes, scales = qc.quantize_int8(torch.from_numpy(x).to(dev))
+        scales = scales[:, 0].contiguous()
+        zps, zf = None, None
+    w = qc.cint8_weights(W, WS, None, n, k, 1)
+    a = qc.cint8_weights(codes, scales, zf, m, k, 1)
+    y = torch.full((m, n), 7.0, device=dev)
+    assert qc.cint8_quantized_gemm_raw(w, a, y, zps) == 0
+    rs = W.to(torch.int32).sum(dim=1).to(torch.int32) if affine else None
+    want = qc.int8_gemm(W, codes, WS, scales, rs, zps, affine)
+    assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+
+
+@pytest.mark.parametrize("wgroups,waffine,agroups,aaffine,int_zeros",
+                         [(8, False, 1, False, False), (1, True, 1, False, False),
+                          (1, False, 4, True, False), (1, False, 1, True, False),
+                          (16, True, 2, True, False)])
+def test_quantized_gemm_generic_route(qc, oracle, dev, wgroups, waffine, agroups, aaffine,
+                                      int_zeros):
+    """Group scales, affine weights or activation zero points given only as
+    floats: the f32 decode-and-FMA kernel, against the f64 product of the
+    exactly decoded operands within the 1e-4 normalised contract."""
+    import torch
+    m, n, k = 9, 700, 2048
+    print(f"cint8 quantized gemm generic wg={wgroups} wa={waffine} ag={agroups} aa={aaffine}",
+          flush=True)
+    rng = np.random.default_rng(wgroups * 7 + agroups)
+    wc = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    ac = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    wsc = (rng.random(n * wgroups, dtype=np.float32) * 1e-2 + 1e-5).astype(np.float32)
+    asc = (rng.random(m * agroups, dtype=np.float32) * 1e-1 + 1e-4).astype(np.float32)
+    wz = rng.integers(-20, 21, n * wgroups).astype(np.float32) if waffine else None
+    az = rng.integers(-20, 21, m * agroups).astype(np.float32) if aaffine else None
+    T = lambda a: None if a is None else torch.from_numpy(a).to(dev)   # noqa: E731
+    keep = [T(wc), T(wsc), T(wz), T(ac), T(asc), T(az)]
+    w = qc.cint8_weights(keep[0], keep[1], keep[2], n, k, wgroups)
+    a = qc.cint8_weights(keep[3], keep[4], keep[5], m, k, agroups)
+    y = torch.full((m, n), 7.0, device=dev)
+    assert qc.cint8_quantized_gemm_raw(w, a, y) == 0
+    wh = oracle.cint8_dequant(wc, wsc, wz, n, k, wgroups).astype(np.float64)
+    ah = oracle.cint8_dequant(ac, asc, az, m, k, agroups).astype(np.float64)
+    y64 = ah @ wh.T
+    bound = 1e-4 * np.linalg.norm(ah, axis=1)[:, None] * np.linalg.norm(wh, axis=1)[None, :]
+    assert np.all(np.abs(y.cpu().numpy() - y64) <= bound)
+
+
+def test_quantized_gemm_validation(qc, dev):
+    import torch
+    t = torch.zeros(64, device=dev)
+    c = torch.zeros(64, dtype=torch.int8, device=dev)
+    w = qc.cint8_weights(c, t, None, 8, 8, 1)
+    assert qc.cint8_quantized_gemm_raw(w, qc.cint8_weights(c, t, None, 2, 16, 1), t) == 1
+    assert qc.cint8_quantized_gemm_raw(w, qc.cint8_weights(c, t, None, 0, 8, 1), t) == 1
+    assert qc.cint8_quantized_gemm_raw(w, qc.cint8_weights(c, t, None, 2, 8, 3), t) == 1
+    assert qc.cint8_quantized_gemm_raw(w, qc.cint8_weights(None, t, None, 2, 8, 1), t) == 3
+    assert qc.cint8_quantized_gemm_raw(w, qc.cint8_weights(c, t, None, 2, 8, 1), None) == 3
