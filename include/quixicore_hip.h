@@ -365,12 +365,16 @@ int qc_hip_set_qgemm_panel(int mode);
  * 1 = always.  Tuning and test knob with no reference counterpart. */
 int qc_hip_set_qgemm_rows(int mode);
 
-/* Canonical int8 projections (qc_hip_cint8_project), any number of
- * activation rows: 0 (default) = the kernels with exact int8 digit dots (the
- * GEMV's encoding of x) where it applies (K % 64 == 0, codes 16-byte aligned,
- * row scales or groups of >= 32 columns), -1 = always the f32 multiply-add
- * kernel.  Both stay within the contract tolerance.  Tuning and test knob
- * with no reference counterpart. */
+/* Canonical int8 projections (qc_hip_cint8_project): 0 (default) = three or
+ * more activation rows with one scale per weight row run on the row-plane
+ * route (three int8 digit planes of each activation row under one row
+ * exponent, the int8 MFMA GEMM, an exact int64 combination; K % 32 == 0,
+ * K <= 16384, codes 16-byte aligned, not the RoPE mode), everything else on
+ * the kernels with exact int8 digit dots per 32-element block (the GEMV's
+ * encoding of x) where they apply (K % 64 == 0, codes 16-byte aligned, row
+ * scales or groups of >= 32 columns); 1 = never the row-plane route; -1 =
+ * always the f32 multiply-add kernel.  All stay within the contract
+ * tolerance.  Tuning and test knob with no reference counterpart. */
 int qc_hip_set_cint8_dot(int mode);
 
 /* Small-batch MFMA kernels with int8 digit activations (2 <= m <= 8 per

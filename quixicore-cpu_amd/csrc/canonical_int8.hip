@@ -845,6 +845,271 @@ hipError_t launch_mb(const CSegs& sg, bool grp, bool aff, const void* x, int xty
 
 }  // namespace
 
+// ---- Row-plane route: two or more activation rows, one scale per weight row
+//
+// Every activation row m is encoded once as 22-bit fixed point under one
+// exponent for the whole row: e(m) = frexp(max_k |x[m][k]|) - 21 and
+// q = rint(x * 2^-e), clamped to [-2^21, 2^21 - 1], split into three int8
+// planes q = 2^14 d0 + 2^7 d1 + d2 (d0 in [-128, 127], d1, d2 in [0, 127])
+// that are rows 3m + t of an int8 matrix [3M][K].  The int8 MFMA GEMM
+// (launch_int8_gemm, the W8A8 kernels) gives the exact int32 sums
+// D_t[m][n] = sum_k code[n][k] d_t[m][k] of all planes in one launch per
+// matrix; the finish kernel forms 2^14 D0 + 2^7 D1 + D2 exactly in int64
+// (minus z (2^14 S0 + 2^7 S1 + S2), S_t = sum_k d_t[m][k], for an integral
+// zero point z), rounds it once to f32 and scales it by 2^e and the row's
+// scale, then runs the shared epilogue.  Each x is held to within
+// 2^-21 max_k |x_m|, so |y - y_exact| <= sqrt(K) 2^-21 ||x_m|| ||w_hat_n||:
+// 3.1e-5 at K = 4096 and 6.1e-5 at K = 16384 after the contract's
+// normalisation.  A row holding NaN or +-inf is computed in f32 from the
+// codes and x instead (the reference's result class).
+namespace {
+
+constexpr int kPlanesMaxK = 16384;
+constexpr int kPlanesChunkM = 1024;     // activation rows per pass: bounds the scratch
+constexpr int kPlanesMinM = 3;     // M = 2: 22 us on the digit-dot kernel against 32 us here (N=14336, K=4096)
+constexpr int kPlanesNonfinite = 0x40000000;
+
+// Workgroup reductions of the prep kernel: the maximum of one float and the
+// sums of three ints, each with one LDS round.
+__device__ __forceinline__ float block_max(float v, float* red) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+
+__device__ __forceinline__ void block_sum3(int (&v)[3], int (*red)[kWaves]) {
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    for (int off = 32; off > 0; off >>= 1) v[t] += __shfl_xor(v[t], off);
+    if ((threadIdx.x & 63) == 0) red[t][threadIdx.x >> 6] = v[t];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    int r = red[t][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) r += red[t][w];
+    v[t] = r;
+  }
+}
+
+// Four consecutive activations of row xr at column c (16-byte loads for
+// aligned f32 rows).
+__device__ __forceinline__ void load4(const void* x, long long xr, int c, int xtype, bool vec,
+                                      float (&v)[4]) {
+  if (vec) {
+    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + xr + c);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = load_x(x, xr + c + i, xtype);
+  }
+}
+
+// One workgroup per activation row (x rows blockIdx.x, ldx apart).  A row
+// holding NaN or +-inf gets the maximum +inf, zero digits and the flag
+// exponent kPlanesNonfinite.
+__global__ __launch_bounds__(kThreads) void cint8_planes_prep(const void* __restrict__ x, int xtype,
+                                                              long long ldx, int k, bool vec,
+                                                              int8_t* __restrict__ planes,
+                                                              int* __restrict__ rexp,
+                                                              int* __restrict__ dsum) {
+  __shared__ float fred[kWaves];
+  __shared__ int ired[3][kWaves];
+  const int m = blockIdx.x;
+  const long long xr = static_cast<long long>(m) * ldx;
+  float mx = 0.0f;
+  for (int c = 4 * static_cast<int>(threadIdx.x); c < k; c += 4 * kThreads) {
+    float v[4];
+    load4(x, xr, c, xtype, vec, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, isfinite(v[i]) ? fabsf(v[i]) : INFINITY);
+  }
+  mx = block_max(mx, fred);
+  const bool bad = !isfinite(mx);
+  int ex = 0;
+  (void)frexpf(mx, &ex);                       // mx < 2^ex
+  const int e = ex - 21;
+  int sum[3] = {0, 0, 0};
+  int8_t* p0 = planes + (3LL * m) * k;
+  for (int c = 4 * static_cast<int>(threadIdx.x); c < k; c += 4 * kThreads) {
+    float v[4];
+    load4(x, xr, c, xtype, vec, v);
+    uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int q = bad ? 0 : __float2int_rn(ldexpf(v[i], -e));
+      q = q > 2097151 ? 2097151 : q;
+      const int d0 = q >> 14, d1 = (q >> 7) & 127, d2 = q & 127;
+      sum[0] += d0;
+      sum[1] += d1;
+      sum[2] += d2;
+      w0 |= static_cast<uint32_t>(d0 & 0xFF) << (8 * i);
+      w1 |= static_cast<uint32_t>(d1) << (8 * i);
+      w2 |= static_cast<uint32_t>(d2) << (8 * i);
+    }
+    *reinterpret_cast<uint32_t*>(p0 + c) = w0;
+    *reinterpret_cast<uint32_t*>(p0 + k + c) = w1;
+    *reinterpret_cast<uint32_t*>(p0 + 2LL * k + c) = w2;
+  }
+  block_sum3(sum, ired);
+  if (threadIdx.x == 0) {
+    rexp[m] = bad ? kPlanesNonfinite : e;
+    dsum[3 * m] = sum[0];
+    dsum[3 * m + 1] = sum[1];
+    dsum[3 * m + 2] = sum[2];
+  }
+}
+
+struct PlaneAcc {
+  const int32_t* acc[3];   // per matrix: [3 mc][rows]
+  int rows[3];
+};
+
+// One matrix of the finish kernel, as plain values: the kernel reads its
+// argument tables into locals with constant indices and selects by value
+// (indexing an argument array, or taking its address, moves the whole
+// argument to private memory in every thread).
+struct PlaneMat {
+  const int8_t* w;
+  const float* scale;
+  const float* zero;
+  const int32_t* acc;
+  long long rows;
+};
+
+// Projection of activation row (m0 + mm) on row n of one matrix.
+__device__ __forceinline__ float plane_value(const int8_t* w, const float* scale, const float* zp,
+                                             const int32_t* a, long long r, int n, int mm, int m0,
+                                             const int* rexp, const int* dsum, const void* x,
+                                             int xtype, long long ldx, int k) {
+  const int e = rexp[mm];
+  const float sc = scale[n];
+  if (e == kPlanesNonfinite) {        // the reference's f32 form, block by block
+    const int8_t* codes = w + static_cast<long long>(n) * k;
+    const long long xr = static_cast<long long>(m0 + mm) * ldx;
+    const float z = zp != nullptr ? zp[n] : 0.0f;
+    float acc = 0.0f;
+    for (int b = 0; b < k; b += 32) acc += cint8_block_f32(codes + b, x, xr + b, xtype, z);
+    return sc * acc;
+  }
+  // 2^14 D0 + 2^7 D1 + D2 (|D_t| < 2^26 for K <= 16384) and the zero-point
+  // term are integers below 2^53: exact in double, then rounded once to f32
+  const double d = fma(static_cast<double>(a[(3LL * mm) * r + n]), 16384.0,
+                       fma(static_cast<double>(a[(3LL * mm + 1) * r + n]), 128.0,
+                           static_cast<double>(a[(3LL * mm + 2) * r + n])));
+  float f;
+  if (zp != nullptr) {
+    const double sx = fma(static_cast<double>(dsum[3 * mm]), 16384.0,
+                          fma(static_cast<double>(dsum[3 * mm + 1]), 128.0,
+                              static_cast<double>(dsum[3 * mm + 2])));
+    int zi;
+    if (integral_zero(zp[n], zi)) {
+      f = static_cast<float>(fma(-static_cast<double>(zi), sx, d));   // exact: |z sx| < 2^52
+    } else {
+      f = fmaf(-zp[n], static_cast<float>(sx), static_cast<float>(d));
+    }
+  } else {
+    f = static_cast<float>(d);
+  }
+  return sc * ldexpf(f, e);
+}
+
+// One thread per (activation row, output unit): activation row blockIdx.y,
+// unit blockIdx.x * kThreads + threadIdx.x -- mode 0 a logical row (matrix
+// by the segment starts), mode 1 a gate / up pair.  The stores are the
+// shared epilogue's (bias and activation on matrix 0; SiLU(gate) * up).
+__global__ __launch_bounds__(kThreads) void cint8_planes_finish(
+    const CSegs sg, const PlaneAcc pa, const int* __restrict__ rexp, const int* __restrict__ dsum,
+    const void* __restrict__ x, int xtype, long long ldx, int m0, int k) {
+  const int mm = blockIdx.y;
+  const int m = m0 + mm;
+  const int u = static_cast<int>(blockIdx.x) * kThreads + static_cast<int>(threadIdx.x);
+  const PlaneMat t0{sg.w[0], sg.scale[0], sg.zero[0], pa.acc[0], pa.rows[0]};
+  const PlaneMat t1{sg.w[1], sg.scale[1], sg.zero[1], pa.acc[1], pa.rows[1]};
+  const PlaneMat t2{sg.w[2], sg.scale[2], sg.zero[2], pa.acc[2], pa.rows[2]};
+  if (sg.mode == 1) {
+    if (u >= t0.rows) return;
+    const float gate = plane_value(t0.w, t0.scale, t0.zero, t0.acc, t0.rows, u, mm, m0, rexp,
+                                   dsum, x, xtype, ldx, k);
+    const float up = plane_value(t1.w, t1.scale, t1.zero, t1.acc, t1.rows, u, mm, m0, rexp,
+                                 dsum, x, xtype, ldx, k);
+    const float silu = gate / (1.0f + expf(-gate));
+    store_y(sg.y[0], m * sg.ld[0] + u, sg.ytype[0], silu * up);
+    return;
+  }
+  const int nseg = sg.nseg, s1 = sg.start[1], s2 = sg.start[2];
+  const int total = nseg == 1 ? s1 : nseg == 2 ? s2 : sg.start[3];
+  if (u >= total) return;
+  const int seg = (nseg > 2 && u >= s2) ? 2 : (nseg > 1 && u >= s1) ? 1 : 0;
+  const PlaneMat t = seg == 0 ? t0 : seg == 1 ? t1 : t2;
+  const int row = u - (seg == 2 ? s2 : seg == 1 ? s1 : 0);
+  float v = plane_value(t.w, t.scale, t.zero, t.acc, t.rows, row, mm, m0, rexp, dsum, x, xtype,
+                        ldx, k);
+  if (seg == 0 && (sg.bias != nullptr || sg.act != 0)) {
+    if (sg.bias != nullptr) v += sg.bias[row];
+    v = linear_activation(v, sg.act);
+  }
+  void* const y = seg == 0 ? sg.y[0] : seg == 1 ? sg.y[1] : sg.y[2];
+  const long long ld = seg == 0 ? sg.ld[0] : seg == 1 ? sg.ld[1] : sg.ld[2];
+  const int yt = seg == 0 ? sg.ytype[0] : seg == 1 ? sg.ytype[1] : sg.ytype[2];
+  store_y(y, m * ld + row, yt, v);
+}
+
+size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
+hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hipStream_t s) {
+  const int nmat = L.mode == 1 ? 2 : L.nw;
+  const size_t es = L.xtype == QC_STORAGE_F32 ? 4 : 2;
+  for (int m0 = 0; m0 < m; m0 += kPlanesChunkM) {
+    const int mc = std::min(kPlanesChunkM, m - m0);
+    size_t bytes = up256(3ull * mc * k) + up256(4ull * mc) + up256(12ull * mc);
+    for (int i = 0; i < nmat; ++i) bytes += up256(12ull * mc * static_cast<size_t>(L.w[i].rows));
+    uint8_t* base = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&base), bytes, s);
+    if (e != hipSuccess) return e;
+    int8_t* planes = reinterpret_cast<int8_t*>(base);
+    int* rexp = reinterpret_cast<int*>(base + up256(3ull * mc * k));
+    int* dsum = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rexp) + up256(4ull * mc));
+    uint8_t* cur = reinterpret_cast<uint8_t*>(dsum) + up256(12ull * mc);
+    PlaneAcc pa{};
+    const void* xc = static_cast<const uint8_t*>(L.x) + es * static_cast<size_t>(m0) * L.ldx;
+    const bool vec = L.xtype == QC_STORAGE_F32 && reinterpret_cast<uintptr_t>(L.x) % 16 == 0 &&
+                     L.ldx % 4 == 0;
+    cint8_planes_prep<<<mc, kThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, planes, rexp, dsum);
+    e = hipGetLastError();
+    for (int i = 0; i < nmat && e == hipSuccess; ++i) {
+      int32_t* acc = reinterpret_cast<int32_t*>(cur);
+      cur += up256(12ull * mc * static_cast<size_t>(L.w[i].rows));
+      pa.acc[i] = acc;
+      pa.rows[i] = static_cast<int>(L.w[i].rows);
+      e = launch_int8_gemm(L.w[i].codes, planes, nullptr, nullptr, nullptr, nullptr, nullptr, acc,
+                           3LL * mc, L.w[i].rows, k, false, nullptr, s);
+    }
+    if (e == hipSuccess) {
+      const long long units = L.mode == 1 ? L.w[0].rows : sg.start[sg.nseg];
+      const dim3 grid(static_cast<unsigned>((units + kThreads - 1) / kThreads),
+                      static_cast<unsigned>(mc));
+      cint8_planes_finish<<<grid, kThreads, 0, s>>>(sg, pa, rexp, dsum, L.x, L.xtype, L.ldx, m0,
+                                                    k);
+      e = hipGetLastError();
+    }
+    const hipError_t f = hipFreeAsync(base, s);
+    if (e != hipSuccess) return e;
+    if (f != hipSuccess) return f;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
 // Host entry (all checks done by the caller): see CInt8Launch in qc_internal.h.
 hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   CSegs sg{};
@@ -885,6 +1150,11 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   bool fast = k % 16 == 0 && (!grp || (sg.gsize >= 16 && (1 << sg.gshift) == sg.gsize));
   for (int i = 0; i < L.nw; ++i)
     fast = fast && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
+  // Two or more activation rows with one scale per weight row: the digit
+  // planes on the int8 MFMA GEMM (row-plane route above).
+  if (fast && L.dot == 0 && L.mode != 2 && !grp && m >= kPlanesMinM && k % 32 == 0 &&
+      k <= kPlanesMaxK)
+    return launch_planes(sg, L, m, k, s);
   // Exact digit dots over 64-column block pairs, two rows per wave, passes of
   // up to four activation rows
   // (M = 1, K=4096, 14336 rows: 13.9 us against 15.3 / 16.6 us with 4 / 8

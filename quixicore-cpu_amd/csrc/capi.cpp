@@ -724,7 +724,7 @@ int qc_hip_set_qgemm_rows(int mode) {
 }
 
 int qc_hip_set_cint8_dot(int mode) {
-  if (mode < -1 || mode > 0) return QC_INVALID_ARGUMENT;
+  if (mode < -1 || mode > 1) return QC_INVALID_ARGUMENT;
   g_knobs.cint8_dot.store(mode, std::memory_order_relaxed);
   return QC_OK;
 }

@@ -107,7 +107,8 @@ struct CInt8Launch {
   const float* rope_cos = nullptr;
   const float* rope_sin = nullptr;
   int rows_per_wave = 0;        // 2, 4 or (M = 1 digit kernel) 8; 0: from the shape
-  int dot = 0;                  // M = 1 digit-dot kernel: 0 where it applies, -1 never
+  int dot = 0;                  // 0: row-plane route (M >= 2) / digit-dot kernels where they
+                                // apply; 1: digit-dot kernels only; -1: the f32 kernel
 };
 hipError_t launch_cint8(const CInt8Launch& launch, hipStream_t s);
 

@@ -74,9 +74,11 @@ def _dev(qc, dev, arr, offset=0):
     (4096, 4096, 32, True, 1, 0, -1),
     (1000, 14336, 1, True, 1, 0, 0),      # affine channel scales, K in 4 chunks
     (600, 4096, 128, True, 1, 0, 0),      # groups of 32
-    (4096, 14336, 1, False, 2, 0, 0),     # 2-4 rows: digit dots, codes loaded once per pass
+    (4096, 14336, 1, False, 2, 0, 1),     # 2-4 rows: digit dots, codes loaded once per pass
+    (4096, 14336, 1, False, 3, 0, 0),     # 3 rows: the row-plane route (int8 MFMA)
     (2048, 4096, 32, True, 3, 0, 0),      # affine groups of 128, 3 rows
-    (1000, 14336, 1, True, 4, 0, 0),      # affine channel scales, 4 rows, K in 4 chunks
+    (1000, 14336, 1, True, 4, 0, 1),      # affine channel scales, 4 rows, K in 4 chunks
+    (1000, 14336, 1, True, 4, 0, 0),      # the same on the row-plane route
     (1000, 14336, 1, True, 4, 0, -1),     # the same on the f32 multiply-add kernel
     (600, 4096, 128, True, 2, 0, 0),      # groups of 32, 2 rows
     (1024, 4096, 64, False, 7, 0, 0),     # passes of 4 activation rows
@@ -184,7 +186,8 @@ def test_cint8_nonfinite_activations(qc, oracle, synth, dev, groups, affine, x_t
 @pytest.mark.parametrize("groups,affine,x_type,m", [(1, False, 0, 2), (1, True, 0, 3), (32, True, 2, 4),
                                                     (32, False, 1, 4)])
 def test_cint8_rows_match_one_row(qc, oracle, synth, dev, groups, affine, x_type, m):
-    """2-4 activation rows on the digit-dot kernel: every output row is
+    """2-4 activation rows on the digit-dot kernel (forced: row scales would
+    take the row-plane route by default): every output row is
     bit-identical to the one-row call on that row (same digits, order and
     finish), finite rows and rows holding +-inf or NaN alike."""
     import torch
@@ -205,7 +208,11 @@ def test_cint8_rows_match_one_row(qc, oracle, synth, dev, groups, affine, x_type
         X = torch.from_numpy(_bf16_bits(xs).view(np.int16).copy()).to(dev)
     print(f"cint8 rows vs one row groups={groups} affine={affine} x_type={x_type} m={m}", flush=True)
     Y = torch.empty((m, rows), dtype=torch.float32, device=dev)
-    assert qc.cint8_project_raw(0, [w], X, x_type, m, [Y], [0]) == 0
+    qc.set_cint8_dot(1)                       # the digit-dot kernels, not the row-plane route
+    try:
+        assert qc.cint8_project_raw(0, [w], X, x_type, m, [Y], [0]) == 0
+    finally:
+        qc.set_cint8_dot(0)
     Y = Y.cpu().numpy()
     for r in range(m):
         y1 = torch.empty(rows, dtype=torch.float32, device=dev)
@@ -323,3 +330,168 @@ def test_cint8_affine_codes_at_zero_point(qc, oracle, synth, dev, groups, m, fra
     if not fractional:
         for r in (3, 64, 159):
             assert np.all(yf[:, r] == 0.0), r
+
+
+def _planes_case(qc, oracle, synth, dev, rows, cols, m, affine, seed, fractional=False):
+    codes, scales, zeros = _tensor(synth, seed, rows, cols, 1, affine)
+    if fractional:
+        zeros = (zeros + np.float32(0.25)).astype(np.float32)
+    keep = [_dev(qc, dev, a) for a in (codes, scales, zeros)]
+    w = qc.cint8_weights(keep[0], keep[1], keep[2], rows, cols, 1)
+    what = oracle.cint8_dequant(codes, scales, zeros, rows, cols, 1)
+    return w, keep, what
+
+
+def _check_contract(y, x, what):
+    y64, wn = oracle_f64(x, what)
+    xn = np.linalg.norm(x.astype(np.float64), axis=1)[:, None]
+    bound = TOL * xn * wn[None, :]
+    err = np.abs(y.astype(np.float64) - y64)
+    assert np.all(err <= bound), float(np.max(err / np.maximum(bound, 1e-300))) * TOL
+
+
+def oracle_f64(x, what):
+    w = what.astype(np.float64)
+    return np.asarray(x, np.float64) @ w.T, np.linalg.norm(w, axis=1)
+
+
+@pytest.mark.parametrize("rows,cols,m,affine,fractional", [
+    (14336, 4096, 16, False, False),      # decoder shape, symmetric channel scales
+    (14336, 4096, 16, True, False),       # affine, integral zero points (exact int64 form)
+    (4096, 4096, 64, True, True),         # fractional zero points (f32 form)
+    (4096, 14336, 8, False, False),       # long K (down projection)
+    (300, 16384, 5, True, False),         # the largest K of the route
+    (1000, 2048, 512, False, False),      # prefill
+    (130, 512, 1100, True, False),        # two passes of 1024 activation rows
+    (70, 96, 3, False, False),            # K = 96: not a multiple of 64
+])
+def test_cint8_row_plane_route_contract(qc, oracle, synth, dev, rows, cols, m, affine,
+                                        fractional):
+    """The row-plane route (activation digit planes on the int8 MFMA GEMM,
+    an exact int64 combination): every output of sampled activation rows
+    within the 1e-4 normalised contract of the f64 product over the exactly
+    decoded weights, and the same call on the digit-dot / f32 kernels within
+    the same bound of it."""
+    import torch
+    print(f"cint8 planes rows={rows} cols={cols} m={m} affine={affine} frac={fractional}",
+          flush=True)
+    w, keep, what = _planes_case(qc, oracle, synth, dev, rows, cols, m, affine, 31 + m, fractional)
+    x = synth.normal_fast(900 + m, m * cols).reshape(m, cols)
+    x[0] *= np.float32(1e-30)                 # a tiny row and a huge one: per-row exponents
+    if m > 2:
+        x[2] *= np.float32(1e25)
+    X = torch.from_numpy(x).to(dev)
+    Y = torch.full((m, rows), 7.0, device=dev)
+    assert qc.cint8_project_raw(0, [w], X, 0, m, [Y], [0]) == 0
+    Y = Y.cpu().numpy()
+    sample = sorted({0, 1, m // 2, m - 1, min(2, m - 1)})
+    _check_contract(Y[sample], x[sample], what)
+    qc.set_cint8_dot(1)
+    try:
+        Z = torch.full((m, rows), 7.0, device=dev)
+        assert qc.cint8_project_raw(0, [w], X, 0, m, [Z], [0]) == 0
+    finally:
+        qc.set_cint8_dot(0)
+    _check_contract(Z.cpu().numpy()[sample], x[sample], what)
+
+
+def test_cint8_row_plane_route_epilogues(qc, oracle, synth, dev):
+    """The row-plane route's epilogues at M = 6: three matrices with their
+    own output types, bias + GELU on one matrix, SwiGLU over gate / up, and
+    f16 / bf16 activations; each against the f32 outputs of the digit-dot
+    kernels' plain projection within the contract (fused forms: against the
+    f64 epilogue of those projections within a few f32 ulp)."""
+    import torch
+    m, cols = 6, 4096
+    mats = [_planes_case(qc, oracle, synth, dev, r, cols, m, a, 70 + i)
+            for i, (r, a) in enumerate(((512, False), (256, False), (256, False)))]
+    x = synth.normal_fast(77, m * cols).reshape(m, cols)
+    X = torch.from_numpy(x).to(dev)
+    print("cint8 planes epilogues m=6", flush=True)
+    ys = [torch.empty((m, r), dtype=torch.int16 if t else torch.float32, device=dev)
+          for r, t in ((512, 0), (256, 1), (256, 2))]
+    assert qc.cint8_project_raw(0, [w for w, _, _ in mats], X, 0, m, ys, [0, 1, 2]) == 0
+    for (w, _, what), yv, t in zip(mats, ys, (0, 1, 2)):
+        plain = torch.empty((m, what.shape[0]), device=dev)
+        assert qc.cint8_project_raw(0, [w], X, 0, m, [plain], [0]) == 0
+        p = plain.cpu().numpy()
+        _check_contract(p, x, what)
+        got = yv.cpu().numpy()
+        if t == 1:
+            assert np.array_equal(got.view(np.uint16), p.astype(np.float16).view(np.uint16))
+        elif t == 2:
+            assert np.array_equal(got.view(np.uint16), _bf16_bits(p))
+        else:
+            assert np.array_equal(got.view(np.uint32), p.view(np.uint32))
+    # bias + GELU-tanh on one matrix
+    w, _, what = mats[0]
+    bias = torch.from_numpy(synth.normal_fast(5, 512)).to(dev)
+    yb = torch.empty((m, 512), device=dev)
+    assert qc.cint8_project_raw(0, [w], X, 0, m, [yb], [0], bias=bias, activation=2) == 0
+    plain = torch.empty((m, 512), device=dev)
+    assert qc.cint8_project_raw(0, [w], X, 0, m, [plain], [0]) == 0
+    v = plain.cpu().numpy().astype(np.float64) + bias.cpu().numpy()[None, :]
+    want = oracle.linear_activation_f64(v, 2)
+    assert np.allclose(yb.cpu().numpy(), want, rtol=1e-5, atol=1e-6)
+    # SwiGLU over two matrices of the same shape
+    g, gk, gwhat = _planes_case(qc, oracle, synth, dev, 256, cols, m, True, 91)
+    u, uk, uwhat = _planes_case(qc, oracle, synth, dev, 256, cols, m, True, 92)
+    out = torch.empty((m, 256), device=dev)
+    assert qc.cint8_project_raw(1, [g, u], X, 0, m, [out], [0]) == 0
+    pg, pu = torch.empty((m, 256), device=dev), torch.empty((m, 256), device=dev)
+    assert qc.cint8_project_raw(0, [g, u], X, 0, m, [pg, pu], [0, 0]) == 0
+    gv = pg.cpu().numpy().astype(np.float64)
+    want = gv / (1.0 + np.exp(-gv)) * pu.cpu().numpy().astype(np.float64)
+    assert np.allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-6)
+    # 16-bit activations decode exactly: the f32 call on the decoded values
+    for t in (1, 2):
+        if t == 1:
+            xh = x.astype(np.float16)
+            Xt = torch.from_numpy(xh.view(np.int16).copy()).to(dev)
+            xd = xh.astype(np.float32)
+        else:
+            xb = _bf16_bits(x)
+            Xt = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+            xd = (xb.astype(np.uint32) << 16).view(np.float32).reshape(m, cols)
+        a = torch.empty((m, 512), device=dev)
+        b = torch.empty((m, 512), device=dev)
+        assert qc.cint8_project_raw(0, [mats[0][0]], Xt, t, m, [a], [0]) == 0
+        assert qc.cint8_project_raw(0, [mats[0][0]], torch.from_numpy(xd).to(dev), 0, m, [b],
+                                    [0]) == 0
+        assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
+
+
+def test_cint8_row_plane_route_nonfinite_rows(qc, oracle, synth, dev):
+    """Activation rows holding +-inf or NaN on the row-plane route: those
+    rows get the reference's f32 result class per output, the finite rows
+    are bit-identical to the same call with the bad rows zeroed."""
+    import torch
+    rows, cols, m = 300, 4096, 6
+    codes, scales, zeros = _tensor(synth, 55, rows, cols, 1, True)
+    codes[:, 200] = 0
+    zeros[::5] = 0.0
+    keep = [_dev(qc, dev, a) for a in (codes, scales, zeros)]
+    w = qc.cint8_weights(keep[0], keep[1], keep[2], rows, cols, 1)
+    what = oracle.cint8_dequant(codes, scales, zeros, rows, cols, 1).astype(np.float64)
+    x = synth.normal_fast(66, m * cols).reshape(m, cols)
+    x[1, 200] = np.inf
+    x[3, 77] = -np.inf
+    x[3, 3000] = np.inf
+    x[4, 1234] = np.nan
+    print("cint8 planes nonfinite rows", flush=True)
+    Y = torch.empty((m, rows), device=dev)
+    assert qc.cint8_project_raw(0, [w], torch.from_numpy(x).to(dev), 0, m, [Y], [0]) == 0
+    Y = Y.cpu().numpy()
+    xz = x.copy()
+    xz[[1, 3, 4]] = 0.0
+    Z = torch.empty((m, rows), device=dev)
+    assert qc.cint8_project_raw(0, [w], torch.from_numpy(xz).to(dev), 0, m, [Z], [0]) == 0
+    Z = Z.cpu().numpy()
+    for r in (0, 2, 5):
+        assert np.array_equal(Y[r].view(np.uint32), Z[r].view(np.uint32)), r
+    for r in (1, 3, 4):
+        with np.errstate(invalid="ignore", over="ignore"):
+            y64 = (what * x[r].astype(np.float64)[None, :]).sum(axis=1)
+        for got, want in ((np.isnan(Y[r]), np.isnan(y64)), (np.isposinf(Y[r]), np.isposinf(y64)),
+                          (np.isneginf(Y[r]), np.isneginf(y64))):
+            assert np.array_equal(got, want), (r, np.flatnonzero(got != want)[:5])

@@ -50,7 +50,11 @@ def route(request, qc):
                                    # steady-state loops of the deep-K tiles: 128 x 128 with a
                                    # 4-deep ring (M 129..256, wide N) and 256 x 256 with a
                                    # 2-deep ring, 8 whole 128-B K steps plus a ragged 32-B one
-                                   (256, 14336, 4096), (1030, 9990, 1056)])
+                                   (256, 14336, 4096), (1030, 9990, 1056),
+                                   # up to 32 rows on a wide N: the 64 x 32 tile with an
+                                   # 8-deep ring (ragged K, a single row, ragged N)
+                                   (7, 14336, 4096), (32, 12352, 1056), (1, 12288, 160),
+                                   (19, 12300, 4128)])
 def test_accumulators_exact(qc, dev, route, m, n, k):
     import torch
     print(f"int8 acc route={route} m={m} n={n} k={k}", flush=True)
@@ -67,7 +71,7 @@ def test_accumulators_exact(qc, dev, route, m, n, k):
 
 
 @pytest.mark.parametrize("asym", [False, True])
-@pytest.mark.parametrize("m,n,k", [(300, 200, 4096), (700, 390, 1376)])
+@pytest.mark.parametrize("m,n,k", [(300, 200, 4096), (700, 390, 1376), (24, 12300, 1056)])
 def test_epilogue_bit_exact(qc, oracle, dev, route, m, n, k, asym):
     """Full f32 epilogue (with and without the zero-point correction) on every
     kernel route, bit-exact against the oracle over the whole matrix."""
