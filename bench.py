@@ -49,11 +49,12 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--only", choices=["headline", "all", "copy", "stream", "w8a8", "qgemm", "prefill",
-                                      "legs", "cint8"],
+                                      "legs", "cint8", "decode", "layer"],
                    default="all",
                    help="copy: a plain 64 MiB device copy, the calibration kernel for "
-                        "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm / prefill / legs: "
-                        "only those cases (for profiling), no JSON line")
+                        "FETCH_SIZE / WRITE_SIZE counter runs; w8a8 / qgemm / prefill / legs / "
+                        "cint8 / decode (qgemv_w8a8, fused up_gate and QKV) / layer (the "
+                        "config-4 sweep): only those cases (for profiling), no JSON line")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--rows-per-wave", type=int, default=0)
@@ -65,7 +66,14 @@ def parse():
 EAGER = False
 
 
+# When set, every case keeps one copy of its inputs (cache-resident figures:
+# the 256 MB Infinity Cache holds the weights between steps).
+RESIDENT = False
+
+
 def rotation(footprint):
+    if RESIDENT:
+        return 1
     return int(math.ceil(MALL_BYTES / footprint)) + 1
 
 
@@ -781,7 +789,7 @@ def print_cases(cases):
 
 def main():
     args = parse()
-    global EAGER
+    global EAGER, RESIDENT
     EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for --gpus {args.gpus}); "
@@ -808,9 +816,19 @@ def main():
         print_cases(stream_ceiling(qc, args.steps, args.warmup))
         return
     K, W = args.steps, args.warmup
-    if args.only in ("w8a8", "qgemm", "prefill", "legs", "cint8"):
+    if args.only in ("w8a8", "qgemm", "prefill", "legs", "cint8", "decode", "layer"):
         s = {}
-        if args.only == "legs":
+        if args.only == "decode":
+            s["q4_0_gemv_w8a8_k4096_n14336"] = gemv_w8a8_case(qc, 1, 14336, 4096, K, W, seed=11)
+            s["q8_0_gemv_w8a8_k4096_n4096"] = gemv_w8a8_case(qc, 0, 4096, 4096, K, W, seed=12)
+            s["q4_0_up_gate_k4096_n2x14336"] = fused_case(qc, "up_gate", 1, (14336, 14336), 4096,
+                                                          K, W, seed=13, gate=True)
+            s["q4_0_qkv_k4096_n3x4096"] = fused_case(qc, "qkv", 1, (4096, 4096, 4096), 4096, K, W,
+                                                     seed=14, gate=True)
+        elif args.only == "layer":
+            for key, r in layer_sweep(qc, K, W).items():
+                s[f"decoder_layer_{key}"] = r
+        elif args.only == "legs":
             # the metric's legs in the order the JSON line lists them
             s["q4_0_gemv_k4096_n14336"], *_ = gemv_case(qc, 1, 14336, 4096, K, W, seed=1)
             s["q8_0_gemv_k4096_n14336"], *_ = gemv_case(qc, 0, 14336, 4096, K, W, seed=5)
@@ -828,6 +846,8 @@ def main():
             s["cint8_group128_m1_k4096_n14336"] = cint8_case(qc, 14336, 4096, 1, K, W, groups=32)
             s["cint8_channel_m4_k4096_n14336"] = cint8_case(qc, 14336, 4096, 4, K, W)
             s["cint8_swiglu_m1_k4096_n2x14336"] = cint8_case(qc, 14336, 4096, 1, K, W, mode=1)
+            s["cint8_channel_m16_k4096_n14336"] = cint8_case(qc, 14336, 4096, 16, K, W)
+            s["cint8_channel_m64_k4096_n14336"] = cint8_case(qc, 14336, 4096, 64, K, W)
         elif args.only == "w8a8":
             s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
             s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
@@ -879,8 +899,19 @@ def main():
         s["cint8_group128_m1_k4096_n14336"] = cint8_case(qc, 14336, 4096, 1, K, W, groups=32)
         s["cint8_channel_m4_k4096_n14336"] = cint8_case(qc, 14336, 4096, 4, K, W)
         s["cint8_swiglu_m1_k4096_n2x14336"] = cint8_case(qc, 14336, 4096, 1, K, W, mode=1)
+        s["cint8_channel_m16_k4096_n14336"] = cint8_case(qc, 14336, 4096, 16, K, W)
         for key, r in layer_sweep(qc, max(20, K // 4), W).items():
             s[f"decoder_layer_{key}"] = r
+        # the same GEMV legs with one weight copy: cache-resident (Infinity
+        # Cache) figures beside the rotated, HBM-streaming ones above
+        RESIDENT = True
+        try:
+            for fmt, name, n_, k_ in ((1, "q4_0", 14336, 4096), (0, "q8_0", 14336, 4096),
+                                      (0, "q8_0", 4096, 4096), (1, "q4_0", 4096, 14336)):
+                r, *_ = gemv_case(qc, fmt, n_, k_, K, W, seed=21)
+                s[f"{name}_gemv_k{k_}_n{n_}_cache_resident"] = r
+        finally:
+            RESIDENT = False
         print_cases(s)
         secondary = s
 
