@@ -869,19 +869,24 @@ constexpr int kPlanesChunkM = 1024;     // activation rows per pass: bounds the 
 constexpr int kPlanesMinM = 3;     // M = 2: 22 us on the digit-dot kernel against 32 us here (N=14336, K=4096)
 constexpr int kPlanesNonfinite = 0x40000000;
 
-// Workgroup reductions of the prep kernel: the maximum of one float and the
-// sums of three ints, each with one LDS round.
+// The prep kernel: 1024 threads per activation row, each holding up to 16 of
+// its values (four groups of four, K <= 16384) in registers, so the row is
+// read once with every load in flight.
+constexpr int kPrepThreads = 1024;
+constexpr int kPrepWaves = kPrepThreads / 64;
+constexpr int kPrepGroups = kPlanesMaxK / (4 * kPrepThreads);
+
 __device__ __forceinline__ float block_max(float v, float* red) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   float r = red[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) r = fmaxf(r, red[w]);
+  for (int w = 1; w < kPrepWaves; ++w) r = fmaxf(r, red[w]);
   return r;
 }
 
-__device__ __forceinline__ void block_sum3(int (&v)[3], int (*red)[kWaves]) {
+__device__ __forceinline__ void block_sum3(int (&v)[3], int (*red)[kPrepWaves]) {
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
     for (int off = 32; off > 0; off >>= 1) v[t] += __shfl_xor(v[t], off);
@@ -892,7 +897,7 @@ __device__ __forceinline__ void block_sum3(int (&v)[3], int (*red)[kWaves]) {
   for (int t = 0; t < 3; ++t) {
     int r = red[t][0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) r += red[t][w];
+    for (int w = 1; w < kPrepWaves; ++w) r += red[t][w];
     v[t] = r;
   }
 }
@@ -916,22 +921,29 @@ __device__ __forceinline__ void load4(const void* x, long long xr, int c, int xt
 // One workgroup per activation row (x rows blockIdx.x, ldx apart).  A row
 // holding NaN or +-inf gets the maximum +inf, zero digits and the flag
 // exponent kPlanesNonfinite.
-__global__ __launch_bounds__(kThreads) void cint8_planes_prep(const void* __restrict__ x, int xtype,
-                                                              long long ldx, int k, bool vec,
-                                                              int8_t* __restrict__ planes,
-                                                              int* __restrict__ rexp,
-                                                              int* __restrict__ dsum) {
-  __shared__ float fred[kWaves];
-  __shared__ int ired[3][kWaves];
+__global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
+    const void* __restrict__ x, int xtype, long long ldx, int k, bool vec,
+    int8_t* __restrict__ planes, int* __restrict__ rexp, int* __restrict__ dsum) {
+  __shared__ float fred[kPrepWaves];
+  __shared__ int ired[3][kPrepWaves];
   const int m = blockIdx.x;
   const long long xr = static_cast<long long>(m) * ldx;
+  float v[kPrepGroups][4];
   float mx = 0.0f;
-  for (int c = 4 * static_cast<int>(threadIdx.x); c < k; c += 4 * kThreads) {
-    float v[4];
-    load4(x, xr, c, xtype, vec, v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, isfinite(v[i]) ? fabsf(v[i]) : INFINITY);
+  for (int g = 0; g < kPrepGroups; ++g) {
+    const int c = 4 * (static_cast<int>(threadIdx.x) + g * kPrepThreads);
+    if (c < k) {
+      load4(x, xr, c, xtype, vec, v[g]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[g][i] = 0.0f;
+    }
   }
+#pragma unroll
+  for (int g = 0; g < kPrepGroups; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, isfinite(v[g][i]) ? fabsf(v[g][i]) : INFINITY);
   mx = block_max(mx, fred);
   const bool bad = !isfinite(mx);
   int ex = 0;
@@ -939,13 +951,14 @@ __global__ __launch_bounds__(kThreads) void cint8_planes_prep(const void* __rest
   const int e = ex - 21;
   int sum[3] = {0, 0, 0};
   int8_t* p0 = planes + (3LL * m) * k;
-  for (int c = 4 * static_cast<int>(threadIdx.x); c < k; c += 4 * kThreads) {
-    float v[4];
-    load4(x, xr, c, xtype, vec, v);
+#pragma unroll
+  for (int g = 0; g < kPrepGroups; ++g) {
+    const int c = 4 * (static_cast<int>(threadIdx.x) + g * kPrepThreads);
+    if (c >= k) continue;
     uint32_t w0 = 0, w1 = 0, w2 = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      int q = bad ? 0 : __float2int_rn(ldexpf(v[i], -e));
+      int q = bad ? 0 : __float2int_rn(ldexpf(v[g][i], -e));
       q = q > 2097151 ? 2097151 : q;
       const int d0 = q >> 14, d1 = (q >> 7) & 127, d2 = q & 127;
       sum[0] += d0;
@@ -1083,7 +1096,7 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
     const void* xc = static_cast<const uint8_t*>(L.x) + es * static_cast<size_t>(m0) * L.ldx;
     const bool vec = L.xtype == QC_STORAGE_F32 && reinterpret_cast<uintptr_t>(L.x) % 16 == 0 &&
                      L.ldx % 4 == 0;
-    cint8_planes_prep<<<mc, kThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, planes, rexp, dsum);
+    cint8_planes_prep<<<mc, kPrepThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, planes, rexp, dsum);
     e = hipGetLastError();
     for (int i = 0; i < nmat && e == hipSuccess; ++i) {
       int32_t* acc = reinterpret_cast<int32_t*>(cur);
