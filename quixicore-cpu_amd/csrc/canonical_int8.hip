@@ -19,9 +19,11 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "qc_device.h"
 #include "qc_digits.h"
+#include "qc_int8_ring.h"
 #include "qc_internal.h"
 
 namespace qc {
@@ -850,14 +852,22 @@ hipError_t launch_mb(const CSegs& sg, bool grp, bool aff, const void* x, int xty
 // Every activation row m is encoded once as 22-bit fixed point under one
 // exponent for the whole row: e(m) = frexp(max_k |x[m][k]|) - 21 and
 // q = rint(x * 2^-e), clamped to [-2^21, 2^21 - 1], split into three int8
-// planes q = 2^14 d0 + 2^7 d1 + d2 (d0 in [-128, 127], d1, d2 in [0, 127])
-// that are rows 3m + t of an int8 matrix [3M][K].  The int8 MFMA GEMM
-// (launch_int8_gemm, the W8A8 kernels) gives the exact int32 sums
-// D_t[m][n] = sum_k code[n][k] d_t[m][k] of all planes in one launch per
-// matrix; the finish kernel forms 2^14 D0 + 2^7 D1 + D2 exactly in int64
-// (minus z (2^14 S0 + 2^7 S1 + S2), S_t = sum_k d_t[m][k], for an integral
-// zero point z), rounds it once to f32 and scales it by 2^e and the row's
-// scale, then runs the shared epilogue.  Each x is held to within
+// planes q = 2^14 d0 + 2^7 d1 + d2 (d0 in [-128, 127], d1, d2 in [0, 127]).
+// The int8 MFMA main loop gives the exact int32 sums
+// D_t[m][n] = sum_k code[n][k] d_t[m][k] of all planes.
+//  * Up to kPlanesFusedM activation rows, mode 0: the planes of row m are
+//    rows 4m + t (t < 3; row 4m + 3 is zero) of an int8 matrix [4M][K], the
+//    main loop's operand A against the weight codes as operand B
+//    (qc_int8_ring.h), so each lane's accumulators hold D_0..D_2 of one
+//    (m, n) and the GEMM's epilogue finishes the output: one launch per
+//    matrix after the prep.
+//  * Otherwise the planes are rows 3m + t of [3M][K], launch_int8_gemm
+//    writes every D_t[m][n] of a matrix to scratch and a finish kernel
+//    combines them (and pairs gate / up for SwiGLU).
+// The combination forms 2^14 D0 + 2^7 D1 + D2 exactly (an integer below
+// 2^53, in double), minus z (2^14 S0 + 2^7 S1 + S2), S_t = sum_k d_t[m][k],
+// for an integral zero point z, rounds it once to f32 and scales it by 2^e
+// and the row's scale, then runs the shared epilogue.  Each x is held to within
 // 2^-21 max_k |x_m|, so |y - y_exact| <= sqrt(K) 2^-21 ||x_m|| ||w_hat_n||:
 // 3.1e-5 at K = 4096 and 6.1e-5 at K = 16384 after the contract's
 // normalisation.  A row holding NaN or +-inf is computed in f32 from the
@@ -866,7 +876,8 @@ namespace {
 
 constexpr int kPlanesMaxK = 16384;
 constexpr int kPlanesChunkM = 1024;     // activation rows per pass: bounds the scratch
-constexpr int kPlanesMinM = 3;     // M = 2: 22 us on the digit-dot kernel against 32 us here (N=14336, K=4096)
+constexpr int kPlanesMinM = 2;     // N=14336, K=4096, M = 2: 22.9 us on the digit-dot kernel, 18.9 here at M = 3
+constexpr int kPlanesFusedM = 64;  // activation rows of the one-launch (fused epilogue) form
 constexpr int kPlanesNonfinite = 0x40000000;
 
 // The prep kernel: 1024 threads per activation row, each holding up to 16 of
@@ -918,9 +929,11 @@ __device__ __forceinline__ void load4(const void* x, long long xr, int c, int xt
   }
 }
 
-// One workgroup per activation row (x rows blockIdx.x, ldx apart).  A row
-// holding NaN or +-inf gets the maximum +inf, zero digits and the flag
+// One workgroup per activation row (x rows blockIdx.x, ldx apart); the
+// planes of row m are rows PR * m + t (PR = 4: row PR * m + 3 is zeroed).  A
+// row holding NaN or +-inf gets the maximum +inf, zero digits and the flag
 // exponent kPlanesNonfinite.
+template <int PR>
 __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     const void* __restrict__ x, int xtype, long long ldx, int k, bool vec,
     int8_t* __restrict__ planes, int* __restrict__ rexp, int* __restrict__ dsum) {
@@ -950,7 +963,7 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
   (void)frexpf(mx, &ex);                       // mx < 2^ex
   const int e = ex - 21;
   int sum[3] = {0, 0, 0};
-  int8_t* p0 = planes + (3LL * m) * k;
+  int8_t* p0 = planes + (static_cast<long long>(PR) * m) * k;
 #pragma unroll
   for (int g = 0; g < kPrepGroups; ++g) {
     const int c = 4 * (static_cast<int>(threadIdx.x) + g * kPrepThreads);
@@ -971,6 +984,7 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     *reinterpret_cast<uint32_t*>(p0 + c) = w0;
     *reinterpret_cast<uint32_t*>(p0 + k + c) = w1;
     *reinterpret_cast<uint32_t*>(p0 + 2LL * k + c) = w2;
+    if constexpr (PR == 4) *reinterpret_cast<uint32_t*>(p0 + 3LL * k + c) = 0u;
   }
   block_sum3(sum, ired);
   if (threadIdx.x == 0) {
@@ -998,11 +1012,12 @@ struct PlaneMat {
   long long rows;
 };
 
-// Projection of activation row (m0 + mm) on row n of one matrix.
-__device__ __forceinline__ float plane_value(const int8_t* w, const float* scale, const float* zp,
-                                             const int32_t* a, long long r, int n, int mm, int m0,
-                                             const int* rexp, const int* dsum, const void* x,
-                                             int xtype, long long ldx, int k) {
+// Projection of activation row (m0 + mm) on row n of one matrix from its
+// plane sums a0..a2 (D_0..D_2).
+__device__ __forceinline__ float plane_value(int32_t a0, int32_t a1, int32_t a2, const int8_t* w,
+                                             const float* scale, const float* zp, long long n,
+                                             int mm, int m0, const int* rexp, const int* dsum,
+                                             const void* x, int xtype, long long ldx, int k) {
   const int e = rexp[mm];
   const float sc = scale[n];
   if (e == kPlanesNonfinite) {        // the reference's f32 form, block by block
@@ -1015,9 +1030,8 @@ __device__ __forceinline__ float plane_value(const int8_t* w, const float* scale
   }
   // 2^14 D0 + 2^7 D1 + D2 (|D_t| < 2^26 for K <= 16384) and the zero-point
   // term are integers below 2^53: exact in double, then rounded once to f32
-  const double d = fma(static_cast<double>(a[(3LL * mm) * r + n]), 16384.0,
-                       fma(static_cast<double>(a[(3LL * mm + 1) * r + n]), 128.0,
-                           static_cast<double>(a[(3LL * mm + 2) * r + n])));
+  const double d = fma(static_cast<double>(a0), 16384.0,
+                       fma(static_cast<double>(a1), 128.0, static_cast<double>(a2)));
   float f;
   if (zp != nullptr) {
     const double sx = fma(static_cast<double>(dsum[3 * mm]), 16384.0,
@@ -1035,6 +1049,16 @@ __device__ __forceinline__ float plane_value(const int8_t* w, const float* scale
   return sc * ldexpf(f, e);
 }
 
+// plane_value from the finish kernel's scratch: D_t of activation row mm at
+// [(3 mm + t) rows + n].
+__device__ __forceinline__ float plane_value_at(const PlaneMat& t, int n, int mm, int m0,
+                                                const int* rexp, const int* dsum, const void* x,
+                                                int xtype, long long ldx, int k) {
+  const int32_t* a = t.acc + (3LL * mm) * t.rows + n;
+  return plane_value(a[0], a[t.rows], a[2 * t.rows], t.w, t.scale, t.zero, n, mm, m0, rexp, dsum,
+                     x, xtype, ldx, k);
+}
+
 // One thread per (activation row, output unit): activation row blockIdx.y,
 // unit blockIdx.x * kThreads + threadIdx.x -- mode 0 a logical row (matrix
 // by the segment starts), mode 1 a gate / up pair.  The stores are the
@@ -1050,10 +1074,8 @@ __global__ __launch_bounds__(kThreads) void cint8_planes_finish(
   const PlaneMat t2{sg.w[2], sg.scale[2], sg.zero[2], pa.acc[2], pa.rows[2]};
   if (sg.mode == 1) {
     if (u >= t0.rows) return;
-    const float gate = plane_value(t0.w, t0.scale, t0.zero, t0.acc, t0.rows, u, mm, m0, rexp,
-                                   dsum, x, xtype, ldx, k);
-    const float up = plane_value(t1.w, t1.scale, t1.zero, t1.acc, t1.rows, u, mm, m0, rexp,
-                                 dsum, x, xtype, ldx, k);
+    const float gate = plane_value_at(t0, u, mm, m0, rexp, dsum, x, xtype, ldx, k);
+    const float up = plane_value_at(t1, u, mm, m0, rexp, dsum, x, xtype, ldx, k);
     const float silu = gate / (1.0f + expf(-gate));
     store_y(sg.y[0], m * sg.ld[0] + u, sg.ytype[0], silu * up);
     return;
@@ -1064,8 +1086,7 @@ __global__ __launch_bounds__(kThreads) void cint8_planes_finish(
   const int seg = (nseg > 2 && u >= s2) ? 2 : (nseg > 1 && u >= s1) ? 1 : 0;
   const PlaneMat t = seg == 0 ? t0 : seg == 1 ? t1 : t2;
   const int row = u - (seg == 2 ? s2 : seg == 1 ? s1 : 0);
-  float v = plane_value(t.w, t.scale, t.zero, t.acc, t.rows, row, mm, m0, rexp, dsum, x, xtype,
-                        ldx, k);
+  float v = plane_value_at(t, row, mm, m0, rexp, dsum, x, xtype, ldx, k);
   if (seg == 0 && (sg.bias != nullptr || sg.act != 0)) {
     if (sg.bias != nullptr) v += sg.bias[row];
     v = linear_activation(v, sg.act);
@@ -1076,18 +1097,141 @@ __global__ __launch_bounds__(kThreads) void cint8_planes_finish(
   store_y(y, m * ld + row, yt, v);
 }
 
+// One matrix of the fused form: its codes, scales, zero points, output and
+// (matrix 0 of mode 0) bias and activation.
+struct PlaneOut {
+  const int8_t* w;
+  const float* scale;
+  const float* zero;
+  void* y;
+  long long ld;
+  int ytype;
+  int rows;
+  const float* bias;
+  int act;           // with epi != 0: bias (when given), then linear_activation
+  int epi;
+};
+
+// The fused form: planes [4 mc][k] (operand A, TN rows per tile) against the
+// weight codes (operand B, TM rows per tile), then for each (activation row,
+// weight row) the combination and epilogue of the finish kernel, stored as
+// y[(m0 + r) * ld + n].  Lanes 0-31 of a store hold 32 consecutive n.
+template <int TN, int TM, int S, int WGN, int WGM>
+__global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
+    const int8_t* __restrict__ planes, int mc, const PlaneOut o, const int* __restrict__ rexp,
+    const int* __restrict__ dsum, const void* __restrict__ x, int xtype, long long ldx, int m0,
+    int k, int tiles_n, int tiles_m) {
+  using R = Int8Ring<TN, TM, S, WGN, WGM, 128>;
+  __shared__ __attribute__((aligned(1024))) int8_t ring[R::kBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tn, tm;
+  tile_of(blockIdx.x, tiles_n * tiles_m, tiles_n, tiles_m, tn, tm);
+  const long long p0 = static_cast<long long>(tn) * TN + R::wave_n(wave);   // plane rows
+  const long long n0 = static_cast<long long>(tm) * TM + R::wave_m(wave);   // weight rows
+  v16i acc[R::FN][R::FM];
+  R::run(planes, o.w, o.rows, 4 * mc, k, static_cast<long long>(tn) * TN,
+         static_cast<long long>(tm) * TM, ring, acc);
+#pragma unroll
+  for (int j = 0; j < R::FM; ++j) {
+    const long long n = n0 + 32 * j + (lane & 31);
+    if (n >= o.rows) continue;
+#pragma unroll
+    for (int i = 0; i < R::FN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = static_cast<int>((p0 + 32 * i + 8 * g + 4 * (lane >> 5)) >> 2);
+        if (r >= mc) continue;
+        float v = plane_value(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], o.w,
+                              o.scale, o.zero, n, r, m0, rexp, dsum, x, xtype, ldx, k);
+        if (o.epi) {
+          if (o.bias != nullptr) v += o.bias[n];
+          v = linear_activation(v, o.act);
+        }
+        store_y(o.y, static_cast<long long>(m0 + r) * o.ld + n, o.ytype, v);
+      }
+  }
+}
+
+template <int TN, int TM, int S, int WGN, int WGM>
+hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
+                              const int* dsum, const void* x, int xtype, long long ldx, int m0,
+                              int k, hipStream_t s) {
+  const int tiles_n = (4 * mc + TN - 1) / TN;
+  const int tiles_m = (o.rows + TM - 1) / TM;
+  cint8_planes_gemm<TN, TM, S, WGN, WGM><<<tiles_n * tiles_m, 64 * WGN * WGM, 0, s>>>(
+      planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, tiles_n, tiles_m);
+  return hipGetLastError();
+}
+
+// Tile by plane rows (4 mc <= 4 kPlanesFusedM): the whole plane matrix in
+// one A tile, 64 weight rows per workgroup (224 workgroups at N = 14336).
+hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
+                        const int* dsum, const void* x, int xtype, long long ldx, int m0, int k,
+                        hipStream_t s) {
+  if (mc <= 8)
+    return launch_planes_gemm<32, 64, 8, 1, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+  if (mc <= 16)
+    return launch_planes_gemm<64, 64, 6, 1, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+  if (mc <= 32)
+    return launch_planes_gemm<128, 64, 4, 2, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+  return launch_planes_gemm<256, 64, 3, 4, 1>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+}
+static_assert(kPlanesFusedM <= 64, "launch_fused tiles cover 256 plane rows");
+
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
+// The call's scratch: buffer 0 of its stream's cache entry, whose call lock
+// `hold` keeps until the caller's last launch.
+hipError_t call_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex>& hold,
+                        void** out) {
+  StreamWorkspace* ws = nullptr;
+  const hipError_t e = stream_workspace(s, &ws);
+  if (e != hipSuccess) return e;
+  hold = std::unique_lock<std::mutex>(ws->call);
+  return stream_buffer(ws, s, bytes, 0, out);
+}
 
 hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hipStream_t s) {
   const int nmat = L.mode == 1 ? 2 : L.nw;
   const size_t es = L.xtype == QC_STORAGE_F32 ? 4 : 2;
+  bool aligned = true;
+  for (int i = 0; i < nmat; ++i) aligned = aligned && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
+  if (L.mode == 0 && m <= kPlanesFusedM && aligned) {
+    const size_t bytes = up256(4ull * m * k) + up256(4ull * m) + up256(12ull * m);
+    std::unique_lock<std::mutex> hold;
+    uint8_t* base = nullptr;
+    hipError_t e = call_scratch(s, bytes, hold, reinterpret_cast<void**>(&base));
+    if (e != hipSuccess) return e;
+    int8_t* planes = reinterpret_cast<int8_t*>(base);
+    int* rexp = reinterpret_cast<int*>(base + up256(4ull * m * k));
+    int* dsum = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rexp) + up256(4ull * m));
+    const bool vec = L.xtype == QC_STORAGE_F32 && reinterpret_cast<uintptr_t>(L.x) % 16 == 0 &&
+                     L.ldx % 4 == 0;
+    cint8_planes_prep<4><<<m, kPrepThreads, 0, s>>>(L.x, L.xtype, L.ldx, k, vec, planes, rexp,
+                                                    dsum);
+    e = hipGetLastError();
+    for (int i = 0; i < nmat && e == hipSuccess; ++i) {
+      const PlaneOut o{sg.w[i], sg.scale[i], sg.zero[i], sg.y[i], sg.ld[i], sg.ytype[i],
+                       static_cast<int>(L.w[i].rows), sg.bias, sg.act,
+                       i == 0 && (sg.bias != nullptr || sg.act != 0) ? 1 : 0};
+      e = launch_fused(planes, m, o, rexp, dsum, L.x, L.xtype, L.ldx, 0, k, s);
+    }
+    return e;
+  }
+  // chunks of kPlanesChunkM rows, one after the other in one buffer
+  auto chunk_bytes = [&](int mc) {
+    size_t b = up256(3ull * mc * k) + up256(4ull * mc) + up256(12ull * mc);
+    for (int i = 0; i < nmat; ++i) b += up256(12ull * mc * static_cast<size_t>(L.w[i].rows));
+    return b;
+  };
+  std::unique_lock<std::mutex> hold;
+  uint8_t* base = nullptr;
+  hipError_t e = call_scratch(s, chunk_bytes(std::min(kPlanesChunkM, m)), hold,
+                              reinterpret_cast<void**>(&base));
+  if (e != hipSuccess) return e;
   for (int m0 = 0; m0 < m; m0 += kPlanesChunkM) {
     const int mc = std::min(kPlanesChunkM, m - m0);
-    size_t bytes = up256(3ull * mc * k) + up256(4ull * mc) + up256(12ull * mc);
-    for (int i = 0; i < nmat; ++i) bytes += up256(12ull * mc * static_cast<size_t>(L.w[i].rows));
-    uint8_t* base = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&base), bytes, s);
-    if (e != hipSuccess) return e;
     int8_t* planes = reinterpret_cast<int8_t*>(base);
     int* rexp = reinterpret_cast<int*>(base + up256(3ull * mc * k));
     int* dsum = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rexp) + up256(4ull * mc));
@@ -1096,7 +1240,8 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
     const void* xc = static_cast<const uint8_t*>(L.x) + es * static_cast<size_t>(m0) * L.ldx;
     const bool vec = L.xtype == QC_STORAGE_F32 && reinterpret_cast<uintptr_t>(L.x) % 16 == 0 &&
                      L.ldx % 4 == 0;
-    cint8_planes_prep<<<mc, kPrepThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, planes, rexp, dsum);
+    cint8_planes_prep<3><<<mc, kPrepThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, planes, rexp,
+                                                     dsum);
     e = hipGetLastError();
     for (int i = 0; i < nmat && e == hipSuccess; ++i) {
       int32_t* acc = reinterpret_cast<int32_t*>(cur);
@@ -1114,9 +1259,7 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
                                                     k);
       e = hipGetLastError();
     }
-    const hipError_t f = hipFreeAsync(base, s);
     if (e != hipSuccess) return e;
-    if (f != hipSuccess) return f;
   }
   return hipSuccess;
 }
@@ -1198,7 +1341,8 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   }
   float* p = nullptr;
   const size_t bytes = sizeof(float) * static_cast<size_t>(total) * m;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&p), bytes ? bytes : 4, s);
+  std::unique_lock<std::mutex> hold;
+  hipError_t e = call_scratch(s, bytes, hold, reinterpret_cast<void**>(&p));
   if (e != hipSuccess) return e;
   const long long items = static_cast<long long>(total) * m;
   cint8_generic<<<static_cast<unsigned>((items + kWaves - 1) / kWaves), kThreads, 0, s>>>(
@@ -1209,8 +1353,7 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
     cint8_finish<<<static_cast<unsigned>((units + kThreads - 1) / kThreads), kThreads, 0, s>>>(sg, p, m);
     e = hipGetLastError();
   }
-  const hipError_t f = hipFreeAsync(p, s);
-  return e != hipSuccess ? e : f;
+  return e;
 }
 
 // ---- Decode and storage conversion (model load / inspection, not the
@@ -1330,7 +1473,8 @@ hipError_t launch_cint8_dual(const qc_cint8_weights& w, const qc_cint8_weights& 
                             m, n, k, false, nullptr, s, int8_route);
   // affine activations: dot - z * row_sum(w), the weights' row sums summed here
   int32_t* sums = nullptr;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&sums), sizeof(int32_t) * n, s);
+  std::unique_lock<std::mutex> hold;
+  hipError_t e = call_scratch(s, sizeof(int32_t) * n, hold, reinterpret_cast<void**>(&sums));
   if (e != hipSuccess) return e;
   const unsigned grid = static_cast<unsigned>(std::min<long long>((n + kWaves - 1) / kWaves, 4096));
   cint8_row_sums<<<grid, kThreads, 0, s>>>(w.codes, n, k, sums);
@@ -1338,8 +1482,7 @@ hipError_t launch_cint8_dual(const qc_cint8_weights& w, const qc_cint8_weights& 
   if (e == hipSuccess)
     e = launch_int8_gemm(w.codes, a.codes, w.scales, a.scales, sums, a_int_zero_points, y,
                          nullptr, m, n, k, true, nullptr, s, int8_route);
-  const hipError_t f = hipFreeAsync(sums, s);
-  return e != hipSuccess ? e : f;
+  return e;
 }
 
 hipError_t launch_storage_to_f32(const void* x, int type, long long count, float* out,

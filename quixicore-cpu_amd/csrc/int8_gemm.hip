@@ -22,12 +22,12 @@
 // of step k+2, computes step k from the other buffer, then meets the
 // workgroup at a single barrier.
 #include "qc_device.h"
+#include "qc_int8_ring.h"
 #include "qc_internal.h"
 
 namespace qc {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 // 16-byte store that only assumes the 4-byte alignment of a float pointer
 // (global_store_dwordx4 accepts dword-aligned addresses).
 typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -118,32 +118,6 @@ __device__ __forceinline__ void write_tile(const v4i (&acc)[FN][FM], long long m
   if (status != nullptr && __any(bad) && lane == 0) *status = 3;
 }
 
-// Output tile of workgroup `b` in an XCD-aware order.  Workgroups are handed
-// to the 8 XCDs round-robin (b % 8), each with its own L2, so the tiles one
-// XCD runs are made a contiguous range of a banded order (bands of kBandM
-// m-tiles, n-tiles within a band): an XCD then reads few W and X panels.
-constexpr int kXcds = 8;
-constexpr int kBandM = 4;
-__device__ __forceinline__ void tile_of(int b, int total, int tiles_n, int tiles_m, int& tn,
-                                        int& tm) {
-  const int q = total / kXcds, r = total % kXcds;
-  const int xcd = b % kXcds, idx = b / kXcds;
-  const int t = xcd * q + (xcd < r ? xcd : r) + idx;
-  const int band = t / (tiles_n * kBandM);
-  const int rem = t - band * tiles_n * kBandM;
-  const int left = tiles_m - band * kBandM;
-  const int gm = left < kBandM ? left : kBandM;
-  tn = rem / gm;
-  tm = band * kBandM + rem % gm;
-}
-
-// s_waitcnt vmcnt(N), leaving expcnt and lgkmcnt unconstrained (gfx9
-// encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 // Waits until at most G * min(D, ahead) loads are outstanding: the loads of
 // the `ahead` steps issued after the one needed now (at most D of them).
 template <int G, int D>
@@ -154,28 +128,6 @@ __device__ __forceinline__ void wait_step(int ahead) {
     if (ahead >= D) wait_vmcnt<G * D>();
     else wait_step<G, D - 1>(ahead);
   }
-}
-__device__ __forceinline__ void wait_lgkmcnt0() {
-  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
-}
-
-// global_load_lds_dwordx4: every lane sends 16 bytes from its own global
-// address to LDS byte lds + 16 * lane (`lds` is wave-uniform, passed in M0).
-// The address-space cast only exists in the device pass.
-__device__ __forceinline__ void load_lds16(const int8_t* g, int8_t* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-#endif
-}
-
-// Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() would
-// make the compiler drain every outstanding global->LDS load (vmcnt(0)) and
-// defeat the multi-stage prefetch; here the waits are explicit and the empty
-// asm statements only stop the compiler moving memory accesses across.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // Direct-to-LDS pipelined kernel (K % 64 == 0).  An S-deep ring of LDS stages,
@@ -274,8 +226,6 @@ __global__ __launch_bounds__(kThreads) void int8_gemm_dma(
                      status);
 }
 
-typedef int v16i __attribute__((ext_vector_type(16)));
-
 // Epilogue for 32 x 32 accumulator tiles (v_mfma_i32_32x32x32_i8 C layout:
 // the lane holds m column lane&31 and, in register e, n row
 // 8*(e>>2) + 4*(lane>>5) + (e&3): four runs of 4 consecutive n).  Every
@@ -360,194 +310,26 @@ __device__ __forceinline__ void write_tile32(const v16i (&acc)[FN][FM], long lon
   if (status != nullptr && __any(bad) && lane == 0) *status = 3;
 }
 
-// Full-line ring kernel (K % 32 == 0).  Each K step covers 128 bytes of every
-// W and X row of the tile, i.e. whole 128-byte cache lines: the global->LDS
-// path delivers markedly more per CU for whole lines than for half lines.
-//
-// LDS: an S-deep ring of stages; a stage holds W[TN][128] then X[TM][128],
-// row-major, with the 16-byte chunk c of row r stored at position
-// c ^ ((r >> 1) & 7).  A global_load_lds_dwordx4 moves 8 rows (1 KB): lane l
-// writes position l&7 of row l>>3 and so fetches logical chunk
-// (l&7) ^ ((r >> 1) & 7).
-//
-// MFMA: v_mfma_i32_32x32x32_i8 (one wavefront sustains close to the CU's
-// int8 rate with it, unlike the 16x16x64 form).  A step is four K quarters
-// of 32; the operand of quarter q for a 32-row fragment is, in lane l,
-// row l&31, chunk 2q + (l>>5), the same lane->k map for W and X.  Those 64
-// reads fall on all 16 four-bank slots 4 times each under the swizzle above.
-//
-// Schedule (wavefront-uniform, branch-free in the steady state):
-//   prologue: issue the loads of steps 0..S-1 into stages 0..S-1;
-//   step k, quarter q = 0..2: read the fragments of quarter q+1 while the
-//     MFMAs of quarter q run;
-//   quarter 3: wait for this wave's loads of step k+1, barrier (all waves'
-//     loads are in and every wave has finished reading stage k), issue the
-//     loads of step k+S into stage k (with S >= 3 only the first quarter of
-//     them; the rest go out before the MFMAs of quarters 1..3 of step k+1),
-//     read quarter 0 of step k+1, then the MFMAs of quarter 3.
-// Past the last step the loads repeat the last step into stages that are
-// never read again, which keeps every wait count a constant.  The last step
-// runs separately and, when K is not a multiple of 128, skips the quarters
-// past K (their loads read a clamped in-row address and are never used).
+// The W8A8 GEMM over the full-line ring (qc_int8_ring.h): A = W (n), B = X
+// (m), and the reference's epilogue on the wave's accumulators.
 template <int TN, int TM, int S, int WGN, int WGM, int KL>
 __global__ __launch_bounds__(64 * WGN * WGM) void int8_gemm_ring(
     const int8_t* __restrict__ W, const int8_t* __restrict__ X, const float* __restrict__ ws,
     const float* __restrict__ as, const int32_t* __restrict__ row_sum, const int* __restrict__ zp,
     float* __restrict__ y, int32_t* __restrict__ acc_out, int M, int N, int K, int tiles_n,
     int tiles_m, int asym, int* status) {
-  static_assert(KL == 128 || KL == 64, "K step is a whole or a half cache line");
-  constexpr int kLine = KL;
-  constexpr int QPS = KL / 32;                       // K quarters per step
-  constexpr int RPL = 1024 / KL;                     // rows per 1 KB load
-  constexpr int CPR = KL / 16;                       // 16-byte chunks per row
-  constexpr int NW = WGN * WGM;                      // WGN x WGM grid of wavefronts
-  constexpr int WN = TN / WGN, WM = TM / WGM;        // wave tile
-  constexpr int FN = WN / 32, FM = WM / 32;          // 32 x 32 tiles per wave
-  constexpr int GW = TN / RPL / NW, GX = TM / RPL / NW;  // 1 KB loads per wave per step
-  constexpr int G = GW + GX;
-  constexpr int kStage = (TN + TM) * kLine;
-  static_assert(FN >= 1 && FM >= 1 && GW >= 1 && GX >= 1 && S >= 2, "tile shape");
-  static_assert(KL == 64 || (GW % 2 == 0 && GX % 2 == 0), "8-row groups alternate swizzle parity");
-  static_assert(G * (S - 1) < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) int8_t ring[S * kStage];
-
+  using R = Int8Ring<TN, TM, S, WGN, WGM, KL>;
+  __shared__ __attribute__((aligned(1024))) int8_t ring[R::kBytes];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int tn, tm;
   tile_of(blockIdx.x, tiles_n * tiles_m, tiles_n, tiles_m, tn, tm);
   const long long n0 = static_cast<long long>(tn) * TN;
   const long long m0 = static_cast<long long>(tm) * TM;
-
-  // Load j of a wave covers operand rows r = RPL * (wave * GW + j) + lane / CPR
-  // (W; likewise X with GX), lane writing slot lane % CPR of its row.  Swizzle
-  // key of row r: (r >> 1) & (CPR - 1).  128-byte lines: 4 * (j & 1) +
-  // (lane >> 4), as GW and GX are even; 64-byte halves: (lane >> 3) & 3.
-  const int8_t* src[G];
-  int coff[2];
-#pragma unroll
-  for (int par = 0; par < 2; ++par)
-    coff[par] = KL == 128 ? ((lane & 7) ^ (4 * par + (lane >> 4))) * 16
-                          : ((lane & 3) ^ ((lane >> 3) & 3)) * 16;
-#pragma unroll
-  for (int j = 0; j < GW; ++j) {
-    long long r = n0 + RPL * (wave * GW + j) + lane / CPR;
-    r = r < N ? r : N - 1;
-    src[j] = W + r * K;
-  }
-#pragma unroll
-  for (int j = 0; j < GX; ++j) {
-    long long r = m0 + RPL * (wave * GX + j) + lane / CPR;
-    r = r < M ? r : M - 1;
-    src[GW + j] = X + r * K;
-  }
-  auto issue = [&](int step, int stage) {
-    int8_t* base = ring + stage * kStage;
-    const int k0 = step * kLine;
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      int off = k0 + coff[j & 1];
-      off = off < K - 16 ? off : K - 16;
-      int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
-                           : base + TN * kLine + (wave * GX + (j - GW)) * 1024;
-      load_lds16(src[j] + off, dst);
-    }
-  };
-
-  // Fragment offsets of quarter q within a 32-row block: row lane&31,
-  // logical chunk 2q + (lane>>5), stored at that chunk ^ key(row).
-  const int t = KL == 128 ? (lane >> 5) ^ ((lane >> 1) & 7) : (lane >> 5) ^ ((lane >> 1) & 3);
-  int foff[QPS];
-#pragma unroll
-  for (int q = 0; q < QPS; ++q) foff[q] = (lane & 31) * kLine + ((2 * q) ^ t) * 16;
-
-  v16i acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
-
-  const int wn = (wave / WGM) * WN;
-  const int wm = (wave % WGM) * WM;
-  const int nq = K / 32;                    // K quarters in total
-  const int nk = (nq + QPS - 1) / QPS;      // steps
-
-  v4i fa[2][FN], fb[2][FM];
-  auto read_frags = [&](int stage, int q, int slot) {
-    const int8_t* sw = ring + stage * kStage + wn * kLine + foff[q];
-    const int8_t* sx = ring + stage * kStage + (TN + wm) * kLine + foff[q];
-#pragma unroll
-    for (int i = 0; i < FN; ++i) fa[slot][i] = *reinterpret_cast<const v4i*>(sw + 32 * i * kLine);
-#pragma unroll
-    for (int j = 0; j < FM; ++j) fb[slot][j] = *reinterpret_cast<const v4i*>(sx + 32 * j * kLine);
-  };
-  auto mfmas = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot][i], fb[slot][j], acc[i][j],
-                                                          0, 0, 0);
-  };
-
-#pragma unroll
-  for (int st = 0; st < S; ++st) issue(st < nk ? st : nk - 1, st);
-  wait_vmcnt<G * (S - 1)>();
-  ring_barrier();
-  read_frags(0, 0, 0);
-  // With three or more stages the loads of a step are spread over the
-  // quarters of the next one (part 0 after the barrier, part q before
-  // quarter q's MFMAs) instead of being queued by all waves at once: they
-  // are needed only S - 2 steps later.  With two stages they are needed at
-  // the end of the next step and go out together.
-  constexpr int SPREAD = S >= 3 ? QPS : 1;
-  int stage = 0;
-  int pstep = 0, pstage = 0;                // the step being loaded and its stage
-  auto issue_part = [&](int part) {
-    int8_t* base = ring + pstage * kStage;
-    const int k0 = pstep * kLine;
-#pragma unroll
-    for (int j = part * G / SPREAD; j < (part + 1) * G / SPREAD; ++j) {
-      int off = k0 + coff[j & 1];
-      off = off < K - 16 ? off : K - 16;
-      int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
-                           : base + TN * kLine + (wave * GX + (j - GW)) * 1024;
-      load_lds16(src[j] + off, dst);
-    }
-  };
-  for (int k = 0; k + 1 < nk; ++k) {
-#pragma unroll
-    for (int q = 1; q < QPS; ++q) {
-      if (q < SPREAD && k > 0) issue_part(q);
-      read_frags(stage, q, q & 1);
-      mfmas((q - 1) & 1);
-    }
-    // Loads issued: steps up to k+S-1, all parts; step k+1 must be in.
-    wait_vmcnt<G * (S - 2)>();
-    wait_lgkmcnt0();
-    ring_barrier();
-    pstep = k + S < nk ? k + S : nk - 1;
-    pstage = stage;
-    issue_part(0);
-    stage = stage + 1 < S ? stage + 1 : 0;
-    read_frags(stage, 0, 0);
-    mfmas((QPS - 1) & 1);
-  }
-  {
-    const int qn = nq - QPS * (nk - 1);    // 1..QPS quarters in the last step
-#pragma unroll
-    for (int q = 1; q < QPS; ++q) {
-      if (q < qn) read_frags(stage, q, q & 1);
-      if (q - 1 < qn) mfmas((q - 1) & 1);
-    }
-    if (QPS - 1 < qn) mfmas((QPS - 1) & 1);
-  }
-  // No global->LDS load may still be in flight when the workgroup's LDS is
-  // released.
-  wait_vmcnt<0>();
-  write_tile32<FN, FM>(acc, m0 + wm, n0 + wn, lane, M, N, ws, as, row_sum, zp, y, acc_out, asym,
-                       status);
+  v16i acc[R::FN][R::FM];
+  R::run(W, X, M, N, K, n0, m0, ring, acc);
+  write_tile32<R::FN, R::FM>(acc, m0 + R::wave_m(wave), n0 + R::wave_n(wave), lane, M, N, ws,
+                             as, row_sum, zp, y, acc_out, asym, status);
 }
 
 template <int TN, int TM>

@@ -5,12 +5,38 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "quixicore_hip.h"
 
 namespace qc {
 
 // Compute units of the current device (the grid planners size by it).
 int device_cu_count();
+
+// Scratch of the allocating entry points: one cache entry per (device,
+// stream).  A call takes its stream's entry, holds the entry's `call` lock
+// from its first use of the buffers to its last launch (host threads sharing
+// a stream then enqueue whole calls, and stream order keeps one call's
+// kernels from reading another's scratch), and asks for buffer `tag` of at
+// least `bytes`.  A buffer only grows.  The one it replaces is freed after
+// the stream drains, unless it was handed out while the stream was being
+// captured into a graph (the graph has its address baked in): such a buffer
+// is retired and kept until the process ends.  Calls on different streams
+// never share a buffer; graphs captured on one stream share its buffers and
+// must not be replayed concurrently.  An entry point that holds `call` must
+// not call another that takes it.
+constexpr int kStreamBuffers = 2;
+struct StreamWorkspace {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex call;
+  void* ptr[kStreamBuffers] = {nullptr, nullptr};
+  size_t bytes[kStreamBuffers] = {0, 0};
+  bool captured[kStreamBuffers] = {false, false};
+};
+hipError_t stream_workspace(hipStream_t s, StreamWorkspace** out);
+hipError_t stream_buffer(StreamWorkspace* w, hipStream_t s, size_t bytes, int tag, void** out);
 
 struct GemvTuning {
   int rows_per_wave = 0;  // GEMV rows per wavefront (1, 2, 4, 7, 8, 14; 0 = from the shape)

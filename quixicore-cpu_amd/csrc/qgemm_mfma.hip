@@ -983,47 +983,10 @@ __global__ __launch_bounds__(64 * NW * KG) void qgemm_mfma(
 
 // Scratch (activation fragments, q4 bias, partial sums, row exponents) of
 // one qgemm call.  Region 0 holds one pass's fragments and partial sums,
-// region 1 the call's row exponents (live across all passes).
+// region 1 the call's row exponents (live across all passes).  Allocating
+// entry points take buffers 0 and 1 of the stream's cache entry
+// (stream_workspace, qc_internal.h).
 //
-// Allocating entry points take it from a per-(device, stream) cache: a call
-// holds that entry's `call` lock from its first use of the buffers to its
-// last launch, so two host threads on one stream enqueue whole calls, and
-// stream order then keeps one call's kernels from reading the other's
-// fragments.  A buffer only grows.  The one it replaces is freed after the
-// stream drains, unless it was handed out while the stream was being
-// captured into a graph (the graph has its address baked in): such a
-// buffer is retired and kept until the process ends.  Calls on different
-// streams never share a buffer.
-struct StreamWorkspace {
-  int device;
-  hipStream_t stream;
-  std::mutex call;
-  void* ptr[2] = {nullptr, nullptr};
-  size_t bytes[2] = {0, 0};
-  bool captured[2] = {false, false};
-};
-
-std::mutex g_ws_mu;                                        // guards the two lists below
-std::vector<std::unique_ptr<StreamWorkspace>> g_ws_table;  // entries live until exit
-std::vector<void*> g_ws_retired;
-
-hipError_t stream_workspace(hipStream_t s, StreamWorkspace** out) {
-  int dev = 0;
-  const hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  for (auto& w : g_ws_table)
-    if (w->device == dev && w->stream == s) {
-      *out = w.get();
-      return hipSuccess;
-    }
-  g_ws_table.push_back(std::make_unique<StreamWorkspace>());
-  g_ws_table.back()->device = dev;
-  g_ws_table.back()->stream = s;
-  *out = g_ws_table.back().get();
-  return hipSuccess;
-}
-
 // Where a call's scratch comes from: a per-stream cache entry (whose `call`
 // lock the caller holds), or a fixed region given by the caller -- region 1
 // at [0, fixed_split), region 0 at [fixed_split, fixed_bytes).  A fixed
@@ -1044,31 +1007,7 @@ struct Scratch {
       *out = fixed + lo;
       return hipSuccess;
     }
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    hipError_t e = hipStreamIsCapturing(s, &cap);
-    if (e != hipSuccess) return e;
-    const bool capturing = cap != hipStreamCaptureStatusNone;
-    if (w->bytes[tag] >= bytes) {
-      w->captured[tag] = w->captured[tag] || capturing;
-      *out = w->ptr[tag];
-      return hipSuccess;
-    }
-    if (w->ptr[tag] != nullptr) {
-      if (capturing || w->captured[tag]) {
-        std::lock_guard<std::mutex> lock(g_ws_mu);
-        g_ws_retired.push_back(w->ptr[tag]);
-      } else {
-        if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
-        if ((e = hipFree(w->ptr[tag])) != hipSuccess) return e;
-      }
-      w->ptr[tag] = nullptr;
-      w->bytes[tag] = 0;
-    }
-    if ((e = hipMalloc(&w->ptr[tag], bytes)) != hipSuccess) return e;
-    w->bytes[tag] = bytes;
-    w->captured[tag] = capturing;
-    *out = w->ptr[tag];
-    return hipSuccess;
+    return stream_buffer(w, s, bytes, tag, out);
   }
 };
 
