@@ -855,12 +855,12 @@ hipError_t launch_mb(const CSegs& sg, bool grp, bool aff, const void* x, int xty
 // planes q = 2^14 d0 + 2^7 d1 + d2 (d0 in [-128, 127], d1, d2 in [0, 127]).
 // The int8 MFMA main loop gives the exact int32 sums
 // D_t[m][n] = sum_k code[n][k] d_t[m][k] of all planes.
-//  * Up to kPlanesFusedM activation rows, mode 0: the planes of row m are
-//    rows 4m + t (t < 3; row 4m + 3 is zero) of an int8 matrix [4M][K], the
-//    main loop's operand A against the weight codes as operand B
+//  * Up to kPlanesFusedM activation rows: the planes of row m are rows
+//    4m + t (t < 3; row 4m + 3 is zero) of an int8 matrix [4M][K], the main
+//    loop's operand A against the weight codes as operand B
 //    (qc_int8_ring.h), so each lane's accumulators hold D_0..D_2 of one
-//    (m, n) and the GEMM's epilogue finishes the output: one launch per
-//    matrix after the prep.
+//    (m, n) and the GEMM's epilogue finishes the output: after the prep,
+//    one launch per matrix, or one for SwiGLU over gate and up together.
 //  * Otherwise the planes are rows 3m + t of [3M][K], launch_int8_gemm
 //    writes every D_t[m][n] of a matrix to scratch and a finish kernel
 //    combines them (and pairs gate / up for SwiGLU).
@@ -1097,12 +1097,17 @@ __global__ __launch_bounds__(kThreads) void cint8_planes_finish(
   store_y(y, m * ld + row, yt, v);
 }
 
-// One matrix of the fused form: its codes, scales, zero points, output and
-// (matrix 0 of mode 0) bias and activation.
+// The fused form's matrices and output.  Mode 0: one matrix (w, scale,
+// zero) with, on matrix 0 of the call, bias and activation (epi != 0).
+// SwiGLU: gate (w, scale, zero) and up (w2, scale2, zero2) of `rows` rows
+// each, y = SiLU(gate) * up.
 struct PlaneOut {
   const int8_t* w;
   const float* scale;
   const float* zero;
+  const int8_t* w2;
+  const float* scale2;
+  const float* zero2;
   void* y;
   long long ld;
   int ytype;
@@ -1112,29 +1117,56 @@ struct PlaneOut {
   int epi;
 };
 
+// Operand B of the SwiGLU form: 32-row blocks alternate between gate (even
+// blocks) and up (odd blocks), blocks 2c and 2c + 1 covering rows 32c..32c+31
+// of both matrices (rows past the last clamped to it).
+struct PairedRows {
+  const int8_t* gate;
+  const int8_t* up;
+  long long rows, k;
+  __device__ const int8_t* operator()(long long r) const {
+    const long long blk = r >> 5;
+    long long n = (blk >> 1) * 32 + (r & 31);
+    n = n < rows ? n : rows - 1;
+    // a bitwise select: a conditional between the two pointers is compiled
+    // as an indexed load from a two-entry array in private memory
+    const uint64_t g = reinterpret_cast<uintptr_t>(gate), u = reinterpret_cast<uintptr_t>(up);
+    const uint64_t base = g ^ ((g ^ u) & (0 - static_cast<uint64_t>(blk & 1)));
+    return reinterpret_cast<const int8_t*>(base) + n * k;
+  }
+};
+
 // The fused form: planes [4 mc][k] (operand A, TN rows per tile) against the
 // weight codes (operand B, TM rows per tile), then for each (activation row,
-// weight row) the combination and epilogue of the finish kernel, stored as
-// y[(m0 + r) * ld + n].  Lanes 0-31 of a store hold 32 consecutive n.
-template <int TN, int TM, int S, int WGN, int WGM>
+// weight row n) the combination and epilogue of the finish kernel, stored as
+// y[(m0 + r) * ld + n].  Lanes 0-31 of a store hold 32 consecutive n.  With
+// SWIGLU the B tiles pair gate and up blocks (PairedRows): in a wave tile of
+// 64 B rows (FM even), fragments j and j + 1 hold gate and up of the same n.
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU>
 __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
     const int8_t* __restrict__ planes, int mc, const PlaneOut o, const int* __restrict__ rexp,
     const int* __restrict__ dsum, const void* __restrict__ x, int xtype, long long ldx, int m0,
     int k, int tiles_n, int tiles_m) {
   using R = Int8Ring<TN, TM, S, WGN, WGM, 128>;
+  static_assert(!SWIGLU || R::FM % 2 == 0, "gate / up fragment pairs");
   __shared__ __attribute__((aligned(1024))) int8_t ring[R::kBytes];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int tn, tm;
   tile_of(blockIdx.x, tiles_n * tiles_m, tiles_n, tiles_m, tn, tm);
   const long long p0 = static_cast<long long>(tn) * TN + R::wave_n(wave);   // plane rows
-  const long long n0 = static_cast<long long>(tm) * TM + R::wave_m(wave);   // weight rows
+  const long long b0 = static_cast<long long>(tm) * TM + R::wave_m(wave);   // B rows
   v16i acc[R::FN][R::FM];
-  R::run(planes, o.w, o.rows, 4 * mc, k, static_cast<long long>(tn) * TN,
-         static_cast<long long>(tm) * TM, ring, acc);
+  if constexpr (SWIGLU)
+    R::run_rows(planes, PairedRows{o.w, o.w2, o.rows, k}, 4 * mc, k,
+                static_cast<long long>(tn) * TN, static_cast<long long>(tm) * TM, ring, acc);
+  else
+    R::run(planes, o.w, o.rows, 4 * mc, k, static_cast<long long>(tn) * TN,
+           static_cast<long long>(tm) * TM, ring, acc);
+  constexpr int JS = SWIGLU ? 2 : 1;
 #pragma unroll
-  for (int j = 0; j < R::FM; ++j) {
-    const long long n = n0 + 32 * j + (lane & 31);
+  for (int j = 0; j < R::FM; j += JS) {
+    const long long n = (SWIGLU ? b0 / 2 + 16 * j : b0 + 32 * j) + (lane & 31);
     if (n >= o.rows) continue;
 #pragma unroll
     for (int i = 0; i < R::FN; ++i)
@@ -1144,7 +1176,12 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
         if (r >= mc) continue;
         float v = plane_value(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], o.w,
                               o.scale, o.zero, n, r, m0, rexp, dsum, x, xtype, ldx, k);
-        if (o.epi) {
+        if constexpr (SWIGLU) {
+          const float up = plane_value(acc[i][j + 1][4 * g], acc[i][j + 1][4 * g + 1],
+                                       acc[i][j + 1][4 * g + 2], o.w2, o.scale2, o.zero2, n, r,
+                                       m0, rexp, dsum, x, xtype, ldx, k);
+          v = (v / (1.0f + expf(-v))) * up;
+        } else if (o.epi) {
           if (o.bias != nullptr) v += o.bias[n];
           v = linear_activation(v, o.act);
         }
@@ -1153,29 +1190,41 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
   }
 }
 
-template <int TN, int TM, int S, int WGN, int WGM>
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU>
 hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                               const int* dsum, const void* x, int xtype, long long ldx, int m0,
                               int k, hipStream_t s) {
   const int tiles_n = (4 * mc + TN - 1) / TN;
-  const int tiles_m = (o.rows + TM - 1) / TM;
-  cint8_planes_gemm<TN, TM, S, WGN, WGM><<<tiles_n * tiles_m, 64 * WGN * WGM, 0, s>>>(
+  // SwiGLU: 64 B rows per 32 output rows
+  const long long brows = SWIGLU ? 64LL * ((o.rows + 31) / 32) : o.rows;
+  const int tiles_m = static_cast<int>((brows + TM - 1) / TM);
+  cint8_planes_gemm<TN, TM, S, WGN, WGM, SWIGLU><<<tiles_n * tiles_m, 64 * WGN * WGM, 0, s>>>(
       planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, tiles_n, tiles_m);
   return hipGetLastError();
 }
 
 // Tile by plane rows (4 mc <= 4 kPlanesFusedM): the whole plane matrix in
-// one A tile, 64 weight rows per workgroup (224 workgroups at N = 14336).
+// one A tile; 64 output rows per workgroup (224 workgroups at N = 14336):
+// 64 weight rows, or 64 gate and 64 up rows in wave tiles of 64 B rows.
+template <bool SWIGLU>
 hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                         const int* dsum, const void* x, int xtype, long long ldx, int m0, int k,
                         hipStream_t s) {
+  constexpr int TM = SWIGLU ? 128 : 64;
   if (mc <= 8)
-    return launch_planes_gemm<32, 64, 8, 1, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+    return launch_planes_gemm<32, TM, SWIGLU ? 6 : 8, 1, 2, SWIGLU>(planes, mc, o, rexp, dsum, x,
+                                                                    xtype, ldx, m0, k, s);
   if (mc <= 16)
-    return launch_planes_gemm<64, 64, 6, 1, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+    return launch_planes_gemm<64, TM, SWIGLU ? 4 : 6, 1, 2, SWIGLU>(planes, mc, o, rexp, dsum, x,
+                                                                    xtype, ldx, m0, k, s);
   if (mc <= 32)
-    return launch_planes_gemm<128, 64, 4, 2, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
-  return launch_planes_gemm<256, 64, 3, 4, 1>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+    return launch_planes_gemm<128, TM, 4, 2, 2, SWIGLU>(planes, mc, o, rexp, dsum, x, xtype, ldx,
+                                                        m0, k, s);
+  if constexpr (SWIGLU)
+    return launch_planes_gemm<256, TM, 3, 4, 2, true>(planes, mc, o, rexp, dsum, x, xtype, ldx,
+                                                      m0, k, s);
+  return launch_planes_gemm<256, TM, 3, 4, 1, false>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0,
+                                                     k, s);
 }
 static_assert(kPlanesFusedM <= 64, "launch_fused tiles cover 256 plane rows");
 
@@ -1197,7 +1246,7 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
   const size_t es = L.xtype == QC_STORAGE_F32 ? 4 : 2;
   bool aligned = true;
   for (int i = 0; i < nmat; ++i) aligned = aligned && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
-  if (L.mode == 0 && m <= kPlanesFusedM && aligned) {
+  if (m <= kPlanesFusedM && aligned) {
     const size_t bytes = up256(4ull * m * k) + up256(4ull * m) + up256(12ull * m);
     std::unique_lock<std::mutex> hold;
     uint8_t* base = nullptr;
@@ -1211,11 +1260,17 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
     cint8_planes_prep<4><<<m, kPrepThreads, 0, s>>>(L.x, L.xtype, L.ldx, k, vec, planes, rexp,
                                                     dsum);
     e = hipGetLastError();
+    if (e == hipSuccess && L.mode == 1) {
+      const PlaneOut o{sg.w[0], sg.scale[0], sg.zero[0], sg.w[1], sg.scale[1], sg.zero[1],
+                       sg.y[0], sg.ld[0], sg.ytype[0], static_cast<int>(L.w[0].rows),
+                       nullptr, 0, 0};
+      return launch_fused<true>(planes, m, o, rexp, dsum, L.x, L.xtype, L.ldx, 0, k, s);
+    }
     for (int i = 0; i < nmat && e == hipSuccess; ++i) {
-      const PlaneOut o{sg.w[i], sg.scale[i], sg.zero[i], sg.y[i], sg.ld[i], sg.ytype[i],
-                       static_cast<int>(L.w[i].rows), sg.bias, sg.act,
+      const PlaneOut o{sg.w[i], sg.scale[i], sg.zero[i], nullptr, nullptr, nullptr, sg.y[i],
+                       sg.ld[i], sg.ytype[i], static_cast<int>(L.w[i].rows), sg.bias, sg.act,
                        i == 0 && (sg.bias != nullptr || sg.act != 0) ? 1 : 0};
-      e = launch_fused(planes, m, o, rexp, dsum, L.x, L.xtype, L.ldx, 0, k, s);
+      e = launch_fused<false>(planes, m, o, rexp, dsum, L.x, L.xtype, L.ldx, 0, k, s);
     }
     return e;
   }

@@ -60,6 +60,15 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Operand B rows of a plain [M][K] matrix (rows past M clamped to M - 1).
+struct Int8Rows {
+  const int8_t* b;
+  long long rows, k;
+  __device__ const int8_t* operator()(long long r) const {
+    return b + (r < rows ? r : rows - 1) * k;
+  }
+};
+
 // Full-line ring (K % 32 == 0, both operands 16-byte aligned with rows K
 // bytes apart).  Each K step covers KL bytes of every A and B row of the
 // tile; with KL = 128 that is whole 128-byte cache lines, for which the
@@ -116,6 +125,14 @@ struct Int8Ring {
   __device__ static void run(const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M,
                              int N, int K, long long n0, long long m0, int8_t* ring,
                              v16i (&acc)[FN][FM]) {
+    run_rows(A, Int8Rows{B, M, K}, N, K, n0, m0, ring, acc);
+  }
+
+  // The same with operand B row r at brow(r) (K bytes, 16-byte aligned, any
+  // r the tile touches mapped to a readable row).
+  template <class BRow>
+  __device__ static void run_rows(const int8_t* __restrict__ A, const BRow& brow, int N, int K,
+                                  long long n0, long long m0, int8_t* ring, v16i (&acc)[FN][FM]) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
@@ -136,11 +153,7 @@ struct Int8Ring {
       src[j] = A + r * K;
     }
 #pragma unroll
-    for (int j = 0; j < GX; ++j) {
-      long long r = m0 + RPL * (wave * GX + j) + lane / CPR;
-      r = r < M ? r : M - 1;
-      src[GW + j] = B + r * K;
-    }
+    for (int j = 0; j < GX; ++j) src[GW + j] = brow(m0 + RPL * (wave * GX + j) + lane / CPR);
     auto issue = [&](int step, int stage) {
       int8_t* base = ring + stage * kStage;
       const int k0 = step * KL;

@@ -461,6 +461,42 @@ def test_cint8_row_plane_route_epilogues(qc, oracle, synth, dev):
         assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("m,rows", [(2, 300), (12, 300), (20, 96), (40, 1000), (64, 130)])
+def test_cint8_row_plane_swiglu_sizes(qc, oracle, synth, dev, m, rows):
+    """SwiGLU on the row-plane route (gate and up paired in one GEMM) at each
+    tile size of the one-launch form and at row counts that are not a
+    multiple of 32: every finite output within a few f32 ulp of SiLU(gate) *
+    up over the same call's plain projections (themselves within the
+    contract of the f64 oracle), and the row holding +inf in the class those
+    projections give."""
+    import torch
+    cols = 1024
+    affine = m % 4 == 0                   # both matrices alike (a call's matrices share the form)
+    g, gk, gwhat = _planes_case(qc, oracle, synth, dev, rows, cols, m, affine, 101 + m)
+    u, uk, uwhat = _planes_case(qc, oracle, synth, dev, rows, cols, m, affine, 202 + m)
+    x = synth.normal_fast(303 + m, m * cols).reshape(m, cols)
+    bad = m - 1
+    x[bad, 5] = np.inf
+    X = torch.from_numpy(x).to(dev)
+    print(f"cint8 planes swiglu m={m} rows={rows}", flush=True)
+    out = torch.full((m, rows), 7.0, device=dev)
+    assert qc.cint8_project_raw(1, [g, u], X, 0, m, [out], [0]) == 0
+    pg, pu = torch.empty((m, rows), device=dev), torch.empty((m, rows), device=dev)
+    assert qc.cint8_project_raw(0, [g, u], X, 0, m, [pg, pu], [0, 0]) == 0
+    pg, pu, out = pg.cpu().numpy(), pu.cpu().numpy(), out.cpu().numpy()
+    fin = [r for r in range(m) if r != bad]
+    _check_contract(pg[fin], x[fin], gwhat)
+    _check_contract(pu[fin], x[fin], uwhat)
+    gv = pg.astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = gv / (1.0 + np.exp(-gv)) * pu.astype(np.float64)
+    assert np.allclose(out[fin], want[fin], rtol=1e-5, atol=1e-6)
+    for got, ref in ((np.isnan(out[bad]), np.isnan(want[bad])),
+                     (np.isposinf(out[bad]), np.isposinf(want[bad])),
+                     (np.isneginf(out[bad]), np.isneginf(want[bad]))):
+        assert np.array_equal(got, ref), np.flatnonzero(got != ref)[:5]
+
+
 def test_cint8_row_plane_route_nonfinite_rows(qc, oracle, synth, dev):
     """Activation rows holding +-inf or NaN on the row-plane route: those
     rows get the reference's f32 result class per output, the finite rows
