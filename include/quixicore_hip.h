@@ -23,6 +23,13 @@
  *     instead: the inputs are scanned first, the call blocks, returns 3 and
  *     writes no output if any value is non-finite.
  *   - Results are deterministic: rerunning a call gives bit-identical output.
+ *   - Scratch: entry points whose kernels need device scratch (qc_hip_qgemm
+ *     from M = 2, the canonical int8 projections from M = 2, the affine
+ *     canonical W8A8 route) take it from a per-(device, stream) cache that
+ *     only grows; the first call on a stream, or one needing more, allocates
+ *     (hipMalloc), later calls do not.  Calls on one stream share its buffers
+ *     in stream order; graphs captured on a stream keep that stream's buffers
+ *     and must not be replayed concurrently with each other.
  */
 #ifndef QUIXICORE_HIP_H
 #define QUIXICORE_HIP_H
