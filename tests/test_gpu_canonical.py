@@ -461,12 +461,14 @@ def test_cint8_row_plane_route_epilogues(qc, oracle, synth, dev):
         assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
 
 
-@pytest.mark.parametrize("m,rows", [(2, 300), (12, 300), (20, 96), (40, 1000), (64, 130)])
+@pytest.mark.parametrize("m,rows", [(2, 300), (12, 300), (20, 96), (40, 1000), (64, 130),
+                                    (100, 200)])
 def test_cint8_row_plane_swiglu_sizes(qc, oracle, synth, dev, m, rows):
     """SwiGLU on the row-plane route (gate and up paired in one GEMM) at each
-    tile size of the one-launch form and at row counts that are not a
-    multiple of 32: every finite output within a few f32 ulp of SiLU(gate) *
-    up over the same call's plain projections (themselves within the
+    tile size of the one-launch form, above 64 rows (the finish kernel), and
+    at row counts that are not a multiple of 32: every finite output within
+    a few f32 ulp of SiLU(gate) * up over the same call's plain projections
+    (themselves within the
     contract of the f64 oracle), and the row holding +inf in the class those
     projections give."""
     import torch
