@@ -468,9 +468,8 @@ def test_cint8_row_plane_swiglu_sizes(qc, oracle, synth, dev, m, rows):
     tile size of the one-launch form, above 64 rows (the finish kernel), and
     at row counts that are not a multiple of 32: every finite output within
     a few f32 ulp of SiLU(gate) * up over the same call's plain projections
-    (themselves within the
-    contract of the f64 oracle), and the row holding +inf in the class those
-    projections give."""
+    (themselves within the contract of the f64 oracle), and the row holding
+    +inf in the class those projections give."""
     import torch
     cols = 1024
     affine = m % 4 == 0                   # both matrices alike (a call's matrices share the form)
