@@ -855,15 +855,14 @@ hipError_t launch_mb(const CSegs& sg, bool grp, bool aff, const void* x, int xty
 // planes q = 2^14 d0 + 2^7 d1 + d2 (d0 in [-128, 127], d1, d2 in [0, 127]).
 // The int8 MFMA main loop gives the exact int32 sums
 // D_t[m][n] = sum_k code[n][k] d_t[m][k] of all planes.
-//  * Up to kPlanesFusedM activation rows: the planes of row m are rows
-//    4m + t (t < 3; row 4m + 3 is zero) of an int8 matrix [4M][K], the main
-//    loop's operand A against the weight codes as operand B
-//    (qc_int8_ring.h), so each lane's accumulators hold D_0..D_2 of one
-//    (m, n) and the GEMM's epilogue finishes the output: after the prep,
-//    one launch per matrix, or one for SwiGLU over gate and up together.
-//  * Otherwise the planes are rows 3m + t of [3M][K], launch_int8_gemm
-//    writes every D_t[m][n] of a matrix to scratch and a finish kernel
-//    combines them (and pairs gate / up for SwiGLU).
+// The planes of row m are rows 4m + t (t < 3; row 4m + 3 is zero) of an
+// int8 matrix [4M][K], the main loop's operand A against the weight codes as
+// operand B (qc_int8_ring.h), so each lane's accumulators hold D_0..D_2 of
+// one (m, n) and the GEMM's epilogue finishes the output: after the prep, one
+// launch per matrix, or one for SwiGLU over gate and up together (per chunk
+// of kPlanesChunkM rows).  Writing every D_t to scratch for a separate
+// finish kernel instead took 1.5x as long at M = 512 (208 against 137 us,
+// N = 14336, K = 4096): 88 MB of int32 sums written and read back.
 // The combination forms 2^14 D0 + 2^7 D1 + D2 exactly (an integer below
 // 2^53, in double), minus z (2^14 S0 + 2^7 S1 + S2), S_t = sum_k d_t[m][k],
 // for an integral zero point z, rounds it once to f32 and scales it by 2^e
@@ -877,7 +876,6 @@ namespace {
 constexpr int kPlanesMaxK = 16384;
 constexpr int kPlanesChunkM = 1024;     // activation rows per pass: bounds the scratch
 constexpr int kPlanesMinM = 2;     // N=14336, K=4096, M = 2: 22.9 us on the digit-dot kernel, 18.9 here at M = 3
-constexpr int kPlanesFusedM = 64;  // activation rows of the one-launch (fused epilogue) form
 constexpr int kPlanesNonfinite = 0x40000000;
 
 // The prep kernel: 1024 threads per activation row, each holding up to 16 of
@@ -930,10 +928,9 @@ __device__ __forceinline__ void load4(const void* x, long long xr, int c, int xt
 }
 
 // One workgroup per activation row (x rows blockIdx.x, ldx apart); the
-// planes of row m are rows PR * m + t (PR = 4: row PR * m + 3 is zeroed).  A
-// row holding NaN or +-inf gets the maximum +inf, zero digits and the flag
-// exponent kPlanesNonfinite.
-template <int PR>
+// planes of row m are rows 4m + t (row 4m + 3 is zeroed).  A row holding NaN
+// or +-inf gets the maximum +inf, zero digits and the flag exponent
+// kPlanesNonfinite.
 __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     const void* __restrict__ x, int xtype, long long ldx, int k, bool vec,
     int8_t* __restrict__ planes, int* __restrict__ rexp, int* __restrict__ dsum) {
@@ -963,7 +960,7 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
   (void)frexpf(mx, &ex);                       // mx < 2^ex
   const int e = ex - 21;
   int sum[3] = {0, 0, 0};
-  int8_t* p0 = planes + (static_cast<long long>(PR) * m) * k;
+  int8_t* p0 = planes + (4LL * m) * k;
 #pragma unroll
   for (int g = 0; g < kPrepGroups; ++g) {
     const int c = 4 * (static_cast<int>(threadIdx.x) + g * kPrepThreads);
@@ -984,7 +981,7 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     *reinterpret_cast<uint32_t*>(p0 + c) = w0;
     *reinterpret_cast<uint32_t*>(p0 + k + c) = w1;
     *reinterpret_cast<uint32_t*>(p0 + 2LL * k + c) = w2;
-    if constexpr (PR == 4) *reinterpret_cast<uint32_t*>(p0 + 3LL * k + c) = 0u;
+    *reinterpret_cast<uint32_t*>(p0 + 3LL * k + c) = 0u;
   }
   block_sum3(sum, ired);
   if (threadIdx.x == 0) {
@@ -994,23 +991,6 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     dsum[3 * m + 2] = sum[2];
   }
 }
-
-struct PlaneAcc {
-  const int32_t* acc[3];   // per matrix: [3 mc][rows]
-  int rows[3];
-};
-
-// One matrix of the finish kernel, as plain values: the kernel reads its
-// argument tables into locals with constant indices and selects by value
-// (indexing an argument array, or taking its address, moves the whole
-// argument to private memory in every thread).
-struct PlaneMat {
-  const int8_t* w;
-  const float* scale;
-  const float* zero;
-  const int32_t* acc;
-  long long rows;
-};
 
 // Projection of activation row (m0 + mm) on row n of one matrix from its
 // plane sums a0..a2 (D_0..D_2).
@@ -1047,54 +1027,6 @@ __device__ __forceinline__ float plane_value(int32_t a0, int32_t a1, int32_t a2,
     f = static_cast<float>(d);
   }
   return sc * ldexpf(f, e);
-}
-
-// plane_value from the finish kernel's scratch: D_t of activation row mm at
-// [(3 mm + t) rows + n].
-__device__ __forceinline__ float plane_value_at(const PlaneMat& t, int n, int mm, int m0,
-                                                const int* rexp, const int* dsum, const void* x,
-                                                int xtype, long long ldx, int k) {
-  const int32_t* a = t.acc + (3LL * mm) * t.rows + n;
-  return plane_value(a[0], a[t.rows], a[2 * t.rows], t.w, t.scale, t.zero, n, mm, m0, rexp, dsum,
-                     x, xtype, ldx, k);
-}
-
-// One thread per (activation row, output unit): activation row blockIdx.y,
-// unit blockIdx.x * kThreads + threadIdx.x -- mode 0 a logical row (matrix
-// by the segment starts), mode 1 a gate / up pair.  The stores are the
-// shared epilogue's (bias and activation on matrix 0; SiLU(gate) * up).
-__global__ __launch_bounds__(kThreads) void cint8_planes_finish(
-    const CSegs sg, const PlaneAcc pa, const int* __restrict__ rexp, const int* __restrict__ dsum,
-    const void* __restrict__ x, int xtype, long long ldx, int m0, int k) {
-  const int mm = blockIdx.y;
-  const int m = m0 + mm;
-  const int u = static_cast<int>(blockIdx.x) * kThreads + static_cast<int>(threadIdx.x);
-  const PlaneMat t0{sg.w[0], sg.scale[0], sg.zero[0], pa.acc[0], pa.rows[0]};
-  const PlaneMat t1{sg.w[1], sg.scale[1], sg.zero[1], pa.acc[1], pa.rows[1]};
-  const PlaneMat t2{sg.w[2], sg.scale[2], sg.zero[2], pa.acc[2], pa.rows[2]};
-  if (sg.mode == 1) {
-    if (u >= t0.rows) return;
-    const float gate = plane_value_at(t0, u, mm, m0, rexp, dsum, x, xtype, ldx, k);
-    const float up = plane_value_at(t1, u, mm, m0, rexp, dsum, x, xtype, ldx, k);
-    const float silu = gate / (1.0f + expf(-gate));
-    store_y(sg.y[0], m * sg.ld[0] + u, sg.ytype[0], silu * up);
-    return;
-  }
-  const int nseg = sg.nseg, s1 = sg.start[1], s2 = sg.start[2];
-  const int total = nseg == 1 ? s1 : nseg == 2 ? s2 : sg.start[3];
-  if (u >= total) return;
-  const int seg = (nseg > 2 && u >= s2) ? 2 : (nseg > 1 && u >= s1) ? 1 : 0;
-  const PlaneMat t = seg == 0 ? t0 : seg == 1 ? t1 : t2;
-  const int row = u - (seg == 2 ? s2 : seg == 1 ? s1 : 0);
-  float v = plane_value_at(t, row, mm, m0, rexp, dsum, x, xtype, ldx, k);
-  if (seg == 0 && (sg.bias != nullptr || sg.act != 0)) {
-    if (sg.bias != nullptr) v += sg.bias[row];
-    v = linear_activation(v, sg.act);
-  }
-  void* const y = seg == 0 ? sg.y[0] : seg == 1 ? sg.y[1] : sg.y[2];
-  const long long ld = seg == 0 ? sg.ld[0] : seg == 1 ? sg.ld[1] : sg.ld[2];
-  const int yt = seg == 0 ? sg.ytype[0] : seg == 1 ? sg.ytype[1] : sg.ytype[2];
-  store_y(y, m * ld + row, yt, v);
 }
 
 // The fused form's matrices and output.  Mode 0: one matrix (w, scale,
@@ -1138,7 +1070,7 @@ struct PairedRows {
 
 // The fused form: planes [4 mc][k] (operand A, TN rows per tile) against the
 // weight codes (operand B, TM rows per tile), then for each (activation row,
-// weight row n) the combination and epilogue of the finish kernel, stored as
+// weight row n) the combination and the shared epilogue, stored as
 // y[(m0 + r) * ld + n].  Lanes 0-31 of a store hold 32 consecutive n.  With
 // SWIGLU the B tiles pair gate and up blocks (PairedRows): in a wave tile of
 // 64 B rows (FM even), fragments j and j + 1 hold gate and up of the same n.
@@ -1203,9 +1135,11 @@ hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, c
   return hipGetLastError();
 }
 
-// Tile by plane rows (4 mc <= 4 kPlanesFusedM): the whole plane matrix in
-// one A tile; 64 output rows per workgroup (224 workgroups at N = 14336):
-// 64 weight rows, or 64 gate and 64 up rows in wave tiles of 64 B rows.
+// Tile by plane rows: up to 64 activation rows the whole plane matrix in one
+// A tile and 64 output rows per workgroup (224 workgroups at N = 14336): 64
+// weight rows, or 64 gate and 64 up rows in wave tiles of 64 B rows; up to
+// 128 rows two A tiles of 256 by 128 B rows (224 workgroups at N = 14336, where
+// 448 of 256 x 64 took 1.4x as long); above, the W8A8 kernel's 256 x 256 tile.
 template <bool SWIGLU>
 hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                         const int* dsum, const void* x, int xtype, long long ldx, int m0, int k,
@@ -1220,13 +1154,19 @@ hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const i
   if (mc <= 32)
     return launch_planes_gemm<128, TM, 4, 2, 2, SWIGLU>(planes, mc, o, rexp, dsum, x, xtype, ldx,
                                                         m0, k, s);
-  if constexpr (SWIGLU)
-    return launch_planes_gemm<256, TM, 3, 4, 2, true>(planes, mc, o, rexp, dsum, x, xtype, ldx,
-                                                      m0, k, s);
-  return launch_planes_gemm<256, TM, 3, 4, 1, false>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0,
-                                                     k, s);
+  if (mc <= 64) {
+    if constexpr (SWIGLU)
+      return launch_planes_gemm<256, TM, 3, 4, 2, true>(planes, mc, o, rexp, dsum, x, xtype, ldx,
+                                                        m0, k, s);
+    return launch_planes_gemm<256, TM, 3, 4, 1, false>(planes, mc, o, rexp, dsum, x, xtype, ldx,
+                                                       m0, k, s);
+  }
+  if (mc <= 128)
+    return launch_planes_gemm<256, 128, 3, 4, 2, SWIGLU>(planes, mc, o, rexp, dsum, x, xtype, ldx,
+                                                         m0, k, s);
+  return launch_planes_gemm<256, 256, 2, 4, 2, SWIGLU>(planes, mc, o, rexp, dsum, x, xtype, ldx,
+                                                       m0, k, s);
 }
-static_assert(kPlanesFusedM <= 64, "launch_fused tiles cover 256 plane rows");
 
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
@@ -1241,82 +1181,42 @@ hipError_t call_scratch(hipStream_t s, size_t bytes, std::unique_lock<std::mutex
   return stream_buffer(ws, s, bytes, 0, out);
 }
 
+// All checks done by the caller, which routes only 16-byte aligned codes here.
 hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hipStream_t s) {
   const int nmat = L.mode == 1 ? 2 : L.nw;
   const size_t es = L.xtype == QC_STORAGE_F32 ? 4 : 2;
-  bool aligned = true;
-  for (int i = 0; i < nmat; ++i) aligned = aligned && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
-  if (m <= kPlanesFusedM && aligned) {
-    const size_t bytes = up256(4ull * m * k) + up256(4ull * m) + up256(12ull * m);
-    std::unique_lock<std::mutex> hold;
-    uint8_t* base = nullptr;
-    hipError_t e = call_scratch(s, bytes, hold, reinterpret_cast<void**>(&base));
-    if (e != hipSuccess) return e;
+  const bool vec = L.xtype == QC_STORAGE_F32 && reinterpret_cast<uintptr_t>(L.x) % 16 == 0 &&
+                   L.ldx % 4 == 0;
+  // chunks of kPlanesChunkM rows, one after the other in one buffer
+  const int mc0 = std::min(kPlanesChunkM, m);
+  const size_t bytes = up256(4ull * mc0 * k) + up256(4ull * mc0) + up256(12ull * mc0);
+  std::unique_lock<std::mutex> hold;
+  uint8_t* base = nullptr;
+  hipError_t e = call_scratch(s, bytes, hold, reinterpret_cast<void**>(&base));
+  if (e != hipSuccess) return e;
+  for (int m0 = 0; m0 < m && e == hipSuccess; m0 += kPlanesChunkM) {
+    const int mc = std::min(kPlanesChunkM, m - m0);
     int8_t* planes = reinterpret_cast<int8_t*>(base);
-    int* rexp = reinterpret_cast<int*>(base + up256(4ull * m * k));
-    int* dsum = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rexp) + up256(4ull * m));
-    const bool vec = L.xtype == QC_STORAGE_F32 && reinterpret_cast<uintptr_t>(L.x) % 16 == 0 &&
-                     L.ldx % 4 == 0;
-    cint8_planes_prep<4><<<m, kPrepThreads, 0, s>>>(L.x, L.xtype, L.ldx, k, vec, planes, rexp,
-                                                    dsum);
+    int* rexp = reinterpret_cast<int*>(base + up256(4ull * mc * k));
+    int* dsum = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rexp) + up256(4ull * mc));
+    const void* xc = static_cast<const uint8_t*>(L.x) + es * static_cast<size_t>(m0) * L.ldx;
+    cint8_planes_prep<<<mc, kPrepThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, planes, rexp, dsum);
     e = hipGetLastError();
     if (e == hipSuccess && L.mode == 1) {
       const PlaneOut o{sg.w[0], sg.scale[0], sg.zero[0], sg.w[1], sg.scale[1], sg.zero[1],
                        sg.y[0], sg.ld[0], sg.ytype[0], static_cast<int>(L.w[0].rows),
                        nullptr, 0, 0};
-      return launch_fused<true>(planes, m, o, rexp, dsum, L.x, L.xtype, L.ldx, 0, k, s);
+      e = launch_fused<true>(planes, mc, o, rexp, dsum, L.x, L.xtype, L.ldx, m0, k, s);
+      continue;
     }
     for (int i = 0; i < nmat && e == hipSuccess; ++i) {
       const PlaneOut o{sg.w[i], sg.scale[i], sg.zero[i], nullptr, nullptr, nullptr, sg.y[i],
                        sg.ld[i], sg.ytype[i], static_cast<int>(L.w[i].rows), sg.bias, sg.act,
                        i == 0 && (sg.bias != nullptr || sg.act != 0) ? 1 : 0};
-      e = launch_fused<false>(planes, m, o, rexp, dsum, L.x, L.xtype, L.ldx, 0, k, s);
+      e = launch_fused<false>(planes, mc, o, rexp, dsum, L.x, L.xtype, L.ldx, m0, k, s);
     }
-    return e;
   }
-  // chunks of kPlanesChunkM rows, one after the other in one buffer
-  auto chunk_bytes = [&](int mc) {
-    size_t b = up256(3ull * mc * k) + up256(4ull * mc) + up256(12ull * mc);
-    for (int i = 0; i < nmat; ++i) b += up256(12ull * mc * static_cast<size_t>(L.w[i].rows));
-    return b;
-  };
-  std::unique_lock<std::mutex> hold;
-  uint8_t* base = nullptr;
-  hipError_t e = call_scratch(s, chunk_bytes(std::min(kPlanesChunkM, m)), hold,
-                              reinterpret_cast<void**>(&base));
-  if (e != hipSuccess) return e;
-  for (int m0 = 0; m0 < m; m0 += kPlanesChunkM) {
-    const int mc = std::min(kPlanesChunkM, m - m0);
-    int8_t* planes = reinterpret_cast<int8_t*>(base);
-    int* rexp = reinterpret_cast<int*>(base + up256(3ull * mc * k));
-    int* dsum = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rexp) + up256(4ull * mc));
-    uint8_t* cur = reinterpret_cast<uint8_t*>(dsum) + up256(12ull * mc);
-    PlaneAcc pa{};
-    const void* xc = static_cast<const uint8_t*>(L.x) + es * static_cast<size_t>(m0) * L.ldx;
-    const bool vec = L.xtype == QC_STORAGE_F32 && reinterpret_cast<uintptr_t>(L.x) % 16 == 0 &&
-                     L.ldx % 4 == 0;
-    cint8_planes_prep<3><<<mc, kPrepThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, planes, rexp,
-                                                     dsum);
-    e = hipGetLastError();
-    for (int i = 0; i < nmat && e == hipSuccess; ++i) {
-      int32_t* acc = reinterpret_cast<int32_t*>(cur);
-      cur += up256(12ull * mc * static_cast<size_t>(L.w[i].rows));
-      pa.acc[i] = acc;
-      pa.rows[i] = static_cast<int>(L.w[i].rows);
-      e = launch_int8_gemm(L.w[i].codes, planes, nullptr, nullptr, nullptr, nullptr, nullptr, acc,
-                           3LL * mc, L.w[i].rows, k, false, nullptr, s);
-    }
-    if (e == hipSuccess) {
-      const long long units = L.mode == 1 ? L.w[0].rows : sg.start[sg.nseg];
-      const dim3 grid(static_cast<unsigned>((units + kThreads - 1) / kThreads),
-                      static_cast<unsigned>(mc));
-      cint8_planes_finish<<<grid, kThreads, 0, s>>>(sg, pa, rexp, dsum, L.x, L.xtype, L.ldx, m0,
-                                                    k);
-      e = hipGetLastError();
-    }
-    if (e != hipSuccess) return e;
-  }
-  return hipSuccess;
+  return e;
 }
 
 }  // namespace
