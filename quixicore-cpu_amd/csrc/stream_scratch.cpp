@@ -56,7 +56,9 @@ hipError_t stream_buffer(StreamWorkspace* w, hipStream_t s, size_t bytes, int ta
     w->ptr[tag] = nullptr;
     w->bytes[tag] = 0;
   }
-  if ((e = hipMalloc(&w->ptr[tag], bytes ? bytes : 256)) != hipSuccess) return e;
+  void* p = nullptr;
+  if ((e = hipMalloc(&p, bytes ? bytes : 256)) != hipSuccess) return e;
+  w->ptr[tag] = p;
   w->bytes[tag] = bytes ? bytes : 256;
   w->captured[tag] = capturing;
   *out = w->ptr[tag];
