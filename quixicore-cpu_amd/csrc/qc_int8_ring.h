@@ -50,6 +50,13 @@ __device__ __forceinline__ void load_lds16(const int8_t* g, int8_t* lds) {
 #endif
 }
 
+// The same with 4 bytes per lane, to LDS byte lds + 4 * lane.
+__device__ __forceinline__ void load_lds4(const void* g, int8_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+#endif
+}
+
 // Workgroup barrier for the direct-to-LDS pipeline.  __syncthreads() would
 // make the compiler drain every outstanding global->LDS load (vmcnt(0)) and
 // defeat the multi-stage prefetch; here the waits are explicit and the empty
@@ -59,6 +66,27 @@ __device__ __forceinline__ void ring_barrier() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+
+// The default per-step hook of Int8Ring::run_rows: nothing.
+struct Int8NoStep {
+  template <class Acc>
+  __device__ void operator()(int, Acc&) const {}
+};
+
+// The default side data of Int8Ring::run_rows: none.  A side policy moves,
+// per K step, kLoads global->LDS gathers of 4 bytes per lane and wave
+// (issue(step, wave, stage_base): slots wave * kLoads + q, 256 bytes each,
+// of that stage's side area) beside the operand tiles, on the same path, so
+// the ring's waits and barriers cover them; read(step, stage_base) is called
+// once per step, in order, while that step's stage is valid, to move what
+// the step hook needs into registers.  (A plain global load whose result is
+// used while global->LDS loads are in flight makes the compiler wait for all
+// of them: per-step data that way would drain the ring every step.)
+struct Int8NoSide {
+  static constexpr int kLoads = 0;
+  __device__ void issue(int, int, int8_t*) const {}
+  __device__ void read(int, const int8_t*) {}
+};
 
 // Operand B rows of a plain [M][K] matrix (rows past M clamped to M - 1).
 struct Int8Rows {
@@ -112,6 +140,9 @@ struct Int8Ring {
   static constexpr int G = GW + GX;
   static constexpr int kStage = (TN + TM) * KL;
   static constexpr int kBytes = S * kStage;
+  // LDS bytes with a side policy: its areas follow the S operand stages.
+  template <class Side>
+  static constexpr int kBytesWith = kBytes + S * NW * Side::kLoads * 256;
   static_assert(FN >= 1 && FM >= 1 && GW >= 1 && GX >= 1 && S >= 2, "tile shape");
   static_assert(KL == 64 || (GW % 2 == 0 && GX % 2 == 0), "8-row groups alternate swizzle parity");
   static_assert(G * (S - 1) < 64, "vmcnt range");
@@ -129,12 +160,20 @@ struct Int8Ring {
   }
 
   // The same with operand B row r at brow(r) (K bytes, 16-byte aligned, any
-  // r the tile touches mapped to a readable row).
-  template <class BRow>
+  // r the tile touches mapped to a readable row), and step(k, acc) called
+  // once the MFMAs of K step k are in acc (it may fold and clear them: the
+  // next step accumulates onto whatever it leaves).  With a side policy,
+  // `ring` holds kBytesWith<Side> bytes.
+  template <class BRow, class Step = Int8NoStep, class Side = Int8NoSide>
   __device__ static void run_rows(const int8_t* __restrict__ A, const BRow& brow, int N, int K,
-                                  long long n0, long long m0, int8_t* ring, v16i (&acc)[FN][FM]) {
+                                  long long n0, long long m0, int8_t* ring, v16i (&acc)[FN][FM],
+                                  Step step = Step(), Side* side = nullptr) {
+    constexpr int XL = Side::kLoads;
+    constexpr int GT = G + XL;                // loads per wave per step
+    static_assert(GT * (S - 1) < 64, "vmcnt range");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    auto side_base = [&](int stage) { return ring + kBytes + stage * NW * XL * 256; };
 
     // Load j of a wave covers operand rows r = RPL * (wave * GW + j) + lane / CPR
     // (A; likewise B with GX), lane writing slot lane % CPR of its row.  Swizzle
@@ -165,6 +204,7 @@ struct Int8Ring {
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
         load_lds16(src[j] + off, dst);
       }
+      if constexpr (XL > 0) side->issue(step, wave, side_base(stage));
     };
 
     // Fragment offsets of quarter q within a 32-row block: row lane&31,
@@ -206,7 +246,7 @@ struct Int8Ring {
 
 #pragma unroll
     for (int st = 0; st < S; ++st) issue(st < nk ? st : nk - 1, st);
-    wait_vmcnt<G * (S - 1)>();
+    wait_vmcnt<GT * (S - 1)>();
     ring_barrier();
     read_frags(0, 0, 0);
     // With three or more stages the loads of a step are spread over the
@@ -228,16 +268,21 @@ struct Int8Ring {
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
         load_lds16(src[j] + off, dst);
       }
+      if constexpr (XL > 0)
+        if (part == 0) side->issue(pstep, wave, side_base(pstage));
     };
+    static_assert(XL == 0 || QPS > 1, "side data read in quarter 1");
     for (int k = 0; k + 1 < nk; ++k) {
 #pragma unroll
       for (int q = 1; q < QPS; ++q) {
         if (q < SPREAD && k > 0) issue_part(q);
         read_frags(stage, q, q & 1);
+        if constexpr (XL > 0)
+          if (q == 1) side->read(k, side_base(stage));
         mfmas((q - 1) & 1);
       }
       // Loads issued: steps up to k+S-1, all parts; step k+1 must be in.
-      wait_vmcnt<G * (S - 2)>();
+      wait_vmcnt<GT * (S - 2)>();
       wait_lgkmcnt0();
       ring_barrier();
       pstep = k + S < nk ? k + S : nk - 1;
@@ -246,8 +291,10 @@ struct Int8Ring {
       stage = stage + 1 < S ? stage + 1 : 0;
       read_frags(stage, 0, 0);
       mfmas((QPS - 1) & 1);
+      step(k, acc);
     }
     {
+      if constexpr (XL > 0) side->read(nk - 1, side_base(stage));
       const int qn = nq - QPS * (nk - 1);    // 1..QPS quarters in the last step
 #pragma unroll
       for (int q = 1; q < QPS; ++q) {
@@ -255,6 +302,7 @@ struct Int8Ring {
         if (q - 1 < qn) mfmas((q - 1) & 1);
       }
       if (QPS - 1 < qn) mfmas((QPS - 1) & 1);
+      step(nk - 1, acc);
     }
     // No global->LDS load may still be in flight when the workgroup's LDS is
     // released.

@@ -498,6 +498,79 @@ def test_cint8_row_plane_swiglu_sizes(qc, oracle, synth, dev, m, rows):
         assert np.array_equal(got, ref), np.flatnonzero(got != ref)[:5]
 
 
+@pytest.mark.parametrize("groups,affine,fractional,m,mode,wide", [
+    (16, False, False, 12, 0, False),   # groups of 128 columns
+    (16, True, False, 3, 0, False),     # integral zero points (exact int32 group sums), 3 rows
+    (8, True, True, 40, 0, False),      # groups of 256, fractional zero points (f32 form)
+    (4, True, False, 100, 0, False),    # groups of 512 above 64 rows (256 x 128 tiles)
+    (4, True, False, 24, 0, True),      # integral zero points past the int32 bound (int64)
+    (16, True, False, 20, 1, False),    # SwiGLU with group scales
+])
+def test_cint8_row_plane_route_groups(qc, oracle, synth, dev, groups, affine, fractional, m,
+                                      mode, wide):
+    """Group-scaled weights on the row-plane route (groups of a multiple of 128
+    columns): each group's plane sums folded into f32 at the end of its last K
+    step.  Every finite output within the 1e-4 normalised contract of the f64
+    product over the exactly decoded weights (SwiGLU: within a few f32 ulp of
+    the f64 epilogue of the same call's plain projections), an activation row
+    holding +-inf in the class of the digit-dot kernels' result, and a weight
+    row whose codes all equal their integral zero points exactly 0.  `wide`:
+    rows 20-29 get integral zero points near 4e4, past the bound (32639 for
+    groups of 512) up to which D_t - z S_t is formed in int32."""
+    import torch
+    rows, cols = 300, 2048
+    print(f"cint8 planes groups={groups} affine={affine} frac={fractional} m={m} mode={mode} "
+          f"wide={wide}", flush=True)
+    mats = []
+    for i in range(2 if mode == 1 else 1):
+        codes, scales, zeros = _tensor(synth, 500 + 7 * i + groups, rows, cols, groups, affine)
+        if affine and fractional:
+            zeros = (zeros + np.float32(0.25)).astype(np.float32)
+        if wide:
+            zeros[20 * groups:30 * groups] += np.float32(40000)
+        if affine and not fractional:
+            g = cols // groups
+            codes[7] = np.repeat(zeros[7 * groups:8 * groups], g).astype(np.int8)   # w_hat row 7 = 0
+        keep = [_dev(qc, dev, a) for a in (codes, scales, zeros)]
+        w = qc.cint8_weights(keep[0], keep[1], keep[2], rows, cols, groups)
+        what = oracle.cint8_dequant(codes, scales, zeros, rows, cols, groups)
+        mats.append((w, keep, what))
+    x = synth.normal_fast(600 + m, m * cols).reshape(m, cols)
+    x[0] *= np.float32(1e-20)
+    bad = m - 1
+    x[bad, 33] = -np.inf
+    X = torch.from_numpy(x).to(dev)
+    fin = [r for r in range(m) if r != bad]
+    ws = [w for w, _, _ in mats]
+    Y = torch.full((m, rows), 7.0, device=dev)
+    assert qc.cint8_project_raw(mode, ws, X, 0, m, [Y], [0]) == 0
+    Y = Y.cpu().numpy()
+    qc.set_cint8_dot(1)
+    try:
+        Z = torch.full((m, rows), 7.0, device=dev)
+        assert qc.cint8_project_raw(mode, ws, X, 0, m, [Z], [0]) == 0
+    finally:
+        qc.set_cint8_dot(0)
+    Z = Z.cpu().numpy()
+    for got, ref in ((np.isnan(Y[bad]), np.isnan(Z[bad])),
+                     (np.isposinf(Y[bad]), np.isposinf(Z[bad])),
+                     (np.isneginf(Y[bad]), np.isneginf(Z[bad]))):
+        assert np.array_equal(got, ref), np.flatnonzero(got != ref)[:5]
+    if mode == 0:
+        _check_contract(Y[fin], x[fin], mats[0][2])
+        if affine and not fractional:
+            assert np.all(Y[fin, 7] == 0.0)
+    else:
+        pg, pu = torch.empty((m, rows), device=dev), torch.empty((m, rows), device=dev)
+        assert qc.cint8_project_raw(0, ws, X, 0, m, [pg, pu], [0, 0]) == 0
+        pg, pu = pg.cpu().numpy(), pu.cpu().numpy()
+        _check_contract(pg[fin], x[fin], mats[0][2])
+        _check_contract(pu[fin], x[fin], mats[1][2])
+        gv = pg.astype(np.float64)
+        want = gv / (1.0 + np.exp(-gv)) * pu.astype(np.float64)
+        assert np.allclose(Y[fin], want[fin], rtol=1e-5, atol=1e-6)
+
+
 def test_cint8_row_plane_route_nonfinite_rows(qc, oracle, synth, dev):
     """Activation rows holding +-inf or NaN on the row-plane route: those
     rows get the reference's f32 result class per output, the finite rows

@@ -85,23 +85,25 @@ def test_qgemv_qgemm_graph_replay(qc, dev, fmt, m, n):
     _replay(lambda: _ok(call()), [y], lambda: _ok(other()))
 
 
-@pytest.mark.parametrize("mode,m,rows", [(0, 16, 4096), (0, 3, 1000), (1, 16, 2048),
-                                         (1, 100, 512), (0, 300, 1024)])
-def test_cint8_project_graph_replay(qc, dev, mode, m, rows):
-    """Canonical int8 projections on the row-plane route: the one-launch form
-    (m <= 64, plain and SwiGLU) and the finish-kernel form above, each with
-    its scratch from the stream's cache."""
+@pytest.mark.parametrize("mode,m,rows,groups", [(0, 16, 4096, 1), (0, 3, 1000, 1),
+                                                (1, 16, 2048, 1), (1, 100, 512, 1),
+                                                (0, 300, 1024, 1), (0, 24, 2048, 16),
+                                                (1, 8, 1024, 16)])
+def test_cint8_project_graph_replay(qc, dev, mode, m, rows, groups):
+    """Canonical int8 projections on the row-plane route (plain and SwiGLU,
+    row scales and groups of 128 columns), each call a prep and one GEMM per
+    matrix with the scratch from the stream's cache."""
     import torch
     k = 2048
-    print(f"graph cint8 mode={mode} m={m} rows={rows}", flush=True)
+    print(f"graph cint8 mode={mode} m={m} rows={rows} groups={groups}", flush=True)
     gen = torch.Generator(device=dev).manual_seed(11 + m)
     keep, ws = [], []
     for _ in range(2 if mode == 1 else 1):
         codes = torch.randint(-127, 128, (rows, k), generator=gen, device=dev, dtype=torch.int8)
-        scales = torch.rand(rows, generator=gen, device=dev) * 1e-3 + 1e-5
-        zeros = torch.randint(-4, 5, (rows,), generator=gen, device=dev).float()
+        scales = torch.rand(rows * groups, generator=gen, device=dev) * 1e-3 + 1e-5
+        zeros = torch.randint(-4, 5, (rows * groups,), generator=gen, device=dev).float()
         keep += [codes, scales, zeros]
-        ws.append(qc.cint8_weights(codes, scales, zeros, rows, k, 1))
+        ws.append(qc.cint8_weights(codes, scales, zeros, rows, k, groups))
     x = torch.randn((m, k), generator=gen, device=dev)
     x2 = torch.randn((m, k), generator=gen, device=dev)
     y = torch.empty((m, rows), device=dev)
