@@ -373,9 +373,10 @@ int qc_hip_set_qgemm_panel(int mode);
 int qc_hip_set_qgemm_rows(int mode);
 
 /* Canonical int8 projections (qc_hip_cint8_project): 0 (default) = two or
- * more activation rows with one scale per weight row run on the row-plane
- * route (three int8 digit planes of each activation row under one row
- * exponent, the int8 MFMA GEMM, an exact combination; K % 32 == 0,
+ * more activation rows with one scale per weight row, or three or more with
+ * scale groups of a multiple of 128 columns, run on the row-plane route
+ * (three int8 digit planes of each activation row under one row exponent,
+ * the int8 MFMA GEMM, an exact combination per row or per group; K % 32 == 0,
  * K <= 16384, codes 16-byte aligned, not the RoPE mode), everything else on
  * the kernels with exact int8 digit dots per 32-element block (the GEMV's
  * encoding of x) where they apply (K % 64 == 0, codes 16-byte aligned, row
