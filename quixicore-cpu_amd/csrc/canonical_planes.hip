@@ -308,12 +308,13 @@ __device__ __forceinline__ const T* pick(const T* a, const T* b, bool second) {
 }
 
 // The grouped fold's side data (an Int8Ring side policy): per K step, for
-// that step's group, the scales (lanes 0-31) and zero points (lanes 32-63;
-// the scales again when there are none) of each 32-row block of the tile's
-// B rows (slots 0..TS-1), then the digit sums S_0..S_2 of 16 activation rows
-// per slot (lanes 0-47).  Slots past those repeat the first scale.  Each
-// wave issues kLoads slots; read() keeps, at a group's last step (ready),
-// what the wave's fragments need.
+// that step's group, the scale and zero point (lanes 2r, 2r + 1; the scale
+// again when there are no zero points) of row r of each 32-row block of the
+// tile's B rows (slots 0..TS-1), then the digit sums S_0..S_2 of 16
+// activation rows per slot (lanes 4r + t, t < 3; lane 4r + 3 repeats S_2), so
+// that a row's values are one 8- or 16-byte LDS read.  Slots past those
+// repeat the first scale.  Each wave issues kLoads slots; read() keeps, at a
+// group's last step (ready), what the wave's fragments need.
 template <int TN, int TM, int WGN, int WGM, bool SWIGLU>
 struct GroupSide {
   static constexpr int NW = WGN * WGM;
@@ -341,19 +342,19 @@ struct GroupSide {
       if (t < TS) {
         const long long c = static_cast<long long>(tm) * (TM / 32) + t;   // B block
         const bool second = SWIGLU && (c & 1);
-        long long n = (SWIGLU ? (c >> 1) * 32 : c * 32) + (lane & 31);
+        long long n = (SWIGLU ? (c >> 1) * 32 : c * 32) + (lane >> 1);
         n = n < o.rows ? n : o.rows - 1;
         const float* scale = second ? o.scale2 : o.scale;
         const float* zero = second ? o.zero2 : o.zero;
         zero = zero != nullptr ? zero : scale;
-        src[q] = reinterpret_cast<const int8_t*>(pick(scale, zero, lane >= 32) + n * o.groups);
+        src[q] = reinterpret_cast<const int8_t*>(pick(scale, zero, lane & 1) + n * o.groups);
         stride[q] = 4;
       } else if (t < T) {
-        const int l = lane < 48 ? lane : lane - 48;
-        int r = tn * (TN / 4) + 16 * (t - TS) + l / 3;
+        int r = tn * (TN / 4) + 16 * (t - TS) + (lane >> 2);
         r = r < mc ? r : mc - 1;
+        const int comp = (lane & 3) < 3 ? (lane & 3) : 2;
         src[q] = reinterpret_cast<const int8_t*>(dsum + static_cast<long long>(r) * o.groups * 3 +
-                                                 l % 3);
+                                                 comp);
         stride[q] = 12;
       } else {
         src[q] = reinterpret_cast<const int8_t*>(o.scale);
@@ -372,22 +373,22 @@ struct GroupSide {
     if (!ready) return;
     rleft = spg;
     const int lane = threadIdx.x & 63;
-    const float* f = reinterpret_cast<const float*>(base);
-    const int* v = reinterpret_cast<const int*>(base);
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int bj = wm / 32 + j;
-      sc[j] = f[bj * 64 + (lane & 31)];
-      zr[j] = f[bj * 64 + 32 + (lane & 31)];
+      const float2 sz = reinterpret_cast<const float2*>(base)[bj * 32 + (lane & 31)];
+      sc[j] = sz.x;
+      zr[j] = sz.y;
     }
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int row = wn / 4 + 8 * i + 2 * g + (lane >> 5);
-        const int off = (TS + row / 16) * 64 + (row % 16) * 3;
-#pragma unroll
-        for (int t = 0; t < 3; ++t) sx[i][g][t] = v[off + t];
+        const int4 v = reinterpret_cast<const int4*>(base)[(TS + row / 16) * 16 + row % 16];
+        sx[i][g][0] = v.x;
+        sx[i][g][1] = v.y;
+        sx[i][g][2] = v.z;
       }
   }
 };

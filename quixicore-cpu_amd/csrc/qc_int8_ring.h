@@ -271,15 +271,17 @@ struct Int8Ring {
       if constexpr (XL > 0)
         if (part == 0) side->issue(pstep, wave, side_base(pstage));
     };
-    static_assert(XL == 0 || QPS > 1, "side data read in quarter 1");
+    // Side data is read after the MFMAs of the step's last in-loop quarter,
+    // so the reads overlap them and the barrier's LDS wait covers them.
+    static_assert(XL == 0 || QPS > 1, "side data read within the quarter loop");
     for (int k = 0; k + 1 < nk; ++k) {
 #pragma unroll
       for (int q = 1; q < QPS; ++q) {
         if (q < SPREAD && k > 0) issue_part(q);
         read_frags(stage, q, q & 1);
-        if constexpr (XL > 0)
-          if (q == 1) side->read(k, side_base(stage));
         mfmas((q - 1) & 1);
+        if constexpr (XL > 0)
+          if (q == QPS - 1) side->read(k, side_base(stage));
       }
       // Loads issued: steps up to k+S-1, all parts; step k+1 must be in.
       wait_vmcnt<GT * (S - 2)>();
