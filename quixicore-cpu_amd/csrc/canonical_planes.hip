@@ -23,7 +23,7 @@
 namespace qc {
 
 // ---- Row-plane route: two or more activation rows, one scale per weight row
-// (or three or more, with scale groups of a multiple of 128 columns)
+// (or three or more, with scale groups of 64 or a multiple of 128 columns)
 //
 // Every activation row m is encoded once as 22-bit fixed point under one
 // exponent for the whole row: e(m) = frexp(max_k |x[m][k]|) - 21 and
@@ -109,10 +109,10 @@ __device__ __forceinline__ void load4(const void* x, long long xr, int c, int xt
 // planes of row m are rows 4m + t (row 4m + 3 is zeroed).  A row holding NaN
 // or +-inf gets the maximum +inf, zero digits and the flag exponent
 // kPlanesNonfinite.  The digit sums S_t go to dsum[(m * ngroups + g) * 3 + t]
-// over each group g of gsize columns (GROUPED: gsize a multiple of 128, so
-// the 128 columns of a half wave's loads lie in one group), else over the
-// row (ngroups = 1).
-constexpr int kPlanesMaxGroups = kPlanesMaxK / 128;
+// over each group g of gsize columns (GROUPED: gsize 64 or a multiple of 128,
+// with k % 128 == 0, so the 4 gsize / 4 lanes of a group, at most a half
+// wave, lie in one half wave), else over the row (ngroups = 1).
+constexpr int kPlanesMaxGroups = kPlanesMaxK / 64;
 template <bool GROUPED>
 __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     const void* __restrict__ x, int xtype, long long ldx, int k, bool vec, int gsize,
@@ -171,11 +171,13 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     *reinterpret_cast<uint32_t*>(p0 + 2LL * k + c) = w2;
     *reinterpret_cast<uint32_t*>(p0 + 3LL * k + c) = 0u;
     if constexpr (GROUPED) {
-      // the half wave's 128 columns: one group
+      // the gl consecutive lanes of one group (4 columns each)
+      const int gl = gsize < 128 ? gsize / 4 : 32;
 #pragma unroll
       for (int t = 0; t < 3; ++t)
-        for (int off = 16; off > 0; off >>= 1) sum[t] += __shfl_xor(sum[t], off);
-      if ((threadIdx.x & 31) == 0) {
+        for (int off = 16; off > 0; off >>= 1)
+          if (off < gl) sum[t] += __shfl_xor(sum[t], off);
+      if ((threadIdx.x & (gl - 1)) == 0) {
         const int grp = c / gsize;
 #pragma unroll
         for (int t = 0; t < 3; ++t) atomicAdd(&gsum[3 * grp + t], sum[t]);
@@ -315,7 +317,7 @@ __device__ __forceinline__ const T* pick(const T* a, const T* b, bool second) {
 // that a row's values are one 8- or 16-byte LDS read.  Slots past those
 // repeat the first scale.  Each wave issues kLoads slots; read() keeps, at a
 // group's last step (ready), what the wave's fragments need.
-template <int TN, int TM, int WGN, int WGM, bool SWIGLU>
+template <int TN, int TM, int WGN, int WGM, bool SWIGLU, int KL>
 struct GroupSide {
   static constexpr int NW = WGN * WGM;
   static constexpr int FN = TN / WGN / 32, FM = TM / WGM / 32;
@@ -331,7 +333,7 @@ struct GroupSide {
   __device__ void init(const PlaneOut& o, const int* dsum, int mc, int tn, int tm, int wave,
                        int wn_, int wm_) {
     const int lane = threadIdx.x & 63;
-    spg = o.gsize / 128;
+    spg = o.gsize / KL;
     rleft = spg;
     ready = false;
     wn = wn_;
@@ -399,7 +401,8 @@ struct GroupSide {
 // y[(m0 + r) * ld + n].  Lanes 0-31 of a store hold 32 consecutive n.  With
 // SWIGLU the B tiles pair gate and up blocks (PairedRows): in a wave tile of
 // 64 B rows (FM even), fragments j and j + 1 hold gate and up of the same n.
-// GROUPED (gsize a multiple of the 128-column K step): at the end of each
+// GROUPED (gsize a multiple of the KL-column K step: 64-column half-line
+// steps for groups of 64, else 128-column steps): at the end of each
 // group's last step the int32 plane sums of the group are folded into f32,
 // s_g * (2^14 A0 + 2^7 A1 + A2) with A_t = D_t - z_g S_t exact for an
 // integral zero point (else 2^14 D0 + ... - z_g (2^14 S0 + ...) in f32),
@@ -410,13 +413,13 @@ struct GroupSide {
 // of 128), else in int64 on a branch the wave takes only when one of its
 // lanes needs it; each A_t is then rounded to f32 once, so the two forms give
 // the same bits.
-template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED>
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL>
 __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
     const int8_t* __restrict__ planes, int mc, const PlaneOut o, const int* __restrict__ rexp,
     const int* __restrict__ dsum, const void* __restrict__ x, int xtype, long long ldx, int m0,
     int k, int tiles_n, int tiles_m) {
-  using R = Int8Ring<TN, TM, S, WGN, WGM, 128>;
-  using Side = std::conditional_t<GROUPED, GroupSide<TN, TM, WGN, WGM, SWIGLU>, Int8NoSide>;
+  using R = Int8Ring<TN, TM, S, WGN, WGM, KL>;
+  using Side = std::conditional_t<GROUPED, GroupSide<TN, TM, WGN, WGM, SWIGLU, KL>, Int8NoSide>;
   static_assert(!SWIGLU || R::FM % 2 == 0, "gate / up fragment pairs");
   __shared__ __attribute__((aligned(1024))) int8_t ring[R::template kBytesWith<Side>];
   const int lane = threadIdx.x & 63;
@@ -562,7 +565,7 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
   }
 }
 
-template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED>
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL>
 hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                               const int* dsum, const void* x, int xtype, long long ldx, int m0,
                               int k, hipStream_t s) {
@@ -570,8 +573,9 @@ hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, c
   // SwiGLU: 64 B rows per 32 output rows
   const long long brows = SWIGLU ? 64LL * ((o.rows + 31) / 32) : o.rows;
   const int tiles_m = static_cast<int>((brows + TM - 1) / TM);
-  cint8_planes_gemm<TN, TM, S, WGN, WGM, SWIGLU, GROUPED><<<tiles_n * tiles_m, 64 * WGN * WGM, 0, s>>>(
-      planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, tiles_n, tiles_m);
+  cint8_planes_gemm<TN, TM, S, WGN, WGM, SWIGLU, GROUPED, KL>
+      <<<tiles_n * tiles_m, 64 * WGN * WGM, 0, s>>>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0,
+                                                    k, tiles_n, tiles_m);
   return hipGetLastError();
 }
 
@@ -580,25 +584,31 @@ hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, c
 // weight rows, or 64 gate and 64 up rows in wave tiles of 64 B rows; up to
 // 128 rows two A tiles of 256 by 128 B rows (224 workgroups at N = 14336, where
 // 448 of 256 x 64 took 1.4x as long); above, the W8A8 kernel's 256 x 256 tile.
-template <bool SWIGLU, bool GROUPED>
+// KL = 64 (groups of 64 columns: one group per half-line K step): the same
+// tiles with twice the stages (half the bytes each), within the 6-bit vmcnt
+// and the 160 KB of LDS.
+template <bool SWIGLU, bool GROUPED, int KL>
 hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                         const int* dsum, const void* x, int xtype, long long ldx, int m0, int k,
                         hipStream_t s) {
+  static_assert(KL == 128 || GROUPED, "half-line steps only for groups of 64");
   constexpr int TM = SWIGLU ? 128 : 64;
-#define QC_PLANES(TN_, TM_, S_, WGN_, WGM_, SW_) \
-  launch_planes_gemm<TN_, TM_, S_, WGN_, WGM_, SW_, GROUPED>(planes, mc, o, rexp, dsum, x, xtype, \
-                                                             ldx, m0, k, s)
+  constexpr bool H = KL == 64;
+#define QC_PLANES(TN_, TM_, S_, WGN_, WGM_, SW_)                                          \
+  launch_planes_gemm<TN_, TM_, S_, WGN_, WGM_, SW_, GROUPED, KL>(planes, mc, o, rexp, dsum, x, \
+                                                                 xtype, ldx, m0, k, s)
   // (grouped SwiGLU: 5 stages, as its side loads would take 6 past the vmcnt range)
-  if (mc <= 8) return QC_PLANES(32, TM, SWIGLU ? (GROUPED ? 5 : 6) : 8, 1, 2, SWIGLU);
-  if (mc <= 16) return QC_PLANES(64, TM, SWIGLU ? 4 : 6, 1, 2, SWIGLU);
-  if (mc <= 32) return QC_PLANES(128, TM, 4, 2, 2, SWIGLU);
+  if (mc <= 8)
+    return QC_PLANES(32, TM, H ? (SWIGLU ? 8 : 12) : SWIGLU ? (GROUPED ? 5 : 6) : 8, 1, 2, SWIGLU);
+  if (mc <= 16) return QC_PLANES(64, TM, H ? (SWIGLU ? 8 : 10) : SWIGLU ? 4 : 6, 1, 2, SWIGLU);
+  if (mc <= 32) return QC_PLANES(128, TM, H ? 8 : 4, 2, 2, SWIGLU);
   if (mc <= 64) {
-    if constexpr (SWIGLU) return QC_PLANES(256, TM, 3, 4, 2, true);
-    else return QC_PLANES(256, TM, 3, 4, 1, false);
+    if constexpr (SWIGLU) return QC_PLANES(256, TM, H ? 6 : 3, 4, 2, true);
+    else return QC_PLANES(256, TM, H ? 6 : 3, 4, 1, false);
   }
   // group sums in registers beside 256 x 256 tiles would spill: 256 x 128 above 64 rows
   if constexpr (GROUPED) {
-    return QC_PLANES(256, 128, 3, 4, 2, SWIGLU);
+    return QC_PLANES(256, 128, H ? 6 : 3, 4, 2, SWIGLU);
   } else {
     if (mc <= 128) return QC_PLANES(256, 128, 3, 4, 2, SWIGLU);
     return QC_PLANES(256, 256, 2, 4, 2, SWIGLU);
@@ -606,10 +616,22 @@ hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const i
 #undef QC_PLANES
 }
 
+// Groups of 64 columns take half-line K steps (one group per step).
+template <bool SWIGLU, bool GROUPED>
+hipError_t launch_fused_kl(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
+                           const int* dsum, const void* x, int xtype, long long ldx, int m0,
+                           int k, hipStream_t s) {
+  if constexpr (GROUPED)
+    if (o.gsize == 64)
+      return launch_fused<SWIGLU, true, 64>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+  return launch_fused<SWIGLU, GROUPED, 128>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+}
+
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
 // All checks done by the caller, which routes only 16-byte aligned codes here
-// and, with groups, group sizes that are multiples of 128 columns.
+// and, with groups, k % 128 == 0 and group sizes of 64 or a multiple of 128
+// columns.
 template <bool GROUPED>
 hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hipStream_t s) {
   const int nmat = L.mode == 1 ? 2 : L.nw;
@@ -638,14 +660,16 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
       const PlaneOut o{sg.w[0], sg.scale[0], sg.zero[0], sg.w[1], sg.scale[1], sg.zero[1],
                        sg.y[0], sg.ld[0], sg.ytype[0], static_cast<int>(L.w[0].rows),
                        nullptr, 0, 0, ngroups, gsize};
-      e = launch_fused<true, GROUPED>(planes, mc, o, rexp, dsum, L.x, L.xtype, L.ldx, m0, k, s);
+      e = launch_fused_kl<true, GROUPED>(planes, mc, o, rexp, dsum, L.x, L.xtype, L.ldx, m0, k,
+                                         s);
       continue;
     }
     for (int i = 0; i < nmat && e == hipSuccess; ++i) {
       const PlaneOut o{sg.w[i], sg.scale[i], sg.zero[i], nullptr, nullptr, nullptr, sg.y[i],
                        sg.ld[i], sg.ytype[i], static_cast<int>(L.w[i].rows), sg.bias, sg.act,
                        i == 0 && (sg.bias != nullptr || sg.act != 0) ? 1 : 0, ngroups, gsize};
-      e = launch_fused<false, GROUPED>(planes, mc, o, rexp, dsum, L.x, L.xtype, L.ldx, m0, k, s);
+      e = launch_fused_kl<false, GROUPED>(planes, mc, o, rexp, dsum, L.x, L.xtype, L.ldx, m0, k,
+                                          s);
     }
   }
   return e;

@@ -48,7 +48,8 @@ constexpr int kPlanesMinMGrouped = 3;
 
 // The projections of L over the row-plane route (all checks done by the
 // caller: 16-byte aligned codes, K % 32 == 0, K <= kPlanesMaxK, not the RoPE
-// mode; grouped: group sizes a multiple of 128 columns).
+// mode; grouped: K % 128 == 0 and group sizes of 64 or a multiple of 128
+// columns).
 hipError_t launch_cint8_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, bool grouped,
                                hipStream_t s);
 
