@@ -855,6 +855,8 @@ def main():
             s["cint8_group128_m64_k4096_n14336"] = cint8_case(qc, 14336, 4096, 64, K, W, groups=32)
             s["cint8_group128_m512_k4096_n14336"] = cint8_case(qc, 14336, 4096, 512, max(5, K // 4),
                                                                W, groups=32)
+            s["cint8_group64_m16_k4096_n14336"] = cint8_case(qc, 14336, 4096, 16, K, W, groups=64)
+            s["cint8_group64_m64_k4096_n14336"] = cint8_case(qc, 14336, 4096, 64, K, W, groups=64)
         elif args.only == "w8a8":
             s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
             s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)
