@@ -857,6 +857,8 @@ def main():
                                                                W, groups=32)
             s["cint8_group64_m16_k4096_n14336"] = cint8_case(qc, 14336, 4096, 16, K, W, groups=64)
             s["cint8_group64_m64_k4096_n14336"] = cint8_case(qc, 14336, 4096, 64, K, W, groups=64)
+            s["cint8_group32_m16_k4096_n14336"] = cint8_case(qc, 14336, 4096, 16, K, W, groups=128)
+            s["cint8_group32_m64_k4096_n14336"] = cint8_case(qc, 14336, 4096, 64, K, W, groups=128)
         elif args.only == "w8a8":
             s["quantize_int8_m2048_k4096"] = quant_case(qc, 2048, 4096, K, W)
             s["rms_norm_add_quant_int8_m2048_k4096"] = norm_quant_case(qc, 2048, 4096, K, W)

@@ -374,7 +374,8 @@ int qc_hip_set_qgemm_rows(int mode);
 
 /* Canonical int8 projections (qc_hip_cint8_project): 0 (default) = two or
  * more activation rows with one scale per weight row, or three or more with
- * scale groups of 64 or a multiple of 128 columns, run on the row-plane route
+ * scale groups of 64 or a multiple of 128 columns (five or more with groups
+ * of 32; K % 128 == 0 with groups), run on the row-plane route
  * (three int8 digit planes of each activation row under one row exponent,
  * the int8 MFMA GEMM, an exact combination per row or per group; K % 32 == 0,
  * K <= 16384, codes 16-byte aligned, not the RoPE mode), everything else on

@@ -818,13 +818,16 @@ hipError_t launch_cint8(const CInt8Launch& L, hipStream_t s) {
   bool fast = k % 16 == 0 && (!grp || (sg.gsize >= 16 && (1 << sg.gshift) == sg.gsize));
   for (int i = 0; i < L.nw; ++i)
     fast = fast && reinterpret_cast<uintptr_t>(L.w[i].codes) % 16 == 0;
-  // Two or more activation rows with row scales, or three or more with scale
-  // groups of 64 or a multiple of 128 columns: the digit planes on the int8
-  // MFMA GEMM (the row-plane route, canonical_planes.hip).
+  // Two or more activation rows with row scales, three or more with scale
+  // groups of 64 or a multiple of 128 columns, five or more with groups of
+  // 32: the digit planes on the int8 MFMA GEMM (the row-plane route,
+  // canonical_planes.hip).
   if (fast && L.dot == 0 && L.mode != 2 && m >= kPlanesMinM && k % 32 == 0 &&
       k <= kPlanesMaxK) {
     if (!grp) return launch_cint8_planes(sg, L, m, k, false, s);
     if ((sg.gsize % 128 == 0 || sg.gsize == 64) && k % 128 == 0 && m >= kPlanesMinMGrouped)
+      return launch_cint8_planes(sg, L, m, k, true, s);
+    if (sg.gsize == 32 && k % 128 == 0 && m >= kPlanesMinMGroups32)
       return launch_cint8_planes(sg, L, m, k, true, s);
   }
   // Exact digit dots over 64-column block pairs, two rows per wave, passes of

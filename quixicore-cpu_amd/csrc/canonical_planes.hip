@@ -23,7 +23,8 @@
 namespace qc {
 
 // ---- Row-plane route: two or more activation rows, one scale per weight row
-// (or three or more, with scale groups of 64 or a multiple of 128 columns)
+// (or three or more with scale groups of 64 or a multiple of 128 columns,
+// five or more with groups of 32)
 //
 // Every activation row m is encoded once as 22-bit fixed point under one
 // exponent for the whole row: e(m) = frexp(max_k |x[m][k]|) - 21 and
@@ -310,38 +311,46 @@ __device__ __forceinline__ const T* pick(const T* a, const T* b, bool second) {
 }
 
 // The grouped fold's side data (an Int8Ring side policy): per K step, for
-// that step's group, the scale and zero point (lanes 2r, 2r + 1; the scale
-// again when there are no zero points) of row r of each 32-row block of the
-// tile's B rows (slots 0..TS-1), then the digit sums S_0..S_2 of 16
-// activation rows per slot (lanes 4r + t, t < 3; lane 4r + 3 repeats S_2), so
-// that a row's values are one 8- or 16-byte LDS read.  Slots past those
-// repeat the first scale.  Each wave issues kLoads slots; read() keeps, at a
-// group's last step (ready), what the wave's fragments need.
-template <int TN, int TM, int WGN, int WGM, bool SWIGLU, int KL>
+// each of its GPS groups u (one, or two for groups of 32 columns in 64-column
+// steps), the scale and zero point (lanes 2r, 2r + 1; the scale again when
+// there are no zero points) of row r of each 32-row block of the tile's B
+// rows (slots u T + 0..TS-1), then the digit sums S_0..S_2 of 16 activation
+// rows per slot (lanes 4r + t, t < 3; lane 4r + 3 repeats S_2), so that a
+// row's values are one 8- or 16-byte LDS read.  Slots past those repeat the
+// first scale.  Each wave issues kLoads slots; read() keeps, at a group's
+// last step (ready), what the wave's fragments need.
+template <int TN, int TM, int WGN, int WGM, bool SWIGLU, int KL, int GPS>
 struct GroupSide {
   static constexpr int NW = WGN * WGM;
   static constexpr int FN = TN / WGN / 32, FM = TM / WGM / 32;
   static constexpr int TS = TM / 32, TD = (TN / 4 + 15) / 16, T = TS + TD;
-  static constexpr int kLoads = (T + NW - 1) / NW;
+  static constexpr int kLoads = (GPS * T + NW - 1) / NW;
   const int8_t* src[kLoads];   // this lane's address for group 0
   int stride[kLoads];          // bytes per group (wave-uniform)
+  int gofs[kLoads];            // the slot's group within its step (GPS > 1)
   int spg, rleft, wn, wm;
   bool ready;
-  float sc[FM], zr[FM];
-  int sx[FN][4][3];
+  float sc[GPS][FM], zr[GPS][FM];
+  int sx[GPS][FN][4][3];
 
   __device__ void init(const PlaneOut& o, const int* dsum, int mc, int tn, int tm, int wave,
                        int wn_, int wm_) {
     const int lane = threadIdx.x & 63;
-    spg = o.gsize / KL;
+    spg = GPS == 1 ? o.gsize / KL : 1;
     rleft = spg;
     ready = false;
     wn = wn_;
     wm = wm_;
 #pragma unroll
     for (int q = 0; q < kLoads; ++q) {
-      const int t = wave * kLoads + q;          // wave-uniform
-      if (t < TS) {
+      const int slot = wave * kLoads + q;       // wave-uniform
+      const int t = slot % T;
+      gofs[q] = slot / T;
+      if (slot >= GPS * T) {
+        src[q] = reinterpret_cast<const int8_t*>(o.scale);
+        stride[q] = 0;
+        gofs[q] = 0;
+      } else if (t < TS) {
         const long long c = static_cast<long long>(tm) * (TM / 32) + t;   // B block
         const bool second = SWIGLU && (c & 1);
         long long n = (SWIGLU ? (c >> 1) * 32 : c * 32) + (lane >> 1);
@@ -351,47 +360,53 @@ struct GroupSide {
         zero = zero != nullptr ? zero : scale;
         src[q] = reinterpret_cast<const int8_t*>(pick(scale, zero, lane & 1) + n * o.groups);
         stride[q] = 4;
-      } else if (t < T) {
+      } else {
         int r = tn * (TN / 4) + 16 * (t - TS) + (lane >> 2);
         r = r < mc ? r : mc - 1;
         const int comp = (lane & 3) < 3 ? (lane & 3) : 2;
         src[q] = reinterpret_cast<const int8_t*>(dsum + static_cast<long long>(r) * o.groups * 3 +
                                                  comp);
         stride[q] = 12;
-      } else {
-        src[q] = reinterpret_cast<const int8_t*>(o.scale);
-        stride[q] = 0;
       }
     }
   }
   __device__ void issue(int step, int wave, int8_t* base) const {
-    const int grp = step / spg;
 #pragma unroll
-    for (int q = 0; q < kLoads; ++q)
+    for (int q = 0; q < kLoads; ++q) {
+      const int grp = GPS == 1 ? step / spg : step * GPS + gofs[q];
       load_lds4(src[q] + grp * stride[q], base + (wave * kLoads + q) * 256);
+    }
   }
   __device__ void read(int, const int8_t* base) {
-    ready = --rleft == 0;
-    if (!ready) return;
-    rleft = spg;
+    if constexpr (GPS == 1) {
+      ready = --rleft == 0;
+      if (!ready) return;
+      rleft = spg;
+    } else {
+      ready = true;
+    }
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int bj = wm / 32 + j;
-      const float2 sz = reinterpret_cast<const float2*>(base)[bj * 32 + (lane & 31)];
-      sc[j] = sz.x;
-      zr[j] = sz.y;
-    }
+    for (int u = 0; u < GPS; ++u) {
+      const int8_t* b = base + u * T * 256;
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int row = wn / 4 + 8 * i + 2 * g + (lane >> 5);
-        const int4 v = reinterpret_cast<const int4*>(base)[(TS + row / 16) * 16 + row % 16];
-        sx[i][g][0] = v.x;
-        sx[i][g][1] = v.y;
-        sx[i][g][2] = v.z;
+      for (int j = 0; j < FM; ++j) {
+        const int bj = wm / 32 + j;
+        const float2 sz = reinterpret_cast<const float2*>(b)[bj * 32 + (lane & 31)];
+        sc[u][j] = sz.x;
+        zr[u][j] = sz.y;
       }
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int row = wn / 4 + 8 * i + 2 * g + (lane >> 5);
+          const int4 v = reinterpret_cast<const int4*>(b)[(TS + row / 16) * 16 + row % 16];
+          sx[u][i][g][0] = v.x;
+          sx[u][i][g][1] = v.y;
+          sx[u][i][g][2] = v.z;
+        }
+    }
   }
 };
 
@@ -401,8 +416,9 @@ struct GroupSide {
 // y[(m0 + r) * ld + n].  Lanes 0-31 of a store hold 32 consecutive n.  With
 // SWIGLU the B tiles pair gate and up blocks (PairedRows): in a wave tile of
 // 64 B rows (FM even), fragments j and j + 1 hold gate and up of the same n.
-// GROUPED (gsize a multiple of the KL-column K step: 64-column half-line
-// steps for groups of 64, else 128-column steps): at the end of each
+// GROUPED (gsize a multiple of the KL-column K step -- 64-column half-line
+// steps for groups of 64, else 128-column steps -- or, GPS = 2, groups of 32
+// in 64-column steps, folded after each 32-column quarter): at the end of each
 // group's last step the int32 plane sums of the group are folded into f32,
 // s_g * (2^14 A0 + 2^7 A1 + A2) with A_t = D_t - z_g S_t exact for an
 // integral zero point (else 2^14 D0 + ... - z_g (2^14 S0 + ...) in f32),
@@ -413,13 +429,14 @@ struct GroupSide {
 // of 128), else in int64 on a branch the wave takes only when one of its
 // lanes needs it; each A_t is then rounded to f32 once, so the two forms give
 // the same bits.
-template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL>
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL, int GPS>
 __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
     const int8_t* __restrict__ planes, int mc, const PlaneOut o, const int* __restrict__ rexp,
     const int* __restrict__ dsum, const void* __restrict__ x, int xtype, long long ldx, int m0,
     int k, int tiles_n, int tiles_m) {
   using R = Int8Ring<TN, TM, S, WGN, WGM, KL>;
-  using Side = std::conditional_t<GROUPED, GroupSide<TN, TM, WGN, WGM, SWIGLU, KL>, Int8NoSide>;
+  using Side =
+      std::conditional_t<GROUPED, GroupSide<TN, TM, WGN, WGM, SWIGLU, KL, GPS>, Int8NoSide>;
   static_assert(!SWIGLU || R::FM % 2 == 0, "gate / up fragment pairs");
   __shared__ __attribute__((aligned(1024))) int8_t ring[R::template kBytesWith<Side>];
   const int lane = threadIdx.x & 63;
@@ -453,16 +470,20 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
   const int zlim = GROUPED ? static_cast<int>(((1LL << 31) - 1 - (gs << 14)) / (gs << 7)) : 0;
   // (SwiGLU: gate and up both have zero points or neither)
   const bool has_zero = o.zero != nullptr;
-  auto fold = [&](int, v16i (&a)[R::FN][R::FM]) {
+  auto fold = [&](int, int q, v16i (&a)[R::FN][R::FM]) {
     if constexpr (GROUPED) {
+      // a group's last quarter (q is a constant in the unrolled quarter loops)
+      constexpr int QPG = R::QPS / GPS;
+      if ((q + 1) % QPG != 0) return;
+      const int u = (q + 1) / QPG - 1;
       if (!side.ready) return;                  // uniform: not the group's last step
 #pragma unroll
       for (int j = 0; j < R::FM; ++j) {
         // zi: the integral zero point the int32 form subtracts (0 for none,
         // a fractional one or one beyond zlim); zf: the zero point the f32
         // form subtracts (0 for none or an integral one within zlim)
-        const float sg = side.sc[j];
-        const float z = has_zero ? side.zr[j] : 0.0f;
+        const float sg = side.sc[u][j];
+        const float z = has_zero ? side.zr[u][j] : 0.0f;
         int zr = 0;
         const bool integral = integral_zero(z, zr);
         const bool narrow = integral && zr >= -zlim && zr <= zlim;
@@ -474,7 +495,7 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
         for (int i = 0; i < R::FN; ++i)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const int* sx = side.sx[i][g];     // (zi = 0 without zero points)
+            const int* sx = side.sx[u][i][g];  // (zi = 0 without zero points)
             fv[i][g] = combine(a[i][j][4 * g] + __mul24(-zi, sx[0]),
                                a[i][j][4 * g + 1] + __mul24(-zi, sx[1]),
                                a[i][j][4 * g + 2] + __mul24(-zi, sx[2]));
@@ -485,7 +506,7 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
             for (int i = 0; i < R::FN; ++i)
 #pragma unroll
               for (int g = 0; g < 4; ++g) {
-                const int* sx = side.sx[i][g];
+                const int* sx = side.sx[u][i][g];
                 fv[i][g] = fmaf(-zf, combine(sx[0], sx[1], sx[2]), fv[i][g]);
               }
           }
@@ -494,7 +515,7 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
             for (int i = 0; i < R::FN; ++i)
 #pragma unroll
               for (int g = 0; g < 4; ++g) {
-                const int* sx = side.sx[i][g];
+                const int* sx = side.sx[u][i][g];
                 const long long d0 = a[i][j][4 * g], d1 = a[i][j][4 * g + 1];
                 const long long d2 = a[i][j][4 * g + 2];
                 if (wide)
@@ -565,7 +586,7 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
   }
 }
 
-template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL>
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL, int GPS>
 hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                               const int* dsum, const void* x, int xtype, long long ldx, int m0,
                               int k, hipStream_t s) {
@@ -573,7 +594,7 @@ hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, c
   // SwiGLU: 64 B rows per 32 output rows
   const long long brows = SWIGLU ? 64LL * ((o.rows + 31) / 32) : o.rows;
   const int tiles_m = static_cast<int>((brows + TM - 1) / TM);
-  cint8_planes_gemm<TN, TM, S, WGN, WGM, SWIGLU, GROUPED, KL>
+  cint8_planes_gemm<TN, TM, S, WGN, WGM, SWIGLU, GROUPED, KL, GPS>
       <<<tiles_n * tiles_m, 64 * WGN * WGM, 0, s>>>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0,
                                                     k, tiles_n, tiles_m);
   return hipGetLastError();
@@ -584,31 +605,37 @@ hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, c
 // weight rows, or 64 gate and 64 up rows in wave tiles of 64 B rows; up to
 // 128 rows two A tiles of 256 by 128 B rows (224 workgroups at N = 14336, where
 // 448 of 256 x 64 took 1.4x as long); above, the W8A8 kernel's 256 x 256 tile.
-// KL = 64 (groups of 64 columns: one group per half-line K step): the same
-// tiles with twice the stages (half the bytes each), within the 6-bit vmcnt
-// and the 160 KB of LDS.
-template <bool SWIGLU, bool GROUPED, int KL>
+// KL = 64 (groups of 64 or 32 columns: one or two groups per half-line K
+// step): the same tiles with about twice the stages (half the bytes each),
+// within the 6-bit vmcnt and the 160 KB of LDS; GPS = 2 carries twice the
+// side loads.
+template <bool SWIGLU, bool GROUPED, int KL, int GPS = 1>
 hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                         const int* dsum, const void* x, int xtype, long long ldx, int m0, int k,
                         hipStream_t s) {
-  static_assert(KL == 128 || GROUPED, "half-line steps only for groups of 64");
+  static_assert(KL == 128 || GROUPED, "half-line steps only for small groups");
+  static_assert(GPS == 1 || KL == 64, "two groups per step: groups of 32");
   constexpr int TM = SWIGLU ? 128 : 64;
-  constexpr bool H = KL == 64;
-#define QC_PLANES(TN_, TM_, S_, WGN_, WGM_, SW_)                                          \
-  launch_planes_gemm<TN_, TM_, S_, WGN_, WGM_, SW_, GROUPED, KL>(planes, mc, o, rexp, dsum, x, \
-                                                                 xtype, ldx, m0, k, s)
+  constexpr bool H = KL == 64, T2 = GPS == 2;
+#define QC_PLANES(TN_, TM_, S_, WGN_, WGM_, SW_)                                            \
+  launch_planes_gemm<TN_, TM_, S_, WGN_, WGM_, SW_, GROUPED, KL, GPS>(planes, mc, o, rexp, dsum, \
+                                                                      x, xtype, ldx, m0, k, s)
   // (grouped SwiGLU: 5 stages, as its side loads would take 6 past the vmcnt range)
   if (mc <= 8)
-    return QC_PLANES(32, TM, H ? (SWIGLU ? 8 : 12) : SWIGLU ? (GROUPED ? 5 : 6) : 8, 1, 2, SWIGLU);
-  if (mc <= 16) return QC_PLANES(64, TM, H ? (SWIGLU ? 8 : 10) : SWIGLU ? 4 : 6, 1, 2, SWIGLU);
+    return QC_PLANES(32, TM,
+                     H ? (SWIGLU ? (T2 ? 7 : 8) : (T2 ? 10 : 12))
+                       : SWIGLU ? (GROUPED ? 5 : 6) : 8,
+                     1, 2, SWIGLU);
+  if (mc <= 16)
+    return QC_PLANES(64, TM, H ? (SWIGLU ? (T2 ? 6 : 8) : 10) : SWIGLU ? 4 : 6, 1, 2, SWIGLU);
   if (mc <= 32) return QC_PLANES(128, TM, H ? 8 : 4, 2, 2, SWIGLU);
   if (mc <= 64) {
-    if constexpr (SWIGLU) return QC_PLANES(256, TM, H ? 6 : 3, 4, 2, true);
+    if constexpr (SWIGLU) return QC_PLANES(256, TM, H ? (T2 ? 5 : 6) : 3, 4, 2, true);
     else return QC_PLANES(256, TM, H ? 6 : 3, 4, 1, false);
   }
   // group sums in registers beside 256 x 256 tiles would spill: 256 x 128 above 64 rows
   if constexpr (GROUPED) {
-    return QC_PLANES(256, 128, H ? 6 : 3, 4, 2, SWIGLU);
+    return QC_PLANES(256, 128, H ? (T2 ? 5 : 6) : 3, 4, 2, SWIGLU);
   } else {
     if (mc <= 128) return QC_PLANES(256, 128, 3, 4, 2, SWIGLU);
     return QC_PLANES(256, 256, 2, 4, 2, SWIGLU);
@@ -616,22 +643,27 @@ hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const i
 #undef QC_PLANES
 }
 
-// Groups of 64 columns take half-line K steps (one group per step).
+// Groups of 64 columns take half-line K steps (one group per step), groups of
+// 32 the same steps with a fold after each quarter (two groups per step).
 template <bool SWIGLU, bool GROUPED>
 hipError_t launch_fused_kl(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                            const int* dsum, const void* x, int xtype, long long ldx, int m0,
                            int k, hipStream_t s) {
-  if constexpr (GROUPED)
+  if constexpr (GROUPED) {
     if (o.gsize == 64)
       return launch_fused<SWIGLU, true, 64>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
+    if (o.gsize == 32)
+      return launch_fused<SWIGLU, true, 64, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k,
+                                               s);
+  }
   return launch_fused<SWIGLU, GROUPED, 128>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
 }
 
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
 // All checks done by the caller, which routes only 16-byte aligned codes here
-// and, with groups, k % 128 == 0 and group sizes of 64 or a multiple of 128
-// columns.
+// and, with groups, k % 128 == 0 and group sizes of 32, 64 or a multiple of
+// 128 columns.
 template <bool GROUPED>
 hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hipStream_t s) {
   const int nmat = L.mode == 1 ? 2 : L.nw;

@@ -41,14 +41,16 @@ struct CSegs {
 // Row-plane route limits (canonical_planes.hip): K, and the fewest
 // activation rows it takes (N = 14336, K = 4096 at M = 2: row scales 22.9 us
 // on the digit-dot kernel, 18.8 there; groups of 128 22.0 on the digit-dot
-// kernel, 26.5 there; M = 3 with groups: 34.6 against 26.4).
+// kernel, 26.5 there; M = 3 with groups of 128 or 64: 34 against 26 / 34;
+// groups of 32 at M = 4: 40 against 44.5, at M = 5-8: 62-79 against 46).
 constexpr int kPlanesMaxK = 16384;
 constexpr int kPlanesMinM = 2;
 constexpr int kPlanesMinMGrouped = 3;
+constexpr int kPlanesMinMGroups32 = 5;
 
 // The projections of L over the row-plane route (all checks done by the
 // caller: 16-byte aligned codes, K % 32 == 0, K <= kPlanesMaxK, not the RoPE
-// mode; grouped: K % 128 == 0 and group sizes of 64 or a multiple of 128
+// mode; grouped: K % 128 == 0 and group sizes of 32, 64 or a multiple of 128
 // columns).
 hipError_t launch_cint8_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, bool grouped,
                                hipStream_t s);

@@ -67,10 +67,10 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// The default per-step hook of Int8Ring::run_rows: nothing.
+// The default per-quarter hook of Int8Ring::run_rows: nothing.
 struct Int8NoStep {
   template <class Acc>
-  __device__ void operator()(int, Acc&) const {}
+  __device__ void operator()(int, int, Acc&) const {}
 };
 
 // The default side data of Int8Ring::run_rows: none.  A side policy moves,
@@ -78,8 +78,9 @@ struct Int8NoStep {
 // (issue(step, wave, stage_base): slots wave * kLoads + q, 256 bytes each,
 // of that stage's side area) beside the operand tiles, on the same path, so
 // the ring's waits and barriers cover them; read(step, stage_base) is called
-// once per step, in order, while that step's stage is valid, to move what
-// the step hook needs into registers.  (A plain global load whose result is
+// once per step, in order, before the hook of the step's quarter QPS - 2
+// (its last quarter in the loop body, where the stage is still valid), to
+// move what the hooks need into registers.  (A plain global load whose result is
 // used while global->LDS loads are in flight makes the compiler wait for all
 // of them: per-step data that way would drain the ring every step.)
 struct Int8NoSide {
@@ -160,10 +161,11 @@ struct Int8Ring {
   }
 
   // The same with operand B row r at brow(r) (K bytes, 16-byte aligned, any
-  // r the tile touches mapped to a readable row), and step(k, acc) called
-  // once the MFMAs of K step k are in acc (it may fold and clear them: the
-  // next step accumulates onto whatever it leaves).  With a side policy,
-  // `ring` holds kBytesWith<Side> bytes.
+  // r the tile touches mapped to a readable row), and step(k, q, acc)
+  // called once the MFMAs of quarter q (32 columns) of K step k are in acc,
+  // quarters in order (it may fold and clear them: the next quarter
+  // accumulates onto whatever it leaves).  With a side policy, `ring` holds
+  // kBytesWith<Side> bytes.
   template <class BRow, class Step = Int8NoStep, class Side = Int8NoSide>
   __device__ static void run_rows(const int8_t* __restrict__ A, const BRow& brow, int N, int K,
                                   long long n0, long long m0, int8_t* ring, v16i (&acc)[FN][FM],
@@ -271,17 +273,18 @@ struct Int8Ring {
       if constexpr (XL > 0)
         if (part == 0) side->issue(pstep, wave, side_base(pstage));
     };
-    // Side data is read after the MFMAs of the step's last in-loop quarter,
-    // so the reads overlap them and the barrier's LDS wait covers them.
+    // Side data is read with the fragments of the step's last in-loop quarter
+    // (the stage is refilled after the barrier).
     static_assert(XL == 0 || QPS > 1, "side data read within the quarter loop");
     for (int k = 0; k + 1 < nk; ++k) {
 #pragma unroll
       for (int q = 1; q < QPS; ++q) {
         if (q < SPREAD && k > 0) issue_part(q);
         read_frags(stage, q, q & 1);
-        mfmas((q - 1) & 1);
         if constexpr (XL > 0)
           if (q == QPS - 1) side->read(k, side_base(stage));
+        mfmas((q - 1) & 1);
+        step(k, q - 1, acc);
       }
       // Loads issued: steps up to k+S-1, all parts; step k+1 must be in.
       wait_vmcnt<GT * (S - 2)>();
@@ -293,7 +296,7 @@ struct Int8Ring {
       stage = stage + 1 < S ? stage + 1 : 0;
       read_frags(stage, 0, 0);
       mfmas((QPS - 1) & 1);
-      step(k, acc);
+      step(k, QPS - 1, acc);
     }
     {
       if constexpr (XL > 0) side->read(nk - 1, side_base(stage));
@@ -301,10 +304,15 @@ struct Int8Ring {
 #pragma unroll
       for (int q = 1; q < QPS; ++q) {
         if (q < qn) read_frags(stage, q, q & 1);
-        if (q - 1 < qn) mfmas((q - 1) & 1);
+        if (q - 1 < qn) {
+          mfmas((q - 1) & 1);
+          step(nk - 1, q - 1, acc);
+        }
       }
-      if (QPS - 1 < qn) mfmas((QPS - 1) & 1);
-      step(nk - 1, acc);
+      if (QPS - 1 < qn) {
+        mfmas((QPS - 1) & 1);
+        step(nk - 1, QPS - 1, acc);
+      }
     }
     // No global->LDS load may still be in flight when the workgroup's LDS is
     // released.

@@ -509,6 +509,10 @@ def test_cint8_row_plane_swiglu_sizes(qc, oracle, synth, dev, m, rows):
     (32, True, False, 40, 0, False),
     (32, True, True, 100, 0, False),
     (32, True, False, 6, 1, False),
+    (64, False, False, 12, 0, False),   # groups of 32 columns (two folds per K step)
+    (64, True, False, 40, 0, False),
+    (64, True, True, 100, 0, False),
+    (64, True, False, 8, 1, False),
 ])
 def test_cint8_row_plane_route_groups(qc, oracle, synth, dev, groups, affine, fractional, m,
                                       mode, wide):

@@ -88,7 +88,8 @@ def test_qgemv_qgemm_graph_replay(qc, dev, fmt, m, n):
 @pytest.mark.parametrize("mode,m,rows,groups", [(0, 16, 4096, 1), (0, 3, 1000, 1),
                                                 (1, 16, 2048, 1), (1, 100, 512, 1),
                                                 (0, 300, 1024, 1), (0, 24, 2048, 16),
-                                                (1, 8, 1024, 16), (0, 40, 1024, 32)])
+                                                (1, 8, 1024, 16), (0, 40, 1024, 32),
+                                                (1, 12, 1024, 64)])
 def test_cint8_project_graph_replay(qc, dev, mode, m, rows, groups):
     """Canonical int8 projections on the row-plane route (plain and SwiGLU,
     row scales and groups of 128 or 64 columns), each call a prep and one GEMM
