@@ -110,10 +110,11 @@ __device__ __forceinline__ void load4(const void* x, long long xr, int c, int xt
 // planes of row m are rows 4m + t (row 4m + 3 is zeroed).  A row holding NaN
 // or +-inf gets the maximum +inf, zero digits and the flag exponent
 // kPlanesNonfinite.  The digit sums S_t go to dsum[(m * ngroups + g) * 3 + t]
-// over each group g of gsize columns (GROUPED: gsize 64 or a multiple of 128,
-// with k % 128 == 0, so the 4 gsize / 4 lanes of a group, at most a half
+// over each group g of gsize columns (GROUPED: gsize 32, 64 or a multiple of
+// 128, with k % 128 == 0, so the gsize / 4 lanes of a group, at most a half
 // wave, lie in one half wave), else over the row (ngroups = 1).
-constexpr int kPlanesMaxGroups = kPlanesMaxK / 64;
+constexpr int kPlanesMaxGroups = kPlanesMaxK / 32;
+static_assert(kPlanesMaxGroups * 32 >= kPlanesMaxK, "group sums of the smallest groups");
 template <bool GROUPED>
 __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     const void* __restrict__ x, int xtype, long long ldx, int k, bool vec, int gsize,

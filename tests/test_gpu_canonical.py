@@ -580,6 +580,31 @@ def test_cint8_row_plane_route_groups(qc, oracle, synth, dev, groups, affine, fr
         assert np.allclose(Y[fin], want[fin], rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("rows,cols,groups,m", [
+    (200, 16384, 512, 6),     # the largest K: 512 groups of 32
+    (200, 16384, 256, 6),     # 256 groups of 64
+    (200, 16384, 128, 40),    # 128 groups of 128
+    (130, 512, 16, 1100),     # groups of 32 over two chunks of activation rows
+])
+def test_cint8_row_plane_route_groups_sizes(qc, oracle, synth, dev, rows, cols, groups, m):
+    """Group-scaled weights on the row-plane route at the largest K (the most
+    groups the prep's per-group digit sums hold) and with more activation rows
+    than one pass takes: every output within the 1e-4 normalised contract of
+    the f64 product over the exactly decoded weights (affine, integral zero
+    points)."""
+    import torch
+    print(f"cint8 planes groups sizes rows={rows} cols={cols} groups={groups} m={m}", flush=True)
+    codes, scales, zeros = _tensor(synth, 900 + groups, rows, cols, groups, True)
+    keep = [_dev(qc, dev, a) for a in (codes, scales, zeros)]
+    w = qc.cint8_weights(keep[0], keep[1], keep[2], rows, cols, groups)
+    what = oracle.cint8_dequant(codes, scales, zeros, rows, cols, groups)
+    x = synth.normal_fast(950 + m, m * cols).reshape(m, cols)
+    X = torch.from_numpy(x).to(dev)
+    Y = torch.full((m, rows), 7.0, device=dev)
+    assert qc.cint8_project_raw(0, [w], X, 0, m, [Y], [0]) == 0
+    _check_contract(Y.cpu().numpy(), x, what)
+
+
 def test_cint8_row_plane_route_nonfinite_rows(qc, oracle, synth, dev):
     """Activation rows holding +-inf or NaN on the row-plane route: those
     rows get the reference's f32 result class per output, the finite rows
