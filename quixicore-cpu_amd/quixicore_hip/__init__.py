@@ -342,9 +342,9 @@ def set_qgemm_rows(mode=0):
 
 def set_cint8_dot(mode=0):
     """Canonical int8 projections: 0 = the row-plane route (int8 MFMA) for two
-    or more activation rows with row scales, else the exact digit-dot kernels
-    where they apply; 1 = never the row-plane route; -1 = always the f32
-    kernel."""
+    or more activation rows (three, or five for groups of 32, with group
+    scales), else the exact digit-dot kernels where they apply; 1 = never the
+    row-plane route; -1 = always the f32 kernel."""
     _check(lib.qc_hip_set_cint8_dot(mode), "set_cint8_dot")
 
 
