@@ -627,12 +627,22 @@ hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const i
                      H ? (SWIGLU ? (T2 ? 7 : 8) : (T2 ? 10 : 12))
                        : SWIGLU ? (GROUPED ? 5 : 6) : 8,
                      1, 2, SWIGLU);
+  // From 9 rows, wave tiles of 32 plane rows (more waves per tile, so each
+  // holds a quarter or half of the fragments and of the grouped fold's work):
+  // K=4096, N=14336, M=16: row scales 23.8 -> 22.6 us, groups of 128 32.3 ->
+  // 27.8, of 64 46.7 -> 37.3; M=32: 27.5 -> 26.8 / 33.0 -> 31.7; M=64: 35.5 ->
+  // 33.4 / 49.9 -> 45.1.  (64-column steps have too few B rows per wave's
+  // load at 8 waves; SwiGLU at 33-64 rows gained nothing.)
   if (mc <= 16)
-    return QC_PLANES(64, TM, H ? (SWIGLU ? (T2 ? 6 : 8) : 10) : SWIGLU ? 4 : 6, 1, 2, SWIGLU);
-  if (mc <= 32) return QC_PLANES(128, TM, H ? 8 : 4, 2, 2, SWIGLU);
+    return QC_PLANES(64, TM, H ? (SWIGLU ? (T2 ? 6 : 8) : 10) : SWIGLU ? 4 : 6, 2, 2, SWIGLU);
+  if (mc <= 32) {
+    if constexpr (H) return QC_PLANES(128, TM, 8, 2, 2, SWIGLU);
+    else return QC_PLANES(128, TM, 4, 4, 2, SWIGLU);
+  }
   if (mc <= 64) {
     if constexpr (SWIGLU) return QC_PLANES(256, TM, H ? (T2 ? 5 : 6) : 3, 4, 2, true);
-    else return QC_PLANES(256, TM, H ? 6 : 3, 4, 1, false);
+    else if constexpr (H) return QC_PLANES(256, TM, 6, 4, 1, false);
+    else return QC_PLANES(256, TM, 3, 8, 1, false);
   }
   // group sums in registers beside 256 x 256 tiles would spill: 256 x 128 above 64 rows
   if constexpr (GROUPED) {

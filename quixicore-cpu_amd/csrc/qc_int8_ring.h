@@ -145,7 +145,6 @@ struct Int8Ring {
   template <class Side>
   static constexpr int kBytesWith = kBytes + S * NW * Side::kLoads * 256;
   static_assert(FN >= 1 && FM >= 1 && GW >= 1 && GX >= 1 && S >= 2, "tile shape");
-  static_assert(KL == 64 || (GW % 2 == 0 && GX % 2 == 0), "8-row groups alternate swizzle parity");
   static_assert(G * (S - 1) < 64, "vmcnt range");
 
   // Wave tile origin within the workgroup tile (A rows, B rows).
@@ -179,14 +178,17 @@ struct Int8Ring {
 
     // Load j of a wave covers operand rows r = RPL * (wave * GW + j) + lane / CPR
     // (A; likewise B with GX), lane writing slot lane % CPR of its row.  Swizzle
-    // key of row r: (r >> 1) & (CPR - 1).  128-byte lines: 4 * (j & 1) +
-    // (lane >> 4), as GW and GX are even; 64-byte halves: (lane >> 3) & 3.
+    // key of row r: (r >> 1) & (CPR - 1).  128-byte lines: 4 * (the parity of
+    // the load's 8-row block, wave * GW + j) + (lane >> 4) (j & 1 when GW is
+    // even); 64-byte halves: (lane >> 3) & 3.
     const int8_t* src[G];
-    int coff[2];
+    int coff[G];
 #pragma unroll
-    for (int par = 0; par < 2; ++par)
-      coff[par] = KL == 128 ? ((lane & 7) ^ (4 * par + (lane >> 4))) * 16
-                            : ((lane & 3) ^ ((lane >> 3) & 3)) * 16;
+    for (int j = 0; j < G; ++j) {
+      const int par = (j < GW ? wave * GW + j : wave * GX + (j - GW)) & 1;
+      coff[j] = KL == 128 ? ((lane & 7) ^ (4 * par + (lane >> 4))) * 16
+                          : ((lane & 3) ^ ((lane >> 3) & 3)) * 16;
+    }
 #pragma unroll
     for (int j = 0; j < GW; ++j) {
       long long r = n0 + RPL * (wave * GW + j) + lane / CPR;
@@ -200,7 +202,7 @@ struct Int8Ring {
       const int k0 = step * KL;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        int off = k0 + coff[j & 1];
+        int off = k0 + coff[j];
         off = off < K - 16 ? off : K - 16;
         int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
@@ -264,7 +266,7 @@ struct Int8Ring {
       const int k0 = pstep * KL;
 #pragma unroll
       for (int j = part * G / SPREAD; j < (part + 1) * G / SPREAD; ++j) {
-        int off = k0 + coff[j & 1];
+        int off = k0 + coff[j];
         off = off < K - 16 ? off : K - 16;
         int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
