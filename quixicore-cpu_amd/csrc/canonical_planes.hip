@@ -64,28 +64,56 @@ constexpr int kPrepThreads = 1024;
 constexpr int kPrepWaves = kPrepThreads / 64;
 constexpr int kPrepGroups = kPlanesMaxK / (4 * kPrepThreads);
 
+// Maximum over the workgroup of non-negative values (DPP within each wave,
+// then the 16 wave maxima read back as four 16-byte words), to every lane.
 __device__ __forceinline__ float block_max(float v, float* red) {
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  v = wave_max_nonneg(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  float r = red[0];
+  const float4* r4 = reinterpret_cast<const float4*>(red);
+  float r = 0.0f;
 #pragma unroll
-  for (int w = 1; w < kPrepWaves; ++w) r = fmaxf(r, red[w]);
+  for (int w = 0; w < kPrepWaves / 4; ++w) {
+    const float4 q = r4[w];
+    r = fmaxf(r, fmaxf(fmaxf(q.x, q.y), fmaxf(q.z, q.w)));
+  }
   return r;
 }
 
+// Sum over the 64 lanes of a wavefront, in lane 63 (row sums by row_shr, then
+// row broadcasts; lanes a DPP mask leaves out add 0).
+template <int CTRL, int ROW_MASK, int BANK_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ int dpp_i32_masked(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO);
+}
+__device__ __forceinline__ int wave_sum_lane63_i32(int v) {
+  int t = v + dpp_i32_masked<0x111, 0xF, 0xF, true>(v);
+  t += dpp_i32_masked<0x112, 0xF, 0xF, true>(v);
+  t += dpp_i32_masked<0x113, 0xF, 0xF, true>(v);
+  t += dpp_i32_masked<0x114, 0xF, 0xE, false>(t);
+  t += dpp_i32_masked<0x118, 0xF, 0xC, false>(t);
+  t += dpp_i32_masked<0x142, 0xA, 0xF, false>(t);
+  t += dpp_i32_masked<0x143, 0xC, 0xF, false>(t);
+  return t;
+}
+
+// The three digit sums over the workgroup (exact in int32), to every lane.
 __device__ __forceinline__ void block_sum3(int (&v)[3], int (*red)[kPrepWaves]) {
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
-    for (int off = 32; off > 0; off >>= 1) v[t] += __shfl_xor(v[t], off);
-    if ((threadIdx.x & 63) == 0) red[t][threadIdx.x >> 6] = v[t];
+    v[t] = wave_sum_lane63_i32(v[t]);
+    if ((threadIdx.x & 63) == 63) red[t][threadIdx.x >> 6] = v[t];
   }
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
-    int r = red[t][0];
+    const int4* r4 = reinterpret_cast<const int4*>(red[t]);
+    int r = 0;
 #pragma unroll
-    for (int w = 1; w < kPrepWaves; ++w) r += red[t][w];
+    for (int w = 0; w < kPrepWaves / 4; ++w) {
+      const int4 q = r4[w];
+      r += (q.x + q.y) + (q.z + q.w);
+    }
     v[t] = r;
   }
 }
@@ -112,18 +140,23 @@ __device__ __forceinline__ void load4(const void* x, long long xr, int c, int xt
 // kPlanesNonfinite.  The digit sums S_t go to dsum[(m * ngroups + g) * 3 + t]
 // over each group g of gsize columns (GROUPED: gsize 32, 64 or a multiple of
 // 128, with k % 128 == 0, so the gsize / 4 lanes of a group, at most a half
-// wave, lie in one half wave), else over the row (ngroups = 1).
+// wave, lie in one half wave), else over the row (ngroups = 1); only the
+// zero-point terms read them, so without zero points (sums false) they are
+// neither formed nor written.
 constexpr int kPlanesMaxGroups = kPlanesMaxK / 32;
 static_assert(kPlanesMaxGroups * 32 >= kPlanesMaxK, "group sums of the smallest groups");
+static_assert(kPrepWaves % 4 == 0, "wave partials read as 16-byte words");
 template <bool GROUPED>
 __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     const void* __restrict__ x, int xtype, long long ldx, int k, bool vec, int gsize,
-    int ngroups, int8_t* __restrict__ planes, int* __restrict__ rexp, int* __restrict__ dsum) {
-  __shared__ float fred[kPrepWaves];
-  __shared__ int ired[3][kPrepWaves];
+    int ngroups, bool sums, int8_t* __restrict__ planes, int* __restrict__ rexp,
+    int* __restrict__ dsum) {
+  __shared__ __attribute__((aligned(16))) float fred[kPrepWaves];
+  __shared__ __attribute__((aligned(16))) int ired[3][kPrepWaves];
   __shared__ int gsum[GROUPED ? 3 * kPlanesMaxGroups : 1];
   if constexpr (GROUPED) {
-    for (int i = threadIdx.x; i < 3 * ngroups; i += kPrepThreads) gsum[i] = 0;
+    if (sums)
+      for (int i = threadIdx.x; i < 3 * ngroups; i += kPrepThreads) gsum[i] = 0;
   }
   const int m = blockIdx.x;
   const long long xr = static_cast<long long>(m) * ldx;
@@ -172,7 +205,7 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
     *reinterpret_cast<uint32_t*>(p0 + k + c) = w1;
     *reinterpret_cast<uint32_t*>(p0 + 2LL * k + c) = w2;
     *reinterpret_cast<uint32_t*>(p0 + 3LL * k + c) = 0u;
-    if constexpr (GROUPED) {
+    if (GROUPED && sums) {
       // the gl consecutive lanes of one group (4 columns each)
       const int gl = gsize < 128 ? gsize / 4 : 32;
 #pragma unroll
@@ -186,15 +219,15 @@ __global__ __launch_bounds__(kPrepThreads) void cint8_planes_prep(
       }
     }
   }
+  if (threadIdx.x == 0) rexp[m] = bad ? kPlanesNonfinite : e;
+  if (!sums) return;
   if constexpr (GROUPED) {
     __syncthreads();
-    if (threadIdx.x == 0) rexp[m] = bad ? kPlanesNonfinite : e;
     for (int i = threadIdx.x; i < 3 * ngroups; i += kPrepThreads)
       dsum[3LL * m * ngroups + i] = gsum[i];
   } else {
     block_sum3(sum, ired);
     if (threadIdx.x == 0) {
-      rexp[m] = bad ? kPlanesNonfinite : e;
       dsum[3 * m] = sum[0];
       dsum[3 * m + 1] = sum[1];
       dsum[3 * m + 2] = sum[2];
@@ -683,6 +716,9 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
                    L.ldx % 4 == 0;
   const int ngroups = GROUPED ? sg.groups : 1;
   const int gsize = GROUPED ? sg.gsize : k;
+  // the digit sums only enter the zero-point terms
+  bool sums = false;
+  for (int i = 0; i < nmat; ++i) sums = sums || sg.zero[i] != nullptr;
   // chunks of kPlanesChunkM rows, one after the other in one buffer
   const int mc0 = std::min(kPlanesChunkM, m);
   const size_t bytes = up256(4ull * mc0 * k) + up256(4ull * mc0) + up256(12ull * mc0 * ngroups);
@@ -697,7 +733,7 @@ hipError_t launch_planes(const CSegs& sg, const CInt8Launch& L, int m, int k, hi
     int* dsum = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rexp) + up256(4ull * mc));
     const void* xc = static_cast<const uint8_t*>(L.x) + es * static_cast<size_t>(m0) * L.ldx;
     cint8_planes_prep<GROUPED><<<mc, kPrepThreads, 0, s>>>(xc, L.xtype, L.ldx, k, vec, gsize,
-                                                           ngroups, planes, rexp, dsum);
+                                                           ngroups, sums, planes, rexp, dsum);
     e = hipGetLastError();
     if (e == hipSuccess && L.mode == 1) {
       const PlaneOut o{sg.w[0], sg.scale[0], sg.zero[0], sg.w[1], sg.scale[1], sg.zero[1],

@@ -142,10 +142,12 @@ def test_qgemm_small_batch(qc, oracle, synth, dev, fmt, m):
                                         (0, 3, 5, 64), (1, 7, 3, 128), (0, 20, 130, 320),
                                         (1, 4, 14336, 4096), (0, 8, 4096, 4096),
                                         (1, 6, 1000, 14336), (0, 4, 700, 8256),
-                                        (1, 9, 260, 4096), (0, 12, 4096, 448)])
+                                        (1, 9, 260, 4096), (0, 12, 4096, 448),
+                                        (0, 10, 300, 8192), (1, 12, 300, 16448)])
 def test_qgemm_mfma_shapes(qc, oracle, synth, dev, fmt, m, n, k):
     """Small-batch GEMM shapes that exercise M beyond one 32-row launch,
-    partial last K stages, ragged N and split-K partial sums."""
+    partial last K stages, ragged N and split-K partial sums (K up to 16448
+    on the f16 / bf16 layouts)."""
     import torch
     print(f"qgemm shapes fmt={fmt} m={m} n={n} k={k}", flush=True)
     packed, _ = _case(oracle, synth, fmt, n, k, 77 + m)
