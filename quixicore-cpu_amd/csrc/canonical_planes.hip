@@ -664,17 +664,22 @@ hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const i
   // holds a quarter or half of the fragments and of the grouped fold's work):
   // K=4096, N=14336, M=16: row scales 23.8 -> 22.6 us, groups of 128 32.3 ->
   // 27.8, of 64 46.7 -> 37.3; M=32: 27.5 -> 26.8 / 33.0 -> 31.7; M=64: 35.5 ->
-  // 33.4 / 49.9 -> 45.1.  (64-column steps have too few B rows per wave's
-  // load at 8 waves; SwiGLU at 33-64 rows gained nothing.)
+  // 33.4 / 49.9 -> 45.1.  64-column steps: 8 waves over a B tile of 64 rows
+  // (four 1 KB blocks, loaded by waves 0..3) from 33 rows, and for groups of
+  // 32 or SwiGLU from 17: groups of 64 at M=48 / 64 75.2 / 75.0 -> 67.8 / 66.8
+  // us, groups of 32 at M=24 / 32 / 48 / 64 68.2 / 68.8 / 116 / 117 -> 54.0 /
+  // 54.7 / 90.1 / 91.2, SwiGLU M=32 73.6 -> 64.5 (groups of 64) and 117 ->
+  // 92.6 (32); groups of 64 at 17-32 rows were 2.6 us slower that way.  (SwiGLU
+  // at 33-64 rows gained nothing from 8 waves.)
   if (mc <= 16)
     return QC_PLANES(64, TM, H ? (SWIGLU ? (T2 ? 6 : 8) : 10) : SWIGLU ? 4 : 6, 2, 2, SWIGLU);
   if (mc <= 32) {
-    if constexpr (H) return QC_PLANES(128, TM, 8, 2, 2, SWIGLU);
+    if constexpr (H) return QC_PLANES(128, TM, 8, (T2 || SWIGLU) ? 4 : 2, 2, SWIGLU);
     else return QC_PLANES(128, TM, 4, 4, 2, SWIGLU);
   }
   if (mc <= 64) {
     if constexpr (SWIGLU) return QC_PLANES(256, TM, H ? (T2 ? 5 : 6) : 3, 4, 2, true);
-    else if constexpr (H) return QC_PLANES(256, TM, 6, 4, 1, false);
+    else if constexpr (H) return QC_PLANES(256, TM, 6, 8, 1, false);
     else return QC_PLANES(256, TM, 3, 8, 1, false);
   }
   // group sums in registers beside 256 x 256 tiles would spill: 256 x 128 above 64 rows

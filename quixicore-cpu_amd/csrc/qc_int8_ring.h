@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "qc_lds_dma.h"
 
 namespace qc {
@@ -137,7 +139,11 @@ struct Int8Ring {
   static constexpr int NW = WGN * WGM;                     // WGN x WGM grid of wavefronts
   static constexpr int WN = TN / WGN, WM = TM / WGM;       // wave tile
   static constexpr int FN = WN / 32, FM = WM / 32;         // 32 x 32 tiles per wave
-  static constexpr int GW = TN / RPL / NW, GX = TM / RPL / NW;  // 1 KB loads per wave per step
+  static constexpr int GW = TN / RPL / NW;                 // 1 KB loads per wave per step (A)
+  // B: GX per wave; when the B tile has fewer 1 KB blocks than there are
+  // waves (BSPLIT), waves 0 .. TM / RPL - 1 load one each and the others none.
+  static constexpr bool BSPLIT = TM / RPL < NW;
+  static constexpr int GX = BSPLIT ? 1 : TM / RPL / NW;
   static constexpr int G = GW + GX;
   static constexpr int kStage = (TN + TM) * KL;
   static constexpr int kBytes = S * kStage;
@@ -145,6 +151,7 @@ struct Int8Ring {
   template <class Side>
   static constexpr int kBytesWith = kBytes + S * NW * Side::kLoads * 256;
   static_assert(FN >= 1 && FM >= 1 && GW >= 1 && GX >= 1 && S >= 2, "tile shape");
+  static_assert(!BSPLIT || TM % RPL == 0, "whole B blocks");
   static_assert(G * (S - 1) < 64, "vmcnt range");
 
   // Wave tile origin within the workgroup tile (A rows, B rows).
@@ -175,9 +182,22 @@ struct Int8Ring {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     auto side_base = [&](int stage) { return ring + kBytes + stage * NW * XL * 256; };
+    // (BSPLIT) this wave loads a B block: its loads per step are GT, else GT - 1
+    const bool has_b = !BSPLIT || wave < TM / RPL;
+    auto load_j = [&](int j) { return j < GW || has_b; };
+    // wait until at most n steps' loads of this wave are in flight
+    auto wait_steps = [&](auto n) {
+      if constexpr (BSPLIT) {
+        if (has_b) wait_vmcnt<GT * decltype(n)::value>();
+        else wait_vmcnt<(GT - 1) * decltype(n)::value>();
+      } else {
+        wait_vmcnt<GT * decltype(n)::value>();
+      }
+    };
 
     // Load j of a wave covers operand rows r = RPL * (wave * GW + j) + lane / CPR
-    // (A; likewise B with GX), lane writing slot lane % CPR of its row.  Swizzle
+    // (A; likewise B with GX, which with BSPLIT is block `wave` for the waves
+    // that load one), lane writing slot lane % CPR of its row.  Swizzle
     // key of row r: (r >> 1) & (CPR - 1).  128-byte lines: 4 * (the parity of
     // the load's 8-row block, wave * GW + j) + (lane >> 4) (j & 1 when GW is
     // even); 64-byte halves: (lane >> 3) & 3.
@@ -206,7 +226,7 @@ struct Int8Ring {
         off = off < K - 16 ? off : K - 16;
         int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
-        load_lds16(src[j] + off, dst);
+        if (load_j(j)) load_lds16(src[j] + off, dst);
       }
       if constexpr (XL > 0) side->issue(step, wave, side_base(stage));
     };
@@ -250,7 +270,7 @@ struct Int8Ring {
 
 #pragma unroll
     for (int st = 0; st < S; ++st) issue(st < nk ? st : nk - 1, st);
-    wait_vmcnt<GT * (S - 1)>();
+    wait_steps(std::integral_constant<int, S - 1>());
     ring_barrier();
     read_frags(0, 0, 0);
     // With three or more stages the loads of a step are spread over the
@@ -270,7 +290,7 @@ struct Int8Ring {
         off = off < K - 16 ? off : K - 16;
         int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
-        load_lds16(src[j] + off, dst);
+        if (load_j(j)) load_lds16(src[j] + off, dst);
       }
       if constexpr (XL > 0)
         if (part == 0) side->issue(pstep, wave, side_base(pstage));
@@ -289,7 +309,7 @@ struct Int8Ring {
         step(k, q - 1, acc);
       }
       // Loads issued: steps up to k+S-1, all parts; step k+1 must be in.
-      wait_vmcnt<GT * (S - 2)>();
+      wait_steps(std::integral_constant<int, S - 2>());
       wait_lgkmcnt0();
       ring_barrier();
       pstep = k + S < nk ? k + S : nk - 1;

@@ -513,6 +513,8 @@ def test_cint8_row_plane_swiglu_sizes(qc, oracle, synth, dev, m, rows):
     (64, True, False, 40, 0, False),
     (64, True, True, 100, 0, False),
     (64, True, False, 8, 1, False),
+    (64, True, False, 24, 0, False),    # 8-wave 128 x 64 tiles, B loads on waves 0..3
+    (32, True, True, 28, 1, False),     # SwiGLU, groups of 64, 8-wave 128 x 128 tiles
 ])
 def test_cint8_row_plane_route_groups(qc, oracle, synth, dev, groups, affine, fractional, m,
                                       mode, wide):
