@@ -463,7 +463,19 @@ struct GroupSide {
 // of 128), else in int64 on a branch the wave takes only when one of its
 // lanes needs it; each A_t is then rounded to f32 once, so the two forms give
 // the same bits.
-template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL, int GPS>
+// The GEMM's per-quarter hook for the ring, with the ring's fresh-sum period.
+template <int FRESH, class F>
+struct FoldStep {
+  static constexpr int kFresh = FRESH;
+  F f;
+  template <class Acc>
+  __device__ void operator()(int k, int q, Acc& a) const {
+    f(k, q, a);
+  }
+};
+
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL, int GPS,
+          bool SPAN>
 __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
     const int8_t* __restrict__ planes, int mc, const PlaneOut o, const int* __restrict__ rexp,
     const int* __restrict__ dsum, const void* __restrict__ x, int xtype, long long ldx, int m0,
@@ -504,6 +516,12 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
   const int zlim = GROUPED ? static_cast<int>(((1LL << 31) - 1 - (gs << 14)) / (gs << 7)) : 0;
   // (SwiGLU: gate and up both have zero points or neither)
   const bool has_zero = o.zero != nullptr;
+  // Groups that lie within one K step (GPS per step) end at fixed quarters:
+  // the ring starts each group's sums from zero.  A group spanning several
+  // steps (SPAN: 256 columns and more) carries its sums over steps, and the
+  // fold clears them.
+  static_assert(!SPAN || (GROUPED && KL == 128 && GPS == 1), "multi-step groups");
+  constexpr int FRESH = GROUPED && !SPAN ? R::QPS / GPS : 0;
   auto fold = [&](int, int q, v16i (&a)[R::FN][R::FM]) {
     if constexpr (GROUPED) {
       // a group's last quarter (q is a constant in the unrolled quarter loops)
@@ -563,22 +581,27 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
         for (int i = 0; i < R::FN; ++i)
 #pragma unroll
           for (int g = 0; g < 4; ++g) facc[i][j][g] = fmaf(sg, fv[i][g], facc[i][j][g]);
-        // plane row 3 of every activation row is zero: its sums stay 0
+        // the next group's sums start from zero: its first MFMAs take a zero
+        // accumulator (FRESH), or the sums are cleared here (plane row 3 of
+        // every activation row is zero: its sums stay 0)
+        if constexpr (FRESH == 0) {
 #pragma unroll
-        for (int i = 0; i < R::FN; ++i)
+          for (int i = 0; i < R::FN; ++i)
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
-            if ((e & 3) != 3) a[i][j][e] = 0;
+            for (int e = 0; e < 16; ++e)
+              if ((e & 3) != 3) a[i][j][e] = 0;
+        }
       }
     }
   };
+  const FoldStep<FRESH, decltype(fold)> step{fold};
   if constexpr (SWIGLU)
     R::run_rows(planes, PairedRows{o.w, o.w2, o.rows, k}, 4 * mc, k,
-                static_cast<long long>(tn) * TN, static_cast<long long>(tm) * TM, ring, acc, fold,
+                static_cast<long long>(tn) * TN, static_cast<long long>(tm) * TM, ring, acc, step,
                 &side);
   else
     R::run_rows(planes, Int8Rows{o.w, o.rows, k}, 4 * mc, k, static_cast<long long>(tn) * TN,
-                static_cast<long long>(tm) * TM, ring, acc, fold, &side);
+                static_cast<long long>(tm) * TM, ring, acc, step, &side);
   // projection of activation row r on the row of fragment j
   auto value = [&](int i, int j, int g, int r, long long n) -> float {
     const bool second = SWIGLU && (j & 1);
@@ -620,7 +643,8 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
   }
 }
 
-template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL, int GPS>
+template <int TN, int TM, int S, int WGN, int WGM, bool SWIGLU, bool GROUPED, int KL, int GPS,
+          bool SPAN>
 hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                               const int* dsum, const void* x, int xtype, long long ldx, int m0,
                               int k, hipStream_t s) {
@@ -628,7 +652,7 @@ hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, c
   // SwiGLU: 64 B rows per 32 output rows
   const long long brows = SWIGLU ? 64LL * ((o.rows + 31) / 32) : o.rows;
   const int tiles_m = static_cast<int>((brows + TM - 1) / TM);
-  cint8_planes_gemm<TN, TM, S, WGN, WGM, SWIGLU, GROUPED, KL, GPS>
+  cint8_planes_gemm<TN, TM, S, WGN, WGM, SWIGLU, GROUPED, KL, GPS, SPAN>
       <<<tiles_n * tiles_m, 64 * WGN * WGM, 0, s>>>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0,
                                                     k, tiles_n, tiles_m);
   return hipGetLastError();
@@ -643,7 +667,7 @@ hipError_t launch_planes_gemm(const int8_t* planes, int mc, const PlaneOut& o, c
 // step): the same tiles with about twice the stages (half the bytes each),
 // within the 6-bit vmcnt and the 160 KB of LDS; GPS = 2 carries twice the
 // side loads.
-template <bool SWIGLU, bool GROUPED, int KL, int GPS = 1>
+template <bool SWIGLU, bool GROUPED, int KL, int GPS = 1, bool SPAN = false>
 hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const int* rexp,
                         const int* dsum, const void* x, int xtype, long long ldx, int m0, int k,
                         hipStream_t s) {
@@ -651,9 +675,9 @@ hipError_t launch_fused(const int8_t* planes, int mc, const PlaneOut& o, const i
   static_assert(GPS == 1 || KL == 64, "two groups per step: groups of 32");
   constexpr int TM = SWIGLU ? 128 : 64;
   constexpr bool H = KL == 64, T2 = GPS == 2;
-#define QC_PLANES(TN_, TM_, S_, WGN_, WGM_, SW_)                                            \
-  launch_planes_gemm<TN_, TM_, S_, WGN_, WGM_, SW_, GROUPED, KL, GPS>(planes, mc, o, rexp, dsum, \
-                                                                      x, xtype, ldx, m0, k, s)
+#define QC_PLANES(TN_, TM_, S_, WGN_, WGM_, SW_)                                     \
+  launch_planes_gemm<TN_, TM_, S_, WGN_, WGM_, SW_, GROUPED, KL, GPS, SPAN>(              \
+      planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s)
   // (grouped SwiGLU: 5 stages, as its side loads would take 6 past the vmcnt range)
   if (mc <= 8)
     return QC_PLANES(32, TM,
@@ -705,6 +729,9 @@ hipError_t launch_fused_kl(const int8_t* planes, int mc, const PlaneOut& o, cons
       return launch_fused<SWIGLU, true, 64, 2>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k,
                                                s);
   }
+  if (GROUPED && o.gsize > 128)   // groups of several 128-column steps
+    return launch_fused<SWIGLU, GROUPED, 128, 1, GROUPED>(planes, mc, o, rexp, dsum, x, xtype, ldx,
+                                                          m0, k, s);
   return launch_fused<SWIGLU, GROUPED, 128>(planes, mc, o, rexp, dsum, x, xtype, ldx, m0, k, s);
 }
 

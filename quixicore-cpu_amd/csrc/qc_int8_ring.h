@@ -69,8 +69,12 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// The default per-quarter hook of Int8Ring::run_rows: nothing.
+// The default per-quarter hook of Int8Ring::run_rows: nothing.  A hook
+// whose kFresh is n > 0 consumes the sums of every n quarters (n dividing
+// the quarters of a step): the MFMAs of each n-quarter run's first quarter
+// then start from zero instead of accumulating, and the hook need not clear.
 struct Int8NoStep {
+  static constexpr int kFresh = 0;
   template <class Acc>
   __device__ void operator()(int, int, Acc&) const {}
 };
@@ -259,13 +263,19 @@ struct Int8Ring {
 #pragma unroll
       for (int j = 0; j < FM; ++j) fb[slot][j] = *reinterpret_cast<const v4i*>(sx + 32 * j * KL);
     };
-    auto mfmas = [&](int slot) {
+    // quarter qq of a step (a constant once the quarter loops are unrolled)
+    constexpr int FRESH = Step::kFresh;
+    static_assert(FRESH == 0 || QPS % FRESH == 0, "fresh runs within a step");
+    auto mfmas = [&](int slot, int qq) {
+      const bool fresh = FRESH > 0 && qq % (FRESH > 0 ? FRESH : 1) == 0;
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot][i], fb[slot][j], acc[i][j],
-                                                            0, 0, 0);
+          acc[i][j] = fresh ? __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot][i], fb[slot][j],
+                                                                    v16i{}, 0, 0, 0)
+                            : __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot][i], fb[slot][j],
+                                                                    acc[i][j], 0, 0, 0);
     };
 
 #pragma unroll
@@ -305,7 +315,7 @@ struct Int8Ring {
         read_frags(stage, q, q & 1);
         if constexpr (XL > 0)
           if (q == QPS - 1) side->read(k, side_base(stage));
-        mfmas((q - 1) & 1);
+        mfmas((q - 1) & 1, q - 1);
         step(k, q - 1, acc);
       }
       // Loads issued: steps up to k+S-1, all parts; step k+1 must be in.
@@ -317,7 +327,7 @@ struct Int8Ring {
       issue_part(0);
       stage = stage + 1 < S ? stage + 1 : 0;
       read_frags(stage, 0, 0);
-      mfmas((QPS - 1) & 1);
+      mfmas((QPS - 1) & 1, QPS - 1);
       step(k, QPS - 1, acc);
     }
     {
@@ -327,12 +337,12 @@ struct Int8Ring {
       for (int q = 1; q < QPS; ++q) {
         if (q < qn) read_frags(stage, q, q & 1);
         if (q - 1 < qn) {
-          mfmas((q - 1) & 1);
+          mfmas((q - 1) & 1, q - 1);
           step(nk - 1, q - 1, acc);
         }
       }
       if (QPS - 1 < qn) {
-        mfmas((QPS - 1) & 1);
+        mfmas((QPS - 1) & 1, QPS - 1);
         step(nk - 1, QPS - 1, acc);
       }
     }
