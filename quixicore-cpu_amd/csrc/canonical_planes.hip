@@ -529,6 +529,27 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
       if ((q + 1) % QPG != 0) return;
       const int u = (q + 1) / QPG - 1;
       if (!side.ready) return;                  // uniform: not the group's last step
+      if (!has_zero) {                          // uniform: s_g (2^14 D0 + 2^7 D1 + D2)
+#pragma unroll
+        for (int j = 0; j < R::FM; ++j) {
+          const float sg = side.sc[u][j];
+#pragma unroll
+          for (int i = 0; i < R::FN; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+              facc[i][j][g] = fmaf(sg, combine(a[i][j][4 * g], a[i][j][4 * g + 1],
+                                               a[i][j][4 * g + 2]),
+                                   facc[i][j][g]);
+          if constexpr (FRESH == 0) {
+#pragma unroll
+            for (int i = 0; i < R::FN; ++i)
+#pragma unroll
+              for (int e = 0; e < 16; ++e)
+                if ((e & 3) != 3) a[i][j][e] = 0;
+          }
+        }
+        return;
+      }
 #pragma unroll
       for (int j = 0; j < R::FM; ++j) {
         // zi: the integral zero point the int32 form subtracts (0 for none,
