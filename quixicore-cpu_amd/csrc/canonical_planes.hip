@@ -480,7 +480,11 @@ __global__ __launch_bounds__(64 * WGN * WGM) void cint8_planes_gemm(
     const int8_t* __restrict__ planes, int mc, const PlaneOut o, const int* __restrict__ rexp,
     const int* __restrict__ dsum, const void* __restrict__ x, int xtype, long long ldx, int m0,
     int k, int tiles_n, int tiles_m) {
-  using R = Int8Ring<TN, TM, S, WGN, WGM, KL>;
+  // Tiles of up to 128 plane rows serve up to 32 activation rows, all in one A
+  // tile: each weight row is then read by one workgroup (non-temporal loads;
+  // K=4096, N=14336: M=2 17.3 -> 15.7 us, M=8 18.3 -> 17.2, SwiGLU M=16 32.6 ->
+  // 29.6; with two or more A tiles, M=512, the hint cost 1.5%).
+  using R = Int8Ring<TN, TM, S, WGN, WGM, KL, (TN <= 128)>;
   using Side =
       std::conditional_t<GROUPED, GroupSide<TN, TM, WGN, WGM, SWIGLU, KL, GPS>, Int8NoSide>;
   static_assert(!SWIGLU || R::FM % 2 == 0, "gate / up fragment pairs");

@@ -52,6 +52,13 @@ __device__ __forceinline__ void load_lds16(const int8_t* g, int8_t* lds) {
 #endif
 }
 
+// The same with the non-temporal hint (nt), for bytes read once.
+__device__ __forceinline__ void load_lds16_nt(const int8_t* g, int8_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 2);
+#endif
+}
+
 // The same with 4 bytes per lane, to LDS byte lds + 4 * lane.
 __device__ __forceinline__ void load_lds4(const void* g, int8_t* lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -134,7 +141,10 @@ struct Int8Rows {
 // past K (their loads read a clamped in-row address and are never used).
 // Rows past N (A) or M (B) load a clamped in-range row; the epilogue must
 // not store their products.
-template <int TN, int TM, int S, int WGN, int WGM, int KL>
+//
+// NTB: every operand-B row is read by one workgroup only (one A tile along
+// N), so its loads carry the non-temporal hint.
+template <int TN, int TM, int S, int WGN, int WGM, int KL, bool NTB = false>
 struct Int8Ring {
   static_assert(KL == 128 || KL == 64, "K step is a whole or a half cache line");
   static constexpr int QPS = KL / 32;                      // K quarters per step
@@ -230,7 +240,9 @@ struct Int8Ring {
         off = off < K - 16 ? off : K - 16;
         int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
-        if (load_j(j)) load_lds16(src[j] + off, dst);
+        if (!load_j(j)) continue;
+        if (NTB && j >= GW) load_lds16_nt(src[j] + off, dst);
+        else load_lds16(src[j] + off, dst);
       }
       if constexpr (XL > 0) side->issue(step, wave, side_base(stage));
     };
@@ -300,7 +312,9 @@ struct Int8Ring {
         off = off < K - 16 ? off : K - 16;
         int8_t* dst = j < GW ? base + (wave * GW + j) * 1024
                              : base + TN * KL + (wave * GX + (j - GW)) * 1024;
-        if (load_j(j)) load_lds16(src[j] + off, dst);
+        if (!load_j(j)) continue;
+        if (NTB && j >= GW) load_lds16_nt(src[j] + off, dst);
+        else load_lds16(src[j] + off, dst);
       }
       if constexpr (XL > 0)
         if (part == 0) side->issue(pstep, wave, side_base(pstage));
