@@ -309,16 +309,18 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
         span(j, q0c, nbytes);
         const uint8_t* base = wrow[r] + static_cast<long long>(q0c) * 68;
         // every lane loads (a lane past the item re-reads its last bytes), so
-        // no register waits on a condition; a whole item needs no clamping
+        // no register waits on a condition; a whole item needs no clamping.
+        // The item's lines are read once, in whole: non-temporal loads (q8_0
+        // 4096 x 4096: 5.41 -> 5.19 us).
         const bool whole = nbytes == kQ8Item;   // wave-uniform
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int off = whole ? 16 * lane + 1024 * i : min(16 * (lane + 64 * i), nbytes - 16);
-          const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(base + off);
+          const u32x4_a4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(base + off));
           w[t][4 * i] = v.x; w[t][4 * i + 1] = v.y; w[t][4 * i + 2] = v.z; w[t][4 * i + 3] = v.w;
         }
-        w[t][16] = *reinterpret_cast<const uint32_t*>(
-            base + (whole ? 4096 + 4 * lane : min(4096 + 4 * lane, nbytes - 4)));
+        w[t][16] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
+            base + (whole ? 4096 + 4 * lane : min(4096 + 4 * lane, nbytes - 4))));
       } else {
         const int p = min(p0 + 64 * j, pend - 1);
         load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
