@@ -220,10 +220,17 @@ __device__ __forceinline__ float fused_activation(float v, int act) {
 // costs occupancy from 4 rows per wave on: taken for 1-2 rows per wave only
 // (q8_0 4096 x 4096, 8 waves x 2 rows: 5.93-6.09 -> 5.75-5.85 us; 4096 ->
 // 14336 with 4 rows per wave was 2-5% slower chunked, so it keeps the records).
-constexpr int kQ8Item = 64 * 68;
+template <int FMT>
+constexpr int item_bytes() { return 128 * Fmt<FMT>::block_bytes; }   // 64 pairs
+// 16-byte chunks per lane of an item (2 or 4), then a 256-byte tail of one
+// dword per lane: the pair's dwords of a per-lane record
+template <int FMT>
+constexpr int item_x4() { return item_bytes<FMT>() / 1024; }
+static_assert(item_bytes<kQ4_0>() % 1024 == 256 && item_bytes<kQ8_0>() % 1024 == 256,
+              "whole chunks and a dword tail per lane");
 template <int FMT, int NPM, int RB>
-constexpr bool q8_chunked() { return FMT == kQ8_0 && NPM == 1 && RB <= 2; }
-__host__ __device__ constexpr size_t q8_stage_off(int kc) { return (lds_size(kc) + 15) / 16 * 16; }
+constexpr bool chunked() { return NPM == 1 && (FMT == kQ4_0 || RB <= 2); }
+__host__ __device__ constexpr size_t stage_off(int kc) { return (lds_size(kc) + 15) / 16 * 16; }
 
 // NW wavefronts of RB rows each, up to NPM pairs per lane per K chunk.  The (pair j,
 // row r) items of a chunk are loaded in j-major order with at most WIN items
@@ -247,7 +254,8 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
   constexpr int T = NPM * RB;
   constexpr int NT = 64 * NW;
   constexpr int HPT = (NPM * 256 + NT - 1) / NT;   // half-blocks of x per thread
-  constexpr bool CHUNKED = q8_chunked<FMT, NPM, RB>();   // see kQ8Item
+  constexpr bool CHUNKED = chunked<FMT, NPM, RB>();   // see item_bytes
+  constexpr int IB = item_bytes<FMT>(), X4 = item_x4<FMT>();
   const int lane = threadIdx.x & 63;
   const long long row_bytes = static_cast<long long>(k >> 5) * BB;
   const uint8_t* wrow[RB];
@@ -294,33 +302,33 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
     float xv[HPT][16];
     load_x<HPT, NT, VEC>(xv, x + c0, clen);
     uint32_t w[T][PD];
-    // chunked items: pairs [q0c, q0c + nbytes / 68) of the row (one clamped
-    // pair past the chunk); a chunk that would run past them is moved back
-    // to end with them (its overlap rewrites the same bytes)
+    // chunked items: pairs [q0c, q0c + nbytes / (2 BB)) of the row (one
+    // clamped pair past the chunk); a chunk that would run past them is moved
+    // back to end with them (its overlap rewrites the same bytes)
     auto span = [&](int j, int& q0c, int& nbytes) {
       const int q0 = pbeg + 64 * j;
       q0c = min(q0, pend - 1);
-      nbytes = (q0 < pend ? min(64, pend - q0) : 1) * 68;
+      nbytes = (q0 < pend ? min(64, pend - q0) : 1) * (2 * BB);
     };
     auto issue = [&](int t) {
       const int j = t / RB, r = t % RB;
       if constexpr (CHUNKED) {
         int q0c, nbytes;
         span(j, q0c, nbytes);
-        const uint8_t* base = wrow[r] + static_cast<long long>(q0c) * 68;
+        const uint8_t* base = wrow[r] + static_cast<long long>(q0c) * (2 * BB);
         // every lane loads (a lane past the item re-reads its last bytes), so
         // no register waits on a condition; a whole item needs no clamping.
         // The item's lines are read once, in whole: non-temporal loads (q8_0
-        // 4096 x 4096: 5.41 -> 5.19 us).
-        const bool whole = nbytes == kQ8Item;   // wave-uniform
+        // 4096 x 4096: 5.41 -> 5.12 us).
+        const bool whole = nbytes == IB;   // wave-uniform
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < X4; ++i) {
           const int off = whole ? 16 * lane + 1024 * i : min(16 * (lane + 64 * i), nbytes - 16);
           const u32x4_a4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(base + off));
           w[t][4 * i] = v.x; w[t][4 * i + 1] = v.y; w[t][4 * i + 2] = v.z; w[t][4 * i + 3] = v.w;
         }
-        w[t][16] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
-            base + (whole ? 4096 + 4 * lane : min(4096 + 4 * lane, nbytes - 4))));
+        w[t][4 * X4] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
+            base + (whole ? 1024 * X4 + 4 * lane : min(1024 * X4 + 4 * lane, nbytes - 4))));
       } else {
         const int p = min(p0 + 64 * j, pend - 1);
         load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
@@ -348,30 +356,30 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
           // (lanes read what other lanes stored: wave_lds_sync orders the
           // previous item's reads before these stores, and the stores before
           // this item's reads)
-          uint8_t* const stage = lds + q8_stage_off(kc) + (threadIdx.x >> 6) * kQ8Item;
+          uint8_t* const stage = lds + stage_off(kc) + (threadIdx.x >> 6) * IB;
           int q0c, nbytes;
           span(j, q0c, nbytes);
           wave_lds_sync();
-          if (nbytes == kQ8Item) {   // a whole item (wave-uniform)
+          if (nbytes == IB) {   // a whole item (wave-uniform)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < X4; ++i)
               *reinterpret_cast<u32x4_a4*>(stage + 16 * lane + 1024 * i) =
                   u32x4_a4{w[t][4 * i], w[t][4 * i + 1], w[t][4 * i + 2], w[t][4 * i + 3]};
-            *reinterpret_cast<uint32_t*>(stage + 4096 + 4 * lane) = w[t][16];
+            *reinterpret_cast<uint32_t*>(stage + 1024 * X4 + 4 * lane) = w[t][4 * X4];
           } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < X4; ++i) {
               const int off = 16 * (lane + 64 * i);
               if (off < nbytes)
                 *reinterpret_cast<u32x4_a4*>(stage + min(off, nbytes - 16)) =
                     u32x4_a4{w[t][4 * i], w[t][4 * i + 1], w[t][4 * i + 2], w[t][4 * i + 3]};
             }
-            if (4096 + 4 * lane < nbytes)
-              *reinterpret_cast<uint32_t*>(stage + 4096 + 4 * lane) = w[t][16];
+            if (1024 * X4 + 4 * lane < nbytes)
+              *reinterpret_cast<uint32_t*>(stage + 1024 * X4 + 4 * lane) = w[t][4 * X4];
           }
           wave_lds_sync();
           const uint32_t* rec =
-              reinterpret_cast<const uint32_t*>(stage + (min(p, pend - 1) - q0c) * 68);
+              reinterpret_cast<const uint32_t*>(stage + (min(p, pend - 1) - q0c) * (2 * BB));
           if (p < pend) acc[r] = pair_dot<FMT>(rec, g, acc[r]);
         } else {
           if (p < pend) acc[r] = pair_dot<FMT>(w[t], g, acc[r]);
@@ -926,7 +934,7 @@ hipError_t launch_one(const GemvSegs& sg, const float* x, int k, int* status, hi
   const unsigned grid = static_cast<unsigned>((static_cast<long long>(n) + NW * RB - 1) / (NW * RB));
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;
   // digit records, then (chunked q8_0 items) each wave's item staging area
-  const size_t dlds = q8_chunked<FMT, NPM, RB>() ? q8_stage_off(kc) + static_cast<size_t>(NW) * kQ8Item
+  const size_t dlds = chunked<FMT, NPM, RB>() ? stage_off(kc) + static_cast<size_t>(NW) * item_bytes<FMT>()
                                                  : lds_size(kc);
   if constexpr (KIND == 0) {
     if (vec)
