@@ -209,17 +209,22 @@ __device__ __forceinline__ float fused_activation(float v, int act) {
                   : v / (1.0f + expf(-v));
 }
 
-// q8_0 items with one pair per lane (NPM = 1: 64 consecutive block pairs of
-// one row, 4352 bytes) are read in whole lines -- lane l takes the 16-byte
-// chunks l + 64 i (i < 4) and the dword 1024 + l -- and handed to the lanes
-// through a per-wave LDS staging area, one item at a time: a lane's own
-// 68-byte pair straddles cache lines, and five loads per lane of such records
-// keep re-requesting the same lines (a read of the same rows took 13.1-14.2
-// us as records, 12.0-12.2 us as chunks restaged through LDS).  17 dwords per
-// lane and item, as for the records, but the staging adds ~20 VGPRs, which
-// costs occupancy from 4 rows per wave on: taken for 1-2 rows per wave only
-// (q8_0 4096 x 4096, 8 waves x 2 rows: 5.93-6.09 -> 5.75-5.85 us; 4096 ->
-// 14336 with 4 rows per wave was 2-5% slower chunked, so it keeps the records).
+// Whole-line items: an item (64 consecutive block pairs of one row, one pair
+// per lane: 2304 bytes for q4_0, 4352 for q8_0) is read as 2 or 4 16-byte
+// chunks per lane, contiguous across the wave (lane l takes chunks l + 64 i),
+// and a dword per lane for its last 256 bytes, with the non-temporal hint, and
+// handed to the lanes through a per-wave LDS staging area, one item at a time.
+// A lane's own 36- or 68-byte pair straddles cache lines: per-lane record
+// loads keep re-requesting the same lines, and with the hint fetch them twice.
+// As many dwords per lane as a record.  Measured on MI355X (same process):
+// q4_0 4096 -> 14336 (7 rows per wave) 8.16 -> 7.80 us, q8_0 4096 -> 14336
+// 13.0 -> 11.9, 4096 x 4096 5.41 -> 5.12, q8_0 up+gate 24.4 -> 23.4.  Kept on
+// records: q4_0 with 1-2 rows per wave (4096 x 4096 4.30 -> 4.37 us, QKV 6.62
+// -> 6.75 us that way) and K above 4096 (more than one pair per lane and
+// chunk; the staging area then takes LDS that a second workgroup per CU would
+// use: q8_0 14336 x 14336 42.5 -> 48.6 us, q4_0 14336 -> 4096 9.5 -> 9.9 us;
+// only q8_0 14336 -> 4096, one workgroup per CU either way, gained, 13.8 ->
+// 13.0 us).
 template <int FMT>
 constexpr int item_bytes() { return 128 * Fmt<FMT>::block_bytes; }   // 64 pairs
 // 16-byte chunks per lane of an item (2 or 4), then a 256-byte tail of one
@@ -229,7 +234,7 @@ constexpr int item_x4() { return item_bytes<FMT>() / 1024; }
 static_assert(item_bytes<kQ4_0>() % 1024 == 256 && item_bytes<kQ8_0>() % 1024 == 256,
               "whole chunks and a dword tail per lane");
 template <int FMT, int NPM, int RB>
-constexpr bool chunked() { return NPM == 1 && (FMT == kQ4_0 || RB <= 2); }
+constexpr bool chunked() { return NPM == 1 && (FMT == kQ8_0 || RB >= 4); }
 __host__ __device__ constexpr size_t stage_off(int kc) { return (lds_size(kc) + 15) / 16 * 16; }
 
 // NW wavefronts of RB rows each, up to NPM pairs per lane per K chunk.  The (pair j,
