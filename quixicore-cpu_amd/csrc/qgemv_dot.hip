@@ -237,6 +237,53 @@ template <int FMT, int NPM, int RB>
 constexpr bool chunked() { return NPM == 1 && (FMT == kQ8_0 || RB >= 4); }
 __host__ __device__ constexpr size_t stage_off(int kc) { return (lds_size(kc) + 15) / 16 * 16; }
 
+// The first nbytes (<= item_bytes) of an item at `base` in whole lines:
+// chunk i of lane l holds bytes 16 (l + 64 i), the tail dword bytes 1024 X4 +
+// 4 l; a lane past nbytes re-reads the item's last bytes, so every lane loads
+// and no register waits on a condition.  Lines read once: non-temporal.
+template <int FMT>
+__device__ __forceinline__ void load_item_lines(uint32_t* w, const uint8_t* base, int nbytes,
+                                                int lane) {
+  constexpr int IB = item_bytes<FMT>(), X4 = item_x4<FMT>();
+  const bool whole = nbytes == IB;   // wave-uniform; a whole item needs no clamping
+#pragma unroll
+  for (int i = 0; i < X4; ++i) {
+    const int off = whole ? 16 * lane + 1024 * i : min(16 * (lane + 64 * i), nbytes - 16);
+    const u32x4_a4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(base + off));
+    w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+  }
+  w[4 * X4] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
+      base + (whole ? 1024 * X4 + 4 * lane : min(1024 * X4 + 4 * lane, nbytes - 4))));
+}
+
+// Those bytes into the wave's staging area (lanes then read what other lanes
+// stored: wave_lds_sync orders the previous item's reads before these
+// stores, and the stores before this item's reads).
+template <int FMT>
+__device__ __forceinline__ void stage_item(uint8_t* stage, const uint32_t* w, int nbytes,
+                                           int lane) {
+  constexpr int IB = item_bytes<FMT>(), X4 = item_x4<FMT>();
+  wave_lds_sync();
+  if (nbytes == IB) {   // a whole item (wave-uniform)
+#pragma unroll
+    for (int i = 0; i < X4; ++i)
+      *reinterpret_cast<u32x4_a4*>(stage + 16 * lane + 1024 * i) =
+          u32x4_a4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+    *reinterpret_cast<uint32_t*>(stage + 1024 * X4 + 4 * lane) = w[4 * X4];
+  } else {
+#pragma unroll
+    for (int i = 0; i < X4; ++i) {
+      const int off = 16 * (lane + 64 * i);
+      if (off < nbytes)
+        *reinterpret_cast<u32x4_a4*>(stage + min(off, nbytes - 16)) =
+            u32x4_a4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+    }
+    if (1024 * X4 + 4 * lane < nbytes)
+      *reinterpret_cast<uint32_t*>(stage + 1024 * X4 + 4 * lane) = w[4 * X4];
+  }
+  wave_lds_sync();
+}
+
 // NW wavefronts of RB rows each, up to NPM pairs per lane per K chunk.  The (pair j,
 // row r) items of a chunk are loaded in j-major order with at most WIN items
 // in flight: item t + WIN is issued just before item t is computed, so the
@@ -260,7 +307,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
   constexpr int NT = 64 * NW;
   constexpr int HPT = (NPM * 256 + NT - 1) / NT;   // half-blocks of x per thread
   constexpr bool CHUNKED = chunked<FMT, NPM, RB>();   // see item_bytes
-  constexpr int IB = item_bytes<FMT>(), X4 = item_x4<FMT>();
+  constexpr int IB = item_bytes<FMT>();
   const int lane = threadIdx.x & 63;
   const long long row_bytes = static_cast<long long>(k >> 5) * BB;
   const uint8_t* wrow[RB];
@@ -320,20 +367,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
       if constexpr (CHUNKED) {
         int q0c, nbytes;
         span(j, q0c, nbytes);
-        const uint8_t* base = wrow[r] + static_cast<long long>(q0c) * (2 * BB);
-        // every lane loads (a lane past the item re-reads its last bytes), so
-        // no register waits on a condition; a whole item needs no clamping.
-        // The item's lines are read once, in whole: non-temporal loads (q8_0
-        // 4096 x 4096: 5.41 -> 5.12 us).
-        const bool whole = nbytes == IB;   // wave-uniform
-#pragma unroll
-        for (int i = 0; i < X4; ++i) {
-          const int off = whole ? 16 * lane + 1024 * i : min(16 * (lane + 64 * i), nbytes - 16);
-          const u32x4_a4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(base + off));
-          w[t][4 * i] = v.x; w[t][4 * i + 1] = v.y; w[t][4 * i + 2] = v.z; w[t][4 * i + 3] = v.w;
-        }
-        w[t][4 * X4] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
-            base + (whole ? 1024 * X4 + 4 * lane : min(1024 * X4 + 4 * lane, nbytes - 4))));
+        load_item_lines<FMT>(w[t], wrow[r] + static_cast<long long>(q0c) * (2 * BB), nbytes, lane);
       } else {
         const int p = min(p0 + 64 * j, pend - 1);
         load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
@@ -364,25 +398,7 @@ __global__ __launch_bounds__(64 * NW) void qgemv_dot_kernel(const GemvSegs segs,
           uint8_t* const stage = lds + stage_off(kc) + (threadIdx.x >> 6) * IB;
           int q0c, nbytes;
           span(j, q0c, nbytes);
-          wave_lds_sync();
-          if (nbytes == IB) {   // a whole item (wave-uniform)
-#pragma unroll
-            for (int i = 0; i < X4; ++i)
-              *reinterpret_cast<u32x4_a4*>(stage + 16 * lane + 1024 * i) =
-                  u32x4_a4{w[t][4 * i], w[t][4 * i + 1], w[t][4 * i + 2], w[t][4 * i + 3]};
-            *reinterpret_cast<uint32_t*>(stage + 1024 * X4 + 4 * lane) = w[t][4 * X4];
-          } else {
-#pragma unroll
-            for (int i = 0; i < X4; ++i) {
-              const int off = 16 * (lane + 64 * i);
-              if (off < nbytes)
-                *reinterpret_cast<u32x4_a4*>(stage + min(off, nbytes - 16)) =
-                    u32x4_a4{w[t][4 * i], w[t][4 * i + 1], w[t][4 * i + 2], w[t][4 * i + 3]};
-            }
-            if (1024 * X4 + 4 * lane < nbytes)
-              *reinterpret_cast<uint32_t*>(stage + 1024 * X4 + 4 * lane) = w[t][4 * X4];
-          }
-          wave_lds_sync();
+          stage_item<FMT>(stage, w[t], nbytes, lane);
           const uint32_t* rec =
               reinterpret_cast<const uint32_t*>(stage + (min(p, pend - 1) - q0c) * (2 * BB));
           if (p < pend) acc[r] = pair_dot<FMT>(rec, g, acc[r]);
@@ -691,6 +707,10 @@ __host__ __device__ constexpr size_t w8_terms_off(int kc) {
 __host__ __device__ constexpr size_t w8_lds_size(int kc, int nw, int rb) {
   return w8_terms_off(kc) + static_cast<size_t>(nw) * rb * (kc / 32) * 4;
 }
+// the per-wave staging areas of whole-line items follow
+__host__ __device__ constexpr size_t w8_stage_off(int kc, int nw, int rb) {
+  return (w8_lds_size(kc, nw, rb) + 15) / 16 * 16;
+}
 
 // Codes, scales and (q4_0) code sums of the loaded half-blocks into LDS; the
 // two halves of a block sit in lanes t and t^1.  A block holding NaN or
@@ -783,6 +803,8 @@ __global__ __launch_bounds__(64 * NW) void qgemv_w8a8_kernel(const uint8_t* __re
   constexpr int T = NPM * RB;
   constexpr int NT = 64 * NW;
   constexpr int HPT = (NPM * 256 + NT - 1) / NT;
+  constexpr bool CHUNKED = chunked<FMT, NPM, RB>();   // whole-line items, as in qgemv_dot_kernel
+  constexpr int IB = item_bytes<FMT>();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * NW + wave) * RB;
@@ -800,10 +822,22 @@ __global__ __launch_bounds__(64 * NW) void qgemv_w8a8_kernel(const uint8_t* __re
     float xv[HPT][16];
     load_x<HPT, NT, VEC>(xv, x + c0, clen);
     uint32_t w[T][PD];
+    // chunked items: pairs [q0c, q0c + nbytes / (2 BB)) of the row
+    auto span = [&](int j, int& q0c, int& nbytes) {
+      const int q0 = pbeg + 64 * j;
+      q0c = min(q0, pend - 1);
+      nbytes = (q0 < pend ? min(64, pend - q0) : 1) * (2 * BB);
+    };
     auto issue = [&](int t) {
       const int j = t / RB, r = t % RB;
-      const int p = min(p0 + 64 * j, pend - 1);
-      load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
+      if constexpr (CHUNKED) {
+        int q0c, nbytes;
+        span(j, q0c, nbytes);
+        load_item_lines<FMT>(w[t], wrow[r] + static_cast<long long>(q0c) * (2 * BB), nbytes, lane);
+      } else {
+        const int p = min(p0 + 64 * j, pend - 1);
+        load_pair<FMT>(w[t], wrow[r] + static_cast<long long>(p) * (2 * BB));
+      }
     };
 #pragma unroll
     for (int t = 0; t < T && t < WIN; ++t) issue(t);
@@ -825,9 +859,23 @@ __global__ __launch_bounds__(64 * NW) void qgemv_w8a8_kernel(const uint8_t* __re
       for (int r = 0; r < RB; ++r) {
         const int t = j * RB + r;
         if (t + WIN < T) issue(t + WIN);
+        uint32_t wl[PD];   // this lane's pair (chunked: restaged through LDS)
+        if constexpr (CHUNKED) {
+          uint8_t* const stage = lds + w8_stage_off(kc, NW, RB) + wave * IB;
+          int q0c, nbytes;
+          span(j, q0c, nbytes);
+          stage_item<FMT>(stage, w[t], nbytes, lane);
+          const uint32_t* rec = reinterpret_cast<const uint32_t*>(
+              stage + (min(p, pend - 1) - q0c) * (2 * BB));
+#pragma unroll
+          for (int d = 0; d < PD; ++d) wl[d] = rec[d];
+        } else {
+#pragma unroll
+          for (int d = 0; d < PD; ++d) wl[d] = w[t][d];
+        }
         if (p < pend) {
           float t0, t1;
-          pair_terms<FMT>(w[t], cx, meta, t0, t1);
+          pair_terms<FMT>(wl, cx, meta, t0, t1);
           *reinterpret_cast<float2*>(terms + r * (kc >> 5) + 2 * (p - pbeg)) = make_float2(t0, t1);
         }
       }
@@ -950,7 +998,9 @@ hipError_t launch_one(const GemvSegs& sg, const float* x, int k, int* status, hi
     // the caller guarantees a 16-byte aligned x
     qgemv_dot_kernel<FMT, NW, RB, NPM, WIN, true, true><<<grid, 64 * NW, dlds, s>>>(sg, x, k, kc);
   } else {
-    const size_t lds = w8_lds_size(kc, NW, RB);
+    const size_t lds = chunked<FMT, NPM, RB>()
+                           ? w8_stage_off(kc, NW, RB) + static_cast<size_t>(NW) * item_bytes<FMT>()
+                           : w8_lds_size(kc, NW, RB);
     if (vec)
       qgemv_w8a8_kernel<FMT, NW, RB, NPM, WIN, true><<<grid, 64 * NW, lds, s>>>(sg.w[0], x, sg.y[0], n, k, kc, status);
     else
