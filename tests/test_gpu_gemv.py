@@ -62,25 +62,30 @@ def test_qgemv_baseline_configs(qc, oracle, synth, dev, fmt, n, k):
     _check_rows(oracle, fmt, packed, x, y.cpu().numpy(), n, k)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 0])
-def test_q8_whole_line_items(qc, oracle, synth, dev, rows):
-    """q8_0 with 1-2 rows per wave reads each 64-pair item of a row in whole
-    lines and restages it through LDS: partial items (K not a multiple of
-    4096, a last chunk of one pair), rows of one pair, a misaligned x, and W
-    allocated to its exact size so the last row ends the buffer."""
+@pytest.mark.parametrize("fmt,rows", [(0, 1), (0, 2), (0, 4), (0, 0), (1, 4), (1, 7), (1, 14),
+                                      (1, 0)])
+def test_whole_line_items(qc, oracle, synth, dev, fmt, rows):
+    """Shapes whose GEMV reads each 64-pair item of a row in whole lines and
+    restages it through LDS (q8_0 at any row count, q4_0 from 4 rows per
+    wave, K <= 4096), beside those that keep per-lane records (K > 4096):
+    partial items (K not a multiple of 4096, a last chunk of one pair), rows
+    of one pair, a misaligned x, and W allocated to its exact size so the
+    last row ends the buffer."""
     import torch
+    bb = 34 if fmt == 0 else 18
     qc.set_gemv_rows_per_wave(rows)
     try:
-        for n, k in ((1, 64), (7, 192), (65, 2048), (33, 4160), (130, 6144), (9, 8256)):
+        for n, k in ((1, 64), (7, 192), (65, 2048), (33, 4160), (130, 6144), (9, 8256),
+                     (200, 4096)):
             for x_off in (0, 1):
-                print(f"q8 whole-line rows={rows} n={n} k={k} x_off={x_off}", flush=True)
-                packed, x = _case(oracle, synth, 0, n, k, 4000 + n + k)
+                print(f"whole-line fmt={fmt} rows={rows} n={n} k={k} x_off={x_off}", flush=True)
+                packed, x = _case(oracle, synth, fmt, n, k, 4000 + n + k)
                 P = torch.from_numpy(packed).to(dev)
-                assert P.numel() == n * (k // 32) * 34
+                assert P.numel() == n * (k // 32) * bb
                 buf = torch.zeros(k + x_off, dtype=torch.float32, device=dev)
                 buf[x_off:] = torch.from_numpy(x).to(dev)
-                y = qc.qgemv(0, P, buf[x_off:], n, k)
-                _check_rows(oracle, 0, packed, x, y.cpu().numpy(), n, k)
+                y = qc.qgemv(fmt, P, buf[x_off:], n, k)
+                _check_rows(oracle, fmt, packed, x, y.cpu().numpy(), n, k)
     finally:
         qc.set_gemv_rows_per_wave(0)
 

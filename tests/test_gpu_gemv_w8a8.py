@@ -79,17 +79,21 @@ def test_qgemv_w8a8_misaligned(qc, oracle, synth, dev, w_offset, x_offset):
 
 
 def test_qgemv_w8a8_every_rows_per_wave(qc, oracle, synth, dev):
-    n, k = 1000, 4096
+    """Every rows-per-wave variant, bit for bit: whole-line items restaged
+    through LDS (q8_0, and q4_0 from 4 rows per wave) and per-lane records,
+    whole items (K = 4096) and partial ones (K = 1408: 22 pairs of 64)."""
+    n = 1000
     try:
-        for fmt in (0, 1):
-            packed = _weights(oracle, synth, fmt, n, k, 600 + fmt)
-            x = synth.normal_fast(602, k)
-            _, want = oracle.gemv_w8a8(fmt, packed, x, n, k)
-            for rows in (1, 2, 4, 7, 8, 14):
-                print(f"qgemv_w8a8 fmt={fmt} rows_per_wave={rows}", flush=True)
-                qc.set_gemv_rows_per_wave(rows)
-                st, got = _run(qc, dev, fmt, packed, x, n, k)
-                assert st == 0 and np.array_equal(_bits(got), _bits(want)), rows
+        for k in (4096, 1408):
+            for fmt in (0, 1):
+                packed = _weights(oracle, synth, fmt, n, k, 600 + fmt + k)
+                x = synth.normal_fast(602 + k, k)
+                _, want = oracle.gemv_w8a8(fmt, packed, x, n, k)
+                for rows in (1, 2, 4, 7, 8, 14):
+                    print(f"qgemv_w8a8 fmt={fmt} k={k} rows_per_wave={rows}", flush=True)
+                    qc.set_gemv_rows_per_wave(rows)
+                    st, got = _run(qc, dev, fmt, packed, x, n, k)
+                    assert st == 0 and np.array_equal(_bits(got), _bits(want)), (k, rows)
     finally:
         qc.set_gemv_rows_per_wave(0)
 
