@@ -299,7 +299,13 @@ __global__ __launch_bounds__(kThreads) void cint8_kernel(const CSegs segs, const
 // (three v_dot4 sums per 4 codes) and, for affine weights, xs = 2^e (2^14
 // D0 + 2^7 D1 + D2) ~ sum_j x_j over the same encoded x.  Group scales add
 // s_g (f - z_g xs) per block; row scales finish as s (sum f - z sum xs).
-template <int RB, bool GRP, bool AFF>
+//
+// WL (K above 4096): each row's 4 KB of a chunk is read in whole lines --
+// lane l takes bytes 16 l + 1024 i, non-temporal -- and handed to the lanes
+// through a 4 KB staging area per wave (lanes past a short last chunk re-read
+// its last bytes).  A lane's own 64-byte pair is half a line: per-lane loads
+// re-request lines, and with the hint fetch them twice.
+template <int RB, bool GRP, bool AFF, bool WL = false>
 __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
                                                              const void* __restrict__ x,
                                                              int xtype, int k, bool xvec) {
@@ -371,11 +377,20 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
     // 2. the codes of this lane's pair of every row (and group scales)
     uint4 cw[RB][4];
     float gs[RB][2], gz[RB][2];
+    const int cbytes = 64 * (pend - pbeg);   // this chunk's bytes of a row (WL)
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        cw[r][i] = *reinterpret_cast<const uint4*>(w[r] + 64LL * pc + 16 * i);
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (WL) {
+          const int off = min(16 * lane + 1024 * i, cbytes - 16);
+          const u32x4nt t = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4nt*>(w[r] + 64LL * pbeg + off));
+          cw[r][i] = make_uint4(t.x, t.y, t.z, t.w);
+        } else {
+          cw[r][i] = *reinterpret_cast<const uint4*>(w[r] + 64LL * pc + 16 * i);
+        }
+      }
       if constexpr (GRP) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -391,6 +406,24 @@ __global__ __launch_bounds__(kThreads) void cint8_dot_kernel(const CSegs segs,
     if (c0) lds_barrier();
     if (static_cast<int>(threadIdx.x) < nh) build_half<AFF>(lds, v, threadIdx.x, kc);
     lds_barrier();
+    if constexpr (WL) {
+      // each row's chunk through the wave's staging area, then this lane's pair
+      // (wave_lds_sync orders the previous reads before the stores, and the
+      // stores before the reads; lanes with a clamped offset store the same
+      // bytes as the lane that owns them)
+      uint8_t* const stage = lds + (lds_size(kc) + 15) / 16 * 16 + wave * 4096;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<uint4*>(stage + min(16 * lane + 1024 * i, cbytes - 16)) = cw[r][i];
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          cw[r][i] = *reinterpret_cast<const uint4*>(stage + 64 * (pc - pbeg) + 16 * i);
+      }
+    }
     if (live) {
       PairDigits g;
       read_digits<kQ8_0>(g, lds, p - pbeg, kc);
@@ -731,7 +764,12 @@ hipError_t launch_dot(const CSegs& sg, const void* x, int xtype, long long ldx, 
   const long long row_bytes = ldx * (xtype == QC_STORAGE_F32 ? 4 : 2);
   const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (m == 1 || row_bytes % 16 == 0);
   if constexpr (MB == 1) {
-    cint8_dot_kernel<RB, GRP, AFF><<<grid, kThreads, lds_size(4096), s>>>(sg, x, xtype, k, xvec);
+    if (k > 4096)
+      cint8_dot_kernel<RB, GRP, AFF, true>
+          <<<grid, kThreads, (lds_size(4096) + 15) / 16 * 16 + kWaves * 4096, s>>>(sg, x, xtype, k,
+                                                                               xvec);
+    else
+      cint8_dot_kernel<RB, GRP, AFF><<<grid, kThreads, lds_size(4096), s>>>(sg, x, xtype, k, xvec);
     return hipGetLastError();
   } else {
     for (int m0 = 0; m0 < m; m0 += MB) {

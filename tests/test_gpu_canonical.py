@@ -73,6 +73,9 @@ def _dev(qc, dev, arr, offset=0):
     (4096, 4096, 32, True, 1, 0, 0),      # affine, groups of 128
     (4096, 4096, 32, True, 1, 0, -1),
     (1000, 14336, 1, True, 1, 0, 0),      # affine channel scales, K in 4 chunks
+    (4096, 14336, 1, False, 1, 0, 0),     # down projection: whole-line code loads, 4 chunks
+    (700, 8192, 64, True, 1, 0, 0),       # affine groups of 128, two whole chunks
+    (300, 6208, 97, False, 1, 0, 0),      # groups of 64, a last chunk of 33 pairs
     (600, 4096, 128, True, 1, 0, 0),      # groups of 32
     (4096, 14336, 1, False, 2, 0, 1),     # 2-4 rows: digit dots, codes loaded once per pass
     (4096, 14336, 1, False, 3, 0, 0),     # 3 rows: the row-plane route (int8 MFMA)
